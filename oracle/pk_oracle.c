@@ -1,0 +1,1011 @@
+/*
+ * pk_oracle.c -- CPU restatement of the l4-parakeet-rs quantized-linear path.
+ *
+ * TEST INFRASTRUCTURE ONLY: the parity checker for libpk_linear.so.  Only
+ * tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg load it.
+ *
+ * The reference is Rust + CUDA and cannot be built in this image (no cargo,
+ * no crates, no nvcc), so each function below restates the reference's
+ * arithmetic from its source, citing file:line.  How each function is pinned
+ * (known answers from the reference's own tests, an independent library, a
+ * closed form or brute force) is recorded in tests/test_oracle_*.py; the
+ * functions without such a pin say "parity unpinned" in their comment.
+ */
+#include "pk_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+static int g_threads = 1;
+
+int orc_threads(void) { return g_threads; }
+
+void orc_set_threads(int threads) {
+    g_threads = threads < 1 ? 1 : threads;
+#ifdef _OPENMP
+    omp_set_num_threads(g_threads);
+#endif
+}
+
+static uint32_t f32_bits(float value) {
+    uint32_t bits;
+    memcpy(&bits, &value, 4);
+    return bits;
+}
+
+static float bits_f32(uint32_t bits) {
+    float value;
+    memcpy(&value, &bits, 4);
+    return value;
+}
+
+/* IEEE binary16, round-to-nearest-even (the `half` 2.7.1 crate's f16::from_f32,
+ * used by every reference packer, e.g. artifact.rs:421-423).  Written from the
+ * IEEE 754 definition; pinned against numpy.float16 exhaustively in tests. */
+uint16_t orc_f32_to_f16(float value) {
+    uint32_t x = f32_bits(value);
+    uint16_t sign = (uint16_t)((x >> 16) & 0x8000u);
+    uint32_t a = x & 0x7fffffffu;
+    if (a >= 0x7f800000u) {
+        return (uint16_t)(sign | (a > 0x7f800000u ? 0x7e00u : 0x7c00u));
+    }
+    if (a >= 0x477ff000u) { /* >= 65520 rounds to infinity */
+        return (uint16_t)(sign | 0x7c00u);
+    }
+    if (a < 0x38800000u) { /* below 2^-14: subnormal half, units of 2^-24 */
+        float q = nearbyintf(bits_f32(a) * 16777216.0f);
+        return (uint16_t)(sign | (uint16_t)q);
+    }
+    uint32_t r = a - (112u << 23); /* rebias 127 -> 15 */
+    r = r + 0x0fffu + ((r >> 13) & 1u);
+    return (uint16_t)(sign | (uint16_t)(r >> 13));
+}
+
+float orc_f16_to_f32(uint16_t bits) {
+    uint32_t sign = (uint32_t)(bits & 0x8000u) << 16;
+    uint32_t exponent = (bits >> 10) & 0x1fu;
+    uint32_t mantissa = bits & 0x3ffu;
+    if (exponent == 0) {
+        float magnitude = (float)mantissa * (1.0f / 16777216.0f);
+        return sign ? -magnitude : magnitude;
+    }
+    if (exponent == 31) {
+        return bits_f32(sign | 0x7f800000u | (mantissa << 13));
+    }
+    return bits_f32(sign | ((exponent + 112u) << 23) | (mantissa << 13));
+}
+
+/* OCP FP8 E4M3 ("e4m3fn": bias 7, no infinities, 0x7f/0xff NaN, max 448).
+ * The reference encodes with the float8 0.7.0 crate, F8E4M3::from_f32
+ * (quant_benchmark.rs:797, encoder.rs:410), and on device with the
+ * saturating __nv_fp8_e4m3 constructor (encoder.cu:557, linear.cu:544).
+ * Restated from the OCP 8-bit floating point specification: round to nearest
+ * even, finite overflow and +-inf saturate to +-448, NaN -> 0x7f.  Known
+ * answers 1.0->0x38, -1.0->0xb8, 448->0x7e (quant_benchmark.rs:962-966); the
+ * NaN encoding is parity unpinned (no reference test covers it). */
+uint8_t orc_f32_to_e4m3(float value) {
+    if (isnan(value)) {
+        return 0x7f;
+    }
+    uint8_t sign = signbit(value) ? 0x80 : 0x00;
+    float a = fabsf(value);
+    if (a >= 448.0f) {
+        return (uint8_t)(sign | 0x7e);
+    }
+    if (a < 0.015625f) { /* subnormal range: multiples of 2^-9 */
+        float q = nearbyintf(a * 512.0f);
+        return (uint8_t)(sign | (uint8_t)q);
+    }
+    int e;
+    float m = frexpf(a, &e); /* a = m * 2^e, m in [0.5, 1) */
+    int exponent = e - 1;
+    int mantissa = (int)nearbyintf((2.0f * m - 1.0f) * 8.0f);
+    if (mantissa == 8) {
+        mantissa = 0;
+        exponent += 1;
+    }
+    return (uint8_t)(sign | (uint8_t)(((exponent + 7) << 3) | mantissa));
+}
+
+float orc_e4m3_to_f32(uint8_t bits) {
+    int sign = bits & 0x80;
+    int exponent = (bits >> 3) & 15;
+    int mantissa = bits & 7;
+    float magnitude;
+    if (exponent == 15 && mantissa == 7) {
+        return NAN;
+    }
+    if (exponent == 0) {
+        magnitude = ldexpf((float)mantissa, -9);
+    } else {
+        magnitude = ldexpf(1.0f + (float)mantissa / 8.0f, exponent - 7);
+    }
+    return sign ? -magnitude : magnitude;
+}
+
+/* quant_benchmark.rs:827-829: round half to even, then clamp to +-127. */
+int8_t orc_quantize_i8(float value) {
+    float r = nearbyintf(value);
+    if (r > 127.0f) r = 127.0f;
+    if (r < -127.0f) r = -127.0f;
+    if (isnan(r)) return 0;
+    return (int8_t)r;
+}
+
+/* cuda.rs:809-818: splitmix64 finalizer mapped to [-amplitude, amplitude]. */
+float orc_pattern(uint64_t index, uint64_t salt, float amplitude) {
+    uint64_t value = index + salt * 0x9e3779b97f4a7c15ull;
+    value ^= value >> 30;
+    value *= 0xbf58476d1ce4e5b9ull;
+    value ^= value >> 27;
+    value *= 0x94d049bb133111ebull;
+    value ^= value >> 31;
+    float unit = (float)(value & 0xffffu) / 65535.0f;
+    return (unit * 2.0f - 1.0f) * amplitude;
+}
+
+void orc_pattern_fill(float* out, size_t count, uint64_t first_index, uint64_t salt,
+                      float amplitude) {
+    for (size_t i = 0; i < count; ++i) {
+        out[i] = orc_pattern(first_index + i, salt, amplitude);
+    }
+}
+
+/* ---- size contracts ----------------------------------------------------- */
+
+static size_t round_up(size_t value, size_t multiple) {
+    return (value + multiple - 1) / multiple * multiple;
+}
+
+/* exl3.rs:37-75.  out7 = {padded_in, padded_out, trellis0, trellis1,
+ * trellis2, trellis_bytes, scale_bytes}.  Returns 0, or -1 for empty / -2
+ * for an invalid bit rate (Exl3LayoutError). */
+int orc_exl3_layout(size_t logical_in, size_t logical_out, int qbits, size_t* out7) {
+    if (logical_in == 0 || logical_out == 0) return -1;
+    if (qbits < 1 || qbits > 8) return -2;
+    size_t pin = round_up(logical_in, 128);
+    size_t pout = round_up(logical_out, 128);
+    out7[0] = pin;
+    out7[1] = pout;
+    out7[2] = pin / 16;
+    out7[3] = pout / 16;
+    out7[4] = 16 * (size_t)qbits;
+    out7[5] = pin * pout * (size_t)qbits / 8;
+    out7[6] = 2 * (pin + pout);
+    return 0;
+}
+
+/* packing.rs:71-130.  format: 0 fp16, 1 fp8 e4m3, 2 int8, 3 Q4_K, 4 EXL3.
+ * out6 = {logical_in, logical_out, padded_in, padded_out, payload, metadata}.
+ * Returns 1 when a layout exists, 0 for Q4_K's "None", -1 for Empty. */
+int orc_estimate_linear(int format, size_t logical_in, size_t logical_out, int exl3_bits,
+                        size_t* out6) {
+    if (logical_in == 0 || logical_out == 0) return -1;
+    out6[0] = logical_in;
+    out6[1] = logical_out;
+    switch (format) {
+    case 0:
+    case 1:
+    case 2: {
+        size_t pin = round_up(logical_in, 128);
+        size_t pout = round_up(logical_out, 128);
+        out6[2] = pin;
+        out6[3] = pout;
+        out6[4] = pin * pout * (format == 0 ? 2 : 1);
+        out6[5] = format == 0 ? 0 : pout * 4;
+        return 1;
+    }
+    case 3:
+        if (logical_in % 256 != 0) return 0;
+        out6[2] = logical_in;
+        out6[3] = logical_out;
+        out6[4] = logical_out * (logical_in / 256) * 144;
+        out6[5] = 0;
+        return 1;
+    case 4: {
+        size_t e[7];
+        int status = orc_exl3_layout(logical_in, logical_out, exl3_bits, e);
+        if (status != 0) return status == -1 ? -1 : -2;
+        out6[2] = e[0];
+        out6[3] = e[1];
+        out6[4] = e[5];
+        out6[5] = e[6];
+        return 1;
+    }
+    default:
+        return -3;
+    }
+}
+
+/* ---- weight packers ----------------------------------------------------- */
+
+/* Per-row FP8: quant_benchmark.rs:779-801 and encoder.rs:367-412 (FP8
+ * branch): scale = max|w| / 448, byte = e4m3(w / scale).  An all-zero row
+ * gets scale 1 as in the request-time packer (encoder.cu:1141); the host
+ * packers would divide by zero there. */
+void orc_pack_fp8_rows(const uint16_t* w, int n, int k, uint8_t* q, float* scales) {
+    for (int row = 0; row < n; ++row) {
+        const uint16_t* values = w + (size_t)row * k;
+        float maximum = 0.0f;
+        for (int i = 0; i < k; ++i) maximum = fmaxf(maximum, fabsf(orc_f16_to_f32(values[i])));
+        float scale = maximum > 0.0f ? maximum / 448.0f : 1.0f;
+        scales[row] = scale;
+        for (int i = 0; i < k; ++i) {
+            q[(size_t)row * k + i] = orc_f32_to_e4m3(orc_f16_to_f32(values[i]) / scale);
+        }
+    }
+}
+
+/* Per-row INT8: quant_benchmark.rs:803-829: scale = max|w| / 127,
+ * q = clamp(rne(w / scale), +-127).  Zero rows get scale 1 (see above). */
+void orc_pack_int8_rows(const uint16_t* w, int n, int k, int8_t* q, float* scales) {
+    for (int row = 0; row < n; ++row) {
+        const uint16_t* values = w + (size_t)row * k;
+        float maximum = 0.0f;
+        for (int i = 0; i < k; ++i) maximum = fmaxf(maximum, fabsf(orc_f16_to_f32(values[i])));
+        float scale = maximum > 0.0f ? maximum / 127.0f : 1.0f;
+        scales[row] = scale;
+        for (int i = 0; i < k; ++i) {
+            q[(size_t)row * k + i] = orc_quantize_i8(orc_f16_to_f32(values[i]) / scale);
+        }
+    }
+}
+
+static int clamp_rne(float value, int lo, int hi) {
+    if (isnan(value)) return 0; /* Rust `NaN as i8` is 0 (encoder.rs:396-404) */
+    float r = nearbyintf(value);
+    if (r < (float)lo) r = (float)lo;
+    if (r > (float)hi) r = (float)hi;
+    return (int)r;
+}
+
+/* Per-row symmetric INT4: encoder.rs:378-407 (INT4 branch):
+ * scale = max over the row of max(w/7, -w/8) (folded from 0), q = clamp(rne(w /
+ * scale), -8, 7), byte j = q[2j] & 15 | (q[2j+1] & 15) << 4.  An all-zero row
+ * keeps scale 0 and packs to zero bytes (0/0 is NaN and `NaN as i8` is 0). */
+void orc_pack_int4_rows(const uint16_t* w, int n, int k, uint8_t* q, float* scales) {
+    for (int row = 0; row < n; ++row) {
+        const uint16_t* values = w + (size_t)row * k;
+        float scale = 0.0f;
+        for (int i = 0; i < k; ++i) {
+            float v = orc_f16_to_f32(values[i]);
+            scale = fmaxf(scale, fmaxf(v / 7.0f, -v / 8.0f));
+        }
+        scales[row] = scale;
+        for (int j = 0; j < k / 2; ++j) {
+            int a = clamp_rne(orc_f16_to_f32(values[2 * j]) / scale, -8, 7);
+            int b = clamp_rne(orc_f16_to_f32(values[2 * j + 1]) / scale, -8, 7);
+            q[(size_t)row * (k / 2) + j] = (uint8_t)((a & 15) | ((b & 15) << 4));
+        }
+    }
+}
+
+/* Group-wise asymmetric INT4, groups of 128 along K.  This format has no
+ * counterpart in the reference (its INT4 formats are the per-row symmetric one
+ * above and GGUF Q4_K); parity unpinned against the reference, pinned by its
+ * closed form.  Per (row, group): lo = min(0, min w), hi = max(0, max w),
+ * s = fp16((hi - lo) / 15) (1 if that is 0), z = clamp(rne(-lo / s), 0, 15),
+ * q = clamp(rne(w / s) + z, 0, 15); dequant (q - z) * s.  q is packed eight
+ * per uint32 along K, nibble i of word j holding k = 8j + i.  scales and zeros
+ * are fp16 [n x k/128]; zeros are integers in [0, 15]. */
+void orc_pack_int4_g128(const uint16_t* w, int n, int k, uint32_t* q, uint16_t* scales,
+                        uint16_t* zeros) {
+    int groups = k / 128;
+    for (int row = 0; row < n; ++row) {
+        for (int g = 0; g < groups; ++g) {
+            const uint16_t* values = w + (size_t)row * k + g * 128;
+            float lo = 0.0f, hi = 0.0f;
+            for (int i = 0; i < 128; ++i) {
+                float v = orc_f16_to_f32(values[i]);
+                lo = fminf(lo, v);
+                hi = fmaxf(hi, v);
+            }
+            float s = orc_f16_to_f32(orc_f32_to_f16((hi - lo) / 15.0f));
+            if (!(s > 0.0f)) s = 1.0f;
+            int z = clamp_rne(-lo / s, 0, 15);
+            scales[(size_t)row * groups + g] = orc_f32_to_f16(s);
+            zeros[(size_t)row * groups + g] = orc_f32_to_f16((float)z);
+            for (int j = 0; j < 16; ++j) {
+                uint32_t word = 0;
+                for (int i = 0; i < 8; ++i) {
+                    float v = orc_f16_to_f32(values[8 * j + i]);
+                    int level = clamp_rne(v / s, -64, 64) + z;
+                    level = level < 0 ? 0 : (level > 15 ? 15 : level);
+                    word |= (uint32_t)level << (4 * i);
+                }
+                q[(size_t)row * (k / 8) + g * 16 + j] = word;
+            }
+        }
+    }
+}
+
+/* artifact.rs:430-465 (encode_fp16_linear): f32 [out x in] -> fp16
+ * [padded_out x padded_in], zero padding. */
+void orc_pad_fp16_linear(const float* src, int logical_out, int logical_in, int padded_out,
+                         int padded_in, uint16_t* dst) {
+    memset(dst, 0, (size_t)padded_out * padded_in * 2);
+    for (int row = 0; row < logical_out; ++row) {
+        for (int col = 0; col < logical_in; ++col) {
+            dst[(size_t)row * padded_in + col] = orc_f32_to_f16(src[(size_t)row * logical_in + col]);
+        }
+    }
+}
+
+/* ---- GGUF Q4_K (q4k_benchmark.rs:403-597, linear.cu:431-456) ------------ */
+
+static int nearest_int(float value) { return (int)nearbyintf(value); }
+
+static int clampi(int v, int lo, int hi) { return v < lo ? lo : (v > hi ? hi : v); }
+
+static void q4k_scale_min(const uint8_t* packed, int group, int* scale, int* minimum) {
+    if (group < 4) {
+        *scale = packed[group] & 63;
+        *minimum = packed[group + 4] & 63;
+    } else {
+        *scale = (packed[group + 4] & 0x0f) | ((packed[group - 4] >> 6) << 4);
+        *minimum = (packed[group + 4] >> 4) | ((packed[group] >> 6) << 4);
+    }
+}
+
+/* q4k_benchmark.rs:488-562 (make_qkx2_quants: nmax 15, rmin -1, rdelta 0.1,
+ * 20 steps). */
+static void make_qkx2_quants(const float* x, const float* weights, uint8_t* levels,
+                             float* out_scale, float* out_min) {
+    float minimum = x[0], maximum = x[0];
+    float sum_w = weights[0], sum_x = weights[0] * x[0];
+    for (int i = 1; i < 32; ++i) {
+        minimum = fminf(minimum, x[i]);
+        maximum = fmaxf(maximum, x[i]);
+        sum_w += weights[i];
+        sum_x += weights[i] * x[i];
+    }
+    minimum = fminf(minimum, 0.0f);
+    if (maximum == minimum) {
+        memset(levels, 0, 32);
+        *out_scale = 0.0f;
+        *out_min = -minimum;
+        return;
+    }
+    float iscale = 15.0f / (maximum - minimum);
+    float scale = 1.0f / iscale;
+    float best_error = 0.0f;
+    for (int i = 0; i < 32; ++i) {
+        int l = clampi(nearest_int(iscale * (x[i] - minimum)), 0, 15);
+        levels[i] = (uint8_t)l;
+        float diff = scale * (float)l + minimum - x[i];
+        best_error += weights[i] * diff * diff;
+    }
+    uint8_t aux[32];
+    for (int step = 0; step <= 20; ++step) {
+        iscale = (-1.0f + 0.1f * (float)step + 15.0f) / (maximum - minimum);
+        float sum_l = 0.0f, sum_l2 = 0.0f, sum_xl = 0.0f;
+        for (int i = 0; i < 32; ++i) {
+            int l = clampi(nearest_int(iscale * (x[i] - minimum)), 0, 15);
+            aux[i] = (uint8_t)l;
+            sum_l += weights[i] * (float)l;
+            sum_l2 += weights[i] * (float)(l * l);
+            sum_xl += weights[i] * (float)l * x[i];
+        }
+        float det = sum_w * sum_l2 - sum_l * sum_l;
+        if (det <= 0.0f) continue;
+        float this_scale = (sum_w * sum_xl - sum_x * sum_l) / det;
+        float this_min = (sum_l2 * sum_x - sum_l * sum_xl) / det;
+        if (this_min > 0.0f) {
+            this_min = 0.0f;
+            this_scale = sum_xl / sum_l2;
+        }
+        float error = 0.0f;
+        for (int i = 0; i < 32; ++i) {
+            float diff = this_scale * (float)aux[i] + this_min - x[i];
+            error += weights[i] * diff * diff;
+        }
+        if (error < best_error) {
+            memcpy(levels, aux, 32);
+            best_error = error;
+            scale = this_scale;
+            minimum = this_min;
+        }
+    }
+    *out_scale = scale;
+    *out_min = -minimum;
+}
+
+/* q4k_benchmark.rs:403-486 (encode_q4_k_block). */
+void orc_q4k_encode_block(const uint16_t* src256, uint8_t* block) {
+    memset(block, 0, 144);
+    float x[256];
+    for (int i = 0; i < 256; ++i) x[i] = orc_f16_to_f32(src256[i]);
+    uint8_t levels[256];
+    float scales[8], minimums[8];
+    float max_scale = 0.0f, max_min = 0.0f;
+    for (int g = 0; g < 8; ++g) {
+        const float* v = x + g * 32;
+        float sum_sq = 0.0f;
+        for (int i = 0; i < 32; ++i) sum_sq += v[i] * v[i];
+        float rms = sqrtf(sum_sq / 32.0f);
+        float weights[32];
+        for (int i = 0; i < 32; ++i) weights[i] = rms + fabsf(v[i]);
+        make_qkx2_quants(v, weights, levels + g * 32, &scales[g], &minimums[g]);
+        max_scale = fmaxf(max_scale, scales[g]);
+        max_min = fmaxf(max_min, minimums[g]);
+    }
+    float inv_scale = max_scale > 0.0f ? 63.0f / max_scale : 0.0f;
+    float inv_min = max_min > 0.0f ? 63.0f / max_min : 0.0f;
+    uint8_t packed[12];
+    memset(packed, 0, 12);
+    for (int g = 0; g < 8; ++g) {
+        int ls = clampi(nearest_int(inv_scale * scales[g]), 0, 63);
+        int lm = clampi(nearest_int(inv_min * minimums[g]), 0, 63);
+        if (g < 4) {
+            packed[g] = (uint8_t)ls;
+            packed[g + 4] = (uint8_t)lm;
+        } else {
+            packed[g + 4] = (uint8_t)((ls & 0x0f) | ((lm & 0x0f) << 4));
+            packed[g - 4] |= (uint8_t)((ls >> 4) << 6);
+            packed[g] |= (uint8_t)((lm >> 4) << 6);
+        }
+    }
+    uint16_t d = orc_f32_to_f16(max_scale / 63.0f);
+    uint16_t dmin = orc_f32_to_f16(max_min / 63.0f);
+    block[0] = (uint8_t)(d & 0xff);
+    block[1] = (uint8_t)(d >> 8);
+    block[2] = (uint8_t)(dmin & 0xff);
+    block[3] = (uint8_t)(dmin >> 8);
+    memcpy(block + 4, packed, 12);
+    for (int g = 0; g < 8; ++g) {
+        int sc, mn;
+        q4k_scale_min(packed, g, &sc, &mn);
+        float scale = orc_f16_to_f32(d) * (float)sc;
+        if (scale == 0.0f) continue;
+        float minimum = orc_f16_to_f32(dmin) * (float)mn;
+        for (int i = 0; i < 32; ++i) {
+            levels[g * 32 + i] = (uint8_t)clampi(nearest_int((x[g * 32 + i] + minimum) / scale), 0, 15);
+        }
+    }
+    for (int pair = 0; pair < 4; ++pair) {
+        for (int i = 0; i < 32; ++i) {
+            block[16 + pair * 32 + i] =
+                (uint8_t)(levels[pair * 64 + i] | (levels[pair * 64 + 32 + i] << 4));
+        }
+    }
+}
+
+/* q4k_benchmark.rs:579-597 / linear.cu:445-456: d*sc*q - dmin*m. */
+float orc_q4k_value(const uint8_t* block, int index) {
+    float d = orc_f16_to_f32((uint16_t)(block[0] | (block[1] << 8)));
+    float dmin = orc_f16_to_f32((uint16_t)(block[2] | (block[3] << 8)));
+    int group = index / 32;
+    uint8_t packed = block[16 + (group / 2) * 32 + (index % 32)];
+    int quant = (group % 2 == 0) ? (packed & 0x0f) : (packed >> 4);
+    int sc, mn;
+    q4k_scale_min(block + 4, group, &sc, &mn);
+    return d * (float)sc * (float)quant - dmin * (float)mn;
+}
+
+/* q4k_benchmark.rs:385-401. */
+void orc_q4k_encode(const uint16_t* w, int n, int k, uint8_t* blocks) {
+    int per_row = k / 256;
+    for (int row = 0; row < n; ++row) {
+        for (int b = 0; b < per_row; ++b) {
+            orc_q4k_encode_block(w + (size_t)row * k + b * 256,
+                                 blocks + ((size_t)row * per_row + b) * 144);
+        }
+    }
+}
+
+/* ---- activation quantizers ---------------------------------------------- */
+
+/* linear.cu:537-547 / encoder.cu:549-559: e4m3(f16 * inverse_scale). */
+void orc_quantize_fp8_static(const uint16_t* x, size_t count, float inverse_scale,
+                             uint8_t* out) {
+    for (size_t i = 0; i < count; ++i) out[i] = orc_f32_to_e4m3(orc_f16_to_f32(x[i]) * inverse_scale);
+}
+
+/* linear.cu:549-560: rne(clamp(f16 * inverse_scale, +-127)). */
+void orc_quantize_int8_static(const uint16_t* x, size_t count, float inverse_scale,
+                              int8_t* out) {
+    for (size_t i = 0; i < count; ++i) {
+        float s = orc_f16_to_f32(x[i]) * inverse_scale;
+        s = fminf(127.0f, fmaxf(-127.0f, s));
+        out[i] = (int8_t)nearbyintf(s);
+    }
+}
+
+/* Dynamic per-row FP8 (encoder.cu:264-292 without the norm, and the
+ * request-time row packers encoder.cu:1129-1180): scale = max|x| / 448, 1 for
+ * all-zero rows and for padding rows >= valid_rows (which quantize to 0). */
+void orc_quantize_fp8_rows(const uint16_t* x, int rows, int valid_rows, int k, uint8_t* q,
+                           float* scales) {
+    for (int r = 0; r < rows; ++r) {
+        uint8_t* out = q + (size_t)r * k;
+        if (r >= valid_rows) {
+            memset(out, 0, (size_t)k);
+            scales[r] = 1.0f;
+            continue;
+        }
+        float maximum = 0.0f;
+        for (int i = 0; i < k; ++i) maximum = fmaxf(maximum, fabsf(orc_f16_to_f32(x[(size_t)r * k + i])));
+        float scale = maximum > 0.0f ? maximum / 448.0f : 1.0f;
+        scales[r] = scale;
+        for (int i = 0; i < k; ++i) out[i] = orc_f32_to_e4m3(orc_f16_to_f32(x[(size_t)r * k + i]) / scale);
+    }
+}
+
+/* Dynamic per-token INT8 (BASELINE config 3 "mixed variant"; no reference
+ * counterpart, pinned by closed form): scale = max|x| / 127 (1 if zero),
+ * q = clamp(rne(x / scale), +-127). */
+void orc_quantize_int8_rows(const uint16_t* x, int rows, int valid_rows, int k, int8_t* q,
+                            float* scales) {
+    for (int r = 0; r < rows; ++r) {
+        int8_t* out = q + (size_t)r * k;
+        if (r >= valid_rows) {
+            memset(out, 0, (size_t)k);
+            scales[r] = 1.0f;
+            continue;
+        }
+        float maximum = 0.0f;
+        for (int i = 0; i < k; ++i) maximum = fmaxf(maximum, fabsf(orc_f16_to_f32(x[(size_t)r * k + i])));
+        float scale = maximum > 0.0f ? maximum / 127.0f : 1.0f;
+        scales[r] = scale;
+        for (int i = 0; i < k; ++i) out[i] = (int8_t)clamp_rne(orc_f16_to_f32(x[(size_t)r * k + i]) / scale, -127, 127);
+    }
+}
+
+/* Dynamic per-row INT4 (encoder.cu:264-290, kInt4): scale = max(max(x/7,
+ * -x/8)) (1 if not positive), q = clamp(rne(x / scale), -8, 7), nibble pairs
+ * with the even column low. */
+void orc_quantize_int4_rows(const uint16_t* x, int rows, int valid_rows, int k, uint8_t* q,
+                            float* scales) {
+    for (int r = 0; r < rows; ++r) {
+        uint8_t* out = q + (size_t)r * (k / 2);
+        if (r >= valid_rows) {
+            memset(out, 0, (size_t)k / 2);
+            scales[r] = 1.0f;
+            continue;
+        }
+        float maximum = 0.0f;
+        for (int i = 0; i < k; ++i) {
+            float v = orc_f16_to_f32(x[(size_t)r * k + i]);
+            maximum = fmaxf(maximum, fmaxf(v / 7.0f, -v / 8.0f));
+        }
+        float scale = maximum > 0.0f ? maximum : 1.0f;
+        scales[r] = scale;
+        for (int j = 0; j < k / 2; ++j) {
+            int a = clamp_rne(orc_f16_to_f32(x[(size_t)r * k + 2 * j]) / scale, -8, 7);
+            int b = clamp_rne(orc_f16_to_f32(x[(size_t)r * k + 2 * j + 1]) / scale, -8, 7);
+            out[j] = (uint8_t)((a & 15) | ((b & 15) << 4));
+        }
+    }
+}
+
+/* LayerNorm then dynamic per-row quantization (encoder.cu:211-306).  The
+ * statistics use the reference's reduction shape: 256 partial sums (thread t
+ * adds x[t], x[t+256], x[t+512], x[t+768] in that order), folded by
+ * block_sum_tree_tail (encoder.cu:36-54) -- pairs (t, t+128), (t+64, t+192),
+ * (t+32, t+160), (t+96, t+224), then ((s0+s1)+(s2+s3)), then a 32-lane
+ * shuffle-down tree.  The reference uses the approximate rsqrtf; this
+ * restatement (and the HIP kernel) uses the correctly rounded 1/sqrtf, a
+ * deviation of at most 2 ulp in inverse_std.  Requires k == 1024. */
+static float tree_sum_256(const float* partial) {
+    float lanes[32];
+    for (int lane = 0; lane < 32; ++lane) {
+        float s0 = partial[lane] + partial[lane + 128];
+        float s1 = partial[lane + 64] + partial[lane + 192];
+        float s2 = partial[lane + 32] + partial[lane + 160];
+        float s3 = partial[lane + 96] + partial[lane + 224];
+        lanes[lane] = (s0 + s1) + (s2 + s3);
+    }
+    for (int offset = 16; offset > 0; offset /= 2) {
+        for (int lane = 0; lane < 32; ++lane) {
+            if (lane + offset < 32) lanes[lane] += lanes[lane + offset];
+        }
+    }
+    return lanes[0];
+}
+
+void orc_layer_norm_quantize(const uint16_t* x, const uint16_t* gamma, const uint16_t* beta,
+                             int rows, int valid_rows, int k, float epsilon, int int4,
+                             uint8_t* q, float* scales, uint16_t* normalized) {
+    (void)k; /* fixed at 1024 (kModelWidth) */
+    const int width = 1024;
+    for (int r = 0; r < rows; ++r) {
+        const uint16_t* in = x + (size_t)r * width;
+        if (r >= valid_rows) {
+            if (int4) memset(q + (size_t)r * width / 2, 0, width / 2);
+            else memset(q + (size_t)r * width, 0, width);
+            scales[r] = 1.0f;
+            if (normalized) memset(normalized + (size_t)r * width, 0, width * 2);
+            continue;
+        }
+        float partial[256];
+        float values[1024];
+        for (int t = 0; t < 256; ++t) {
+            float s = 0.0f;
+            for (int item = 0; item < 4; ++item) {
+                values[t + item * 256] = orc_f16_to_f32(in[t + item * 256]);
+                s += values[t + item * 256];
+            }
+            partial[t] = s;
+        }
+        float mean = tree_sum_256(partial) / 1024.0f;
+        for (int t = 0; t < 256; ++t) {
+            float s = 0.0f;
+            for (int item = 0; item < 4; ++item) {
+                float d = values[t + item * 256] - mean;
+                s += d * d;
+            }
+            partial[t] = s;
+        }
+        float inverse_std = 1.0f / sqrtf(tree_sum_256(partial) / 1024.0f + epsilon);
+        float maximum = 0.0f;
+        for (int i = 0; i < width; ++i) {
+            float y = (values[i] - mean) * inverse_std * orc_f16_to_f32(gamma[i]) + orc_f16_to_f32(beta[i]);
+            uint16_t h = orc_f32_to_f16(y);
+            if (normalized) normalized[(size_t)r * width + i] = h;
+            values[i] = orc_f16_to_f32(h);
+            if (int4) maximum = fmaxf(maximum, fmaxf(values[i] / 7.0f, -values[i] / 8.0f));
+            else maximum = fmaxf(maximum, fabsf(values[i]));
+        }
+        float scale = maximum > 0.0f ? (int4 ? maximum : maximum / 448.0f) : 1.0f;
+        scales[r] = scale;
+        if (int4) {
+            for (int j = 0; j < width / 2; ++j) {
+                int a = clamp_rne(values[2 * j] / scale, -8, 7);
+                int b = clamp_rne(values[2 * j + 1] / scale, -8, 7);
+                q[(size_t)r * width / 2 + j] = (uint8_t)((a & 15) | ((b & 15) << 4));
+            }
+        } else {
+            for (int i = 0; i < width; ++i) q[(size_t)r * width + i] = orc_f32_to_e4m3(values[i] / scale);
+        }
+    }
+}
+
+/* 2:4 compression of FP8 activations (encoder.cu:685-704, epilogue 7 at
+ * :1037-1053): in each quartet keep the two largest |e4m3| (bits & 127), ties
+ * to the lower index, in index order.  data is [rows x k/2]; meta is
+ * [rows x k/8] bytes, quartet p's 4-bit field idx0 | idx1 << 2 at bits
+ * 4*(p%2) of byte p/2. */
+void orc_compress_24(const uint8_t* x, int rows, int k, uint8_t* data, uint8_t* meta) {
+    memset(meta, 0, (size_t)rows * k / 8);
+    for (int r = 0; r < rows; ++r) {
+        for (int p = 0; p < k / 4; ++p) {
+            const uint8_t* v = x + (size_t)r * k + 4 * p;
+            int count = 0;
+            int nibble = 0;
+            for (int i = 0; i < 4; ++i) {
+                int rank = 0;
+                for (int j = 0; j < 4; ++j) {
+                    int mi = v[i] & 127, mj = v[j] & 127;
+                    rank += mj > mi || (mj == mi && j < i);
+                }
+                if (rank < 2) {
+                    data[(size_t)r * k / 2 + 2 * p + count] = v[i];
+                    nibble |= i << (2 * count);
+                    ++count;
+                }
+            }
+            meta[(size_t)r * k / 8 + p / 2] |= (uint8_t)(nibble << (4 * (p % 2)));
+        }
+    }
+}
+
+void orc_decompress_24(const uint8_t* data, const uint8_t* meta, int rows, int k, uint8_t* x) {
+    memset(x, 0, (size_t)rows * k);
+    for (int r = 0; r < rows; ++r) {
+        for (int p = 0; p < k / 4; ++p) {
+            int nibble = (meta[(size_t)r * k / 8 + p / 2] >> (4 * (p % 2))) & 15;
+            x[(size_t)r * k + 4 * p + (nibble & 3)] = data[(size_t)r * k / 2 + 2 * p];
+            x[(size_t)r * k + 4 * p + ((nibble >> 2) & 3)] = data[(size_t)r * k / 2 + 2 * p + 1];
+        }
+    }
+}
+
+/* ---- GEMM references ---------------------------------------------------- */
+
+/* Exact i32 dot products (quant_benchmark.rs:872-909). */
+void orc_gemm_i8_i32(const int8_t* x, const int8_t* w, int m, int n, int k, int32_t* acc) {
+#pragma omp parallel for schedule(static) num_threads(g_threads)
+    for (int i = 0; i < m; ++i) {
+        for (int j = 0; j < n; ++j) {
+            const int8_t* a = x + (size_t)i * k;
+            const int8_t* b = w + (size_t)j * k;
+            int32_t s = 0;
+            for (int t = 0; t < k; ++t) s += (int32_t)a[t] * (int32_t)b[t];
+            acc[(size_t)i * n + j] = s;
+        }
+    }
+}
+
+static int s4(uint8_t byte, int high) {
+    int v = high ? (byte >> 4) : (byte & 15);
+    return v >= 8 ? v - 16 : v;
+}
+
+/* s4 x s4 -> exact s32 (the mma...s4.s4 path, encoder.cu:775-782); both
+ * operands packed two per byte, even k in the low nibble. */
+void orc_gemm_s4_i32(const uint8_t* x, const uint8_t* w, int m, int n, int k, int32_t* acc) {
+#pragma omp parallel for schedule(static) num_threads(g_threads)
+    for (int i = 0; i < m; ++i) {
+        for (int j = 0; j < n; ++j) {
+            const uint8_t* a = x + (size_t)i * k / 2;
+            const uint8_t* b = w + (size_t)j * k / 2;
+            int32_t s = 0;
+            for (int t = 0; t < k / 2; ++t) {
+                s += s4(a[t], 0) * s4(b[t], 0) + s4(a[t], 1) * s4(b[t], 1);
+            }
+            acc[(size_t)i * n + j] = s;
+        }
+    }
+}
+
+static float e4m3_table[256];
+static int e4m3_table_ready = 0;
+
+static void init_e4m3_table(void) {
+    if (!e4m3_table_ready) {
+        for (int i = 0; i < 256; ++i) e4m3_table[i] = orc_e4m3_to_f32((uint8_t)i);
+        e4m3_table_ready = 1;
+    }
+}
+
+/* Dequantize-then-fp32 dot products in index order (quant_benchmark.rs:
+ * 832-869: fold over k of f32(x) * f32(w)).  Products of two e4m3 values are
+ * exact in fp32; only the summation rounds. */
+void orc_gemm_e4m3_f32(const uint8_t* x, const uint8_t* w, int m, int n, int k, float* acc) {
+    init_e4m3_table();
+#pragma omp parallel for schedule(static) num_threads(g_threads)
+    for (int i = 0; i < m; ++i) {
+        float* a = (float*)malloc((size_t)k * sizeof(float));
+        for (int t = 0; t < k; ++t) a[t] = e4m3_table[x[(size_t)i * k + t]];
+        for (int j = 0; j < n; ++j) {
+            const uint8_t* b = w + (size_t)j * k;
+            float s = 0.0f;
+            for (int t = 0; t < k; ++t) s += a[t] * e4m3_table[b[t]];
+            acc[(size_t)i * n + j] = s;
+        }
+        free(a);
+    }
+}
+
+/* cuda.rs:821-861: fp16 operands, fp32 fold. */
+void orc_gemm_f16_f32(const uint16_t* x, const uint16_t* w, int m, int n, int k, float* acc) {
+#pragma omp parallel for schedule(static) num_threads(g_threads)
+    for (int i = 0; i < m; ++i) {
+        float* a = (float*)malloc((size_t)k * sizeof(float));
+        for (int t = 0; t < k; ++t) a[t] = orc_f16_to_f32(x[(size_t)i * k + t]);
+        for (int j = 0; j < n; ++j) {
+            const uint16_t* b = w + (size_t)j * k;
+            float s = 0.0f;
+            for (int t = 0; t < k; ++t) s += a[t] * orc_f16_to_f32(b[t]);
+            acc[(size_t)i * n + j] = s;
+        }
+        free(a);
+    }
+}
+
+static int g128_level(const uint32_t* q, int k, int row, int t) {
+    return (int)((q[(size_t)row * (k / 8) + t / 8] >> (4 * (t % 8))) & 15u);
+}
+
+/* W4A16 with group-wise asymmetric INT4 weights: out = sum over groups of
+ * s_g * (sum over the group of x * (q - z)).  Products x * (q - z) are exact
+ * in fp32 (11-bit x 5-bit significands); the group sums fold in k order. */
+void orc_gemm_g128_a16(const uint16_t* x, const uint32_t* q, const uint16_t* scales,
+                       const uint16_t* zeros, int m, int n, int k, float* out) {
+    int groups = k / 128;
+#pragma omp parallel for schedule(static) num_threads(g_threads)
+    for (int i = 0; i < m; ++i) {
+        for (int j = 0; j < n; ++j) {
+            float total = 0.0f;
+            for (int g = 0; g < groups; ++g) {
+                float z = orc_f16_to_f32(zeros[(size_t)j * groups + g]);
+                float s = orc_f16_to_f32(scales[(size_t)j * groups + g]);
+                float part = 0.0f;
+                for (int t = g * 128; t < g * 128 + 128; ++t) {
+                    part += orc_f16_to_f32(x[(size_t)i * k + t]) * ((float)g128_level(q, k, j, t) - z);
+                }
+                total = fmaf(part, s, total);
+            }
+            out[(size_t)i * n + j] = total;
+        }
+    }
+}
+
+/* W4A8: exact i32 per-group accumulators acc_g = sum x_i8 * (q - z) (z is an
+ * integer), then out = x_scale * (sum over g in order of fmaf(acc_g, s_g, .)). */
+void orc_gemm_g128_a8(const int8_t* x, const float* x_scales, const uint32_t* q,
+                      const uint16_t* scales, const uint16_t* zeros, int m, int n, int k,
+                      int32_t* group_acc, float* out) {
+    int groups = k / 128;
+#pragma omp parallel for schedule(static) num_threads(g_threads)
+    for (int i = 0; i < m; ++i) {
+        for (int j = 0; j < n; ++j) {
+            float total = 0.0f;
+            for (int g = 0; g < groups; ++g) {
+                int z = (int)orc_f16_to_f32(zeros[(size_t)j * groups + g]);
+                int32_t a = 0;
+                for (int t = g * 128; t < g * 128 + 128; ++t) {
+                    a += (int32_t)x[(size_t)i * k + t] * (g128_level(q, k, j, t) - z);
+                }
+                if (group_acc) group_acc[((size_t)i * n + j) * groups + g] = a;
+                total = fmaf((float)a, orc_f16_to_f32(scales[(size_t)j * groups + g]), total);
+            }
+            out[(size_t)i * n + j] = total * x_scales[i];
+        }
+    }
+}
+
+/* q4k_benchmark.rs:910-945: fp16 activations times f16(dequant(Q4_K)). */
+void orc_gemm_q4k_f32(const uint16_t* x, const uint8_t* blocks, int m, int n, int k, float* acc) {
+    int per_row = k / 256;
+    float* wd = (float*)malloc((size_t)n * k * sizeof(float));
+    for (int j = 0; j < n; ++j) {
+        for (int t = 0; t < k; ++t) {
+            const uint8_t* block = blocks + ((size_t)j * per_row + t / 256) * 144;
+            wd[(size_t)j * k + t] = orc_f16_to_f32(orc_f32_to_f16(orc_q4k_value(block, t % 256)));
+        }
+    }
+#pragma omp parallel for schedule(static) num_threads(g_threads)
+    for (int i = 0; i < m; ++i) {
+        for (int j = 0; j < n; ++j) {
+            float s = 0.0f;
+            for (int t = 0; t < k; ++t) s += orc_f16_to_f32(x[(size_t)i * k + t]) * wd[(size_t)j * k + t];
+            acc[(size_t)i * n + j] = s;
+        }
+    }
+    free(wd);
+}
+
+/* ---- epilogues ------------------------------------------------------------ */
+
+static float silu(float v) { return v / (1.0f + expf(-v)); }
+
+static float round_f16(float v) { return orc_f16_to_f32(orc_f32_to_f16(v)); }
+
+/* ffn_fp8_async epilogues (encoder.cu:911-1058).  value = acc * row_scale *
+ * w_scale, row_scale = row_scales[r] when given, else in_scale.
+ *   0: SiLU -> fp16                     1: SiLU -> fp16 -> x16 -> e4m3 (out8)
+ *   2: out16 = fp16(fmaf(0.5, value, out16))     (FF contract, residual)
+ *   3: + bias -> fp16                   4: + bias, ReLU -> fp16
+ *   5: GLU over n = 2 * width columns: fp16(v) / (1 + exp(-fp16(g))) with
+ *      v = column c, g = column c + width; rows >= valid_rows write 0
+ *      (out16 is [m x width])
+ *   6: out16 = fp16(value + out16)      (residual, scale 1)
+ *   7: as 1 (the 2:4 compression is orc_compress_24 on its output)
+ *   8: as 2 (sparse-input contract) */
+void orc_epilogue(const float* acc, const float* row_scales, float in_scale,
+                  const float* w_scales, const float* bias, int m, int n, int mode,
+                  int valid_rows, uint16_t* out16, uint8_t* out8) {
+    if (mode == 5) {
+        int width = n / 2;
+        for (int r = 0; r < m; ++r) {
+            float rs = row_scales ? row_scales[r] : in_scale;
+            for (int c = 0; c < width; ++c) {
+                float v = round_f16(acc[(size_t)r * n + c] * rs * w_scales[c]);
+                float g = round_f16(acc[(size_t)r * n + c + width] * rs * w_scales[c + width]);
+                out16[(size_t)r * width + c] = r < valid_rows ? orc_f32_to_f16(v / (1.0f + expf(-g))) : 0;
+            }
+        }
+        return;
+    }
+    for (int r = 0; r < m; ++r) {
+        float rs = row_scales ? row_scales[r] : in_scale;
+        for (int c = 0; c < n; ++c) {
+            size_t idx = (size_t)r * n + c;
+            float value = acc[idx] * rs * w_scales[c];
+            switch (mode) {
+            case 0:
+                out16[idx] = orc_f32_to_f16(silu(value));
+                break;
+            case 1:
+            case 7:
+                out8[idx] = orc_f32_to_e4m3(round_f16(silu(value)) * 16.0f);
+                break;
+            case 2:
+            case 8:
+                out16[idx] = orc_f32_to_f16(fmaf(0.5f, value, orc_f16_to_f32(out16[idx])));
+                break;
+            case 3:
+                out16[idx] = orc_f32_to_f16(value + bias[c]);
+                break;
+            case 4:
+                out16[idx] = orc_f32_to_f16(fmaxf(value + bias[c], 0.0f));
+                break;
+            case 6:
+                out16[idx] = orc_f32_to_f16(fmaf(1.0f, value, orc_f16_to_f32(out16[idx])));
+                break;
+            default:
+                break;
+            }
+        }
+    }
+}
+
+static float activate(float v, int activation) {
+    if (activation == 1) return silu(v);
+    if (activation == 2) return fmaxf(v, 0.0f);
+    return v;
+}
+
+/* FP16 linear epilogue (linear.cu:137-156): v = (acc + bias) * out_scale;
+ * v = fmaf(res_scale, residual, v); act; fp16.  bias/residual may be NULL. */
+void orc_epilogue_linear(const float* acc, const float* bias, const uint16_t* residual,
+                         int m, int n, float out_scale, float res_scale, int activation,
+                         uint16_t* out) {
+    for (int r = 0; r < m; ++r) {
+        for (int c = 0; c < n; ++c) {
+            size_t idx = (size_t)r * n + c;
+            float v = acc[idx];
+            if (bias) v += bias[c];
+            v *= out_scale;
+            if (residual) v = fmaf(res_scale, orc_f16_to_f32(residual[idx]), v);
+            out[idx] = orc_f32_to_f16(activate(v, activation));
+        }
+    }
+}
+
+/* FP8 / INT8 linear epilogue (linear.cu:362-373, 417-428):
+ * act(fmaf(acc, in_scale * w_scale[c], bias[c])) -> fp16.  bias may be NULL. */
+void orc_epilogue_quantized(const float* acc, float in_scale, const float* w_scales,
+                            const float* bias, int m, int n, int activation, uint16_t* out) {
+    for (int r = 0; r < m; ++r) {
+        for (int c = 0; c < n; ++c) {
+            size_t idx = (size_t)r * n + c;
+            float v = fmaf(acc[idx], in_scale * w_scales[c], bias ? bias[c] : 0.0f);
+            out[idx] = orc_f32_to_f16(activate(v, activation));
+        }
+    }
+}
+
+/* ---- joint (decoder.cu:690-759) ----------------------------------------- */
+
+/* score[o] = bias[o] + sum_k W[o,k] * relu(enc[k] + pred[k]).  fp32 products
+ * folded in k order (the reference folds 32 interleaved lanes; the order is
+ * not reproducible, so parity is by tolerance). */
+void orc_joint_scores_f16(const uint16_t* w, const float* bias, const uint16_t* enc,
+                          const float* pred, int outputs, int hidden, float* scores) {
+    for (int o = 0; o < outputs; ++o) {
+        double s = 0.0;
+        for (int t = 0; t < hidden; ++t) {
+            float in = fmaxf(orc_f16_to_f32(enc[t]) + pred[t], 0.0f);
+            s += (double)orc_f16_to_f32(w[(size_t)o * hidden + t]) * (double)in;
+        }
+        scores[o] = (float)(s + (double)bias[o]);
+    }
+}
+
+/* INT8 joint head (a new format; the reference's joint is FP16,
+ * decoder.cu:596-601): score[o] = bias[o] + w_scale[o] * sum_k q[o,k] * in[k]. */
+void orc_joint_scores_i8(const int8_t* w, const float* w_scales, const float* bias,
+                         const uint16_t* enc, const float* pred, int outputs, int hidden,
+                         float* scores) {
+    for (int o = 0; o < outputs; ++o) {
+        double s = 0.0;
+        for (int t = 0; t < hidden; ++t) {
+            float in = fmaxf(orc_f16_to_f32(enc[t]) + pred[t], 0.0f);
+            s += (double)w[(size_t)o * hidden + t] * (double)in;
+        }
+        scores[o] = (float)((double)w_scales[o] * s + (double)bias[o]);
+    }
+}
+
+/* Greedy TDT decision (decoder.cu:34-46, 728-759): token = argmax over the
+ * first token_outputs scores, ties to the lower id; duration = argmax over the
+ * next `durations` scores with strict '>' (first maximum wins). */
+void orc_joint_decide(const float* scores, int token_outputs, int durations, int* token,
+                      int* duration) {
+    int best = 0;
+    for (int o = 1; o < token_outputs; ++o) {
+        if (scores[o] > scores[best]) best = o;
+    }
+    int d = 0;
+    for (int i = 1; i < durations; ++i) {
+        if (scores[token_outputs + i] > scores[token_outputs + d]) d = i;
+    }
+    *token = best;
+    *duration = d;
+}

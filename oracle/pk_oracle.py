@@ -1,0 +1,474 @@
+"""numpy front end for the C oracle (oracle/pk_oracle.c).
+
+TEST INFRASTRUCTURE ONLY: the parity checker.  Only tests/,
+__graft_entry__.smoke() and bench.py's cpu_baseline leg import this module.
+Every function forwards to the C restatement, which cites the reference
+file:line it follows.  fp16 arrays are numpy float16 (same bits as uint16).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "build", "libpk_oracle.so")
+
+_lib = None
+
+
+def build(force: bool = False) -> str:
+    if force or not os.path.exists(LIB_PATH):
+        subprocess.run(["make", "-s", "-C", HERE], check=True)
+    return LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        _lib = ctypes.CDLL(LIB_PATH)
+        _declare(_lib)
+    return _lib
+
+
+P = ctypes.c_void_p
+I = ctypes.c_int
+F = ctypes.c_float
+S = ctypes.c_size_t
+
+
+def _declare(l):
+    sig = {
+        "orc_f32_to_f16": (ctypes.c_uint16, [F]),
+        "orc_f16_to_f32": (F, [ctypes.c_uint16]),
+        "orc_f32_to_e4m3": (ctypes.c_uint8, [F]),
+        "orc_e4m3_to_f32": (F, [ctypes.c_uint8]),
+        "orc_quantize_i8": (ctypes.c_int8, [F]),
+        "orc_pattern": (F, [ctypes.c_uint64, ctypes.c_uint64, F]),
+        "orc_pattern_fill": (None, [P, S, ctypes.c_uint64, ctypes.c_uint64, F]),
+        "orc_estimate_linear": (I, [I, S, S, I, P]),
+        "orc_exl3_layout": (I, [S, S, I, P]),
+        "orc_pack_fp8_rows": (None, [P, I, I, P, P]),
+        "orc_pack_int8_rows": (None, [P, I, I, P, P]),
+        "orc_pack_int4_rows": (None, [P, I, I, P, P]),
+        "orc_pack_int4_g128": (None, [P, I, I, P, P, P]),
+        "orc_pad_fp16_linear": (None, [P, I, I, I, I, P]),
+        "orc_q4k_encode_block": (None, [P, P]),
+        "orc_q4k_value": (F, [P, I]),
+        "orc_q4k_encode": (None, [P, I, I, P]),
+        "orc_quantize_fp8_static": (None, [P, S, F, P]),
+        "orc_quantize_int8_static": (None, [P, S, F, P]),
+        "orc_quantize_fp8_rows": (None, [P, I, I, I, P, P]),
+        "orc_quantize_int8_rows": (None, [P, I, I, I, P, P]),
+        "orc_quantize_int4_rows": (None, [P, I, I, I, P, P]),
+        "orc_layer_norm_quantize": (None, [P, P, P, I, I, I, F, I, P, P, P]),
+        "orc_compress_24": (None, [P, I, I, P, P]),
+        "orc_decompress_24": (None, [P, P, I, I, P]),
+        "orc_gemm_i8_i32": (None, [P, P, I, I, I, P]),
+        "orc_gemm_s4_i32": (None, [P, P, I, I, I, P]),
+        "orc_gemm_e4m3_f32": (None, [P, P, I, I, I, P]),
+        "orc_gemm_f16_f32": (None, [P, P, I, I, I, P]),
+        "orc_gemm_g128_a16": (None, [P, P, P, P, I, I, I, P]),
+        "orc_gemm_g128_a8": (None, [P, P, P, P, P, I, I, I, P, P]),
+        "orc_gemm_q4k_f32": (None, [P, P, I, I, I, P]),
+        "orc_epilogue": (None, [P, P, F, P, P, I, I, I, I, P, P]),
+        "orc_epilogue_linear": (None, [P, P, P, I, I, F, F, I, P]),
+        "orc_epilogue_quantized": (None, [P, F, P, P, I, I, I, P]),
+        "orc_joint_scores_f16": (None, [P, P, P, P, I, I, P]),
+        "orc_joint_scores_i8": (None, [P, P, P, P, P, I, I, P]),
+        "orc_joint_decide": (None, [P, I, I, P, P]),
+        "orc_threads": (I, []),
+        "orc_set_threads": (None, [I]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(l, name)
+        fn.restype = res
+        fn.argtypes = args
+
+
+def _p(a):
+    if a is None:
+        return None
+    assert a.flags["C_CONTIGUOUS"], "oracle arrays must be C-contiguous"
+    return a.ctypes.data
+
+
+def _h(a):
+    """Return a C-contiguous float16 view as the C side's uint16."""
+    a = np.ascontiguousarray(a)
+    assert a.dtype in (np.float16, np.uint16)
+    return a
+
+
+# ---- scalars ---------------------------------------------------------------
+
+def f32_to_e4m3(values) -> np.ndarray:
+    v = np.asarray(values, dtype=np.float32).ravel()
+    f = lib().orc_f32_to_e4m3
+    return np.array([f(float(x)) for x in v], dtype=np.uint8)
+
+
+def e4m3_table() -> np.ndarray:
+    f = lib().orc_e4m3_to_f32
+    return np.array([f(i) for i in range(256)], dtype=np.float32)
+
+
+def e4m3_to_f32(codes) -> np.ndarray:
+    return e4m3_table()[np.asarray(codes, dtype=np.uint8)]
+
+
+def f32_to_f16_bits(values) -> np.ndarray:
+    v = np.asarray(values, dtype=np.float32).ravel()
+    f = lib().orc_f32_to_f16
+    return np.array([f(float(x)) for x in v], dtype=np.uint16)
+
+
+def quantize_i8(value: float) -> int:
+    return int(lib().orc_quantize_i8(float(value)))
+
+
+def pattern(index: int, salt: int, amplitude: float) -> float:
+    return float(lib().orc_pattern(index, salt, amplitude))
+
+
+def pattern_fill(count: int, salt: int, amplitude: float, first: int = 0) -> np.ndarray:
+    out = np.empty(count, dtype=np.float32)
+    lib().orc_pattern_fill(_p(out), count, first, salt, amplitude)
+    return out
+
+
+def set_threads(n: int) -> None:
+    lib().orc_set_threads(int(n))
+
+
+# ---- size contracts ----------------------------------------------------------
+
+FORMATS = {"fp16": 0, "fp8_e4m3": 1, "int8": 2, "q4_k": 3, "exl3": 4}
+
+
+def estimate_linear(fmt: str, logical_in: int, logical_out: int, exl3_bits: int = 4):
+    out = np.zeros(6, dtype=np.uint64)
+    status = lib().orc_estimate_linear(FORMATS[fmt], logical_in, logical_out, exl3_bits, _p(out))
+    if status < 0:
+        raise ValueError(f"estimate_linear error {status}")
+    if status == 0:
+        return None
+    keys = ("logical_in", "logical_out", "padded_in", "padded_out", "payload_bytes",
+            "metadata_bytes")
+    return {k: int(v) for k, v in zip(keys, out)}
+
+
+def exl3_layout(logical_in: int, logical_out: int, qbits: int):
+    out = np.zeros(7, dtype=np.uint64)
+    status = lib().orc_exl3_layout(logical_in, logical_out, qbits, _p(out))
+    if status != 0:
+        raise ValueError(f"exl3 error {status}")
+    o = [int(v) for v in out]
+    return {"padded_in": o[0], "padded_out": o[1], "trellis_shape": o[2:5],
+            "trellis_bytes": o[5], "scale_bytes": o[6]}
+
+
+# ---- packers -------------------------------------------------------------------
+
+def pack_fp8_rows(w16: np.ndarray):
+    w16 = _h(w16)
+    n, k = w16.shape
+    q = np.empty((n, k), np.uint8)
+    s = np.empty(n, np.float32)
+    lib().orc_pack_fp8_rows(_p(w16), n, k, _p(q), _p(s))
+    return q, s
+
+
+def pack_int8_rows(w16: np.ndarray):
+    w16 = _h(w16)
+    n, k = w16.shape
+    q = np.empty((n, k), np.int8)
+    s = np.empty(n, np.float32)
+    lib().orc_pack_int8_rows(_p(w16), n, k, _p(q), _p(s))
+    return q, s
+
+
+def pack_int4_rows(w16: np.ndarray):
+    w16 = _h(w16)
+    n, k = w16.shape
+    q = np.empty((n, k // 2), np.uint8)
+    s = np.empty(n, np.float32)
+    lib().orc_pack_int4_rows(_p(w16), n, k, _p(q), _p(s))
+    return q, s
+
+
+def pack_int4_g128(w16: np.ndarray):
+    w16 = _h(w16)
+    n, k = w16.shape
+    q = np.empty((n, k // 8), np.uint32)
+    s = np.empty((n, k // 128), np.float16)
+    z = np.empty((n, k // 128), np.float16)
+    lib().orc_pack_int4_g128(_p(w16), n, k, _p(q), _p(s), _p(z))
+    return q, s, z
+
+
+def pad_fp16_linear(src: np.ndarray, padded_out: int, padded_in: int) -> np.ndarray:
+    src = np.ascontiguousarray(src, dtype=np.float32)
+    lo, li = src.shape
+    dst = np.empty((padded_out, padded_in), np.float16)
+    lib().orc_pad_fp16_linear(_p(src), lo, li, padded_out, padded_in, _p(dst))
+    return dst
+
+
+def q4k_encode(w16: np.ndarray) -> np.ndarray:
+    w16 = _h(w16)
+    n, k = w16.shape
+    out = np.empty((n, k // 256, 144), np.uint8)
+    lib().orc_q4k_encode(_p(w16), n, k, _p(out))
+    return out
+
+
+def q4k_encode_block(src256: np.ndarray) -> np.ndarray:
+    src = _h(np.asarray(src256, dtype=np.float16))
+    out = np.empty(144, np.uint8)
+    lib().orc_q4k_encode_block(_p(src), _p(out))
+    return out
+
+
+def q4k_dequant(blocks: np.ndarray) -> np.ndarray:
+    blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+    n, per_row, _ = blocks.shape
+    out = np.empty((n, per_row * 256), np.float32)
+    f = lib().orc_q4k_value
+    for r in range(n):
+        for b in range(per_row):
+            ptr = blocks[r, b].ctypes.data
+            for i in range(256):
+                out[r, b * 256 + i] = f(ptr, i)
+    return out
+
+
+# ---- activation quantizers ---------------------------------------------------
+
+def quantize_fp8_static(x16: np.ndarray, inverse_scale: float) -> np.ndarray:
+    x16 = _h(x16)
+    out = np.empty(x16.shape, np.uint8)
+    lib().orc_quantize_fp8_static(_p(x16), x16.size, inverse_scale, _p(out))
+    return out
+
+
+def quantize_int8_static(x16: np.ndarray, inverse_scale: float) -> np.ndarray:
+    x16 = _h(x16)
+    out = np.empty(x16.shape, np.int8)
+    lib().orc_quantize_int8_static(_p(x16), x16.size, inverse_scale, _p(out))
+    return out
+
+
+def quantize_fp8_rows(x16: np.ndarray, valid_rows: int | None = None):
+    x16 = _h(x16)
+    m, k = x16.shape
+    q = np.empty((m, k), np.uint8)
+    s = np.empty(m, np.float32)
+    lib().orc_quantize_fp8_rows(_p(x16), m, m if valid_rows is None else valid_rows, k,
+                                _p(q), _p(s))
+    return q, s
+
+
+def quantize_int8_rows(x16: np.ndarray, valid_rows: int | None = None):
+    x16 = _h(x16)
+    m, k = x16.shape
+    q = np.empty((m, k), np.int8)
+    s = np.empty(m, np.float32)
+    lib().orc_quantize_int8_rows(_p(x16), m, m if valid_rows is None else valid_rows, k,
+                                 _p(q), _p(s))
+    return q, s
+
+
+def quantize_int4_rows(x16: np.ndarray, valid_rows: int | None = None):
+    x16 = _h(x16)
+    m, k = x16.shape
+    q = np.empty((m, k // 2), np.uint8)
+    s = np.empty(m, np.float32)
+    lib().orc_quantize_int4_rows(_p(x16), m, m if valid_rows is None else valid_rows, k,
+                                 _p(q), _p(s))
+    return q, s
+
+
+def layer_norm_quantize(x16, gamma16, beta16, epsilon=1e-5, int4=False, valid_rows=None):
+    x16 = _h(x16)
+    m, k = x16.shape
+    assert k == 1024
+    q = np.empty((m, k // 2 if int4 else k), np.uint8)
+    s = np.empty(m, np.float32)
+    normalized = np.empty((m, k), np.float16)
+    lib().orc_layer_norm_quantize(_p(x16), _p(_h(gamma16)), _p(_h(beta16)), m,
+                                  m if valid_rows is None else valid_rows, k, epsilon,
+                                  1 if int4 else 0, _p(q), _p(s), _p(normalized))
+    return q, s, normalized
+
+
+def compress_24(x8: np.ndarray):
+    x8 = np.ascontiguousarray(x8, dtype=np.uint8)
+    m, k = x8.shape
+    data = np.empty((m, k // 2), np.uint8)
+    meta = np.empty((m, k // 8), np.uint8)
+    lib().orc_compress_24(_p(x8), m, k, _p(data), _p(meta))
+    return data, meta
+
+
+def decompress_24(data: np.ndarray, meta: np.ndarray) -> np.ndarray:
+    data = np.ascontiguousarray(data, dtype=np.uint8)
+    meta = np.ascontiguousarray(meta, dtype=np.uint8)
+    m, half = data.shape
+    out = np.empty((m, half * 2), np.uint8)
+    lib().orc_decompress_24(_p(data), _p(meta), m, half * 2, _p(out))
+    return out
+
+
+# ---- GEMMs --------------------------------------------------------------------
+
+def gemm_i8(x: np.ndarray, w: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.int8)
+    w = np.ascontiguousarray(w, np.int8)
+    m, k = x.shape
+    n = w.shape[0]
+    acc = np.empty((m, n), np.int32)
+    lib().orc_gemm_i8_i32(_p(x), _p(w), m, n, k, _p(acc))
+    return acc
+
+
+def gemm_s4(x: np.ndarray, w: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.uint8)
+    w = np.ascontiguousarray(w, np.uint8)
+    m, kh = x.shape
+    n = w.shape[0]
+    acc = np.empty((m, n), np.int32)
+    lib().orc_gemm_s4_i32(_p(x), _p(w), m, n, kh * 2, _p(acc))
+    return acc
+
+
+def gemm_e4m3(x: np.ndarray, w: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.uint8)
+    w = np.ascontiguousarray(w, np.uint8)
+    m, k = x.shape
+    n = w.shape[0]
+    acc = np.empty((m, n), np.float32)
+    lib().orc_gemm_e4m3_f32(_p(x), _p(w), m, n, k, _p(acc))
+    return acc
+
+
+def gemm_f16(x16: np.ndarray, w16: np.ndarray) -> np.ndarray:
+    x16 = _h(x16)
+    w16 = _h(w16)
+    m, k = x16.shape
+    n = w16.shape[0]
+    acc = np.empty((m, n), np.float32)
+    lib().orc_gemm_f16_f32(_p(x16), _p(w16), m, n, k, _p(acc))
+    return acc
+
+
+def gemm_g128_a16(x16, q, s, z) -> np.ndarray:
+    x16 = _h(x16)
+    m, k = x16.shape
+    n = q.shape[0]
+    out = np.empty((m, n), np.float32)
+    lib().orc_gemm_g128_a16(_p(x16), _p(np.ascontiguousarray(q)), _p(_h(s)), _p(_h(z)),
+                            m, n, k, _p(out))
+    return out
+
+
+def gemm_g128_a8(x8, x_scales, q, s, z, want_group_acc=False):
+    x8 = np.ascontiguousarray(x8, np.int8)
+    m, k = x8.shape
+    n = q.shape[0]
+    out = np.empty((m, n), np.float32)
+    gacc = np.empty((m, n, k // 128), np.int32) if want_group_acc else None
+    lib().orc_gemm_g128_a8(_p(x8), _p(np.ascontiguousarray(x_scales, np.float32)),
+                           _p(np.ascontiguousarray(q)), _p(_h(s)), _p(_h(z)), m, n, k,
+                           _p(gacc), _p(out))
+    return (out, gacc) if want_group_acc else out
+
+
+def gemm_q4k(x16, blocks) -> np.ndarray:
+    x16 = _h(x16)
+    m, k = x16.shape
+    n = blocks.shape[0]
+    acc = np.empty((m, n), np.float32)
+    lib().orc_gemm_q4k_f32(_p(x16), _p(np.ascontiguousarray(blocks, np.uint8)), m, n, k,
+                           _p(acc))
+    return acc
+
+
+# ---- epilogues ----------------------------------------------------------------
+
+def epilogue(acc, mode, w_scales, row_scales=None, in_scale=1.0, bias=None, residual=None,
+             valid_rows=None):
+    """ffn_fp8_async epilogue restatement; returns fp16 or e4m3 array."""
+    acc = np.ascontiguousarray(acc, np.float32)
+    m, n = acc.shape
+    ws = np.ascontiguousarray(w_scales, np.float32)
+    rs = None if row_scales is None else np.ascontiguousarray(row_scales, np.float32)
+    b = None if bias is None else np.ascontiguousarray(bias, np.float32)
+    out8 = None
+    if mode == 5:
+        out16 = np.zeros((m, n // 2), np.float16)
+    elif mode in (2, 6, 8):
+        out16 = np.array(residual, dtype=np.float16, copy=True, order="C")
+    else:
+        out16 = np.zeros((m, n), np.float16)
+    if mode in (1, 7):
+        out8 = np.zeros((m, n), np.uint8)
+    lib().orc_epilogue(_p(acc), _p(rs), in_scale, _p(ws), _p(b), m, n, mode,
+                       m if valid_rows is None else valid_rows, _p(out16), _p(out8))
+    return out8 if mode in (1, 7) else out16
+
+
+def epilogue_linear(acc, bias=None, residual=None, out_scale=1.0, res_scale=0.0,
+                    activation=0) -> np.ndarray:
+    acc = np.ascontiguousarray(acc, np.float32)
+    m, n = acc.shape
+    out = np.empty((m, n), np.float16)
+    b = None if bias is None else np.ascontiguousarray(bias, np.float32)
+    r = None if residual is None else _h(residual)
+    lib().orc_epilogue_linear(_p(acc), _p(b), _p(r), m, n, out_scale, res_scale, activation,
+                              _p(out))
+    return out
+
+
+def epilogue_quantized(acc, in_scale, w_scales, bias=None, activation=0) -> np.ndarray:
+    acc = np.ascontiguousarray(acc, np.float32)
+    m, n = acc.shape
+    out = np.empty((m, n), np.float16)
+    b = None if bias is None else np.ascontiguousarray(bias, np.float32)
+    lib().orc_epilogue_quantized(_p(acc), in_scale, _p(np.ascontiguousarray(w_scales, np.float32)),
+                                 _p(b), m, n, activation, _p(out))
+    return out
+
+
+# ---- joint --------------------------------------------------------------------
+
+def joint_scores_f16(w16, bias, enc16, pred):
+    w16 = _h(w16)
+    o, h = w16.shape
+    out = np.empty(o, np.float32)
+    lib().orc_joint_scores_f16(_p(w16), _p(np.ascontiguousarray(bias, np.float32)), _p(_h(enc16)),
+                               _p(np.ascontiguousarray(pred, np.float32)), o, h, _p(out))
+    return out
+
+
+def joint_scores_i8(wq, w_scales, bias, enc16, pred):
+    wq = np.ascontiguousarray(wq, np.int8)
+    o, h = wq.shape
+    out = np.empty(o, np.float32)
+    lib().orc_joint_scores_i8(_p(wq), _p(np.ascontiguousarray(w_scales, np.float32)),
+                              _p(np.ascontiguousarray(bias, np.float32)), _p(_h(enc16)),
+                              _p(np.ascontiguousarray(pred, np.float32)), o, h, _p(out))
+    return out
+
+
+def joint_decide(scores, token_outputs=1025, durations=5):
+    scores = np.ascontiguousarray(scores, np.float32)
+    tok = ctypes.c_int()
+    dur = ctypes.c_int()
+    lib().orc_joint_decide(_p(scores), token_outputs, durations, ctypes.byref(tok),
+                           ctypes.byref(dur))
+    return tok.value, dur.value
