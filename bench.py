@@ -1,0 +1,326 @@
+"""Benchmark: the 24-layer FastConformer linear stack at T=45000 (60 min audio).
+
+One step = every encoder linear of all 24 layers (FF1 expand/contract, QKV,
+attention out, pointwise1, pointwise2, FF2 expand/contract) on the MI355X
+kernels, each layer's linears in a seeded mix of FP8 / INT8 / INT4-g128
+formats.  Inputs and packed weights are resident in
+HBM before timing; weights are random-init with the real shapes (no
+checkpoint is available), activations are synthetic.  Prints one JSON line.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "l4-parakeet-rs_amd"))
+sys.path.insert(0, os.path.join(ROOT, "oracle"))
+
+T = 45000
+D, FF, CONV = 1024, 4096, 2048
+LAYERS = 24
+# (name, n_out, k_in, epilogue kind)
+LINEARS = [
+    ("ff1_expand", FF, D, "f8"),
+    ("ff1_contract", D, FF, "res_half"),
+    ("qkv", 3 * D, D, "f16"),
+    ("attn_out", D, D, "res"),
+    ("pw1", CONV, D, "f16"),
+    ("pw2", D, D, "res"),
+    ("ff2_expand", FF, D, "f8"),
+    ("ff2_contract", D, FF, "res_half"),
+]
+FORMATS = ("fp8", "int8", "int4g128")
+FLOP_PER_FRAME = sum(2 * n * k for _, n, k, _ in LINEARS) * LAYERS  # 1.1576e9
+PEAK = {"fp8": 5000.0, "int8": 5000.0}  # dense TFLOP/s (TOP/s) MI355X
+
+
+def format_plan(seed=0x5EED0005):
+    import numpy as np
+
+    rng = np.random.default_rng(seed)
+    return [[FORMATS[int(rng.integers(0, 3))] for _ in LINEARS] for _ in range(LAYERS)]
+
+
+class Stack:
+    def __init__(self, pk, torch, t_frames, plan):
+        self.pk, self.torch, self.t, self.plan = pk, torch, t_frames, plan
+        dev = "cuda"
+        g = torch.Generator(device=dev)
+        g.manual_seed(1234)
+        # activations: fp16 source, then per-row FP8 and INT8 copies of width 4096
+        src = torch.randn((t_frames, FF), generator=g, device=dev, dtype=torch.float16)
+        self.x8 = torch.empty((t_frames, FF), dtype=torch.uint8, device=dev)
+        self.xi = torch.empty((t_frames, FF), dtype=torch.int8, device=dev)
+        self.xs8 = torch.empty(t_frames, dtype=torch.float32, device=dev)
+        self.xsi = torch.empty(t_frames, dtype=torch.float32, device=dev)
+        pk.call("pk_quantize_rows", 0, src, self.x8, self.xs8, t_frames, t_frames, FF)
+        pk.call("pk_quantize_rows", 1, src, self.xi, self.xsi, t_frames, t_frames, FF)
+        # the same buffers read as [T x 1024] activations use their first 1024 columns
+        # through separate compact copies (row stride must equal K)
+        self.x8d = self.x8[:, :D].contiguous()
+        self.xid = self.xi[:, :D].contiguous()
+        del src
+        self.out8 = torch.empty((t_frames, FF), dtype=torch.uint8, device=dev)
+        self.out16 = torch.empty((t_frames, 3 * D), dtype=torch.float16, device=dev)
+        self.state = torch.randn((t_frames, D), generator=g, device=dev, dtype=torch.float16)
+        self.weights = []
+        for layer in range(LAYERS):
+            lw = []
+            for (name, n, k, _), fmt in zip(LINEARS, plan[layer]):
+                w16 = (torch.randn((n, k), generator=g, device=dev, dtype=torch.float32) * 0.02).half()
+                if fmt == "fp8":
+                    q = torch.empty((n, k), dtype=torch.uint8, device=dev)
+                    s = torch.empty(n, dtype=torch.float32, device=dev)
+                    pk.call("pk_pack_fp8_rows", w16, n, k, q, s)
+                    lw.append((fmt, q, s, None))
+                elif fmt == "int8":
+                    q = torch.empty((n, k), dtype=torch.int8, device=dev)
+                    s = torch.empty(n, dtype=torch.float32, device=dev)
+                    pk.call("pk_pack_int8_rows", w16, n, k, q, s)
+                    lw.append((fmt, q, s, None))
+                else:
+                    q = torch.empty((n, k // 8), dtype=torch.int32, device=dev)
+                    s = torch.empty((n, k // 128), dtype=torch.float16, device=dev)
+                    z = torch.empty((n, k // 128), dtype=torch.float16, device=dev)
+                    pk.call("pk_pack_int4_g128", w16, n, k, q, s, z)
+                    lw.append((fmt, q, s, z))
+                del w16
+            self.weights.append(lw)
+        torch.cuda.synchronize()
+
+    def linear(self, layer, idx, stream=None):
+        pk = self.pk
+        name, n, k, epi = LINEARS[idx]
+        fmt, q, s, z = self.weights[layer][idx]
+        if fmt == "fp8":
+            a, rows, f = (self.x8 if k == FF else self.x8d), self.xs8, pk.FMT_FP8
+        elif fmt == "int8":
+            a, rows, f = (self.xi if k == FF else self.xid), self.xsi, pk.FMT_I8
+        else:
+            a, rows, f = (self.xi if k == FF else self.xid), self.xsi, pk.FMT_G128A8
+        ws = s if fmt != "int4g128" else None
+        gs, gz = (s, z) if fmt == "int4g128" else (None, None)
+        t = self.t
+        if epi == "f8":
+            pk.gemm(f, pk.EPI_F8, a, q, t, n, k, self.out8, w_scales=ws, row_scales=rows,
+                    g_scales=gs, g_zeros=gz, stream=stream)
+        elif epi == "f16":
+            pk.gemm(f, pk.EPI_F16, a, q, t, n, k, self.out16, w_scales=ws, row_scales=rows,
+                    g_scales=gs, g_zeros=gz, stream=stream)
+        else:
+            pk.gemm(f, pk.EPI_F16, a, q, t, n, k, self.state, w_scales=ws, row_scales=rows,
+                    residual=self.state, out_scale=0.5 if epi == "res_half" else 1.0, res_scale=1.0,
+                    g_scales=gs, g_zeros=gz, stream=stream)
+
+    def step(self, stream=None):
+        for layer in range(LAYERS):
+            for idx in range(len(LINEARS)):
+                self.linear(layer, idx, stream)
+
+
+def time_events(torch, fn, reps, stream):
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(reps):
+        fn()
+    end.record(stream)
+    end.synchronize()
+    return start.elapsed_time(end) / reps  # ms
+
+
+def dominant_kernel(pk, torch, t, stream, reps=20):
+    """FF1 expand 1024 -> 4096 FP8 at T frames with the packed-FP8 epilogue:
+    its average launch time on the bench stream, with the algorithmic flops
+    and bytes of one launch."""
+    dev = "cuda"
+    g = torch.Generator(device=dev)
+    g.manual_seed(99)
+    x = torch.randint(0, 0x7E, (t, D), generator=g, device=dev, dtype=torch.uint8)
+    w = torch.randint(0, 0x7E, (FF, D), generator=g, device=dev, dtype=torch.uint8)
+    xs = torch.rand(t, generator=g, device=dev) * 0.01
+    ws = torch.rand(FF, generator=g, device=dev) * 0.01
+    out = torch.empty((t, FF), dtype=torch.uint8, device=dev)
+
+    def run():
+        pk.gemm(pk.FMT_FP8, pk.EPI_F8, x, w, t, FF, D, out, w_scales=ws, row_scales=xs,
+                stream=stream)
+
+    for _ in range(3):
+        run()
+    ms = time_events(torch, run, reps, stream)
+    flops = 2.0 * t * FF * D
+    nbytes = t * D + FF * D + FF * 4 + t * 4 + t * FF
+    return ms, flops, nbytes
+
+
+def joint_bench(pk, torch, stream, reps=2000):
+    """Batch-1 INT8 joint GEMV 640 -> 1030 (+ decision), one launch per frame."""
+    dev = "cuda"
+    outputs, hidden = 1030, 640
+    g = torch.Generator(device=dev)
+    g.manual_seed(7)
+    w = torch.randint(-127, 128, (outputs, hidden), generator=g, device=dev, dtype=torch.int8)
+    ws = torch.rand(outputs, generator=g, device=dev) * 0.01
+    bias = torch.randn(outputs, generator=g, device=dev)
+    enc = torch.randn((1, hidden), generator=g, device=dev).half()
+    pred = torch.randn(hidden, generator=g, device=dev)
+    scores = torch.empty(outputs, dtype=torch.float32, device=dev)
+    dec = torch.empty(2, dtype=torch.int32, device=dev)
+
+    def run():
+        pk.call("pk_joint_gemv", w, 1, ws, bias, enc, pred, scores, dec, outputs, hidden, 1025, 5,
+                1, hidden, stream=stream)
+
+    for _ in range(20):
+        run()
+    ms = time_events(torch, run, reps, stream)
+    nbytes = outputs * hidden + outputs * 4 + outputs * 4 + hidden * 2 + hidden * 4
+    return ms, nbytes
+
+
+def cpu_baseline(plan, budget_s=20.0):
+    """The oracle (a C restatement of the reference's CPU dequantize-then-
+    matmul path) on a bounded sample: layer 0's eight linears over `rows`
+    frames, all host threads, scaled to TOPS."""
+    import numpy as np
+
+    import pk_oracle as orc
+
+    threads = os.cpu_count() or 1
+    threads = min(threads, 16)
+    orc.set_threads(threads)
+    rng = np.random.default_rng(5)
+    rows = 16
+    flops = 0.0
+    t0 = time.perf_counter()
+    while True:
+        for (name, n, k, _), fmt in zip(LINEARS, plan[0]):
+            w = (rng.standard_normal((n, k)) * 0.02).astype(np.float16)
+            x = rng.standard_normal((rows, k)).astype(np.float16)
+            if fmt == "fp8":
+                wq, _ = orc.pack_fp8_rows(w)
+                xq, _ = orc.quantize_fp8_rows(x)
+                ts = time.perf_counter()
+                orc.gemm_e4m3(xq, wq)
+            elif fmt == "int8":
+                wq, _ = orc.pack_int8_rows(w)
+                xq, _ = orc.quantize_int8_rows(x)
+                ts = time.perf_counter()
+                orc.gemm_i8(xq, wq)
+            else:
+                q, s, z = orc.pack_int4_g128(w)
+                xq, xs = orc.quantize_int8_rows(x)
+                ts = time.perf_counter()
+                orc.gemm_g128_a8(xq, xs, q, s, z)
+            flops += 2.0 * rows * n * k
+        elapsed = time.perf_counter() - t0
+        if elapsed > budget_s * 0.4 or rows >= 256:
+            break
+        rows *= 2
+    # time one clean pass at the final size (packing excluded)
+    compute = 0.0
+    flops = 0.0
+    for (name, n, k, _), fmt in zip(LINEARS, plan[0]):
+        w = (rng.standard_normal((n, k)) * 0.02).astype(np.float16)
+        x = rng.standard_normal((rows, k)).astype(np.float16)
+        if fmt == "fp8":
+            wq, _ = orc.pack_fp8_rows(w)
+            xq, _ = orc.quantize_fp8_rows(x)
+            ts = time.perf_counter()
+            orc.gemm_e4m3(xq, wq)
+        elif fmt == "int8":
+            wq, _ = orc.pack_int8_rows(w)
+            xq, _ = orc.quantize_int8_rows(x)
+            ts = time.perf_counter()
+            orc.gemm_i8(xq, wq)
+        else:
+            q, s, z = orc.pack_int4_g128(w)
+            xq, xs = orc.quantize_int8_rows(x)
+            ts = time.perf_counter()
+            orc.gemm_g128_a8(xq, xs, q, s, z)
+        compute += time.perf_counter() - ts
+        flops += 2.0 * rows * n * k
+    return {"value": flops / compute / 1e12, "unit": "TOPS", "cores": threads, "kind": "port",
+            "sample": f"layer 0's 8 linears (seeded formats {plan[0]}) over {rows} frames, "
+                      f"oracle dequantize/integer matmul, {compute:.2f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--frames", type=int, default=T)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(the linears shard by frames with no exchange; see the design notes)",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import parakeet_linear as pk
+
+    torch.cuda.set_device(0)
+    stream = torch.cuda.current_stream()
+    plan = format_plan()
+    print(f"[bench] building stack T={args.frames}", file=sys.stderr, flush=True)
+    stack = Stack(pk, torch, args.frames, plan)
+    for _ in range(args.warmup):
+        stack.step()
+    torch.cuda.synchronize()
+    print("[bench] timing", file=sys.stderr, flush=True)
+    t0 = time.perf_counter()
+    ms_total = time_events(torch, stack.step, args.steps, stream) * args.steps
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_step = ms_total / args.steps
+    total_flops = FLOP_PER_FRAME * args.frames
+    tops = total_flops / (ms_step * 1e-3) / 1e12
+    del stack
+    torch.cuda.empty_cache()
+
+    k_ms, k_flops, k_bytes = dominant_kernel(pk, torch, args.frames, stream)
+    k_tflops = k_flops / (k_ms * 1e-3) / 1e12
+    j_ms, j_bytes = joint_bench(pk, torch, stream)
+    j_gbs = j_bytes / (j_ms * 1e-3) / 1e9
+    cpu = None if args.no_cpu else cpu_baseline(plan)
+
+    audio_min = args.frames * 0.08 / 60.0
+    line = {
+        "metric": "encoder-linear TOPS & %MFMA peak at T=45000; joint GEMV GB/s; ms/audio-min",
+        "value": round(tops, 2),
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8/int8 (mixed per layer, fp32 accumulate)",
+        "data": "synthetic (random-init weights, random activations)",
+        "config": {"workload": "24-layer FastConformer linear stack, T=45000, seeded FP8/INT8/INT4-g128 mix",
+                   "frames": args.frames, "layers": LAYERS, "flop_per_step": total_flops,
+                   "format_plan_seed": "0x5EED0005", "parallelism": "none (1 GPU)"},
+        "pct_mfma_peak": round(100.0 * tops / PEAK["fp8"], 2),
+        "ms_per_audio_min": round(ms_step / audio_min, 4),
+        "joint_gemv": {"us_per_step": round(j_ms * 1e3, 3), "GBps": round(j_gbs, 2),
+                       "bytes_per_step": j_bytes, "pct_hbm": round(100.0 * j_gbs / 8000.0, 3)},
+        "roofline": {"kernel": "gemm_kernel<FP8, EPI_F8> (FF1 expand 1024->4096, T=45000)",
+                     "bound": "mfma", "achieved": round(k_tflops, 2), "peak": PEAK["fp8"],
+                     "unit": "TFLOP/s", "frac": round(k_tflops / PEAK["fp8"], 4), "traffic": None,
+                     "avg_ms": round(k_ms, 4), "algorithmic_bytes": k_bytes},
+        "cpu_baseline": cpu,
+        "wall_s_timed": round(wall, 3),
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

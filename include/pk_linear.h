@@ -1,0 +1,232 @@
+/*
+ * pk_linear.h -- C ABI of libpk_linear.so, the MI355X (gfx950) quantized-weight
+ * linear path of the Parakeet-TDT encoder and joint.
+ *
+ * Drop-in replacement for the launch surface of l4-parakeet-rs: the Rust host
+ * there loads `pk_sm89_*` kernels from a cubin and launches them with cudarc's
+ * positional launch_builder().arg() (src/cuda.rs:698-740,
+ * src/cuda/quant_benchmark.rs:644-745, src/cuda/encoder.rs:1128-1836).  Each
+ * entry point here keeps that kernel's name (prefix pk_ instead of pk_sm89_),
+ * its argument order and meaning, and appends the stream.  Shape constants the
+ * reference bakes into a kernel (1024 -> 4096 etc.) stay baked into the entry
+ * point of the same name; the pk_gemm_* entries take explicit shapes.
+ *
+ * Conventions:
+ *   - All pointers are device pointers unless stated; fp16 data is passed as
+ *     uint16_t bits; weights are [N x K] row-major (weight_oi, linear.cu:75-77).
+ *   - `stream` is a hipStream_t (NULL = the default stream).  Calls only
+ *     enqueue work; nothing synchronises and nothing allocates device memory.
+ *   - Return 0 on success or a negative PK_E_* code; pk_last_error() returns a
+ *     thread-local message for the last failure on the calling thread.
+ *   - Shapes: K must be a multiple of the format's K-step (128 for FP8/INT8,
+ *     256 for packed INT4, 64 for FP16) and N a multiple of 16; M is free
+ *     (the reference pads M to 16, N to 128 and K to 128, which satisfies
+ *     this).  Operand base pointers must be 16-byte aligned.
+ */
+#ifndef PK_LINEAR_H
+#define PK_LINEAR_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PK_OK 0
+#define PK_E_SHAPE (-1)
+#define PK_E_ALIGN (-2)
+#define PK_E_LAUNCH (-3)
+#define PK_E_ARG (-4)
+
+const char* pk_last_error(void);
+/* Version of this ABI (bumped on any signature change). */
+int32_t pk_abi_version(void);
+
+/* ---- size contracts (host only, no GPU) ---------------------------------- */
+
+/* packing.rs:71-130 (estimate_linear).  format: 0 fp16, 1 fp8 e4m3, 2 int8,
+ * 3 GGML Q4_K, 4 EXL3-derived.  out6 = {logical_in, logical_out, padded_in,
+ * padded_out, payload_bytes, metadata_bytes}.  Returns 1 when a layout exists,
+ * 0 for Q4_K with K % 256 != 0 (the reference's None), PK_E_SHAPE for empty
+ * dimensions, PK_E_ARG for an unknown format or bit rate. */
+int32_t pk_estimate_linear(int32_t format, size_t logical_in, size_t logical_out, int32_t exl3_bits,
+                           size_t* out6);
+/* exl3.rs:37-75 (Exl3Layout).  out7 = {padded_in, padded_out, trellis_shape[3],
+ * trellis_bytes, scale_bytes}.  Returns 0, PK_E_SHAPE or PK_E_ARG. */
+int32_t pk_exl3_layout(size_t logical_in, size_t logical_out, int32_t qbits, size_t* out7);
+
+/* ---- load-time weight packers (fp16 [n x k] -> packed) -------------------- */
+
+/* encoder.rs:361-422 FP8 branch / quant_benchmark.rs:779-801: per-row
+ * scale = max|w| / 448 (1 for an all-zero row), q = e4m3(w / scale). */
+int32_t pk_pack_fp8_rows(const uint16_t* weight, int32_t n, int32_t k, uint8_t* packed, float* scales,
+                         void* stream);
+/* quant_benchmark.rs:803-829: per-row scale = max|w| / 127, q = rne clamp +-127. */
+int32_t pk_pack_int8_rows(const uint16_t* weight, int32_t n, int32_t k, int8_t* packed, float* scales,
+                          void* stream);
+/* encoder.rs:378-407 INT4 branch: scale = max(max(w/7, -w/8)), q in [-8, 7],
+ * byte j = q[2j] & 15 | q[2j+1] << 4; packed is [n x k/2]. */
+int32_t pk_pack_int4_rows(const uint16_t* weight, int32_t n, int32_t k, uint8_t* packed, float* scales,
+                          void* stream);
+/* No reference counterpart: group-wise asymmetric INT4,
+ * 128-K groups, q packed 8 per uint32 ([n x k/8]), fp16 scales and integer
+ * fp16 zero-points ([n x k/128]); dequant (q - z) * s. */
+int32_t pk_pack_int4_g128(const uint16_t* weight, int32_t n, int32_t k, uint32_t* packed,
+                          uint16_t* scales, uint16_t* zeros, void* stream);
+
+/* ---- activation quantizers ------------------------------------------------ */
+
+/* linear.cu:537-547 pk_sm89_quantize_fp8: out = e4m3(in * inverse_scale). */
+int32_t pk_quantize_fp8(const uint16_t* input, uint8_t* output, float inverse_scale, int32_t elements,
+                        void* stream);
+/* linear.cu:549-560 pk_sm89_quantize_int8: rne(clamp(in * inverse_scale, +-127)). */
+int32_t pk_quantize_int8(const uint16_t* input, int8_t* output, float inverse_scale, int32_t elements,
+                         void* stream);
+/* encoder.cu:549-559 pk_sm89_quantize_fp8_fixed (note the argument order). */
+int32_t pk_quantize_fp8_fixed(const uint16_t* input, uint8_t* output, int32_t elements, float inverse_scale,
+                              void* stream);
+/* encoder.cu:1129-1146 pk_sm89_quantize_rows1024: per-row FP8, rows of 1024. */
+int32_t pk_quantize_rows1024(const uint16_t* input, uint8_t* output, float* scales, int32_t rows, void* stream);
+/* encoder.cu:1148-1157 pk_sm89_quantize_rows256: per-row FP8, rows of 256. */
+int32_t pk_quantize_rows256(const uint16_t* input, uint8_t* output, float* scales, int32_t rows, void* stream);
+/* encoder.cu:1159-1180 pk_sm89_quantize_ffn_contract: per-row FP8 of the
+ * [1024 x 4096] FF contract weight (grid = 1024 rows in the reference). */
+int32_t pk_quantize_ffn_contract(const uint16_t* input, uint8_t* output, float* scales, void* stream);
+/* Generalised dynamic per-row quantizers over fp16 [rows x k]; rows >=
+ * valid_rows are written as zeros with scale 1.  kind: 0 FP8 (max/448),
+ * 1 INT8 (max/127, per-token dynamic INT8), 2 INT4 (max(x/7, -x/8), [rows x k/2]). */
+int32_t pk_quantize_rows(int32_t kind, const uint16_t* input, void* output, float* scales, int32_t rows,
+                         int32_t valid_rows, int32_t k, void* stream);
+/* encoder.cu:211-306 pk_sm89_layer_norm_quantize_{fp8,int4}_dynamic: LayerNorm
+ * over 1024 features, fp16 rounding, per-row dynamic FP8 / INT4 (+ scales);
+ * rows in [rows, padded_rows) are zero with scale 1. */
+int32_t pk_layer_norm_quantize_fp8_dynamic(const uint16_t* input, const uint16_t* weight, const uint16_t* bias,
+                                           uint8_t* output, float* scales, int32_t rows, int32_t padded_rows,
+                                           float epsilon, void* stream);
+int32_t pk_layer_norm_quantize_int4_dynamic(const uint16_t* input, const uint16_t* weight, const uint16_t* bias,
+                                            uint8_t* output, float* scales, int32_t rows, int32_t padded_rows,
+                                            float epsilon, void* stream);
+
+/* ---- linears (linear.cu) ---------------------------------------------------- */
+
+/* linear.cu:83-171 pk_sm89_fp16_linear_epilogue (+ the _m64 variant and the
+ * cuBLAS GemmEx fallback, cublas.rs:67-113): Y = act((X W^T + b) * out_scale
+ * + res_scale * R), fp16 in/out, fp32 accumulate.  bias / residual may be NULL;
+ * act 0 none, 1 SiLU, 2 ReLU. */
+int32_t pk_linear_fp16_epilogue(const uint16_t* input, const uint16_t* weight_oi, const float* bias,
+                                const uint16_t* residual, uint16_t* output, int32_t m, int32_t n, int32_t k,
+                                float output_scale, float residual_scale, int32_t activation, void* stream);
+/* linear.cu:176-239 pk_sm89_fp16_qkv: three projections into Q|K|V, each
+ * [m x n] contiguous in `output`. */
+int32_t pk_linear_fp16_qkv(const uint16_t* input, const uint16_t* query_weight, const uint16_t* key_weight,
+                           const uint16_t* value_weight, uint16_t* output, int32_t m, int32_t n, int32_t k,
+                           void* stream);
+/* linear.cu:325-374 pk_sm89_fp8_linear_epilogue: Y = act(fma(sum e4m3*e4m3,
+ * in_scale * w_scale[n], bias[n])) -> fp16.  bias may be NULL. */
+int32_t pk_linear_fp8_epilogue(const uint8_t* input, const uint8_t* weight_oi, const float* weight_scales,
+                               const float* bias, uint16_t* output, int32_t m, int32_t n, int32_t k,
+                               float input_scale, int32_t activation, void* stream);
+/* linear.cu:378-429 pk_sm89_int8_linear_epilogue: exact int32 accumulation,
+ * then the same epilogue as the FP8 linear. */
+int32_t pk_linear_int8_epilogue(const int8_t* input, const int8_t* weight_oi, const float* weight_scales,
+                                const float* bias, uint16_t* output, int32_t m, int32_t n, int32_t k,
+                                float input_scale, int32_t activation, void* stream);
+/* The exact INT8 x INT8 -> INT32 accumulators of pk_linear_int8_epilogue
+ * ([m x n] int32), the bit-exact parity instrument of
+ * quant_benchmark.rs:872-909. */
+int32_t pk_linear_int8_accumulate(const int8_t* input, const int8_t* weight_oi, int32_t* accumulators,
+                                  int32_t m, int32_t n, int32_t k, void* stream);
+/* Per-token dynamic INT8 activations (scales [m]) x per-channel INT8 weights:
+ * Y = (acc * input_scales[row]) * weight_scales[n] (+ bias) -> fp16 or fp32. */
+int32_t pk_linear_int8_dyn(const int8_t* input, const float* input_scales, const int8_t* weight_oi,
+                           const float* weight_scales, const float* bias, void* output, int32_t output_fp32,
+                           int32_t m, int32_t n, int32_t k, void* stream);
+/* Per-row FP8 with dynamic per-row activation scales (the ffn_fp8_async
+ * dynamic_scale path, encoder.cu:972-995), fp16 or fp32 output. */
+int32_t pk_linear_fp8_dyn(const uint8_t* input, const float* input_scales, const uint8_t* weight_oi,
+                          const float* weight_scales, const float* bias, void* output, int32_t output_fp32,
+                          int32_t m, int32_t n, int32_t k, void* stream);
+/* s4 x s4 -> exact int32 (the mma...s4.s4 path of encoder.cu:211-292): both
+ * operands packed two per byte ([m x k/2], [n x k/2]). */
+int32_t pk_linear_int4_accumulate(const uint8_t* input, const uint8_t* weight_oi, int32_t* accumulators,
+                                  int32_t m, int32_t n, int32_t k, void* stream);
+/* No reference counterpart.  fp16 activations x
+ * group-wise INT4 weights (pk_pack_int4_g128 layout), weights dequantized to
+ * fp16 in registers, fp32 accumulate; bias may be NULL; fp16 or fp32 output. */
+int32_t pk_linear_int4g128(const uint16_t* input, const uint32_t* weight_q, const uint16_t* weight_scales,
+                           const uint16_t* weight_zeros, const float* bias, void* output, int32_t output_fp32,
+                           int32_t m, int32_t n, int32_t k, void* stream);
+/* Mixed variant: per-token dynamic INT8 activations x group-wise INT4 weights
+ * on the INT8 MFMA; each 128-K group's int32 sum (exact) is scaled by its fp16
+ * scale in fp32, then by the row scale. */
+int32_t pk_linear_int4g128_a8(const int8_t* input, const float* input_scales, const uint32_t* weight_q,
+                              const uint16_t* weight_scales, const uint16_t* weight_zeros, const float* bias,
+                              void* output, int32_t output_fp32, int32_t m, int32_t n, int32_t k, void* stream);
+
+/* ---- encoder FastConformer linears (encoder.cu ffn_fp8_async wrappers) --------
+ * `rows` is the (padded) frame count; per-row fp32 scales come from the
+ * quantizers above.  Widths are those of the reference kernels. */
+
+/* encoder.cu:1063-1069 pk_sm89_ffn_expand_fp8_async: FF1 1024 -> 4096,
+ * SiLU -> fp16 [rows x 4096].  dynamic_scale != 0 uses input_scales[row],
+ * else input_scale. */
+int32_t pk_ffn_expand_fp8(const uint8_t* input, const uint8_t* weight, const float* weight_scales,
+                          const float* input_scales, uint16_t* output, int32_t rows, float input_scale,
+                          int32_t dynamic_scale, void* stream);
+/* encoder.cu:1071-1077 pk_sm89_ffn_expand_fp8_packed: as above, output
+ * e4m3(fp16(SiLU) * 16) bytes [rows x 4096]. */
+int32_t pk_ffn_expand_fp8_packed(const uint8_t* input, const uint8_t* weight, const float* weight_scales,
+                                 const float* input_scales, uint8_t* output, int32_t rows, float input_scale,
+                                 int32_t dynamic_scale, void* stream);
+/* encoder.cu:1079-1085 pk_sm89_ffn_expand_int4_sparse: s4 activations
+ * [rows x 512 bytes] x s4 weights [4096 x 512 bytes], exact int32, then
+ * SiLU -> fp16 -> x16 -> e4m3, 2:4 compressed: `output` receives
+ * [rows x 2048] data bytes followed by [rows x 512] metadata bytes. */
+int32_t pk_ffn_expand_int4_sparse(const uint8_t* input, const uint8_t* weight, const float* weight_scales,
+                                  const float* input_scales, uint8_t* output, int32_t rows, float input_scale,
+                                  int32_t dynamic_scale, void* stream);
+/* encoder.cu:1095-1103 pk_sm89_ffn_contract_fp8: FF contract 4096 -> 1024 on
+ * FP8 input at scale 1/16; output (fp16 [rows x 1024]) += 0.5 * Y in place. */
+int32_t pk_ffn_contract_fp8(const uint8_t* input, const uint8_t* weight, const float* weight_scales,
+                            uint16_t* output, int32_t rows, void* stream);
+/* encoder.cu:1313-1319 pk_sm89_conv_residual_fp8: pointwise2 1024 -> 1024,
+ * dynamic per-row input scales, output += Y in place. */
+int32_t pk_conv_residual_fp8(const uint8_t* input, const uint8_t* weight, const float* weight_scales,
+                             const float* input_scales, uint16_t* output, int32_t rows, void* stream);
+/* encoder.cu:2099-2107 pk_sm89_attention_output_fp8: o_proj 1024 -> 1024,
+ * input scale 1/28, output += Y in place. */
+int32_t pk_attention_output_fp8(const uint8_t* input, const uint8_t* weight, const float* weight_scales,
+                                uint16_t* output, int32_t rows, void* stream);
+
+/* ---- generic fused GEMM ------------------------------------------------------
+ * format: 0 FP8, 1 INT8, 2 INT4 (s4 x s4), 3 INT4-g128 x INT8, 4 FP16,
+ * 5 INT4-g128 x FP16.  epilogue: 0 fp16 (act(v [+bias]) * out_scale
+ * [+ res_scale * residual]), 1 e4m3(fp16(SiLU(v)) * 16), 2 as 1 + 2:4
+ * compression (metadata to out_meta), 3 fp32 v [+bias], 4 raw int32.
+ * v = acc * row_scale * w_scale with row_scale = row_scales[r] or in_scale. */
+int32_t pk_gemm(int32_t format, int32_t epilogue, const void* a, const void* b, int32_t m, int32_t n, int32_t k,
+                const float* w_scales, const float* row_scales, float in_scale, const float* bias,
+                const uint16_t* residual, float out_scale, float res_scale, int32_t activation,
+                const uint16_t* g_scales, const uint16_t* g_zeros, void* out, uint8_t* out_meta, int32_t ldo,
+                void* stream);
+
+/* ---- TDT joint (decoder.cu:690-759) ------------------------------------------ */
+
+/* Batch-1 joint GEMV for `steps` consecutive frames:
+ *   score[o] = bias[o] + w_scale[o] * sum_k W[o,k] * relu(enc[t,k] + pred[k])
+ * for o < outputs, then decision[2t] = argmax over the first token_outputs
+ * scores (ties to the lower id) and decision[2t+1] = the duration argmax over
+ * the next `durations` scores (first maximum wins).  weight is fp16
+ * (weight_int8 = 0, w_scales ignored, may be NULL) or int8 with per-row fp32
+ * scales.  enc is fp16 [steps x enc_stride], pred fp32 [hidden]; scores
+ * (optional, fp32 [steps x outputs]) and decision (int32 [steps x 2]). */
+int32_t pk_joint_gemv(const void* weight, int32_t weight_int8, const float* w_scales, const float* bias,
+                      const uint16_t* enc, const float* pred, float* scores, int32_t* decision,
+                      int32_t outputs, int32_t hidden, int32_t token_outputs, int32_t durations,
+                      int32_t steps, int32_t enc_stride, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,368 @@
+// extern "C" boundary of libpk_linear.so (declared in include/pk_linear.h).
+// Each entry point validates shapes and pointers on the host, fills a
+// GemmArgs or calls a launcher, and reports failures through pk_last_error().
+#include <stdarg.h>
+#include <stdio.h>
+
+#include <string>
+
+#include "../../include/pk_linear.h"
+#include "pk_kernels.hpp"
+
+namespace pk {
+
+static thread_local std::string g_error;
+
+void set_error(const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_error = buf;
+}
+
+static int check_launch(const char* what) {
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        set_error("%s launch failed: %s", what, hipGetErrorString(e));
+        return PK_E_LAUNCH;
+    }
+    return PK_OK;
+}
+
+static GemmArgs base_args(const void* a, const void* b, int m, int n, int k, void* out, int ldo) {
+    GemmArgs g{};
+    g.a = (const uint8_t*)a;
+    g.b = (const uint8_t*)b;
+    g.m = m;
+    g.n = n;
+    g.k = k;
+    g.in_scale = 1.0f;
+    g.out_scale = 1.0f;
+    g.out = out;
+    g.ldo = ldo;
+    g.valid_rows = m;
+    return g;
+}
+
+static bool need(const void* p, const char* name) {
+    if (!p) set_error("%s must not be NULL", name);
+    return p != nullptr;
+}
+
+}  // namespace pk
+
+using namespace pk;
+
+#define STREAM ((hipStream_t)stream)
+
+extern "C" {
+
+const char* pk_last_error(void) { return g_error.c_str(); }
+int32_t pk_abi_version(void) { return 1; }
+
+// ---- size contracts ---------------------------------------------------------
+
+static size_t round_up(size_t v, size_t m) { return (v + m - 1) / m * m; }
+
+int32_t pk_exl3_layout(size_t logical_in, size_t logical_out, int32_t qbits, size_t* out7) {
+    if (logical_in == 0 || logical_out == 0) { set_error("linear dimensions must be nonzero"); return PK_E_SHAPE; }
+    if (qbits < 1 || qbits > 8) { set_error("EXL3 supports integer rates from 1 through 8 bpw, got %d", qbits); return PK_E_ARG; }
+    const size_t pin = round_up(logical_in, 128), pout = round_up(logical_out, 128);
+    out7[0] = pin;
+    out7[1] = pout;
+    out7[2] = pin / 16;
+    out7[3] = pout / 16;
+    out7[4] = 16 * (size_t)qbits;
+    out7[5] = pin * pout * (size_t)qbits / 8;
+    out7[6] = 2 * (pin + pout);
+    return PK_OK;
+}
+
+int32_t pk_estimate_linear(int32_t format, size_t logical_in, size_t logical_out, int32_t exl3_bits, size_t* out6) {
+    if (logical_in == 0 || logical_out == 0) { set_error("linear dimensions must be nonzero"); return PK_E_SHAPE; }
+    out6[0] = logical_in;
+    out6[1] = logical_out;
+    switch (format) {
+    case 0: case 1: case 2: {
+        const size_t pin = round_up(logical_in, 128), pout = round_up(logical_out, 128);
+        out6[2] = pin;
+        out6[3] = pout;
+        out6[4] = pin * pout * (format == 0 ? 2 : 1);
+        out6[5] = format == 0 ? 0 : pout * 4;
+        return 1;
+    }
+    case 3:
+        if (logical_in % 256 != 0) return 0;
+        out6[2] = logical_in;
+        out6[3] = logical_out;
+        out6[4] = logical_out * (logical_in / 256) * 144;
+        out6[5] = 0;
+        return 1;
+    case 4: {
+        size_t e[7];
+        const int32_t st = pk_exl3_layout(logical_in, logical_out, exl3_bits, e);
+        if (st != PK_OK) return st;
+        out6[2] = e[0];
+        out6[3] = e[1];
+        out6[4] = e[5];
+        out6[5] = e[6];
+        return 1;
+    }
+    default:
+        set_error("unknown linear format %d", format);
+        return PK_E_ARG;
+    }
+}
+
+// ---- packers ------------------------------------------------------------------
+
+static int32_t pack_rows(int kind, const uint16_t* w, int32_t n, int32_t k, void* q, float* s, void* stream) {
+    if (n < 0 || k <= 0 || (kind == 2 && k % 2)) { set_error("invalid packer shape n=%d k=%d", n, k); return PK_E_SHAPE; }
+    if (!need(w, "weight") || !need(q, "packed") || !need(s, "scales")) return PK_E_ARG;
+    launch_pack_rows(kind, w, q, s, n, k, STREAM);
+    return check_launch("pack_rows");
+}
+
+int32_t pk_pack_fp8_rows(const uint16_t* w, int32_t n, int32_t k, uint8_t* q, float* s, void* stream) { return pack_rows(0, w, n, k, q, s, stream); }
+int32_t pk_pack_int8_rows(const uint16_t* w, int32_t n, int32_t k, int8_t* q, float* s, void* stream) { return pack_rows(1, w, n, k, q, s, stream); }
+int32_t pk_pack_int4_rows(const uint16_t* w, int32_t n, int32_t k, uint8_t* q, float* s, void* stream) { return pack_rows(2, w, n, k, q, s, stream); }
+
+int32_t pk_pack_int4_g128(const uint16_t* w, int32_t n, int32_t k, uint32_t* q, uint16_t* s, uint16_t* z, void* stream) {
+    if (n < 0 || k <= 0 || k % 128) { set_error("g128 packer needs k %% 128 == 0 (k=%d)", k); return PK_E_SHAPE; }
+    if (!need(w, "weight") || !need(q, "packed") || !need(s, "scales") || !need(z, "zeros")) return PK_E_ARG;
+    launch_pack_g128(w, q, s, z, n, k, STREAM);
+    return check_launch("pack_int4_g128");
+}
+
+// ---- activation quantizers ------------------------------------------------------
+
+int32_t pk_quantize_fp8(const uint16_t* in, uint8_t* out, float inverse_scale, int32_t elements, void* stream) {
+    if (elements < 0) { set_error("negative element count"); return PK_E_SHAPE; }
+    if (elements && (!need(in, "input") || !need(out, "output"))) return PK_E_ARG;
+    launch_quantize_static(in, out, inverse_scale, (size_t)elements, false, STREAM);
+    return check_launch("quantize_fp8");
+}
+
+int32_t pk_quantize_int8(const uint16_t* in, int8_t* out, float inverse_scale, int32_t elements, void* stream) {
+    if (elements < 0) { set_error("negative element count"); return PK_E_SHAPE; }
+    if (elements && (!need(in, "input") || !need(out, "output"))) return PK_E_ARG;
+    launch_quantize_static(in, out, inverse_scale, (size_t)elements, true, STREAM);
+    return check_launch("quantize_int8");
+}
+
+int32_t pk_quantize_fp8_fixed(const uint16_t* in, uint8_t* out, int32_t elements, float inverse_scale, void* stream) {
+    return pk_quantize_fp8(in, out, inverse_scale, elements, stream);
+}
+
+int32_t pk_quantize_rows(int32_t kind, const uint16_t* in, void* out, float* scales, int32_t rows, int32_t valid_rows,
+                         int32_t k, void* stream) {
+    if (kind < 0 || kind > 2) { set_error("quantize kind must be 0 (fp8), 1 (int8) or 2 (int4)"); return PK_E_ARG; }
+    if (rows < 0 || k <= 0 || k % 8) { set_error("quantize_rows needs k %% 8 == 0 (k=%d)", k); return PK_E_SHAPE; }
+    if (rows && (!need(in, "input") || !need(out, "output") || !need(scales, "scales"))) return PK_E_ARG;
+    if (((uintptr_t)in | (uintptr_t)out) & 15) { set_error("quantize_rows pointers must be 16-byte aligned"); return PK_E_ALIGN; }
+    launch_quantize_rows(kind, in, out, scales, rows, valid_rows < 0 ? 0 : valid_rows, k, STREAM);
+    return check_launch("quantize_rows");
+}
+
+int32_t pk_quantize_rows1024(const uint16_t* in, uint8_t* out, float* scales, int32_t rows, void* stream) {
+    return pk_quantize_rows(0, in, out, scales, rows, rows, 1024, stream);
+}
+int32_t pk_quantize_rows256(const uint16_t* in, uint8_t* out, float* scales, int32_t rows, void* stream) {
+    return pk_quantize_rows(0, in, out, scales, rows, rows, 256, stream);
+}
+int32_t pk_quantize_ffn_contract(const uint16_t* in, uint8_t* out, float* scales, void* stream) {
+    return pk_quantize_rows(0, in, out, scales, 1024, 1024, 4096, stream);
+}
+
+static int32_t ln_quantize(bool int4, const uint16_t* in, const uint16_t* w, const uint16_t* b, uint8_t* out, float* scales,
+                           int32_t rows, int32_t padded_rows, float eps, void* stream) {
+    if (rows < 0 || padded_rows < rows) { set_error("need 0 <= rows <= padded_rows"); return PK_E_SHAPE; }
+    if (padded_rows && (!need(in, "input") || !need(w, "weight") || !need(b, "bias") || !need(out, "output") || !need(scales, "scales")))
+        return PK_E_ARG;
+    launch_layer_norm_quantize(int4, in, w, b, out, scales, nullptr, rows, padded_rows, eps, STREAM);
+    return check_launch("layer_norm_quantize");
+}
+
+int32_t pk_layer_norm_quantize_fp8_dynamic(const uint16_t* in, const uint16_t* w, const uint16_t* b, uint8_t* out, float* scales,
+                                           int32_t rows, int32_t padded_rows, float eps, void* stream) {
+    return ln_quantize(false, in, w, b, out, scales, rows, padded_rows, eps, stream);
+}
+int32_t pk_layer_norm_quantize_int4_dynamic(const uint16_t* in, const uint16_t* w, const uint16_t* b, uint8_t* out, float* scales,
+                                            int32_t rows, int32_t padded_rows, float eps, void* stream) {
+    return ln_quantize(true, in, w, b, out, scales, rows, padded_rows, eps, stream);
+}
+
+// ---- linears ---------------------------------------------------------------------
+
+int32_t pk_gemm(int32_t format, int32_t epilogue, const void* a, const void* b, int32_t m, int32_t n, int32_t k,
+                const float* w_scales, const float* row_scales, float in_scale, const float* bias, const uint16_t* residual,
+                float out_scale, float res_scale, int32_t activation, const uint16_t* g_scales, const uint16_t* g_zeros,
+                void* out, uint8_t* out_meta, int32_t ldo, void* stream) {
+    if (!need(a, "a") || !need(b, "b") || !need(out, "out")) return PK_E_ARG;
+    if ((format == FMT_G128A8 || format == FMT_G128A16) && (!need(g_scales, "g_scales") || !need(g_zeros, "g_zeros"))) return PK_E_ARG;
+    if (epilogue == EPI_F8_24 && !need(out_meta, "out_meta")) return PK_E_ARG;
+    if (activation < 0 || activation > 2) { set_error("activation must be 0, 1 or 2"); return PK_E_ARG; }
+    GemmArgs g = base_args(a, b, m, n, k, out, ldo);
+    g.w_scales = w_scales;
+    g.row_scales = row_scales;
+    g.in_scale = in_scale;
+    g.bias = bias;
+    g.residual = residual;
+    g.out_scale = out_scale;
+    g.res_scale = res_scale;
+    g.act = activation;
+    g.g_scales = g_scales;
+    g.g_zeros = g_zeros;
+    g.out_meta = out_meta;
+    return launch_gemm(format, epilogue, g, STREAM);
+}
+
+int32_t pk_linear_fp16_epilogue(const uint16_t* in, const uint16_t* w, const float* bias, const uint16_t* residual, uint16_t* out,
+                                int32_t m, int32_t n, int32_t k, float out_scale, float res_scale, int32_t act, void* stream) {
+    return pk_gemm(FMT_F16, EPI_F16, in, w, m, n, k, nullptr, nullptr, 1.0f, bias, residual, out_scale, res_scale, act, nullptr,
+                   nullptr, out, nullptr, n, stream);
+}
+
+int32_t pk_linear_fp16_qkv(const uint16_t* in, const uint16_t* wq, const uint16_t* wk, const uint16_t* wv, uint16_t* out, int32_t m,
+                           int32_t n, int32_t k, void* stream) {
+    const uint16_t* ws[3] = {wq, wk, wv};
+    for (int i = 0; i < 3; ++i) {
+        const int32_t st = pk_linear_fp16_epilogue(in, ws[i], nullptr, nullptr, out + (size_t)i * m * n, m, n, k, 1.0f, 0.0f, 0, stream);
+        if (st != PK_OK) return st;
+    }
+    return PK_OK;
+}
+
+static int32_t scaled_linear(int fmt, int epi, const void* in, const float* row_scales, float in_scale, int fused,
+                             const void* w, const float* w_scales, const float* bias, const uint16_t* residual,
+                             float out_scale, int32_t act, void* out, int32_t m, int32_t n, int32_t k, void* stream) {
+    if (!need(in, "input") || !need(w, "weight_oi") || !need(out, "output")) return PK_E_ARG;
+    if (act < 0 || act > 2) { set_error("activation must be 0, 1 or 2"); return PK_E_ARG; }
+    GemmArgs g = base_args(in, w, m, n, k, out, n);
+    g.w_scales = w_scales;
+    g.row_scales = row_scales;
+    g.in_scale = in_scale;
+    g.fused_scale = fused;
+    g.bias = bias;
+    g.residual = residual;
+    g.out_scale = out_scale;
+    g.res_scale = 1.0f;
+    g.act = act;
+    return launch_gemm(fmt, epi, g, STREAM);
+}
+
+int32_t pk_linear_fp8_epilogue(const uint8_t* in, const uint8_t* w, const float* ws, const float* bias, uint16_t* out, int32_t m,
+                               int32_t n, int32_t k, float in_scale, int32_t act, void* stream) {
+    if (!need(ws, "weight_scales")) return PK_E_ARG;
+    return scaled_linear(FMT_FP8, EPI_F16, in, nullptr, in_scale, 1, w, ws, bias, nullptr, 1.0f, act, out, m, n, k, stream);
+}
+
+int32_t pk_linear_int8_epilogue(const int8_t* in, const int8_t* w, const float* ws, const float* bias, uint16_t* out, int32_t m,
+                                int32_t n, int32_t k, float in_scale, int32_t act, void* stream) {
+    if (!need(ws, "weight_scales")) return PK_E_ARG;
+    return scaled_linear(FMT_I8, EPI_F16, in, nullptr, in_scale, 1, w, ws, bias, nullptr, 1.0f, act, out, m, n, k, stream);
+}
+
+int32_t pk_linear_int8_accumulate(const int8_t* in, const int8_t* w, int32_t* acc, int32_t m, int32_t n, int32_t k, void* stream) {
+    return scaled_linear(FMT_I8, EPI_I32, in, nullptr, 1.0f, 0, w, nullptr, nullptr, nullptr, 1.0f, 0, acc, m, n, k, stream);
+}
+
+int32_t pk_linear_int4_accumulate(const uint8_t* in, const uint8_t* w, int32_t* acc, int32_t m, int32_t n, int32_t k, void* stream) {
+    return scaled_linear(FMT_S4, EPI_I32, in, nullptr, 1.0f, 0, w, nullptr, nullptr, nullptr, 1.0f, 0, acc, m, n, k, stream);
+}
+
+int32_t pk_linear_int8_dyn(const int8_t* in, const float* in_scales, const int8_t* w, const float* ws, const float* bias, void* out,
+                           int32_t out_fp32, int32_t m, int32_t n, int32_t k, void* stream) {
+    if (!need(in_scales, "input_scales") || !need(ws, "weight_scales")) return PK_E_ARG;
+    return scaled_linear(FMT_I8, out_fp32 ? EPI_F32 : EPI_F16, in, in_scales, 1.0f, 0, w, ws, bias, nullptr, 1.0f, 0, out, m, n, k,
+                         stream);
+}
+
+int32_t pk_linear_fp8_dyn(const uint8_t* in, const float* in_scales, const uint8_t* w, const float* ws, const float* bias, void* out,
+                          int32_t out_fp32, int32_t m, int32_t n, int32_t k, void* stream) {
+    if (!need(in_scales, "input_scales") || !need(ws, "weight_scales")) return PK_E_ARG;
+    return scaled_linear(FMT_FP8, out_fp32 ? EPI_F32 : EPI_F16, in, in_scales, 1.0f, 0, w, ws, bias, nullptr, 1.0f, 0, out, m, n, k,
+                         stream);
+}
+
+int32_t pk_linear_int4g128(const uint16_t* in, const uint32_t* q, const uint16_t* s, const uint16_t* z, const float* bias, void* out,
+                           int32_t out_fp32, int32_t m, int32_t n, int32_t k, void* stream) {
+    return pk_gemm(FMT_G128A16, out_fp32 ? EPI_F32 : EPI_F16, in, q, m, n, k, nullptr, nullptr, 1.0f, bias, nullptr, 1.0f, 0.0f, 0, s, z,
+                   out, nullptr, n, stream);
+}
+
+int32_t pk_linear_int4g128_a8(const int8_t* in, const float* in_scales, const uint32_t* q, const uint16_t* s, const uint16_t* z,
+                              const float* bias, void* out, int32_t out_fp32, int32_t m, int32_t n, int32_t k, void* stream) {
+    if (!need(in_scales, "input_scales")) return PK_E_ARG;
+    return pk_gemm(FMT_G128A8, out_fp32 ? EPI_F32 : EPI_F16, in, q, m, n, k, nullptr, in_scales, 1.0f, bias, nullptr, 1.0f, 0.0f, 0, s,
+                   z, out, nullptr, n, stream);
+}
+
+// ---- encoder wrappers (fixed widths of the reference kernels) -------------------
+
+int32_t pk_ffn_expand_fp8(const uint8_t* in, const uint8_t* w, const float* ws, const float* in_scales, uint16_t* out, int32_t rows,
+                          float in_scale, int32_t dynamic, void* stream) {
+    if (!need(ws, "weight_scales") || (dynamic && !need(in_scales, "input_scales"))) return PK_E_ARG;
+    return scaled_linear(FMT_FP8, EPI_F16, in, dynamic ? in_scales : nullptr, in_scale, 0, w, ws, nullptr, nullptr, 1.0f, 1, out, rows,
+                         4096, 1024, stream);
+}
+
+int32_t pk_ffn_expand_fp8_packed(const uint8_t* in, const uint8_t* w, const float* ws, const float* in_scales, uint8_t* out,
+                                 int32_t rows, float in_scale, int32_t dynamic, void* stream) {
+    if (!need(ws, "weight_scales") || (dynamic && !need(in_scales, "input_scales"))) return PK_E_ARG;
+    return scaled_linear(FMT_FP8, EPI_F8, in, dynamic ? in_scales : nullptr, in_scale, 0, w, ws, nullptr, nullptr, 1.0f, 0, out, rows,
+                         4096, 1024, stream);
+}
+
+int32_t pk_ffn_expand_int4_sparse(const uint8_t* in, const uint8_t* w, const float* ws, const float* in_scales, uint8_t* out,
+                                  int32_t rows, float in_scale, int32_t dynamic, void* stream) {
+    if (!need(in, "input") || !need(w, "weight") || !need(out, "output") || !need(ws, "weight_scales") ||
+        (dynamic && !need(in_scales, "input_scales")))
+        return PK_E_ARG;
+    if (rows < 0) { set_error("negative rows"); return PK_E_SHAPE; }
+    GemmArgs g = base_args(in, w, rows, 4096, 1024, out, 4096);
+    g.w_scales = ws;
+    g.row_scales = dynamic ? in_scales : nullptr;
+    g.in_scale = in_scale;
+    g.out_meta = out + (size_t)rows * 2048;
+    return launch_gemm(FMT_S4, EPI_F8_24, g, STREAM);
+}
+
+int32_t pk_ffn_contract_fp8(const uint8_t* in, const uint8_t* w, const float* ws, uint16_t* out, int32_t rows, void* stream) {
+    if (!need(ws, "weight_scales")) return PK_E_ARG;
+    return scaled_linear(FMT_FP8, EPI_F16, in, nullptr, 1.0f / 16.0f, 0, w, ws, nullptr, out, 0.5f, 0, out, rows, 1024, 4096, stream);
+}
+
+int32_t pk_conv_residual_fp8(const uint8_t* in, const uint8_t* w, const float* ws, const float* in_scales, uint16_t* out, int32_t rows,
+                             void* stream) {
+    if (!need(ws, "weight_scales") || !need(in_scales, "input_scales")) return PK_E_ARG;
+    return scaled_linear(FMT_FP8, EPI_F16, in, in_scales, 1.0f, 0, w, ws, nullptr, out, 1.0f, 0, out, rows, 1024, 1024, stream);
+}
+
+int32_t pk_attention_output_fp8(const uint8_t* in, const uint8_t* w, const float* ws, uint16_t* out, int32_t rows, void* stream) {
+    if (!need(ws, "weight_scales")) return PK_E_ARG;
+    return scaled_linear(FMT_FP8, EPI_F16, in, nullptr, 1.0f / 28.0f, 0, w, ws, nullptr, out, 1.0f, 0, out, rows, 1024, 1024, stream);
+}
+
+// ---- joint ------------------------------------------------------------------------
+
+int32_t pk_joint_gemv(const void* w, int32_t w_int8, const float* w_scales, const float* bias, const uint16_t* enc, const float* pred,
+                      float* scores, int32_t* decision, int32_t outputs, int32_t hidden, int32_t token_outputs, int32_t durations,
+                      int32_t steps, int32_t enc_stride, void* stream) {
+    if (outputs <= 0 || hidden <= 0 || hidden > 1024 || hidden % 16 || steps < 0 || enc_stride < hidden || token_outputs <= 0 ||
+        durations < 0 || token_outputs + durations > outputs) {
+        set_error("invalid joint shape outputs=%d hidden=%d tokens=%d durations=%d steps=%d stride=%d", outputs, hidden, token_outputs,
+                  durations, steps, enc_stride);
+        return PK_E_SHAPE;
+    }
+    if (!need(w, "weight") || !need(enc, "enc") || !need(pred, "pred") || !need(scores, "scores")) return PK_E_ARG;
+    if (w_int8 && !need(w_scales, "w_scales")) return PK_E_ARG;
+    if (((uintptr_t)w & 15) || ((size_t)enc_stride % 2)) { set_error("joint weight must be 16-byte aligned"); return PK_E_ALIGN; }
+    launch_joint(w, w_int8, w_scales, bias, enc, pred, scores, decision, outputs, hidden, token_outputs, durations, steps, enc_stride,
+                 STREAM);
+    return check_launch("joint_gemv");
+}
+
+}  // extern "C"

@@ -1,0 +1,74 @@
+// Shared device helpers for the gfx950 quantized-linear kernels.
+#pragma once
+
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef int v2i __attribute__((ext_vector_type(2)));
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x8 __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 v2h __attribute__((ext_vector_type(2)));
+
+namespace pk {
+
+// ---- fp16 --------------------------------------------------------------
+__device__ __forceinline__ float h2f(uint16_t bits) {
+    return (float)__builtin_bit_cast(_Float16, bits);
+}
+__device__ __forceinline__ uint16_t f2h(float v) {  // round to nearest even
+    return __builtin_bit_cast(uint16_t, (_Float16)v);
+}
+__device__ __forceinline__ float round_f16(float v) { return (float)(_Float16)v; }
+
+// ---- OCP FP8 E4M3 --------------------------------------------------------
+// gfx950's v_cvt_pk_fp8_f32 encodes OCP E4M3 with round-to-nearest-even.
+// The reference's encoders saturate finite overflow to +-448
+// (encoder.cu:557 `__nv_fp8_e4m3`, quant_benchmark.rs:797), so values are
+// clamped first; NaN is mapped to 0x7f explicitly because the clamp would
+// otherwise turn it into a finite value.
+__device__ __forceinline__ uint32_t e4m3x2(float a, float b) {
+    float ca = __builtin_fminf(__builtin_fmaxf(a, -448.0f), 448.0f);
+    float cb = __builtin_fminf(__builtin_fmaxf(b, -448.0f), 448.0f);
+    uint32_t packed = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(ca, cb, 0, false) & 0xffffu;
+    if (a != a) packed = (packed & 0xff00u) | 0x7fu;
+    if (b != b) packed = (packed & 0x00ffu) | 0x7f00u;
+    return packed;
+}
+__device__ __forceinline__ uint8_t e4m3(float a) { return (uint8_t)(e4m3x2(a, 0.0f) & 0xff); }
+
+__device__ __forceinline__ float e4m3_to_f32(uint32_t byte) {
+    uint32_t e = (byte >> 3) & 15, m = byte & 7;
+    float mag = e == 0 ? (float)m * 0.001953125f
+                       : __builtin_bit_cast(float, ((e + 120u) << 23) | (m << 20));
+    return (byte & 0x80) ? -mag : mag;
+}
+
+// ---- integer helpers -------------------------------------------------------
+__device__ __forceinline__ int rne_clamp(float v, int lo, int hi) {
+    float r = __builtin_rintf(v);
+    r = __builtin_fminf(__builtin_fmaxf(r, (float)lo), (float)hi);
+    return (v != v) ? 0 : (int)r;
+}
+
+// Eight signed nibbles (two per byte) -> eight int8 bytes.  `lo` gets the low
+// nibbles of the four bytes, `hi` the high nibbles.  Each byte x in [0,15]
+// becomes x - 16*(x >= 8) without carries between bytes.
+__device__ __forceinline__ void s4x8_to_s8(uint32_t w, uint32_t& lo, uint32_t& hi) {
+    uint32_t l = w & 0x0f0f0f0fu, h = (w >> 4) & 0x0f0f0f0fu;
+    lo = ((l ^ 0x08080808u) + 0x78787878u) ^ 0x80808080u;
+    hi = ((h ^ 0x08080808u) + 0x78787878u) ^ 0x80808080u;
+}
+
+// ---- reductions over a 256-thread block ------------------------------------
+__device__ __forceinline__ float wave_max(float v) {
+    for (int off = 32; off > 0; off >>= 1) v = __builtin_fmaxf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
+__device__ __forceinline__ float silu(float v) { return v / (1.0f + __expf(-v)); }
+
+}  // namespace pk

@@ -1,0 +1,84 @@
+// Instantiations and the launcher of the byte-tile GEMM engine.
+#include <mutex>
+
+#include "pk_kernels.hpp"
+
+namespace pk {
+
+template <int F, int E>
+static int launch_one(const GemmArgs& a, hipStream_t s) {
+    static std::once_flag once;
+    static hipError_t attr = hipSuccess;
+    std::call_once(once, [] {
+        attr = hipFuncSetAttribute((const void*)gemm_kernel<F, E>, hipFuncAttributeMaxDynamicSharedMemorySize, 2 * kStageBytes);
+    });
+    if (attr != hipSuccess) {
+        set_error("hipFuncSetAttribute(LDS %d bytes) failed: %s", 2 * kStageBytes, hipGetErrorString(attr));
+        return -3;
+    }
+    const unsigned tiles = (unsigned)(((a.m + kBlockM - 1) / kBlockM) * ((a.n + kBlockN - 1) / kBlockN));
+    hipLaunchKernelGGL((gemm_kernel<F, E>), dim3(tiles), dim3(kThreads), 2 * kStageBytes, s, a);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        set_error("gemm launch (fmt %d, epi %d) failed: %s", F, E, hipGetErrorString(e));
+        return -3;
+    }
+    return 0;
+}
+
+template <int F>
+static int by_epi(int epi, const GemmArgs& a, hipStream_t s) {
+    switch (epi) {
+    case EPI_F16: return launch_one<F, EPI_F16>(a, s);
+    case EPI_F32: return launch_one<F, EPI_F32>(a, s);
+    case EPI_F8: return launch_one<F, EPI_F8>(a, s);
+    case EPI_F8_24: return launch_one<F, EPI_F8_24>(a, s);
+    case EPI_I32:
+        if constexpr (F == FMT_I8 || F == FMT_S4) return launch_one<F, EPI_I32>(a, s);
+        break;
+    default: break;
+    }
+    set_error("unsupported epilogue %d for format %d", epi, F);
+    return -4;
+}
+
+static int k_step(int fmt) {
+    switch (fmt) {
+    case FMT_FP8: case FMT_I8: case FMT_G128A8: return 128;
+    case FMT_S4: return 256;
+    default: return 64;
+    }
+}
+
+int launch_gemm(int fmt, int epi, const GemmArgs& a, hipStream_t s) {
+    if (a.m < 0 || a.n <= 0 || a.k <= 0) {
+        set_error("invalid GEMM shape m=%d n=%d k=%d", a.m, a.n, a.k);
+        return -1;
+    }
+    if (a.k % k_step(fmt) != 0 || ((fmt == FMT_G128A8 || fmt == FMT_G128A16) && a.k % 128 != 0)) {
+        set_error("k=%d must be a multiple of %d for format %d", a.k, k_step(fmt), fmt);
+        return -1;
+    }
+    if (a.n % 16 != 0 || a.ldo % 16 != 0 || a.ldo < a.n) {
+        set_error("n=%d and ldo=%d must be multiples of 16 with ldo >= n", a.n, a.ldo);
+        return -1;
+    }
+    if (((uintptr_t)a.a | (uintptr_t)a.b | (uintptr_t)a.out) & 15) {
+        set_error("operand pointers must be 16-byte aligned");
+        return -2;
+    }
+    if (a.m == 0) return 0;
+    switch (fmt) {
+    case FMT_FP8: return by_epi<FMT_FP8>(epi, a, s);
+    case FMT_I8: return by_epi<FMT_I8>(epi, a, s);
+    case FMT_S4: return by_epi<FMT_S4>(epi, a, s);
+    case FMT_G128A8: return by_epi<FMT_G128A8>(epi, a, s);
+    case FMT_F16: return by_epi<FMT_F16>(epi, a, s);
+    case FMT_G128A16: return by_epi<FMT_G128A16>(epi, a, s);
+    default: break;
+    }
+    set_error("unknown format %d", fmt);
+    return -4;
+}
+
+}  // namespace pk

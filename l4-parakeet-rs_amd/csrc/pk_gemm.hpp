@@ -1,0 +1,403 @@
+// Byte-tile GEMM engine for the quantized linears (gfx950 / CDNA4).
+//
+// One workgroup = 8 wave64s computing a 256x256 output tile; wave w owns
+// rows 128*(w/4) .. +128 and columns 64*(w%4) .. +64 as 8x4 MFMA 16x16
+// tiles.  Every K-step moves 128 bytes of each A row (256 rows) and up to 128
+// bytes of each B row (256 rows) global -> registers -> LDS (double
+// buffered, one barrier per step); the 16-byte chunks of each 128-byte LDS row
+// are XOR-swizzled by (row & 7) so the 16 lanes that read one chunk column hit
+// distinct banks.  The operand format only changes how a lane's two 16-byte
+// chunks (K slots [16g, 16g+16) and [64+16g, 64+16g+16) of the step, g =
+// lane/16) are decoded and which MFMA consumes them:
+//   FP8     e4m3 x e4m3   v_mfma_f32_16x16x128_f8f6f4      K/step 128
+//   I8      s8 x s8       2 x v_mfma_i32_16x16x64_i8       K/step 128 (exact)
+//   S4      s4 x s4       nibbles -> s8, 4 x i8 MFMA       K/step 256 (exact)
+//   G128A8  s8 x (q-z)    group-wise INT4 weights, i8 MFMA per 128-K group,
+//                         fp32 fma of each group sum with its fp16 scale
+//   F16     f16 x f16     2 x v_mfma_f32_16x16x32_f16      K/step 64
+//   G128A16 f16 x f16((q-z)*s)  INT4 weights dequantized in registers
+// The epilogue stages each wave's accumulators through LDS (16 rows at a
+// time) so every lane finishes 16 consecutive columns of one row with 16- or
+// 32-byte global stores.
+#pragma once
+
+#include "pk_common.hpp"
+
+namespace pk {
+
+enum Fmt { FMT_FP8 = 0, FMT_I8 = 1, FMT_S4 = 2, FMT_G128A8 = 3, FMT_F16 = 4, FMT_G128A16 = 5 };
+
+enum Epi {
+    EPI_F16 = 0,     // fp16 out: act(scale(acc) [+bias]) * out_scale [+ res_scale * residual]
+    EPI_F8 = 1,      // e4m3 out: e4m3(fp16(silu(scale(acc))) * 16)
+    EPI_F8_24 = 2,   // as EPI_F8, then 2:4 compressed data + 4-bit metadata
+    EPI_F32 = 3,     // fp32 out: scale(acc) [+bias]
+    EPI_I32 = 4,     // raw int32 accumulators (integer formats only)
+    EPI_GLU = 5,     // fp16 out: fp16(v) * sigmoid(fp16(g)), column pairs (c, c + N/2)
+};
+
+struct GemmArgs {
+    const uint8_t* a;           // [M x K] activations, row-major
+    const uint8_t* b;           // [N x K] weights (weight_oi), row-major, format-specific bytes
+    int m, n, k;                // logical sizes, k in elements
+    const float* w_scales;      // [N] per output channel, or null (1.0)
+    const float* row_scales;    // [M] per-row activation scales, or null (in_scale)
+    float in_scale;
+    int fused_scale;            // 1: v = fma(acc, in_scale * w_scale, bias) (linear.cu:362-365)
+                                // 0: v = acc * row_scale * w_scale [+ bias] (encoder.cu:975-995)
+    const float* bias;          // [N] or null
+    const uint16_t* residual;   // fp16 [M x ldo] or null (may alias out)
+    float out_scale;
+    float res_scale;
+    int act;                    // 0 none, 1 SiLU, 2 ReLU
+    const uint16_t* g_scales;   // G128 formats: fp16 [N x K/128]
+    const uint16_t* g_zeros;    // G128 formats: fp16 [N x K/128], integer valued
+    void* out;
+    uint8_t* out_meta;          // EPI_F8_24: [M x ldo/8] metadata bytes
+    int ldo;                    // output row stride in elements (of the output type)
+    int valid_rows;             // EPI_GLU: rows >= valid_rows are written as 0
+};
+
+constexpr int kBlockM = 256;
+constexpr int kBlockN = 256;
+constexpr int kThreads = 512;
+constexpr int kRowBytes = 128;
+constexpr int kTileBytes = kBlockM * kRowBytes;  // one operand tile per stage
+constexpr int kStageBytes = 2 * kTileBytes;
+
+template <int F> struct FmtTraits;
+template <> struct FmtTraits<FMT_FP8> { static constexpr int kStep = 128, bRow = 128, aElemNum = 1, aElemDen = 1, bNum = 1, bDen = 1; static constexpr bool kInt = false; };
+template <> struct FmtTraits<FMT_I8> { static constexpr int kStep = 128, bRow = 128, aElemNum = 1, aElemDen = 1, bNum = 1, bDen = 1; static constexpr bool kInt = true; };
+template <> struct FmtTraits<FMT_S4> { static constexpr int kStep = 256, bRow = 128, aElemNum = 1, aElemDen = 2, bNum = 1, bDen = 2; static constexpr bool kInt = true; };
+template <> struct FmtTraits<FMT_G128A8> { static constexpr int kStep = 128, bRow = 64, aElemNum = 1, aElemDen = 1, bNum = 1, bDen = 2; static constexpr bool kInt = false; };
+template <> struct FmtTraits<FMT_F16> { static constexpr int kStep = 64, bRow = 128, aElemNum = 2, aElemDen = 1, bNum = 2, bDen = 1; static constexpr bool kInt = false; };
+template <> struct FmtTraits<FMT_G128A16> { static constexpr int kStep = 64, bRow = 32, aElemNum = 2, aElemDen = 1, bNum = 1, bDen = 2; static constexpr bool kInt = false; };
+
+__device__ __forceinline__ int swz(int row, int chunk) { return row * kRowBytes + ((chunk ^ (row & 7)) << 4); }
+
+// Four unsigned nibbles (byte j of `w`, low nibble = k j, high = k 4+j) ->
+// eight int8 (q - z), natural k order, as two dwords.
+__device__ __forceinline__ void u4x8_minus_z(uint32_t w, uint32_t zz, uint32_t& first, uint32_t& second) {
+    uint32_t l = w & 0x0f0f0f0fu, h = (w >> 4) & 0x0f0f0f0fu;
+    first = ((l | 0x80808080u) - zz) ^ 0x80808080u;
+    second = ((h | 0x80808080u) - zz) ^ 0x80808080u;
+}
+
+// Eight unsigned nibbles of one word -> eight halves f16((q - z) * s), k order.
+__device__ __forceinline__ v8h u4x8_to_h(uint32_t w, v2h zz, v2h ss) {
+    uint32_t l = w & 0x0f0f0f0fu, h = (w >> 4) & 0x0f0f0f0fu;
+    uint32_t p0 = __builtin_amdgcn_perm(0u, l, 0x0c010c00u) | 0x64006400u;
+    uint32_t p1 = __builtin_amdgcn_perm(0u, l, 0x0c030c02u) | 0x64006400u;
+    uint32_t p2 = __builtin_amdgcn_perm(0u, h, 0x0c010c00u) | 0x64006400u;
+    uint32_t p3 = __builtin_amdgcn_perm(0u, h, 0x0c030c02u) | 0x64006400u;
+    v2h r0 = (__builtin_bit_cast(v2h, p0) - zz) * ss;
+    v2h r1 = (__builtin_bit_cast(v2h, p1) - zz) * ss;
+    v2h r2 = (__builtin_bit_cast(v2h, p2) - zz) * ss;
+    v2h r3 = (__builtin_bit_cast(v2h, p3) - zz) * ss;
+    v8h out = {r0[0], r0[1], r1[0], r1[1], r2[0], r2[1], r3[0], r3[1]};
+    return out;
+}
+
+template <int F>
+__device__ __forceinline__ void mfma_step(v4f& accf, v4i& acci, const uint4& a0, const uint4& a1,
+                                          const uint4& b0, const uint4& b1, float gscale) {
+    if constexpr (F == FMT_FP8) {
+        v8i A = {(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w, (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
+        v8i B = {(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w, (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
+        accf = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A, B, accf, 0, 0, 0, 0, 0, 0);
+    } else if constexpr (F == FMT_I8) {
+        v4i A0 = {(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w};
+        v4i A1 = {(int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
+        v4i B0 = {(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w};
+        v4i B1 = {(int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
+        acci = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0, B0, acci, 0, 0, 0);
+        acci = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1, B1, acci, 0, 0, 0);
+    } else if constexpr (F == FMT_S4) {
+        uint32_t al[8], bl[8];
+        s4x8_to_s8(a0.x, al[0], al[4]); s4x8_to_s8(a0.y, al[1], al[5]);
+        s4x8_to_s8(a0.z, al[2], al[6]); s4x8_to_s8(a0.w, al[3], al[7]);
+        s4x8_to_s8(b0.x, bl[0], bl[4]); s4x8_to_s8(b0.y, bl[1], bl[5]);
+        s4x8_to_s8(b0.z, bl[2], bl[6]); s4x8_to_s8(b0.w, bl[3], bl[7]);
+        v4i A0 = {(int)al[0], (int)al[1], (int)al[2], (int)al[3]}, A1 = {(int)al[4], (int)al[5], (int)al[6], (int)al[7]};
+        v4i B0 = {(int)bl[0], (int)bl[1], (int)bl[2], (int)bl[3]}, B1 = {(int)bl[4], (int)bl[5], (int)bl[6], (int)bl[7]};
+        acci = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0, B0, acci, 0, 0, 0);
+        acci = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1, B1, acci, 0, 0, 0);
+        s4x8_to_s8(a1.x, al[0], al[4]); s4x8_to_s8(a1.y, al[1], al[5]);
+        s4x8_to_s8(a1.z, al[2], al[6]); s4x8_to_s8(a1.w, al[3], al[7]);
+        s4x8_to_s8(b1.x, bl[0], bl[4]); s4x8_to_s8(b1.y, bl[1], bl[5]);
+        s4x8_to_s8(b1.z, bl[2], bl[6]); s4x8_to_s8(b1.w, bl[3], bl[7]);
+        v4i A2 = {(int)al[0], (int)al[1], (int)al[2], (int)al[3]}, A3 = {(int)al[4], (int)al[5], (int)al[6], (int)al[7]};
+        v4i B2 = {(int)bl[0], (int)bl[1], (int)bl[2], (int)bl[3]}, B3 = {(int)bl[4], (int)bl[5], (int)bl[6], (int)bl[7]};
+        acci = __builtin_amdgcn_mfma_i32_16x16x64_i8(A2, B2, acci, 0, 0, 0);
+        acci = __builtin_amdgcn_mfma_i32_16x16x64_i8(A3, B3, acci, 0, 0, 0);
+    } else if constexpr (F == FMT_G128A8) {
+        // b0/b1 already hold (q - z) as int8 (decoded once per step).
+        v4i A0 = {(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w};
+        v4i A1 = {(int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
+        v4i B0 = {(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w};
+        v4i B1 = {(int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
+        v4i zero = {0, 0, 0, 0};
+        v4i g = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0, B0, zero, 0, 0, 0);
+        g = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1, B1, g, 0, 0, 0);
+        accf[0] = __builtin_fmaf((float)g[0], gscale, accf[0]);
+        accf[1] = __builtin_fmaf((float)g[1], gscale, accf[1]);
+        accf[2] = __builtin_fmaf((float)g[2], gscale, accf[2]);
+        accf[3] = __builtin_fmaf((float)g[3], gscale, accf[3]);
+    } else {  // F16 and G128A16 (B already dequantized to halves)
+        v8h A0 = __builtin_bit_cast(v8h, a0), A1 = __builtin_bit_cast(v8h, a1);
+        v8h B0 = __builtin_bit_cast(v8h, b0), B1 = __builtin_bit_cast(v8h, b1);
+        accf = __builtin_amdgcn_mfma_f32_16x16x32_f16(A0, B0, accf, 0, 0, 0);
+        accf = __builtin_amdgcn_mfma_f32_16x16x32_f16(A1, B1, accf, 0, 0, 0);
+    }
+}
+
+// Block index -> (m tile, n tile).  Workgroups are dispatched round-robin over
+// the 8 XCDs; remap so each XCD owns a contiguous run of tiles (N fastest),
+// which keeps an XCD's concurrent tiles on a couple of A row-strips and lets
+// its L2 serve the shared A and B tiles.
+__device__ __forceinline__ void tile_of(int& tm, int& tn, int tiles_n) {
+    const int b = blockIdx.x, nb = gridDim.x;
+    const int q = nb >> 3, r = nb & 7, x = b & 7, local = b >> 3;
+    const int t = x * q + (x < r ? x : r) + local;
+    tm = t / tiles_n;
+    tn = t - tm * tiles_n;
+}
+
+template <int F, int E>
+__global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs p) {
+    using T = FmtTraits<F>;
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 2, wn = wave & 3;
+    const int tiles_n = (p.n + kBlockN - 1) / kBlockN;
+    int tm, tn;
+    tile_of(tm, tn, tiles_n);
+    const int m0 = tm * kBlockM, n0 = tn * kBlockN;
+
+    const size_t lda = (size_t)p.k * T::aElemNum / T::aElemDen;  // bytes per A row
+    const size_t ldb = (size_t)p.k * T::bNum / T::bDen;          // bytes per B row
+    const int steps = p.k / T::kStep;
+
+    // Global -> register staging: A is 256 rows x 8 chunks = 2048 chunks
+    // (4 per thread); B is 256 rows x bRow/16 chunks.
+    constexpr int kBChunks = T::bRow / 16;
+    constexpr int kBLoads = (kBlockN * kBChunks) / kThreads;
+    uint4 ra[4], rb[kBLoads];
+    uint32_t a_off[4], b_off[kBLoads];
+    uint32_t a_dst[4], b_dst[kBLoads];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int q = tid + i * kThreads, row = q >> 3, c = q & 7;
+        const int grow = min(m0 + row, p.m - 1);
+        a_off[i] = (uint32_t)((size_t)grow * lda + c * 16);
+        a_dst[i] = swz(row, c);
+    }
+#pragma unroll
+    for (int i = 0; i < kBLoads; ++i) {
+        const int q = tid + i * kThreads, row = q / kBChunks, c = q % kBChunks;
+        const int grow = min(n0 + row, p.n - 1);
+        b_off[i] = (uint32_t)((size_t)grow * ldb + c * 16);
+        b_dst[i] = T::bRow == 128 ? swz(row, c) : row * T::bRow + c * 16;
+    }
+    const uint8_t* __restrict__ pa = p.a;
+    const uint8_t* __restrict__ pb = p.b;
+
+#define PK_GLOAD(step)                                                                          \
+    {                                                                                           \
+        _Pragma("unroll") for (int i = 0; i < 4; ++i) ra[i] =                                  \
+            *(const uint4*)(pa + a_off[i] + (size_t)(step) * kRowBytes);                        \
+        _Pragma("unroll") for (int i = 0; i < kBLoads; ++i) rb[i] =                            \
+            *(const uint4*)(pb + b_off[i] + (size_t)(step) * T::bRow);                          \
+    }
+#define PK_LSTORE(buf)                                                                          \
+    {                                                                                           \
+        uint8_t* base_ = lds + (buf) * kStageBytes;                                             \
+        _Pragma("unroll") for (int i = 0; i < 4; ++i) *(uint4*)(base_ + a_dst[i]) = ra[i];      \
+        _Pragma("unroll") for (int i = 0; i < kBLoads; ++i)                                     \
+            *(uint4*)(base_ + kTileBytes + b_dst[i]) = rb[i];                                   \
+    }
+
+    v4f accf[8][4];
+    v4i acci[8][4];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            accf[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+            acci[i][j] = v4i{0, 0, 0, 0};
+        }
+
+    const int g = lane >> 4, l16 = lane & 15;
+    PK_GLOAD(0);
+    PK_LSTORE(0);
+    __syncthreads();
+
+    for (int step = 0; step < steps; ++step) {
+        const int buf = step & 1;
+        {
+            const int next = step + 1 < steps ? step + 1 : step;
+            PK_GLOAD(next);
+        }
+        const uint8_t* As = lds + buf * kStageBytes;
+        const uint8_t* Bs = As + kTileBytes;
+
+        // Decode this wave's four B fragments.
+        uint4 b0[4], b1[4];
+        float gs[4] = {1.f, 1.f, 1.f, 1.f};
+#pragma unroll
+        for (int bj = 0; bj < 4; ++bj) {
+            const int row = wn * 64 + bj * 16 + l16;
+            if constexpr (T::bRow == 128) {
+                b0[bj] = *(const uint4*)(Bs + swz(row, g));
+                b1[bj] = *(const uint4*)(Bs + swz(row, 4 + g));
+            } else {
+                const int ncol = min(n0 + row, p.n - 1);
+                const int kg = (step * T::kStep) / 128;
+                const size_t gi = (size_t)ncol * (p.k / 128) + kg;
+                const float z = h2f(p.g_zeros[gi]);
+                if constexpr (F == FMT_G128A8) {
+                    gs[bj] = h2f(p.g_scales[gi]);
+                    const uint32_t zz = (uint32_t)(int)z * 0x01010101u;
+                    const uint2 w0 = *(const uint2*)(Bs + row * 64 + 8 * g);
+                    const uint2 w1 = *(const uint2*)(Bs + row * 64 + 32 + 8 * g);
+                    u4x8_minus_z(w0.x, zz, b0[bj].x, b0[bj].y);
+                    u4x8_minus_z(w0.y, zz, b0[bj].z, b0[bj].w);
+                    u4x8_minus_z(w1.x, zz, b1[bj].x, b1[bj].y);
+                    u4x8_minus_z(w1.y, zz, b1[bj].z, b1[bj].w);
+                } else {  // G128A16
+                    const _Float16 s = __builtin_bit_cast(_Float16, p.g_scales[gi]);
+                    const _Float16 zh = (_Float16)(1024.0f + z);
+                    const v2h ss = {s, s}, zz = {zh, zh};
+                    const uint32_t w0 = *(const uint32_t*)(Bs + row * 32 + 4 * g);
+                    const uint32_t w1 = *(const uint32_t*)(Bs + row * 32 + 16 + 4 * g);
+                    b0[bj] = __builtin_bit_cast(uint4, u4x8_to_h(w0, zz, ss));
+                    b1[bj] = __builtin_bit_cast(uint4, u4x8_to_h(w1, zz, ss));
+                }
+            }
+        }
+#pragma unroll
+        for (int ai = 0; ai < 8; ++ai) {
+            const int row = wm * 128 + ai * 16 + l16;
+            const uint4 a0 = *(const uint4*)(As + swz(row, g));
+            const uint4 a1 = *(const uint4*)(As + swz(row, 4 + g));
+#pragma unroll
+            for (int bj = 0; bj < 4; ++bj) mfma_step<F>(accf[ai][bj], acci[ai][bj], a0, a1, b0[bj], b1[bj], gs[bj]);
+        }
+        PK_LSTORE(buf ^ 1);
+        __syncthreads();
+    }
+
+#undef PK_GLOAD
+#undef PK_LSTORE
+    // ---- epilogue ---------------------------------------------------------
+    float* stage = (float*)(lds + wave * (16 * 68 * 4));
+    const int er = lane >> 2, ec = (lane & 3) * 16;
+#pragma unroll
+    for (int ai = 0; ai < 8; ++ai) {
+#pragma unroll
+        for (int bj = 0; bj < 4; ++bj)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                float v;
+                if constexpr (T::kInt) v = E == EPI_I32 ? __builtin_bit_cast(float, acci[ai][bj][r]) : (float)acci[ai][bj][r];
+                else v = accf[ai][bj][r];
+                stage[(4 * g + r) * 68 + bj * 16 + l16] = v;
+            }
+        __syncthreads();
+        float v[16];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float4 q = *(const float4*)(stage + er * 68 + ec + 4 * j);
+            v[4 * j] = q.x; v[4 * j + 1] = q.y; v[4 * j + 2] = q.z; v[4 * j + 3] = q.w;
+        }
+        __syncthreads();
+        const int grow = m0 + wm * 128 + ai * 16 + er;
+        const int gcol = n0 + wn * 64 + ec;
+        if (grow >= p.m || gcol >= p.n) continue;
+
+        if constexpr (E == EPI_I32) {
+            int32_t* o = (int32_t*)p.out + (size_t)grow * p.ldo + gcol;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) *(int4*)(o + 4 * j) = __builtin_bit_cast(int4, float4{v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]});
+            continue;
+        }
+        const float rs = p.row_scales ? p.row_scales[grow] : p.in_scale;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const float ws = p.w_scales ? p.w_scales[gcol + j] : 1.0f;
+            const float bias = p.bias ? p.bias[gcol + j] : 0.0f;
+            if (p.fused_scale) v[j] = __builtin_fmaf(v[j], rs * ws, bias);
+            else v[j] = v[j] * rs * ws + bias;
+        }
+        if constexpr (E == EPI_F32) {
+            float* o = (float*)p.out + (size_t)grow * p.ldo + gcol;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) *(float4*)(o + 4 * j) = float4{v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]};
+        } else if constexpr (E == EPI_F16) {
+            u32x8 res = {0, 0, 0, 0, 0, 0, 0, 0};
+            if (p.residual) {
+                const uint4* rp = (const uint4*)(p.residual + (size_t)grow * p.ldo + gcol);
+                const uint4 r0 = rp[0], r1 = rp[1];
+                res = u32x8{r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
+            }
+            u32x8 h;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                float x0 = v[2 * j] * p.out_scale, x1 = v[2 * j + 1] * p.out_scale;
+                if (p.residual) {
+                    x0 = __builtin_fmaf(p.res_scale, h2f((uint16_t)(res[j] & 0xffff)), x0);
+                    x1 = __builtin_fmaf(p.res_scale, h2f((uint16_t)(res[j] >> 16)), x1);
+                }
+                if (p.act == 1) { x0 = silu(x0); x1 = silu(x1); }
+                else if (p.act == 2) { x0 = __builtin_fmaxf(x0, 0.0f); x1 = __builtin_fmaxf(x1, 0.0f); }
+                h[j] = (uint32_t)f2h(x0) | ((uint32_t)f2h(x1) << 16);
+            }
+            uint4* o = (uint4*)((uint16_t*)p.out + (size_t)grow * p.ldo + gcol);
+            o[0] = uint4{h[0], h[1], h[2], h[3]};
+            o[1] = uint4{h[4], h[5], h[6], h[7]};
+        } else if constexpr (E == EPI_F8 || E == EPI_F8_24) {
+            uint32_t w[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float x0 = round_f16(silu(v[4 * j])) * 16.0f, x1 = round_f16(silu(v[4 * j + 1])) * 16.0f;
+                const float x2 = round_f16(silu(v[4 * j + 2])) * 16.0f, x3 = round_f16(silu(v[4 * j + 3])) * 16.0f;
+                w[j] = e4m3x2(x0, x1) | (e4m3x2(x2, x3) << 16);
+            }
+            if constexpr (E == EPI_F8) {
+                *(uint4*)((uint8_t*)p.out + (size_t)grow * p.ldo + gcol) = uint4{w[0], w[1], w[2], w[3]};
+            } else {
+                // encoder.cu:685-704: keep the two largest |e4m3| of each
+                // quartet (ties to the lower index), metadata idx0 | idx1 << 2.
+                uint32_t data[2] = {0, 0};
+                uint32_t meta = 0;
+#pragma unroll
+                for (int qd = 0; qd < 4; ++qd) {
+                    uint32_t packed = w[qd], d = 0, md = 0;
+                    int count = 0;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const uint32_t mi = (packed >> (8 * i)) & 127;
+                        int rank = 0;
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) {
+                            const uint32_t mj = (packed >> (8 * j)) & 127;
+                            rank += (mj > mi) || (mj == mi && j < i);
+                        }
+                        if (rank < 2) {
+                            d |= ((packed >> (8 * i)) & 255u) << (8 * count);
+                            md |= (uint32_t)i << (2 * count);
+                            ++count;
+                        }
+                    }
+                    data[qd >> 1] |= d << (16 * (qd & 1));
+                    meta |= md << (4 * qd);
+                }
+                *(uint2*)((uint8_t*)p.out + (size_t)grow * (p.ldo / 2) + gcol / 2) = uint2{data[0], data[1]};
+                *(uint16_t*)(p.out_meta + (size_t)grow * (p.ldo / 8) + gcol / 8) = (uint16_t)meta;
+            }
+        }
+    }
+}
+
+}  // namespace pk

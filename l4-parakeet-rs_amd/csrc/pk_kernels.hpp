@@ -1,0 +1,24 @@
+// Internal launcher declarations shared by the translation units of
+// libpk_linear.so.  Launchers return 0 or a negative PK_E_* status.
+#pragma once
+
+#include <stddef.h>
+
+#include "pk_gemm.hpp"
+
+namespace pk {
+
+int launch_gemm(int fmt, int epi, const GemmArgs& args, hipStream_t stream);
+int launch_quantize_static(const void* in, void* out, float inverse_scale, size_t elements, bool int8, hipStream_t s);
+int launch_quantize_rows(int kind, const void* in, void* out, float* scales, int rows, int valid_rows, int k, hipStream_t s);
+int launch_pack_rows(int kind, const void* w, void* out, float* scales, int n, int k, hipStream_t s);
+int launch_pack_g128(const void* w, uint32_t* q, uint16_t* scales, uint16_t* zeros, int n, int k, hipStream_t s);
+int launch_layer_norm_quantize(bool int4, const void* in, const void* gamma, const void* beta, void* out, float* scales,
+                               void* normalized, int rows, int padded_rows, float epsilon, hipStream_t s);
+int launch_joint(const void* w, int w_int8, const float* w_scales, const float* bias, const void* enc, const float* pred,
+                 float* scores, int* decision, int outputs, int hidden, int token_outputs, int durations, int steps,
+                 int enc_stride, hipStream_t s);
+
+void set_error(const char* fmt, ...);
+
+}  // namespace pk

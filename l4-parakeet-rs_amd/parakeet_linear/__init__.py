@@ -1,0 +1,157 @@
+"""Host-side mirror of the l4-parakeet-rs quantized-linear launch surface.
+
+The reference's Rust host builds each launch with cudarc
+(`launch_fp8_linear`, `launch_int8_linear`, `launch_ffn_expand_fp8`, ...;
+src/cuda/quant_benchmark.rs:644-745, src/cuda/encoder.rs:1128-1836).  This
+module exposes the same operations over the C ABI of libpk_linear.so
+(include/pk_linear.h) for torch-allocated device tensors: torch provides the
+device memory and the current HIP stream, every computation runs in the HIP
+kernels.  There is no fallback: if the library is missing the import fails.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(os.path.dirname(HERE), "build", "libpk_linear.so")
+
+P = ctypes.c_void_p
+I = ctypes.c_int32
+F = ctypes.c_float
+S = ctypes.c_size_t
+
+# name -> argument types (the trailing stream argument included)
+SIGNATURES = {
+    "pk_last_error": (ctypes.c_char_p, []),
+    "pk_abi_version": (I, []),
+    "pk_estimate_linear": (I, [I, S, S, I, P]),
+    "pk_exl3_layout": (I, [S, S, I, P]),
+    "pk_pack_fp8_rows": (I, [P, I, I, P, P, P]),
+    "pk_pack_int8_rows": (I, [P, I, I, P, P, P]),
+    "pk_pack_int4_rows": (I, [P, I, I, P, P, P]),
+    "pk_pack_int4_g128": (I, [P, I, I, P, P, P, P]),
+    "pk_quantize_fp8": (I, [P, P, F, I, P]),
+    "pk_quantize_int8": (I, [P, P, F, I, P]),
+    "pk_quantize_fp8_fixed": (I, [P, P, I, F, P]),
+    "pk_quantize_rows1024": (I, [P, P, P, I, P]),
+    "pk_quantize_rows256": (I, [P, P, P, I, P]),
+    "pk_quantize_ffn_contract": (I, [P, P, P, P]),
+    "pk_quantize_rows": (I, [I, P, P, P, I, I, I, P]),
+    "pk_layer_norm_quantize_fp8_dynamic": (I, [P, P, P, P, P, I, I, F, P]),
+    "pk_layer_norm_quantize_int4_dynamic": (I, [P, P, P, P, P, I, I, F, P]),
+    "pk_linear_fp16_epilogue": (I, [P, P, P, P, P, I, I, I, F, F, I, P]),
+    "pk_linear_fp16_qkv": (I, [P, P, P, P, P, I, I, I, P]),
+    "pk_linear_fp8_epilogue": (I, [P, P, P, P, P, I, I, I, F, I, P]),
+    "pk_linear_int8_epilogue": (I, [P, P, P, P, P, I, I, I, F, I, P]),
+    "pk_linear_int8_accumulate": (I, [P, P, P, I, I, I, P]),
+    "pk_linear_int8_dyn": (I, [P, P, P, P, P, P, I, I, I, I, P]),
+    "pk_linear_fp8_dyn": (I, [P, P, P, P, P, P, I, I, I, I, P]),
+    "pk_linear_int4_accumulate": (I, [P, P, P, I, I, I, P]),
+    "pk_linear_int4g128": (I, [P, P, P, P, P, P, I, I, I, I, P]),
+    "pk_linear_int4g128_a8": (I, [P, P, P, P, P, P, P, I, I, I, I, P]),
+    "pk_ffn_expand_fp8": (I, [P, P, P, P, P, I, F, I, P]),
+    "pk_ffn_expand_fp8_packed": (I, [P, P, P, P, P, I, F, I, P]),
+    "pk_ffn_expand_int4_sparse": (I, [P, P, P, P, P, I, F, I, P]),
+    "pk_ffn_contract_fp8": (I, [P, P, P, P, I, P]),
+    "pk_conv_residual_fp8": (I, [P, P, P, P, P, I, P]),
+    "pk_attention_output_fp8": (I, [P, P, P, P, I, P]),
+    "pk_gemm": (I, [I, I, P, P, I, I, I, P, P, F, P, P, F, F, I, P, P, P, P, I, P]),
+    "pk_joint_gemv": (I, [P, I, P, P, P, P, P, P, I, I, I, I, I, I, P]),
+}
+
+
+class PkError(RuntimeError):
+    pass
+
+
+def _load():
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(
+            f"{LIB_PATH} is not built; run `make -C l4-parakeet-rs_amd` "
+            "(or __graft_entry__.build()) first")
+    lib = ctypes.CDLL(LIB_PATH)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+lib = _load()
+
+
+def last_error() -> str:
+    return lib.pk_last_error().decode()
+
+
+def _ptr(t):
+    if t is None:
+        return None
+    if isinstance(t, int):
+        return t
+    return t.data_ptr()
+
+
+def _stream(stream=None):
+    if stream is not None:
+        return stream if isinstance(stream, int) else stream.cuda_stream
+    import torch
+
+    return torch.cuda.current_stream().cuda_stream
+
+
+def call(name: str, *args, stream=None) -> None:
+    """Call `name` with tensors converted to device pointers; raise on error."""
+    fn = getattr(lib, name)
+    conv = []
+    for a, t in zip(args, fn.argtypes):
+        conv.append(_ptr(a) if t is P else a)
+    status = fn(*conv, _stream(stream))
+    if status < 0:
+        raise PkError(f"{name}: status {status}: {last_error()}")
+
+
+# ---- reference-named helpers (argument order as in the reference) ----------
+
+def launch_fp8_linear(input, weights, weight_scales, bias, output, m, n, k, input_scale,
+                      activation=0, stream=None):
+    """quant_benchmark.rs:644-674."""
+    call("pk_linear_fp8_epilogue", input, weights, weight_scales, bias, output, m, n, k,
+         input_scale, activation, stream=stream)
+
+
+def launch_int8_linear(input, weights, weight_scales, bias, output, m, n, k, input_scale,
+                       activation=0, stream=None):
+    """quant_benchmark.rs:677-707."""
+    call("pk_linear_int8_epilogue", input, weights, weight_scales, bias, output, m, n, k,
+         input_scale, activation, stream=stream)
+
+
+def launch_linear(input, weights, bias, residual, output, m, n, k, output_scale=1.0,
+                  residual_scale=0.0, activation=0, stream=None):
+    """cuda.rs:698-740 (launch_linear_view) and the cuBLAS fallback."""
+    call("pk_linear_fp16_epilogue", input, weights, bias, residual, output, m, n, k,
+         output_scale, residual_scale, activation, stream=stream)
+
+
+def launch_fp8_quantize(input, output, inverse_scale, stream=None):
+    """quant_benchmark.rs:710-727."""
+    call("pk_quantize_fp8", input, output, inverse_scale, input.numel(), stream=stream)
+
+
+def launch_int8_quantize(input, output, inverse_scale, stream=None):
+    """quant_benchmark.rs:729-745."""
+    call("pk_quantize_int8", input, output, inverse_scale, input.numel(), stream=stream)
+
+
+def gemm(fmt, epi, a, b, m, n, k, out, *, w_scales=None, row_scales=None, in_scale=1.0,
+         bias=None, residual=None, out_scale=1.0, res_scale=0.0, act=0, g_scales=None,
+         g_zeros=None, out_meta=None, ldo=None, stream=None):
+    call("pk_gemm", fmt, epi, a, b, m, n, k, w_scales, row_scales, in_scale, bias, residual,
+         out_scale, res_scale, act, g_scales, g_zeros, out, out_meta, n if ldo is None else ldo,
+         stream=stream)
+
+
+FMT_FP8, FMT_I8, FMT_S4, FMT_G128A8, FMT_F16, FMT_G128A16 = range(6)
+EPI_F16, EPI_F8, EPI_F8_24, EPI_F32, EPI_I32 = range(5)

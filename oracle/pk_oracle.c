@@ -290,8 +290,12 @@ void orc_pack_int4_rows(const uint16_t* w, int n, int k, uint8_t* q, float* scal
  * closed form.  Per (row, group): lo = min(0, min w), hi = max(0, max w),
  * s = fp16((hi - lo) / 15) (1 if that is 0), z = clamp(rne(-lo / s), 0, 15),
  * q = clamp(rne(w / s) + z, 0, 15); dequant (q - z) * s.  q is packed eight
- * per uint32 along K, nibble i of word j holding k = 8j + i.  scales and zeros
- * are fp16 [n x k/128]; zeros are integers in [0, 15]. */
+ * per uint32 along K: word j holds k = 8j .. 8j+7, k = 8j+i sitting at bit
+ * 8*(i%4) + 4*(i/4) (byte b carries k 8j+b low and 8j+4+b high), so two masks
+ * give the levels in k order on the GPU.  scales and zeros are fp16
+ * [n x k/128]; zeros are integers in [0, 15]. */
+static int g128_shift(int i) { return 8 * (i & 3) + 4 * (i >> 2); }
+
 void orc_pack_int4_g128(const uint16_t* w, int n, int k, uint32_t* q, uint16_t* scales,
                         uint16_t* zeros) {
     int groups = k / 128;
@@ -315,7 +319,7 @@ void orc_pack_int4_g128(const uint16_t* w, int n, int k, uint32_t* q, uint16_t* 
                     float v = orc_f16_to_f32(values[8 * j + i]);
                     int level = clamp_rne(v / s, -64, 64) + z;
                     level = level < 0 ? 0 : (level > 15 ? 15 : level);
-                    word |= (uint32_t)level << (4 * i);
+                    word |= (uint32_t)level << g128_shift(i);
                 }
                 q[(size_t)row * (k / 8) + g * 16 + j] = word;
             }
@@ -788,7 +792,7 @@ void orc_gemm_f16_f32(const uint16_t* x, const uint16_t* w, int m, int n, int k,
 }
 
 static int g128_level(const uint32_t* q, int k, int row, int t) {
-    return (int)((q[(size_t)row * (k / 8) + t / 8] >> (4 * (t % 8))) & 15u);
+    return (int)((q[(size_t)row * (k / 8) + t / 8] >> g128_shift(t % 8)) & 15u);
 }
 
 /* W4A16 with group-wise asymmetric INT4 weights: out = sum over groups of

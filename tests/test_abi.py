@@ -1,0 +1,91 @@
+"""CPU-side checks of the C ABI: the library loads, exports every symbol the
+header declares, and its host-only size contracts give the reference's
+known answers (no GPU is touched)."""
+import ctypes
+import json
+import os
+import re
+
+import numpy as np
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "pk_linear.h")
+LIB = os.path.join(ROOT, "l4-parakeet-rs_amd", "build", "libpk_linear.so")
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "reference_known_answers.json")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:const char\*|int32_t)\s+(pk_\w+)\s*\(", text, re.M)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(LIB):
+        pytest.fail("libpk_linear.so is not built (run __graft_entry__.build())")
+    return ctypes.CDLL(LIB)
+
+
+def test_header_declares_the_boundary():
+    syms = declared_symbols()
+    assert len(syms) >= 30
+    for name in ("pk_linear_fp8_epilogue", "pk_linear_int8_epilogue", "pk_ffn_contract_fp8",
+                 "pk_joint_gemv", "pk_pack_int4_g128", "pk_estimate_linear"):
+        assert name in syms
+
+
+def test_library_exports_every_declared_symbol(lib):
+    missing = [s for s in declared_symbols() if not hasattr(lib, s)]
+    assert not missing
+
+
+def test_python_mirror_covers_every_symbol():
+    import importlib.util
+
+    spec = importlib.util.spec_from_file_location(
+        "pk_sig", os.path.join(ROOT, "l4-parakeet-rs_amd", "parakeet_linear", "__init__.py"))
+    text = open(spec.origin).read()
+    for s in declared_symbols():
+        assert f'"{s}"' in text, s
+
+
+def _estimate(lib, fmt, lin, lout, bits=4):
+    fn = lib.pk_estimate_linear
+    fn.argtypes = [ctypes.c_int32, ctypes.c_size_t, ctypes.c_size_t, ctypes.c_int32, ctypes.c_void_p]
+    fn.restype = ctypes.c_int32
+    out = np.zeros(6, np.uint64)
+    st = fn(fmt, lin, lout, bits, out.ctypes.data)
+    return st, out
+
+
+def test_estimate_linear_matches_reference_tests(lib):
+    known = json.load(open(GOLDEN))
+    fmts = {"fp16": 0, "fp8_e4m3": 1, "int8": 2, "q4_k": 3, "exl3": 4}
+    for case in known["estimate_linear"]["cases"]:
+        st, out = _estimate(lib, fmts[case["format"]], case["in"], case["out"])
+        if case.get("none"):
+            assert st == 0
+            continue
+        assert st == 1
+        if "total_bytes" in case:
+            assert int(out[4] + out[5]) == case["total_bytes"]
+        for key, idx in (("payload_bytes", 4), ("metadata_bytes", 5), ("padded_in", 2), ("padded_out", 3)):
+            if key in case:
+                assert int(out[idx]) == case[key]
+    assert _estimate(lib, 1, 0, 5)[0] < 0
+
+
+def test_exl3_layout_matches_reference_tests(lib):
+    known = json.load(open(GOLDEN))
+    fn = lib.pk_exl3_layout
+    fn.argtypes = [ctypes.c_size_t, ctypes.c_size_t, ctypes.c_int32, ctypes.c_void_p]
+    fn.restype = ctypes.c_int32
+    for case in known["exl3_layout"]["cases"]:
+        out = np.zeros(7, np.uint64)
+        assert fn(case["in"], case["out"], case["bits"], out.ctypes.data) == 0
+        assert [int(v) for v in out[2:5]] == case["trellis_shape"]
+        if "trellis_bytes" in case:
+            assert int(out[5]) == case["trellis_bytes"] and int(out[6]) == case["scale_bytes"]
+    out = np.zeros(7, np.uint64)
+    assert fn(4, 4, 0, out.ctypes.data) < 0

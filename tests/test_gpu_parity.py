@@ -1,0 +1,405 @@
+"""GPU parity: every HIP entry point against the CPU oracle on seeded inputs.
+
+Integer, byte and index results are compared bit-exactly; fp32-accumulated
+FP8 / FP16 / INT4-g128 outputs within max|err| <= 1e-2 * RMS(reference output),
+the tolerance BASELINE.json's north star states.  All calls go through the
+C ABI (parakeet_linear is a ctypes mirror of include/pk_linear.h).
+"""
+import sys
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+TOL = 1e-2
+
+
+@pytest.fixture(scope="module")
+def pk():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    import parakeet_linear
+
+    return parakeet_linear
+
+
+@pytest.fixture(scope="module")
+def orc(oracle):
+    oracle.set_threads(8)
+    return oracle
+
+
+def dev(a):
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.float16:
+        return torch.from_numpy(a.view(np.int16)).cuda().view(torch.float16)
+    if a.dtype == np.uint32:
+        return torch.from_numpy(a.view(np.int32)).cuda()
+    return torch.from_numpy(a).cuda()
+
+
+def host(t, dtype=None):
+    torch.cuda.synchronize()
+    a = t.cpu()
+    if a.dtype == torch.float16:
+        return a.view(torch.int16).numpy().view(np.float16)
+    return a.numpy() if dtype is None else a.numpy().view(dtype)
+
+
+def empty(shape, dtype):
+    return torch.empty(shape, dtype=dtype, device="cuda")
+
+
+def note(msg):
+    print(f"[gpu-parity] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def assert_close(got, ref, tol=TOL):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    rms = np.sqrt(np.mean(ref ** 2))
+    err = np.max(np.abs(got - ref))
+    assert np.isfinite(got).all()
+    assert err <= tol * rms, f"max err {err} > {tol} * rms {rms}"
+
+
+def weights(n, k, seed, sigma=0.02):
+    return (np.random.default_rng(seed).standard_normal((n, k)) * sigma).astype(np.float16)
+
+
+def acts(m, k, seed, outliers=True):
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    if outliers:
+        mask = rng.random((m, k)) < 1e-3
+        x[mask] = np.where(rng.random(mask.sum()) < 0.5, -20.0, 20.0)
+    return x.astype(np.float16)
+
+
+# ---- conversions and quantizers (bit-exact) ---------------------------------------
+
+def test_quantize_fp8_all_fp16_inputs(pk, orc):
+    note("quantize_fp8 exhaustive")
+    allh = np.arange(65536, dtype=np.uint16).view(np.float16)
+    allh = allh[np.isfinite(allh.astype(np.float32))]
+    x = dev(allh)
+    out = empty(allh.size, torch.uint8)
+    for inv in (1.0, 56.0, 448.0 / 0.125, 1.0 / 3.0, 3.7e-3):
+        pk.launch_fp8_quantize(x, out, inv)
+        assert np.array_equal(host(out), orc.quantize_fp8_static(allh, inv)), inv
+
+
+def test_quantize_int8_all_fp16_inputs(pk, orc):
+    note("quantize_int8 exhaustive")
+    allh = np.arange(65536, dtype=np.uint16).view(np.float16)
+    allh = allh[np.isfinite(allh.astype(np.float32))]
+    x = dev(allh)
+    out = empty(allh.size, torch.int8)
+    for inv in (1.0, 127.0 / 0.125, 0.37):
+        pk.launch_int8_quantize(x, out, inv)
+        assert np.array_equal(host(out), orc.quantize_int8_static(allh, inv)), inv
+
+
+@pytest.mark.parametrize("kind", [0, 1, 2])
+@pytest.mark.parametrize("m,k,valid", [(1, 1024, 1), (37, 1024, 30), (16, 4096, 16), (5, 256, 5)])
+def test_quantize_rows(pk, orc, kind, m, k, valid):
+    note(f"quantize_rows kind={kind} m={m} k={k}")
+    x = acts(m, k, 100 + m + k)
+    if m > 2:
+        x[1] = 0  # all-zero row -> scale 1
+    out = empty((m, k // 2 if kind == 2 else k), torch.uint8)
+    scales = empty(m, torch.float32)
+    pk.call("pk_quantize_rows", kind, dev(x), out, scales, m, valid, k)
+    ref = {0: orc.quantize_fp8_rows, 1: orc.quantize_int8_rows, 2: orc.quantize_int4_rows}[kind](x, valid)
+    assert np.array_equal(host(out).view(np.uint8), ref[0].view(np.uint8))
+    assert np.array_equal(host(scales), ref[1])
+
+
+@pytest.mark.parametrize("int4", [False, True])
+def test_layer_norm_quantize(pk, orc, int4):
+    note(f"layer_norm_quantize int4={int4}")
+    m, pad = 45, 48
+    x = (acts(pad, 1024, 7).astype(np.float32) * 2 + 0.5).astype(np.float16)
+    g = np.random.default_rng(8).uniform(0.5, 1.5, 1024).astype(np.float16)
+    b = (np.random.default_rng(9).standard_normal(1024) * 0.1).astype(np.float16)
+    out = empty((pad, 512 if int4 else 1024), torch.uint8)
+    scales = empty(pad, torch.float32)
+    name = "pk_layer_norm_quantize_int4_dynamic" if int4 else "pk_layer_norm_quantize_fp8_dynamic"
+    pk.call(name, dev(x), dev(g), dev(b), out, scales, m, pad, 1e-5)
+    q, s, _ = orc.layer_norm_quantize(x, g, b, 1e-5, int4, valid_rows=m)
+    assert np.array_equal(host(scales), s)
+    assert np.array_equal(host(out), q)
+
+
+@pytest.mark.parametrize("kind", ["fp8", "int8", "int4"])
+def test_pack_rows(pk, orc, kind):
+    note(f"pack_rows {kind}")
+    n, k = 300, 1024
+    w = weights(n, k, 11)
+    w[5] = 0
+    width = k // 2 if kind == "int4" else k
+    q = empty((n, width), torch.uint8)
+    s = empty(n, torch.float32)
+    pk.call(f"pk_pack_{kind}_rows", dev(w), n, k, q, s)
+    rq, rs = {"fp8": orc.pack_fp8_rows, "int8": orc.pack_int8_rows, "int4": orc.pack_int4_rows}[kind](w)
+    assert np.array_equal(host(q).view(np.uint8), rq.view(np.uint8))
+    assert np.array_equal(host(s), rs)
+
+
+def test_pack_int4_g128(pk, orc):
+    note("pack_int4_g128")
+    n, k = 200, 1024
+    w = weights(n, k, 12)
+    w[3, 128:256] = 0
+    q = empty((n, k // 8), torch.int32)
+    s = empty((n, k // 128), torch.float16)
+    z = empty((n, k // 128), torch.float16)
+    pk.call("pk_pack_int4_g128", dev(w), n, k, q, s, z)
+    rq, rs, rz = orc.pack_int4_g128(w)
+    assert np.array_equal(host(q).view(np.uint32), rq)
+    assert np.array_equal(host(s).view(np.uint16), rs.view(np.uint16))
+    assert np.array_equal(host(z).view(np.uint16), rz.view(np.uint16))
+
+
+# ---- INT8 x INT8 -> INT32 (bit-exact) ------------------------------------------------
+
+@pytest.mark.parametrize("m,n,k", [(750, 4096, 1024), (1, 640, 1024), (257, 1040, 4096), (17, 16, 128)])
+def test_int8_accumulators_exact(pk, orc, m, n, k):
+    note(f"int8 accumulate m={m} n={n} k={k}")
+    rng = np.random.default_rng(m * 7 + n)
+    x = rng.integers(-127, 128, (m, k), dtype=np.int8)
+    w = rng.integers(-127, 128, (n, k), dtype=np.int8)
+    acc = empty((m, n), torch.int32)
+    pk.call("pk_linear_int8_accumulate", dev(x), dev(w), acc, m, n, k)
+    assert np.array_equal(host(acc), orc.gemm_i8(x, w))
+
+
+def test_int8_linear_epilogue_config1(pk, orc):
+    """W[4096x1024] ~N(0,0.02) -> per-row INT8, x[750x1024]."""
+    note("int8 linear config 1")
+    m, n, k = 750, 4096, 1024
+    w = weights(n, k, 0x5EED0001)
+    x = acts(m, k, 0x5EED0002, outliers=False)
+    wq, ws = orc.pack_int8_rows(w)
+    in_scale = 0.125 / 127.0 * 32  # covers |x| <= ~4
+    xq = orc.quantize_int8_static(x, 1.0 / in_scale)
+    bias = (np.random.default_rng(3).standard_normal(n) * 0.1).astype(np.float32)
+    out = empty((m, n), torch.float16)
+    pk.launch_int8_linear(dev(xq), dev(wq), dev(ws), dev(bias), out, m, n, k, in_scale, 0)
+    ref = orc.epilogue_quantized(orc.gemm_i8(xq, wq).astype(np.float32), in_scale, ws, bias, 0)
+    assert np.array_equal(host(out).view(np.uint16), ref.view(np.uint16))
+    pk.launch_int8_linear(dev(xq), dev(wq), dev(ws), dev(bias), out, m, n, k, in_scale, 1)
+    ref = orc.epilogue_quantized(orc.gemm_i8(xq, wq).astype(np.float32), in_scale, ws, bias, 1)
+    assert_close(host(out), ref.astype(np.float32))
+
+
+def test_int8_dynamic_exact(pk, orc):
+    note("int8 dyn")
+    m, n, k = 300, 1024, 4096
+    x = acts(m, k, 21)
+    w = weights(n, k, 22)
+    xq, xs = orc.quantize_int8_rows(x)
+    wq, ws = orc.pack_int8_rows(w)
+    out = empty((m, n), torch.float32)
+    pk.call("pk_linear_int8_dyn", dev(xq), dev(xs), dev(wq), dev(ws), None, out, 1, m, n, k)
+    acc = orc.gemm_i8(xq, wq).astype(np.float32)
+    ref = (acc * xs[:, None]).astype(np.float32) * ws[None, :]
+    assert np.array_equal(host(out), ref.astype(np.float32))
+
+
+# ---- s4 x s4 -------------------------------------------------------------------------
+
+def test_int4_accumulators_exact(pk, orc):
+    note("int4 accumulate")
+    m, n, k = 301, 512, 1024
+    rng = np.random.default_rng(31)
+    x = rng.integers(0, 256, (m, k // 2), dtype=np.uint8)
+    w = rng.integers(0, 256, (n, k // 2), dtype=np.uint8)
+    acc = empty((m, n), torch.int32)
+    pk.call("pk_linear_int4_accumulate", dev(x), dev(w), acc, m, n, k)
+    assert np.array_equal(host(acc), orc.gemm_s4(x, w))
+
+
+def test_ffn_expand_int4_sparse(pk, orc):
+    note("ffn_expand_int4_sparse")
+    rows = 300
+    x = acts(rows, 1024, 41)
+    w = weights(4096, 1024, 42)
+    xq, xs = orc.quantize_int4_rows(x)
+    wq, ws = orc.pack_int4_rows(w)
+    out = empty(rows * 2048 + rows * 512, torch.uint8)
+    pk.call("pk_ffn_expand_int4_sparse", dev(xq), dev(wq), dev(ws), dev(xs), out, rows, 1.0, 1)
+    got = host(out)
+    data, meta = got[: rows * 2048].reshape(rows, 2048), got[rows * 2048:].reshape(rows, 512)
+    acc = orc.gemm_s4(xq, wq).astype(np.float32)
+    dense = orc.epilogue(acc, 7, ws, row_scales=xs)
+    rdata, rmeta = orc.compress_24(dense)
+    # exact int32 accumulators; only SiLU's exp may differ by an ulp, which can
+    # move an fp16 rounding boundary, so compare codes almost everywhere and the
+    # decompressed values within one fp8 step
+    assert np.mean(data == rdata) > 0.999 and np.mean(meta == rmeta) > 0.999
+    table = orc.e4m3_table()
+    assert_close(table[orc.decompress_24(data, meta)], table[orc.decompress_24(rdata, rmeta)], tol=0.05)
+
+
+# ---- FP8 -------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("m,n,k", [(750, 4096, 1024), (33, 1024, 4096), (1, 3072, 1024)])
+def test_fp8_linear_epilogue(pk, orc, m, n, k):
+    note(f"fp8 linear m={m} n={n} k={k}")
+    w = weights(n, k, 51)
+    x = acts(m, k, 52)
+    wq, ws = orc.pack_fp8_rows(w)
+    in_scale = 8.0 / 448.0
+    xq = orc.quantize_fp8_static(x, 1.0 / in_scale)
+    bias = (np.random.default_rng(53).standard_normal(n) * 0.05).astype(np.float32)
+    out = empty((m, n), torch.float16)
+    pk.launch_fp8_linear(dev(xq), dev(wq), dev(ws), dev(bias), out, m, n, k, in_scale, 0)
+    ref = orc.epilogue_quantized(orc.gemm_e4m3(xq, wq), in_scale, ws, bias, 0)
+    assert_close(host(out), ref.astype(np.float32))
+
+
+def test_fp8_dynamic_fp32_out(pk, orc):
+    note("fp8 dyn fp32")
+    m, n, k = 515, 2048, 1024
+    x = acts(m, k, 61)
+    w = weights(n, k, 62)
+    xq, xs = orc.quantize_fp8_rows(x)
+    wq, ws = orc.pack_fp8_rows(w)
+    out = empty((m, n), torch.float32)
+    pk.call("pk_linear_fp8_dyn", dev(xq), dev(xs), dev(wq), dev(ws), None, out, 1, m, n, k)
+    ref = orc.gemm_e4m3(xq, wq) * xs[:, None] * ws[None, :]
+    assert_close(host(out), ref)
+
+
+def test_ffn_expand_fp8_and_packed(pk, orc):
+    note("ffn_expand_fp8 (+packed)")
+    rows = 260
+    x = acts(rows, 1024, 71)
+    w = weights(4096, 1024, 72)
+    wq, ws = orc.pack_fp8_rows(w)
+    in_scale = 8.0 / 448.0
+    xq = orc.quantize_fp8_static(x, 1.0 / in_scale)
+    acc = orc.gemm_e4m3(xq, wq)
+    out = empty((rows, 4096), torch.float16)
+    pk.call("pk_ffn_expand_fp8", dev(xq), dev(wq), dev(ws), None, out, rows, in_scale, 0)
+    assert_close(host(out), orc.epilogue(acc, 0, ws, in_scale=in_scale).astype(np.float32))
+    packed = empty((rows, 4096), torch.uint8)
+    pk.call("pk_ffn_expand_fp8_packed", dev(xq), dev(wq), dev(ws), None, packed, rows, in_scale, 0)
+    table = orc.e4m3_table()
+    ref = orc.epilogue(acc, 1, ws, in_scale=in_scale)
+    assert_close(table[host(packed)], table[ref], tol=0.05)
+
+
+@pytest.mark.parametrize("name", ["pk_ffn_contract_fp8", "pk_conv_residual_fp8", "pk_attention_output_fp8"])
+def test_residual_linears(pk, orc, name):
+    note(name)
+    rows = 300
+    k = 4096 if name == "pk_ffn_contract_fp8" else 1024
+    x = acts(rows, k, 81)
+    w = weights(1024, k, 82)
+    wq, ws = orc.pack_fp8_rows(w)
+    residual = acts(rows, 1024, 83, outliers=False)
+    out = dev(residual.copy())
+    if name == "pk_conv_residual_fp8":
+        xq, xs = orc.quantize_fp8_rows(x)
+        pk.call(name, dev(xq), dev(wq), dev(ws), dev(xs), out, rows)
+        ref = orc.epilogue(orc.gemm_e4m3(xq, wq), 6, ws, row_scales=xs, residual=residual)
+    else:
+        in_scale = 1.0 / 16.0 if name == "pk_ffn_contract_fp8" else 1.0 / 28.0
+        xq = orc.quantize_fp8_static(x, 1.0 / in_scale)
+        pk.call(name, dev(xq), dev(wq), dev(ws), out, rows)
+        mode = 2 if name == "pk_ffn_contract_fp8" else 6
+        ref = orc.epilogue(orc.gemm_e4m3(xq, wq), mode, ws, in_scale=in_scale, residual=residual)
+    delta_ref = ref.astype(np.float32) - residual.astype(np.float32)
+    delta_got = host(out).astype(np.float32) - residual.astype(np.float32)
+    assert_close(delta_got, delta_ref, tol=2e-2)
+
+
+# ---- FP16 ------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("act", [0, 1, 2])
+def test_fp16_linear_epilogue(pk, orc, act):
+    note(f"fp16 linear act={act}")
+    m, n, k = 200, 640, 1024
+    x = acts(m, k, 91, outliers=False)
+    w = weights(n, k, 92)
+    bias = (np.random.default_rng(93).standard_normal(n) * 0.1).astype(np.float32)
+    res = acts(m, n, 94, outliers=False)
+    out = empty((m, n), torch.float16)
+    pk.launch_linear(dev(x), dev(w), dev(bias), dev(res), out, m, n, k, 0.5, 0.25, act)
+    ref = orc.epilogue_linear(orc.gemm_f16(x, w), bias, res, 0.5, 0.25, act)
+    assert_close(host(out), ref.astype(np.float32))
+
+
+def test_fp16_qkv(pk, orc):
+    note("fp16 qkv")
+    m, n, k = 130, 1024, 1024
+    x = acts(m, k, 95, outliers=False)
+    ws = [weights(n, k, 96 + i) for i in range(3)]
+    out = empty((3, m, n), torch.float16)
+    pk.call("pk_linear_fp16_qkv", dev(x), dev(ws[0]), dev(ws[1]), dev(ws[2]), out, m, n, k)
+    got = host(out)
+    for i in range(3):
+        assert_close(got[i], orc.gemm_f16(x, ws[i]))
+
+
+# ---- INT4 g128 ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("m,n,k", [(750, 4096, 1024), (97, 1024, 4096)])
+def test_int4g128_a16(pk, orc, m, n, k):
+    note(f"g128 a16 m={m} n={n} k={k}")
+    x = acts(m, k, 101, outliers=False)
+    w = weights(n, k, 102)
+    q, s, z = orc.pack_int4_g128(w)
+    out = empty((m, n), torch.float32)
+    pk.call("pk_linear_int4g128", dev(x), dev(q), dev(s), dev(z), None, out, 1, m, n, k)
+    assert_close(host(out), orc.gemm_g128_a16(x, q, s, z))
+
+
+@pytest.mark.parametrize("m,n,k", [(750, 4096, 1024), (97, 1024, 4096)])
+def test_int4g128_a8_exact(pk, orc, m, n, k):
+    note(f"g128 a8 m={m} n={n} k={k}")
+    x = acts(m, k, 111)
+    w = weights(n, k, 112)
+    q, s, z = orc.pack_int4_g128(w)
+    xq, xs = orc.quantize_int8_rows(x)
+    out = empty((m, n), torch.float32)
+    pk.call("pk_linear_int4g128_a8", dev(xq), dev(xs), dev(q), dev(s), dev(z), None, out, 1, m, n, k)
+    ref = orc.gemm_g128_a8(xq, xs, q, s, z)
+    assert np.array_equal(host(out), ref)
+
+
+# ---- joint ---------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("int8", [False, True])
+def test_joint_gemv(pk, orc, int8):
+    note(f"joint int8={int8}")
+    outputs, hidden, steps = 1030, 640, 7
+    rng = np.random.default_rng(120)
+    w16 = (rng.standard_normal((outputs, hidden)) * 0.05).astype(np.float16)
+    bias = (rng.standard_normal(outputs) * 0.1).astype(np.float32)
+    enc = rng.standard_normal((steps, hidden)).astype(np.float16)
+    pred = rng.standard_normal(hidden).astype(np.float32)
+    scores = empty((steps, outputs), torch.float32)
+    decision = empty((steps, 2), torch.int32)
+    if int8:
+        wq, ws = orc.pack_int8_rows(w16)
+        pk.call("pk_joint_gemv", dev(wq), 1, dev(ws), dev(bias), dev(enc), dev(pred), scores, decision,
+                outputs, hidden, 1025, 5, steps, hidden)
+    else:
+        pk.call("pk_joint_gemv", dev(w16), 0, None, dev(bias), dev(enc), dev(pred), scores, decision,
+                outputs, hidden, 1025, 5, steps, hidden)
+    got = host(scores)
+    dec = host(decision)
+    for t in range(steps):
+        if int8:
+            ref = orc.joint_scores_i8(wq, ws, bias, enc[t], pred)
+        else:
+            ref = orc.joint_scores_f16(w16, bias, enc[t], pred)
+        assert_close(got[t], ref, tol=1e-4)
+        assert tuple(dec[t]) == orc.joint_decide(got[t])

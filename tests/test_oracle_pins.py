@@ -178,7 +178,7 @@ def test_pack_int4_g128_round_trip(oracle):
     w[3, :128] = 0  # an all-zero group
     q, s, z = oracle.pack_int4_g128(w)
     assert np.all(z.astype(np.float32) == np.round(z.astype(np.float32)))
-    levels = np.stack([(q >> (4 * i)) & 15 for i in range(8)], axis=-1).reshape(16, 512)
+    levels = np.stack([(q >> (8 * (i % 4) + 4 * (i // 4))) & 15 for i in range(8)], axis=-1).reshape(16, 512)
     deq = (levels - np.repeat(z.astype(np.float32), 128, axis=1)) * np.repeat(s.astype(np.float32), 128, axis=1)
     err = np.abs(deq - w.astype(np.float32))
     assert np.all(err <= np.repeat(s.astype(np.float32), 128, axis=1) * 0.5 + 1e-6)
@@ -271,7 +271,7 @@ def test_gemm_g128_paths_match_numpy(oracle):
     rng = np.random.default_rng(12)
     w = _weights(24, 256, 13)
     q, s, z = oracle.pack_int4_g128(w)
-    levels = np.stack([(q >> (4 * i)) & 15 for i in range(8)], axis=-1).reshape(24, 256).astype(np.int64)
+    levels = np.stack([(q >> (8 * (i % 4) + 4 * (i // 4))) & 15 for i in range(8)], axis=-1).reshape(24, 256).astype(np.int64)
     zi = np.repeat(z.astype(np.int64), 128, axis=1)
     x16 = rng.standard_normal((9, 256)).astype(np.float16)
     deq = (levels - zi) * np.repeat(s.astype(np.float64), 128, axis=1)
