@@ -300,8 +300,12 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs p) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 float v;
-                if constexpr (T::kInt) v = E == EPI_I32 ? __builtin_bit_cast(float, acci[ai][bj][r]) : (float)acci[ai][bj][r];
-                else v = accf[ai][bj][r];
+                if constexpr (T::kInt) {
+                    const int iv = acci[ai][bj][r];
+                    v = E == EPI_I32 ? __int_as_float(iv) : (float)iv;
+                } else {
+                    v = accf[ai][bj][r];
+                }
                 stage[(4 * g + r) * 68 + bj * 16 + l16] = v;
             }
         __syncthreads();

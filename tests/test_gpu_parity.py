@@ -67,6 +67,15 @@ def assert_close(got, ref, tol=TOL):
     assert err <= tol * rms, f"max err {err} > {tol} * rms {rms}"
 
 
+def assert_fp8_close(table, got, ref, exact_frac=0.99):
+    """Requantized e4m3 outputs of an fp32-accumulated GEMM: codes agree almost
+    everywhere; where the summation order moved a rounding boundary they differ
+    by at most one e4m3 step (relative 2^-3, or the 2^-9 subnormal step)."""
+    assert np.mean(got == ref) >= exact_frac
+    g, r = table[got].astype(np.float64), table[ref].astype(np.float64)
+    assert np.all(np.abs(g - r) <= np.abs(r) / 8 + 2.0 ** -9 + 1e-12)
+
+
 def weights(n, k, seed, sigma=0.02):
     return (np.random.default_rng(seed).standard_normal((n, k)) * sigma).astype(np.float16)
 
@@ -242,8 +251,7 @@ def test_ffn_expand_int4_sparse(pk, orc):
     # move an fp16 rounding boundary, so compare codes almost everywhere and the
     # decompressed values within one fp8 step
     assert np.mean(data == rdata) > 0.999 and np.mean(meta == rmeta) > 0.999
-    table = orc.e4m3_table()
-    assert_close(table[orc.decompress_24(data, meta)], table[orc.decompress_24(rdata, rmeta)], tol=0.05)
+    assert_fp8_close(orc.e4m3_table(), orc.decompress_24(data, meta), orc.decompress_24(rdata, rmeta), 0.999)
 
 
 # ---- FP8 -------------------------------------------------------------------------------
@@ -290,9 +298,8 @@ def test_ffn_expand_fp8_and_packed(pk, orc):
     assert_close(host(out), orc.epilogue(acc, 0, ws, in_scale=in_scale).astype(np.float32))
     packed = empty((rows, 4096), torch.uint8)
     pk.call("pk_ffn_expand_fp8_packed", dev(xq), dev(wq), dev(ws), None, packed, rows, in_scale, 0)
-    table = orc.e4m3_table()
     ref = orc.epilogue(acc, 1, ws, in_scale=in_scale)
-    assert_close(table[host(packed)], table[ref], tol=0.05)
+    assert_fp8_close(orc.e4m3_table(), host(packed), ref)
 
 
 @pytest.mark.parametrize("name", ["pk_ffn_contract_fp8", "pk_conv_residual_fp8", "pk_attention_output_fp8"])
