@@ -5,19 +5,23 @@
 
 namespace pk {
 
+static int lds_bytes(int fmt) {
+    return 2 * kStageBytes + ((fmt == FMT_G128A8 || fmt == FMT_G128A16) ? kMaxG128Groups * kBlockN * 4 : 0);
+}
+
 template <int F, int E>
 static int launch_one(const GemmArgs& a, hipStream_t s) {
     static std::once_flag once;
     static hipError_t attr = hipSuccess;
     std::call_once(once, [] {
-        attr = hipFuncSetAttribute((const void*)gemm_kernel<F, E>, hipFuncAttributeMaxDynamicSharedMemorySize, 2 * kStageBytes);
+        attr = hipFuncSetAttribute((const void*)gemm_kernel<F, E>, hipFuncAttributeMaxDynamicSharedMemorySize, lds_bytes(F));
     });
     if (attr != hipSuccess) {
-        set_error("hipFuncSetAttribute(LDS %d bytes) failed: %s", 2 * kStageBytes, hipGetErrorString(attr));
+        set_error("hipFuncSetAttribute(LDS %d bytes) failed: %s", lds_bytes(F), hipGetErrorString(attr));
         return -3;
     }
     const unsigned tiles = (unsigned)(((a.m + kBlockM - 1) / kBlockM) * ((a.n + kBlockN - 1) / kBlockN));
-    hipLaunchKernelGGL((gemm_kernel<F, E>), dim3(tiles), dim3(kThreads), 2 * kStageBytes, s, a);
+    hipLaunchKernelGGL((gemm_kernel<F, E>), dim3(tiles), dim3(kThreads), lds_bytes(F), s, a);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
         set_error("gemm launch (fmt %d, epi %d) failed: %s", F, E, hipGetErrorString(e));
@@ -53,6 +57,10 @@ static int k_step(int fmt) {
 int launch_gemm(int fmt, int epi, const GemmArgs& a, hipStream_t s) {
     if (a.m < 0 || a.n <= 0 || a.k <= 0) {
         set_error("invalid GEMM shape m=%d n=%d k=%d", a.m, a.n, a.k);
+        return -1;
+    }
+    if ((fmt == FMT_G128A8 || fmt == FMT_G128A16) && a.k > 128 * kMaxG128Groups) {
+        set_error("k=%d exceeds the %d groups of 128 the g128 kernels stage in LDS", a.k, kMaxG128Groups);
         return -1;
     }
     if (a.k % k_step(fmt) != 0 || ((fmt == FMT_G128A8 || fmt == FMT_G128A16) && a.k % 128 != 0)) {

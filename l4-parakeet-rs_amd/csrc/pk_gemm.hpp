@@ -64,6 +64,7 @@ constexpr int kThreads = 512;
 constexpr int kRowBytes = 128;
 constexpr int kTileBytes = kBlockM * kRowBytes;  // one operand tile per stage
 constexpr int kStageBytes = 2 * kTileBytes;
+constexpr int kMaxG128Groups = 32;  // K <= 4096 for the group-wise INT4 formats
 
 template <int F> struct FmtTraits;
 template <> struct FmtTraits<FMT_FP8> { static constexpr int kStep = 128, bRow = 128, aElemNum = 1, aElemDen = 1, bNum = 1, bDen = 1; static constexpr bool kInt = false; };
@@ -151,6 +152,23 @@ __device__ __forceinline__ void mfma_step(v4f& accf, v4i& acci, const uint4& a0,
     }
 }
 
+// 16 bytes global -> LDS per lane (global_load_lds_dwordx4): lane l writes
+// LDS bytes [lds_addr + 16 l, + 16).  lds_addr must be wave-uniform.
+__device__ __forceinline__ void dma16(const void* src, uint32_t lds_addr) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(__builtin_amdgcn_readfirstlane(lds_addr))
+                 : "memory", "m0");
+}
+
+// Orders this wave's LDS writes before its later LDS reads (and the reads
+// before the next writes) when lanes exchange data through LDS.
+// A wave's LDS instructions execute in order, so only the compiler must be
+// kept from reordering them (no global-memory fence, which would also wait
+// for the wave's outstanding global stores).
+__device__ __forceinline__ void wave_lds_sync() {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_wave_barrier();
+}
+
 // Block index -> (m tile, n tile).  Workgroups are dispatched round-robin over
 // the 8 XCDs; remap so each XCD owns a contiguous run of tiles (N fastest),
 // which keeps an XCD's concurrent tiles on a couple of A row-strips and lets
@@ -179,44 +197,61 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs p) {
     const size_t ldb = (size_t)p.k * T::bNum / T::bDen;          // bytes per B row
     const int steps = p.k / T::kStep;
 
-    // Global -> register staging: A is 256 rows x 8 chunks = 2048 chunks
-    // (4 per thread); B is 256 rows x bRow/16 chunks.
-    constexpr int kBChunks = T::bRow / 16;
-    constexpr int kBLoads = (kBlockN * kBChunks) / kThreads;
-    uint4 ra[4], rb[kBLoads];
-    uint32_t a_off[4], b_off[kBLoads];
-    uint32_t a_dst[4], b_dst[kBLoads];
+    // Global -> LDS with direct-to-LDS loads (global_load_lds_dwordx4): each
+    // wave instruction fills 1 KiB of LDS, lane l writing bytes [16l, 16l+16),
+    // so each lane loads the global chunk the swizzled layout puts there.  A is
+    // 32 KiB per stage (4 loads per wave), B is 256 * bRow bytes.
+    constexpr int kBLoadsPerWave = (kBlockN * T::bRow) / 1024 / 8;
+    uint32_t a_off[4], b_off[kBLoadsPerWave];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const int q = tid + i * kThreads, row = q >> 3, c = q & 7;
+        const int o = (wave * 4 + i) * 1024 + lane * 16;
+        const int row = o >> 7, c = ((o >> 4) & 7) ^ (row & 7);
         const int grow = min(m0 + row, p.m - 1);
         a_off[i] = (uint32_t)((size_t)grow * lda + c * 16);
-        a_dst[i] = swz(row, c);
     }
 #pragma unroll
-    for (int i = 0; i < kBLoads; ++i) {
-        const int q = tid + i * kThreads, row = q / kBChunks, c = q % kBChunks;
+    for (int i = 0; i < kBLoadsPerWave; ++i) {
+        const int o = (wave * kBLoadsPerWave + i) * 1024 + lane * 16;
+        int row, c;
+        if constexpr (T::bRow == 128) {
+            row = o >> 7;
+            c = ((o >> 4) & 7) ^ (row & 7);
+        } else {
+            row = o / T::bRow;
+            c = (o % T::bRow) / 16;
+        }
         const int grow = min(n0 + row, p.n - 1);
         b_off[i] = (uint32_t)((size_t)grow * ldb + c * 16);
-        b_dst[i] = T::bRow == 128 ? swz(row, c) : row * T::bRow + c * 16;
     }
     const uint8_t* __restrict__ pa = p.a;
     const uint8_t* __restrict__ pb = p.b;
+    // The loads are issued from inline asm so that the compiler does not
+    // order every later LDS read behind them (it cannot tell the DMA target
+    // from the buffer being read); the loop waits for them explicitly.
+#define PK_ISSUE(step, buf)                                                                          \
+    {                                                                                                \
+        const uint32_t base_ = lds_base + (buf) * kStageBytes;                                       \
+        _Pragma("unroll") for (int i = 0; i < 4; ++i)                                                \
+            dma16(pa + a_off[i] + (size_t)(step) * kRowBytes, base_ + (wave * 4 + i) * 1024);       \
+        _Pragma("unroll") for (int i = 0; i < kBLoadsPerWave; ++i)                                   \
+            dma16(pb + b_off[i] + (size_t)(step) * T::bRow,                                          \
+                  base_ + kTileBytes + (wave * kBLoadsPerWave + i) * 1024);                          \
+    }
 
-#define PK_GLOAD(step)                                                                          \
-    {                                                                                           \
-        _Pragma("unroll") for (int i = 0; i < 4; ++i) ra[i] =                                  \
-            *(const uint4*)(pa + a_off[i] + (size_t)(step) * kRowBytes);                        \
-        _Pragma("unroll") for (int i = 0; i < kBLoads; ++i) rb[i] =                            \
-            *(const uint4*)(pb + b_off[i] + (size_t)(step) * T::bRow);                          \
+    // G128 formats: the block's fp16 (scale, zero) pairs for all K groups
+    // live in LDS after the two stages ([256 columns x K/128] u32).
+    constexpr bool kG128 = (F == FMT_G128A8 || F == FMT_G128A16);
+    const int groups = p.k / 128;
+    uint32_t* gsz = (uint32_t*)(lds + 2 * kStageBytes);
+    if constexpr (kG128) {
+        for (int idx = tid; idx < kBlockN * groups; idx += kThreads) {
+            const int col = idx / groups, grp = idx - col * groups;
+            const size_t gi = (size_t)min(n0 + col, p.n - 1) * groups + grp;
+            gsz[idx] = (uint32_t)p.g_scales[gi] | ((uint32_t)p.g_zeros[gi] << 16);
+        }
     }
-#define PK_LSTORE(buf)                                                                          \
-    {                                                                                           \
-        uint8_t* base_ = lds + (buf) * kStageBytes;                                             \
-        _Pragma("unroll") for (int i = 0; i < 4; ++i) *(uint4*)(base_ + a_dst[i]) = ra[i];      \
-        _Pragma("unroll") for (int i = 0; i < kBLoads; ++i)                                     \
-            *(uint4*)(base_ + kTileBytes + b_dst[i]) = rb[i];                                   \
-    }
+    const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)lds;
 
     v4f accf[8][4];
     v4i acci[8][4];
@@ -229,18 +264,19 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs p) {
         }
 
     const int g = lane >> 4, l16 = lane & 15;
-    PK_GLOAD(0);
-    PK_LSTORE(0);
-    __syncthreads();
+    PK_ISSUE(0, 0);
 
     for (int step = 0; step < steps; ++step) {
         const int buf = step & 1;
-        {
-            const int next = step + 1 < steps ? step + 1 : step;
-            PK_GLOAD(next);
-        }
+        // This wave's loads for `step` have landed in LDS; the barrier makes
+        // every wave's loads visible and retires all reads of the other buffer
+        // before it is refilled.
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (step + 1 < steps) PK_ISSUE(step + 1, buf ^ 1);
         const uint8_t* As = lds + buf * kStageBytes;
         const uint8_t* Bs = As + kTileBytes;
+
 
         // Decode this wave's four B fragments.
         uint4 b0[4], b1[4];
@@ -252,12 +288,11 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs p) {
                 b0[bj] = *(const uint4*)(Bs + swz(row, g));
                 b1[bj] = *(const uint4*)(Bs + swz(row, 4 + g));
             } else {
-                const int ncol = min(n0 + row, p.n - 1);
                 const int kg = (step * T::kStep) / 128;
-                const size_t gi = (size_t)ncol * (p.k / 128) + kg;
-                const float z = h2f(p.g_zeros[gi]);
+                const uint32_t sz = gsz[row * groups + kg];
+                const float z = h2f((uint16_t)(sz >> 16));
                 if constexpr (F == FMT_G128A8) {
-                    gs[bj] = h2f(p.g_scales[gi]);
+                    gs[bj] = h2f((uint16_t)(sz & 0xffff));
                     const uint32_t zz = (uint32_t)(int)z * 0x01010101u;
                     const uint2 w0 = *(const uint2*)(Bs + row * 64 + 8 * g);
                     const uint2 w1 = *(const uint2*)(Bs + row * 64 + 32 + 8 * g);
@@ -266,7 +301,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs p) {
                     u4x8_minus_z(w1.x, zz, b1[bj].x, b1[bj].y);
                     u4x8_minus_z(w1.y, zz, b1[bj].z, b1[bj].w);
                 } else {  // G128A16
-                    const _Float16 s = __builtin_bit_cast(_Float16, p.g_scales[gi]);
+                    const _Float16 s = __builtin_bit_cast(_Float16, (uint16_t)(sz & 0xffff));
                     const _Float16 zh = (_Float16)(1024.0f + z);
                     const v2h ss = {s, s}, zz = {zh, zh};
                     const uint32_t w0 = *(const uint32_t*)(Bs + row * 32 + 4 * g);
@@ -284,15 +319,30 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs p) {
 #pragma unroll
             for (int bj = 0; bj < 4; ++bj) mfma_step<F>(accf[ai][bj], acci[ai][bj], a0, a1, b0[bj], b1[bj], gs[bj]);
         }
-        PK_LSTORE(buf ^ 1);
-        __syncthreads();
     }
-
-#undef PK_GLOAD
-#undef PK_LSTORE
+    __syncthreads();
+#undef PK_ISSUE
     // ---- epilogue ---------------------------------------------------------
+    // Each lane finishes columns [gcol, gcol + 16) of one row per pass; the
+    // per-column scales / bias and the eight per-pass row scales are loaded
+    // once, up front, so their latency is paid a single time.
     float* stage = (float*)(lds + wave * (16 * 68 * 4));
     const int er = lane >> 2, ec = (lane & 3) * 16;
+    const int gcol = n0 + wn * 64 + ec;
+    const int ccol = min(gcol, p.n - 16);
+    float wsv[16], bsv[16], rsv[8];
+#pragma unroll
+    for (int j = 0; j < 16; j += 4) {
+        const float4 w4 = p.w_scales ? *(const float4*)(p.w_scales + ccol + j) : float4{1.f, 1.f, 1.f, 1.f};
+        const float4 b4 = p.bias ? *(const float4*)(p.bias + ccol + j) : float4{0.f, 0.f, 0.f, 0.f};
+        wsv[j] = w4.x; wsv[j + 1] = w4.y; wsv[j + 2] = w4.z; wsv[j + 3] = w4.w;
+        bsv[j] = b4.x; bsv[j + 1] = b4.y; bsv[j + 2] = b4.z; bsv[j + 3] = b4.w;
+    }
+#pragma unroll
+    for (int ai = 0; ai < 8; ++ai) {
+        const int row = min(m0 + wm * 128 + ai * 16 + er, p.m - 1);
+        rsv[ai] = p.row_scales ? p.row_scales[row] : p.in_scale;
+    }
 #pragma unroll
     for (int ai = 0; ai < 8; ++ai) {
 #pragma unroll
@@ -308,16 +358,15 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs p) {
                 }
                 stage[(4 * g + r) * 68 + bj * 16 + l16] = v;
             }
-        __syncthreads();
+        wave_lds_sync();
         float v[16];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const float4 q = *(const float4*)(stage + er * 68 + ec + 4 * j);
             v[4 * j] = q.x; v[4 * j + 1] = q.y; v[4 * j + 2] = q.z; v[4 * j + 3] = q.w;
         }
-        __syncthreads();
+        wave_lds_sync();
         const int grow = m0 + wm * 128 + ai * 16 + er;
-        const int gcol = n0 + wn * 64 + ec;
         if (grow >= p.m || gcol >= p.n) continue;
 
         if constexpr (E == EPI_I32) {
@@ -326,13 +375,12 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs p) {
             for (int j = 0; j < 4; ++j) *(int4*)(o + 4 * j) = __builtin_bit_cast(int4, float4{v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]});
             continue;
         }
-        const float rs = p.row_scales ? p.row_scales[grow] : p.in_scale;
+        const float rs = rsv[ai];
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
-            const float ws = p.w_scales ? p.w_scales[gcol + j] : 1.0f;
-            const float bias = p.bias ? p.bias[gcol + j] : 0.0f;
-            if (p.fused_scale) v[j] = __builtin_fmaf(v[j], rs * ws, bias);
-            else v[j] = v[j] * rs * ws + bias;
+            const float fused = __builtin_fmaf(v[j], rs * wsv[j], bsv[j]);
+            const float plain = v[j] * rs * wsv[j] + bsv[j];
+            v[j] = p.fused_scale ? fused : plain;
         }
         if constexpr (E == EPI_F32) {
             float* o = (float*)p.out + (size_t)grow * p.ldo + gcol;
@@ -346,15 +394,13 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs p) {
                 res = u32x8{r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
             }
             u32x8 h;
+            const float rsc = p.residual ? p.res_scale : 0.0f;
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                float x0 = v[2 * j] * p.out_scale, x1 = v[2 * j + 1] * p.out_scale;
-                if (p.residual) {
-                    x0 = __builtin_fmaf(p.res_scale, h2f((uint16_t)(res[j] & 0xffff)), x0);
-                    x1 = __builtin_fmaf(p.res_scale, h2f((uint16_t)(res[j] >> 16)), x1);
-                }
-                if (p.act == 1) { x0 = silu(x0); x1 = silu(x1); }
-                else if (p.act == 2) { x0 = __builtin_fmaxf(x0, 0.0f); x1 = __builtin_fmaxf(x1, 0.0f); }
+                float x0 = __builtin_fmaf(rsc, h2f((uint16_t)(res[j] & 0xffff)), v[2 * j] * p.out_scale);
+                float x1 = __builtin_fmaf(rsc, h2f((uint16_t)(res[j] >> 16)), v[2 * j + 1] * p.out_scale);
+                x0 = p.act == 1 ? silu(x0) : (p.act == 2 ? __builtin_fmaxf(x0, 0.0f) : x0);
+                x1 = p.act == 1 ? silu(x1) : (p.act == 2 ? __builtin_fmaxf(x1, 0.0f) : x1);
                 h[j] = (uint32_t)f2h(x0) | ((uint32_t)f2h(x1) << 16);
             }
             uint4* o = (uint4*)((uint16_t*)p.out + (size_t)grow * p.ldo + gcol);
