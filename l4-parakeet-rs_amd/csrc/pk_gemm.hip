@@ -5,8 +5,14 @@
 
 namespace pk {
 
-static int lds_bytes(int fmt) {
-    return 2 * kStageBytes + ((fmt == FMT_G128A8 || fmt == FMT_G128A16) ? kMaxG128Groups * kBlockN * 4 : 0);
+static int cu_count() {
+    static int cus = 0;
+    if (cus == 0) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+            cus = 256;
+    }
+    return cus;
 }
 
 template <int F, int E>
@@ -14,14 +20,17 @@ static int launch_one(const GemmArgs& a, hipStream_t s) {
     static std::once_flag once;
     static hipError_t attr = hipSuccess;
     std::call_once(once, [] {
-        attr = hipFuncSetAttribute((const void*)gemm_kernel<F, E>, hipFuncAttributeMaxDynamicSharedMemorySize, lds_bytes(F));
+        attr = hipFuncSetAttribute((const void*)gemm_kernel<F, E>, hipFuncAttributeMaxDynamicSharedMemorySize, Layout<F>::kBytes);
     });
     if (attr != hipSuccess) {
-        set_error("hipFuncSetAttribute(LDS %d bytes) failed: %s", lds_bytes(F), hipGetErrorString(attr));
+        set_error("hipFuncSetAttribute(LDS %d bytes) failed: %s", Layout<F>::kBytes, hipGetErrorString(attr));
         return -3;
     }
-    const unsigned tiles = (unsigned)(((a.m + kBlockM - 1) / kBlockM) * ((a.n + kBlockN - 1) / kBlockN));
-    hipLaunchKernelGGL((gemm_kernel<F, E>), dim3(tiles), dim3(kThreads), lds_bytes(F), s, a);
+    const int tiles = ((a.m + kBlockM - 1) / kBlockM) * ((a.n + kBlockN - 1) / kBlockN);
+    const int cus = cu_count();
+    // one persistent workgroup per CU; a multiple of 8 keeps the XCD mapping
+    const int grid = tiles < cus ? tiles : cus - cus % 8;
+    hipLaunchKernelGGL((gemm_kernel<F, E>), dim3(grid), dim3(kThreads), Layout<F>::kBytes, s, a);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
         set_error("gemm launch (fmt %d, epi %d) failed: %s", F, E, hipGetErrorString(e));

@@ -169,261 +169,111 @@ __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_wave_barrier();
 }
 
-// Block index -> (m tile, n tile).  Workgroups are dispatched round-robin over
-// the 8 XCDs; remap so each XCD owns a contiguous run of tiles (N fastest),
-// which keeps an XCD's concurrent tiles on a couple of A row-strips and lets
-// its L2 serve the shared A and B tiles.
-__device__ __forceinline__ void tile_of(int& tm, int& tn, int tiles_n) {
-    const int b = blockIdx.x, nb = gridDim.x;
-    const int q = nb >> 3, r = nb & 7, x = b & 7, local = b >> 3;
-    const int t = x * q + (x < r ? x : r) + local;
-    tm = t / tiles_n;
-    tn = t - tm * tiles_n;
-}
-
+// Epilogue: each wave stages 8 rows x 64 columns of fp32 accumulators per
+// pass through its own LDS slab so that lane l finishes columns
+// [8(l%8), 8(l%8)+8) of row l/8 with one contiguous store.  Column scales and
+// bias and the 16 row scales of the lane are loaded once per tile.
 template <int F, int E>
-__global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs p) {
+__device__ __forceinline__ void epilogue(const GemmArgs& p, v4f (&accf)[8][4], v4i (&acci)[8][4], float* stage, int m0,
+                                         int n0, int wm, int wn, int lane) {
     using T = FmtTraits<F>;
-    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 2, wn = wave & 3;
-    const int tiles_n = (p.n + kBlockN - 1) / kBlockN;
-    int tm, tn;
-    tile_of(tm, tn, tiles_n);
-    const int m0 = tm * kBlockM, n0 = tn * kBlockN;
-
-    const size_t lda = (size_t)p.k * T::aElemNum / T::aElemDen;  // bytes per A row
-    const size_t ldb = (size_t)p.k * T::bNum / T::bDen;          // bytes per B row
-    const int steps = p.k / T::kStep;
-
-    // Global -> LDS with direct-to-LDS loads (global_load_lds_dwordx4): each
-    // wave instruction fills 1 KiB of LDS, lane l writing bytes [16l, 16l+16),
-    // so each lane loads the global chunk the swizzled layout puts there.  A is
-    // 32 KiB per stage (4 loads per wave), B is 256 * bRow bytes.
-    constexpr int kBLoadsPerWave = (kBlockN * T::bRow) / 1024 / 8;
-    uint32_t a_off[4], b_off[kBLoadsPerWave];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int o = (wave * 4 + i) * 1024 + lane * 16;
-        const int row = o >> 7, c = ((o >> 4) & 7) ^ (row & 7);
-        const int grow = min(m0 + row, p.m - 1);
-        a_off[i] = (uint32_t)((size_t)grow * lda + c * 16);
-    }
-#pragma unroll
-    for (int i = 0; i < kBLoadsPerWave; ++i) {
-        const int o = (wave * kBLoadsPerWave + i) * 1024 + lane * 16;
-        int row, c;
-        if constexpr (T::bRow == 128) {
-            row = o >> 7;
-            c = ((o >> 4) & 7) ^ (row & 7);
-        } else {
-            row = o / T::bRow;
-            c = (o % T::bRow) / 16;
-        }
-        const int grow = min(n0 + row, p.n - 1);
-        b_off[i] = (uint32_t)((size_t)grow * ldb + c * 16);
-    }
-    const uint8_t* __restrict__ pa = p.a;
-    const uint8_t* __restrict__ pb = p.b;
-    // The loads are issued from inline asm so that the compiler does not
-    // order every later LDS read behind them (it cannot tell the DMA target
-    // from the buffer being read); the loop waits for them explicitly.
-#define PK_ISSUE(step, buf)                                                                          \
-    {                                                                                                \
-        const uint32_t base_ = lds_base + (buf) * kStageBytes;                                       \
-        _Pragma("unroll") for (int i = 0; i < 4; ++i)                                                \
-            dma16(pa + a_off[i] + (size_t)(step) * kRowBytes, base_ + (wave * 4 + i) * 1024);       \
-        _Pragma("unroll") for (int i = 0; i < kBLoadsPerWave; ++i)                                   \
-            dma16(pb + b_off[i] + (size_t)(step) * T::bRow,                                          \
-                  base_ + kTileBytes + (wave * kBLoadsPerWave + i) * 1024);                          \
-    }
-
-    // G128 formats: the block's fp16 (scale, zero) pairs for all K groups
-    // live in LDS after the two stages ([256 columns x K/128] u32).
-    constexpr bool kG128 = (F == FMT_G128A8 || F == FMT_G128A16);
-    const int groups = p.k / 128;
-    uint32_t* gsz = (uint32_t*)(lds + 2 * kStageBytes);
-    if constexpr (kG128) {
-        for (int idx = tid; idx < kBlockN * groups; idx += kThreads) {
-            const int col = idx / groups, grp = idx - col * groups;
-            const size_t gi = (size_t)min(n0 + col, p.n - 1) * groups + grp;
-            gsz[idx] = (uint32_t)p.g_scales[gi] | ((uint32_t)p.g_zeros[gi] << 16);
-        }
-    }
-    const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)lds;
-
-    v4f accf[8][4];
-    v4i acci[8][4];
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            accf[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
-            acci[i][j] = v4i{0, 0, 0, 0};
-        }
-
     const int g = lane >> 4, l16 = lane & 15;
-    PK_ISSUE(0, 0);
-
-    for (int step = 0; step < steps; ++step) {
-        const int buf = step & 1;
-        // This wave's loads for `step` have landed in LDS; the barrier makes
-        // every wave's loads visible and retires all reads of the other buffer
-        // before it is refilled.
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();
-        if (step + 1 < steps) PK_ISSUE(step + 1, buf ^ 1);
-        const uint8_t* As = lds + buf * kStageBytes;
-        const uint8_t* Bs = As + kTileBytes;
-
-
-        // Decode this wave's four B fragments.
-        uint4 b0[4], b1[4];
-        float gs[4] = {1.f, 1.f, 1.f, 1.f};
-#pragma unroll
-        for (int bj = 0; bj < 4; ++bj) {
-            const int row = wn * 64 + bj * 16 + l16;
-            if constexpr (T::bRow == 128) {
-                b0[bj] = *(const uint4*)(Bs + swz(row, g));
-                b1[bj] = *(const uint4*)(Bs + swz(row, 4 + g));
-            } else {
-                const int kg = (step * T::kStep) / 128;
-                const uint32_t sz = gsz[row * groups + kg];
-                const float z = h2f((uint16_t)(sz >> 16));
-                if constexpr (F == FMT_G128A8) {
-                    gs[bj] = h2f((uint16_t)(sz & 0xffff));
-                    const uint32_t zz = (uint32_t)(int)z * 0x01010101u;
-                    const uint2 w0 = *(const uint2*)(Bs + row * 64 + 8 * g);
-                    const uint2 w1 = *(const uint2*)(Bs + row * 64 + 32 + 8 * g);
-                    u4x8_minus_z(w0.x, zz, b0[bj].x, b0[bj].y);
-                    u4x8_minus_z(w0.y, zz, b0[bj].z, b0[bj].w);
-                    u4x8_minus_z(w1.x, zz, b1[bj].x, b1[bj].y);
-                    u4x8_minus_z(w1.y, zz, b1[bj].z, b1[bj].w);
-                } else {  // G128A16
-                    const _Float16 s = __builtin_bit_cast(_Float16, (uint16_t)(sz & 0xffff));
-                    const _Float16 zh = (_Float16)(1024.0f + z);
-                    const v2h ss = {s, s}, zz = {zh, zh};
-                    const uint32_t w0 = *(const uint32_t*)(Bs + row * 32 + 4 * g);
-                    const uint32_t w1 = *(const uint32_t*)(Bs + row * 32 + 16 + 4 * g);
-                    b0[bj] = __builtin_bit_cast(uint4, u4x8_to_h(w0, zz, ss));
-                    b1[bj] = __builtin_bit_cast(uint4, u4x8_to_h(w1, zz, ss));
-                }
-            }
-        }
-#pragma unroll
-        for (int ai = 0; ai < 8; ++ai) {
-            const int row = wm * 128 + ai * 16 + l16;
-            const uint4 a0 = *(const uint4*)(As + swz(row, g));
-            const uint4 a1 = *(const uint4*)(As + swz(row, 4 + g));
-#pragma unroll
-            for (int bj = 0; bj < 4; ++bj) mfma_step<F>(accf[ai][bj], acci[ai][bj], a0, a1, b0[bj], b1[bj], gs[bj]);
-        }
-    }
-    __syncthreads();
-#undef PK_ISSUE
-    // ---- epilogue ---------------------------------------------------------
-    // Each lane finishes columns [gcol, gcol + 16) of one row per pass; the
-    // per-column scales / bias and the eight per-pass row scales are loaded
-    // once, up front, so their latency is paid a single time.
-    float* stage = (float*)(lds + wave * (16 * 68 * 4));
-    const int er = lane >> 2, ec = (lane & 3) * 16;
+    const int er = lane >> 3, ec = (lane & 7) * 8;
     const int gcol = n0 + wn * 64 + ec;
-    const int ccol = min(gcol, p.n - 16);
-    float wsv[16], bsv[16], rsv[8];
+    const int ccol = min(gcol, p.n - 8);
+    float wsv[8], bsv[8], rsv[16];
 #pragma unroll
-    for (int j = 0; j < 16; j += 4) {
+    for (int j = 0; j < 8; j += 4) {
         const float4 w4 = p.w_scales ? *(const float4*)(p.w_scales + ccol + j) : float4{1.f, 1.f, 1.f, 1.f};
         const float4 b4 = p.bias ? *(const float4*)(p.bias + ccol + j) : float4{0.f, 0.f, 0.f, 0.f};
         wsv[j] = w4.x; wsv[j + 1] = w4.y; wsv[j + 2] = w4.z; wsv[j + 3] = w4.w;
         bsv[j] = b4.x; bsv[j + 1] = b4.y; bsv[j + 2] = b4.z; bsv[j + 3] = b4.w;
     }
 #pragma unroll
-    for (int ai = 0; ai < 8; ++ai) {
-        const int row = min(m0 + wm * 128 + ai * 16 + er, p.m - 1);
-        rsv[ai] = p.row_scales ? p.row_scales[row] : p.in_scale;
+    for (int ps = 0; ps < 16; ++ps) {
+        const int row = min(m0 + wm * 128 + ps * 8 + er, p.m - 1);
+        rsv[ps] = p.row_scales ? p.row_scales[row] : p.in_scale;
     }
 #pragma unroll
-    for (int ai = 0; ai < 8; ++ai) {
+    for (int ps = 0; ps < 16; ++ps) {
+        const int ai = ps >> 1, h = ps & 1;
+        if ((g >> 1) == h) {
 #pragma unroll
-        for (int bj = 0; bj < 4; ++bj)
+            for (int bj = 0; bj < 4; ++bj)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                float v;
-                if constexpr (T::kInt) {
-                    const int iv = acci[ai][bj][r];
-                    v = E == EPI_I32 ? __int_as_float(iv) : (float)iv;
-                } else {
-                    v = accf[ai][bj][r];
+                for (int r = 0; r < 4; ++r) {
+                    float v;
+                    if constexpr (T::kInt) {
+                        const int iv = acci[ai][bj][r];
+                        v = E == EPI_I32 ? __int_as_float(iv) : (float)iv;
+                    } else {
+                        v = accf[ai][bj][r];
+                    }
+                    stage[(4 * (g & 1) + r) * 68 + bj * 16 + l16] = v;
                 }
-                stage[(4 * g + r) * 68 + bj * 16 + l16] = v;
-            }
-        wave_lds_sync();
-        float v[16];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const float4 q = *(const float4*)(stage + er * 68 + ec + 4 * j);
-            v[4 * j] = q.x; v[4 * j + 1] = q.y; v[4 * j + 2] = q.z; v[4 * j + 3] = q.w;
         }
         wave_lds_sync();
-        const int grow = m0 + wm * 128 + ai * 16 + er;
+        float v[8];
+        {
+            const float4 q0 = *(const float4*)(stage + er * 68 + ec);
+            const float4 q1 = *(const float4*)(stage + er * 68 + ec + 4);
+            v[0] = q0.x; v[1] = q0.y; v[2] = q0.z; v[3] = q0.w;
+            v[4] = q1.x; v[5] = q1.y; v[6] = q1.z; v[7] = q1.w;
+        }
+        wave_lds_sync();
+        const int grow = m0 + wm * 128 + ps * 8 + er;
         if (grow >= p.m || gcol >= p.n) continue;
 
         if constexpr (E == EPI_I32) {
             int32_t* o = (int32_t*)p.out + (size_t)grow * p.ldo + gcol;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) *(int4*)(o + 4 * j) = __builtin_bit_cast(int4, float4{v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]});
+            *(int4*)o = __builtin_bit_cast(int4, float4{v[0], v[1], v[2], v[3]});
+            *(int4*)(o + 4) = __builtin_bit_cast(int4, float4{v[4], v[5], v[6], v[7]});
             continue;
         }
-        const float rs = rsv[ai];
+        const float rs = rsv[ps];
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
+        for (int j = 0; j < 8; ++j) {
             const float fused = __builtin_fmaf(v[j], rs * wsv[j], bsv[j]);
             const float plain = v[j] * rs * wsv[j] + bsv[j];
             v[j] = p.fused_scale ? fused : plain;
         }
         if constexpr (E == EPI_F32) {
             float* o = (float*)p.out + (size_t)grow * p.ldo + gcol;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) *(float4*)(o + 4 * j) = float4{v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]};
+            *(float4*)o = float4{v[0], v[1], v[2], v[3]};
+            *(float4*)(o + 4) = float4{v[4], v[5], v[6], v[7]};
         } else if constexpr (E == EPI_F16) {
-            u32x8 res = {0, 0, 0, 0, 0, 0, 0, 0};
-            if (p.residual) {
-                const uint4* rp = (const uint4*)(p.residual + (size_t)grow * p.ldo + gcol);
-                const uint4 r0 = rp[0], r1 = rp[1];
-                res = u32x8{r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
-            }
-            u32x8 h;
+            uint4 res = {0, 0, 0, 0};
+            if (p.residual) res = *(const uint4*)(p.residual + (size_t)grow * p.ldo + gcol);
+            const uint32_t rw[4] = {res.x, res.y, res.z, res.w};
             const float rsc = p.residual ? p.res_scale : 0.0f;
+            uint32_t h[4];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                float x0 = __builtin_fmaf(rsc, h2f((uint16_t)(res[j] & 0xffff)), v[2 * j] * p.out_scale);
-                float x1 = __builtin_fmaf(rsc, h2f((uint16_t)(res[j] >> 16)), v[2 * j + 1] * p.out_scale);
+            for (int j = 0; j < 4; ++j) {
+                float x0 = __builtin_fmaf(rsc, h2f((uint16_t)(rw[j] & 0xffff)), v[2 * j] * p.out_scale);
+                float x1 = __builtin_fmaf(rsc, h2f((uint16_t)(rw[j] >> 16)), v[2 * j + 1] * p.out_scale);
                 x0 = p.act == 1 ? silu(x0) : (p.act == 2 ? __builtin_fmaxf(x0, 0.0f) : x0);
                 x1 = p.act == 1 ? silu(x1) : (p.act == 2 ? __builtin_fmaxf(x1, 0.0f) : x1);
                 h[j] = (uint32_t)f2h(x0) | ((uint32_t)f2h(x1) << 16);
             }
-            uint4* o = (uint4*)((uint16_t*)p.out + (size_t)grow * p.ldo + gcol);
-            o[0] = uint4{h[0], h[1], h[2], h[3]};
-            o[1] = uint4{h[4], h[5], h[6], h[7]};
+            *(uint4*)((uint16_t*)p.out + (size_t)grow * p.ldo + gcol) = uint4{h[0], h[1], h[2], h[3]};
         } else if constexpr (E == EPI_F8 || E == EPI_F8_24) {
-            uint32_t w[4];
+            uint32_t w[2];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
+            for (int j = 0; j < 2; ++j) {
                 const float x0 = round_f16(silu(v[4 * j])) * 16.0f, x1 = round_f16(silu(v[4 * j + 1])) * 16.0f;
                 const float x2 = round_f16(silu(v[4 * j + 2])) * 16.0f, x3 = round_f16(silu(v[4 * j + 3])) * 16.0f;
                 w[j] = e4m3x2(x0, x1) | (e4m3x2(x2, x3) << 16);
             }
             if constexpr (E == EPI_F8) {
-                *(uint4*)((uint8_t*)p.out + (size_t)grow * p.ldo + gcol) = uint4{w[0], w[1], w[2], w[3]};
+                *(uint2*)((uint8_t*)p.out + (size_t)grow * p.ldo + gcol) = uint2{w[0], w[1]};
             } else {
                 // encoder.cu:685-704: keep the two largest |e4m3| of each
                 // quartet (ties to the lower index), metadata idx0 | idx1 << 2.
-                uint32_t data[2] = {0, 0};
-                uint32_t meta = 0;
+                uint32_t data = 0, meta = 0;
 #pragma unroll
-                for (int qd = 0; qd < 4; ++qd) {
-                    uint32_t packed = w[qd], d = 0, md = 0;
+                for (int qd = 0; qd < 2; ++qd) {
+                    const uint32_t packed = w[qd];
+                    uint32_t d = 0, md = 0;
                     int count = 0;
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
@@ -440,13 +290,195 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs p) {
                             ++count;
                         }
                     }
-                    data[qd >> 1] |= d << (16 * (qd & 1));
+                    data |= d << (16 * qd);
                     meta |= md << (4 * qd);
                 }
-                *(uint2*)((uint8_t*)p.out + (size_t)grow * (p.ldo / 2) + gcol / 2) = uint2{data[0], data[1]};
-                *(uint16_t*)(p.out_meta + (size_t)grow * (p.ldo / 8) + gcol / 8) = (uint16_t)meta;
+                *(uint32_t*)((uint8_t*)p.out + (size_t)grow * (p.ldo / 2) + gcol / 2) = data;
+                p.out_meta[(size_t)grow * (p.ldo / 8) + gcol / 8] = (uint8_t)meta;
             }
         }
+    }
+}
+
+// Persistent tile schedule.  The grid is one workgroup per CU (G of them);
+// iteration i of workgroup b computes logical tile i*G + slot(b).  Workgroups
+// are dispatched round-robin over the 8 XCDs, so slot() gives each XCD a
+// contiguous run of G/8 logical tiles per iteration; tiles are numbered N
+// fastest, so an XCD's concurrent tiles share one or two A row-strips and the
+// same B columns in its L2.
+__device__ __forceinline__ int tile_slot(int G) {
+    const int b = blockIdx.x;
+    return (G & 7) == 0 ? (b & 7) * (G >> 3) + (b >> 3) : b;
+}
+
+template <int F> struct Layout {
+    static constexpr int kStage = kTileBytes + kBlockN * FmtTraits<F>::bRow;
+    static constexpr int kEpi = 2 * kStage;                      // epilogue staging
+    static constexpr int kEpiBytes = 8 * 8 * 68 * 4;              // 8 waves x 8 rows x 68 floats
+    static constexpr bool kG128 = (F == FMT_G128A8 || F == FMT_G128A16);
+    static constexpr int kGsz = kEpi + kEpiBytes;                  // g128 (scale, zero) table
+    static constexpr int kBytes = kGsz + (kG128 ? kMaxG128Groups * kBlockN * 4 : 0);
+};
+
+template <int F, int E>
+__global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs p) {
+    using T = FmtTraits<F>;
+    using L = Layout<F>;
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 2, wn = wave & 3;
+    const int g = lane >> 4, l16 = lane & 15;
+    const int tiles_n = (p.n + kBlockN - 1) / kBlockN;
+    const int ntiles = ((p.m + kBlockM - 1) / kBlockM) * tiles_n;
+    const int G = gridDim.x;
+    const int slot = tile_slot(G);
+    const size_t lda = (size_t)p.k * T::aElemNum / T::aElemDen;  // bytes per A row
+    const size_t ldb = (size_t)p.k * T::bNum / T::bDen;          // bytes per B row
+    const int steps = p.k / T::kStep;
+    const int groups = p.k >> 7;
+    const uint8_t* __restrict__ pa = p.a;
+    const uint8_t* __restrict__ pb = p.b;
+    const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)lds;
+    uint32_t* gsz = (uint32_t*)(lds + L::kGsz);
+
+    // Direct-to-LDS operand loads (global_load_lds_dwordx4): one wave
+    // instruction fills 1 KiB of LDS, lane l writing bytes [16l, 16l+16), so
+    // each lane loads the global chunk the swizzled layout puts there.
+    constexpr int kBLoadsPerWave = (kBlockN * T::bRow) / 1024 / 8;
+    uint32_t a_off[4], b_off[kBLoadsPerWave];
+    auto set_tile = [&](int t, int& m0, int& n0) {
+        const int tm = t / tiles_n;
+        m0 = tm * kBlockM;
+        n0 = (t - tm * tiles_n) * kBlockN;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int o = (wave * 4 + i) * 1024 + lane * 16;
+            const int row = o >> 7, c = ((o >> 4) & 7) ^ (row & 7);
+            a_off[i] = (uint32_t)((size_t)min(m0 + row, p.m - 1) * lda + c * 16);
+        }
+#pragma unroll
+        for (int i = 0; i < kBLoadsPerWave; ++i) {
+            const int o = (wave * kBLoadsPerWave + i) * 1024 + lane * 16;
+            int row, c;
+            if constexpr (T::bRow == 128) {
+                row = o >> 7;
+                c = ((o >> 4) & 7) ^ (row & 7);
+            } else {
+                row = o / T::bRow;
+                c = (o % T::bRow) / 16;
+            }
+            b_off[i] = (uint32_t)((size_t)min(n0 + row, p.n - 1) * ldb + c * 16);
+        }
+    };
+    // The loads are issued from inline asm so that the compiler does not order
+    // every later LDS read behind them (it cannot tell the DMA target from the
+    // buffer being read); the step loop waits for them explicitly.
+    auto issue = [&](int step, int buf) {
+        const uint32_t base = lds_base + buf * L::kStage;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dma16(pa + a_off[i] + (size_t)step * kRowBytes, base + (wave * 4 + i) * 1024);
+#pragma unroll
+        for (int i = 0; i < kBLoadsPerWave; ++i)
+            dma16(pb + b_off[i] + (size_t)step * T::bRow, base + kTileBytes + (wave * kBLoadsPerWave + i) * 1024);
+    };
+
+    int t = slot;
+    if (t >= ntiles) return;
+    int m0, n0;
+    set_tile(t, m0, n0);
+    issue(0, 0);
+    int buf = 0;
+
+    v4f accf[8][4];
+    v4i acci[8][4];
+    float* stage = (float*)(lds + L::kEpi + wave * (8 * 68 * 4));
+
+    while (true) {
+        const int t_next = t + G;
+        const int cur_m0 = m0, cur_n0 = n0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                accf[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+                acci[i][j] = v4i{0, 0, 0, 0};
+            }
+
+        for (int step = 0; step < steps; ++step) {
+            // This wave's loads for `step` have landed in LDS; the barrier makes
+            // every wave's loads visible and retires all reads of the other
+            // buffer before it is refilled.
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            __syncthreads();
+            if constexpr (L::kG128) {
+                if (step == 0) {
+                    for (int idx = tid; idx < kBlockN * groups; idx += kThreads) {
+                        const int col = idx / groups, grp = idx - col * groups;
+                        const size_t gi = (size_t)min(cur_n0 + col, p.n - 1) * groups + grp;
+                        gsz[idx] = (uint32_t)p.g_scales[gi] | ((uint32_t)p.g_zeros[gi] << 16);
+                    }
+                    __syncthreads();
+                }
+            }
+            if (step + 1 < steps) {
+                issue(step + 1, buf ^ 1);
+            } else if (t_next < ntiles) {
+                set_tile(t_next, m0, n0);
+                issue(0, buf ^ 1);
+            }
+            const uint8_t* As = lds + buf * L::kStage;
+            const uint8_t* Bs = As + kTileBytes;
+            const int n0 = cur_n0;
+            (void)n0;
+
+            // Decode this wave's four B fragments.
+            uint4 b0[4], b1[4];
+            float gs[4] = {1.f, 1.f, 1.f, 1.f};
+    #pragma unroll
+            for (int bj = 0; bj < 4; ++bj) {
+                const int row = wn * 64 + bj * 16 + l16;
+                if constexpr (T::bRow == 128) {
+                    b0[bj] = *(const uint4*)(Bs + swz(row, g));
+                    b1[bj] = *(const uint4*)(Bs + swz(row, 4 + g));
+                } else {
+                    const int kg = (step * T::kStep) >> 7;
+                    const uint32_t sz = gsz[row * groups + kg];
+                    const float z = h2f((uint16_t)(sz >> 16));
+                    if constexpr (F == FMT_G128A8) {
+                        gs[bj] = h2f((uint16_t)(sz & 0xffff));
+                        const uint32_t zz = (uint32_t)(int)z * 0x01010101u;
+                        const uint2 w0 = *(const uint2*)(Bs + row * 64 + 8 * g);
+                        const uint2 w1 = *(const uint2*)(Bs + row * 64 + 32 + 8 * g);
+                        u4x8_minus_z(w0.x, zz, b0[bj].x, b0[bj].y);
+                        u4x8_minus_z(w0.y, zz, b0[bj].z, b0[bj].w);
+                        u4x8_minus_z(w1.x, zz, b1[bj].x, b1[bj].y);
+                        u4x8_minus_z(w1.y, zz, b1[bj].z, b1[bj].w);
+                    } else {  // G128A16
+                        const _Float16 s = __builtin_bit_cast(_Float16, (uint16_t)(sz & 0xffff));
+                        const _Float16 zh = (_Float16)(1024.0f + z);
+                        const v2h ss = {s, s}, zz = {zh, zh};
+                        const uint32_t w0 = *(const uint32_t*)(Bs + row * 32 + 4 * g);
+                        const uint32_t w1 = *(const uint32_t*)(Bs + row * 32 + 16 + 4 * g);
+                        b0[bj] = __builtin_bit_cast(uint4, u4x8_to_h(w0, zz, ss));
+                        b1[bj] = __builtin_bit_cast(uint4, u4x8_to_h(w1, zz, ss));
+                    }
+                }
+            }
+#pragma unroll
+            for (int ai = 0; ai < 8; ++ai) {
+                const int row = wm * 128 + ai * 16 + l16;
+                const uint4 a0 = *(const uint4*)(As + swz(row, g));
+                const uint4 a1 = *(const uint4*)(As + swz(row, 4 + g));
+#pragma unroll
+                for (int bj = 0; bj < 4; ++bj) mfma_step<F>(accf[ai][bj], acci[ai][bj], a0, a1, b0[bj], b1[bj], gs[bj]);
+            }
+            buf ^= 1;
+        }
+
+        epilogue<F, E>(p, accf, acci, stage, cur_m0, cur_n0, wm, wn, lane);
+        if (t_next >= ntiles) break;
+        t = t_next;
     }
 }
 
