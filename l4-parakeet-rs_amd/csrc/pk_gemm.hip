@@ -42,7 +42,7 @@ static int launch_one(const GemmArgs& a, hipStream_t s) {
 template <int F>
 static int by_epi(int epi, const GemmArgs& a, hipStream_t s) {
     switch (epi) {
-    case EPI_F16: return launch_one<F, EPI_F16>(a, s);
+    case EPI_F16: return a.residual ? launch_one<F, EPI_F16_RES>(a, s) : launch_one<F, EPI_F16>(a, s);
     case EPI_F32: return launch_one<F, EPI_F32>(a, s);
     case EPI_F8: return launch_one<F, EPI_F8>(a, s);
     case EPI_F8_24: return launch_one<F, EPI_F8_24>(a, s);

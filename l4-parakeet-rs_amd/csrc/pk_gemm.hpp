@@ -1,24 +1,32 @@
 // Byte-tile GEMM engine for the quantized linears (gfx950 / CDNA4).
 //
-// One workgroup = 8 wave64s computing a 256x256 output tile; wave w owns
-// rows 128*(w/4) .. +128 and columns 64*(w%4) .. +64 as 8x4 MFMA 16x16
-// tiles.  Every K-step moves 128 bytes of each A row (256 rows) and up to 128
-// bytes of each B row (256 rows) global -> registers -> LDS (double
-// buffered, one barrier per step); the 16-byte chunks of each 128-byte LDS row
-// are XOR-swizzled by (row & 7) so the 16 lanes that read one chunk column hit
-// distinct banks.  The operand format only changes how a lane's two 16-byte
-// chunks (K slots [16g, 16g+16) and [64+16g, 64+16g+16) of the step, g =
-// lane/16) are decoded and which MFMA consumes them:
+// A persistent workgroup per CU (8 wave64s) walks 256x256 output tiles; wave
+// w owns output rows 128*(w/4) .. +128 and columns 64*(w%4) .. +64.  Every
+// K-step moves 128 bytes of each of the tile's 256 activation rows and up to
+// 128 bytes of each of its 256 weight rows global -> LDS with direct-to-LDS
+// loads (double buffered, one barrier per step, the next tile's first step
+// prefetched while the current tile finishes).  The 16-byte chunks of each
+// 128-byte LDS row are XOR-swizzled by (row & 7) so that the 16 lanes reading
+// one chunk column hit distinct banks.
+//
+// The weights are the MFMA's first operand and the activations its second,
+// so accumulator register r of lane l holds output column 4*(l/16)+r of row
+// l%16.  Weight rows are assigned to the four 16-row MFMA blocks of a wave
+// (bj) as n = 16*(i/4) + 4*bj + i%4 (i = MFMA row), which makes the 16
+// accumulators a lane holds for one 16-row block of activations exactly the
+// 16 consecutive output columns [16*(l/16), +16) of one row: the epilogue
+// scales, converts and stores them straight from registers.
+//
+// The operand format only changes how a lane's two 16-byte chunks (K slots
+// [16g, 16g+16) and [64+16g, 64+16g+16) of the step, g = lane/16) are decoded
+// and which MFMA consumes them:
 //   FP8     e4m3 x e4m3   v_mfma_f32_16x16x128_f8f6f4      K/step 128
 //   I8      s8 x s8       2 x v_mfma_i32_16x16x64_i8       K/step 128 (exact)
 //   S4      s4 x s4       nibbles -> s8, 4 x i8 MFMA       K/step 256 (exact)
-//   G128A8  s8 x (q-z)    group-wise INT4 weights, i8 MFMA per 128-K group,
+//   G128A8  (q-z) x s8    group-wise INT4 weights, i8 MFMA per 128-K group,
 //                         fp32 fma of each group sum with its fp16 scale
 //   F16     f16 x f16     2 x v_mfma_f32_16x16x32_f16      K/step 64
-//   G128A16 f16 x f16((q-z)*s)  INT4 weights dequantized in registers
-// The epilogue stages each wave's accumulators through LDS (16 rows at a
-// time) so every lane finishes 16 consecutive columns of one row with 16- or
-// 32-byte global stores.
+//   G128A16 f16((q-z)*s) x f16, INT4 weights dequantized in registers
 #pragma once
 
 #include "pk_common.hpp"
@@ -33,7 +41,7 @@ enum Epi {
     EPI_F8_24 = 2,   // as EPI_F8, then 2:4 compressed data + 4-bit metadata
     EPI_F32 = 3,     // fp32 out: scale(acc) [+bias]
     EPI_I32 = 4,     // raw int32 accumulators (integer formats only)
-    EPI_GLU = 5,     // fp16 out: fp16(v) * sigmoid(fp16(g)), column pairs (c, c + N/2)
+    EPI_F16_RES = 5, // EPI_F16 with a residual (chosen by the launcher when one is given)
 };
 
 struct GemmArgs {
@@ -44,7 +52,7 @@ struct GemmArgs {
     const float* row_scales;    // [M] per-row activation scales, or null (in_scale)
     float in_scale;
     int fused_scale;            // 1: v = fma(acc, in_scale * w_scale, bias) (linear.cu:362-365)
-                                // 0: v = acc * row_scale * w_scale [+ bias] (encoder.cu:975-995)
+                                // 0: v = fma(acc * row_scale, w_scale, bias) (encoder.cu:975-995)
     const float* bias;          // [N] or null
     const uint16_t* residual;   // fp16 [M x ldo] or null (may alias out)
     float out_scale;
@@ -55,16 +63,15 @@ struct GemmArgs {
     void* out;
     uint8_t* out_meta;          // EPI_F8_24: [M x ldo/8] metadata bytes
     int ldo;                    // output row stride in elements (of the output type)
-    int valid_rows;             // EPI_GLU: rows >= valid_rows are written as 0
+    int valid_rows;
 };
 
 constexpr int kBlockM = 256;
 constexpr int kBlockN = 256;
 constexpr int kThreads = 512;
 constexpr int kRowBytes = 128;
-constexpr int kTileBytes = kBlockM * kRowBytes;  // one operand tile per stage
-constexpr int kStageBytes = 2 * kTileBytes;
-constexpr int kMaxG128Groups = 32;  // K <= 4096 for the group-wise INT4 formats
+constexpr int kTileBytes = kBlockM * kRowBytes;  // the activation tile of one stage
+constexpr int kMaxG128Groups = 32;               // K <= 4096 for the group-wise INT4 formats
 
 template <int F> struct FmtTraits;
 template <> struct FmtTraits<FMT_FP8> { static constexpr int kStep = 128, bRow = 128, aElemNum = 1, aElemDen = 1, bNum = 1, bDen = 1; static constexpr bool kInt = false; };
@@ -74,7 +81,20 @@ template <> struct FmtTraits<FMT_G128A8> { static constexpr int kStep = 128, bRo
 template <> struct FmtTraits<FMT_F16> { static constexpr int kStep = 64, bRow = 128, aElemNum = 2, aElemDen = 1, bNum = 2, bDen = 1; static constexpr bool kInt = false; };
 template <> struct FmtTraits<FMT_G128A16> { static constexpr int kStep = 64, bRow = 32, aElemNum = 2, aElemDen = 1, bNum = 1, bDen = 2; static constexpr bool kInt = false; };
 
+template <int F> struct Layout {
+    static constexpr int kStage = kTileBytes + kBlockN * FmtTraits<F>::bRow;
+    static constexpr bool kG128 = (F == FMT_G128A8 || F == FMT_G128A16);
+    // G128 tables after the two stages: fp32 scales [group][256 columns] and
+    // u8 zero-points [group][256 columns] of the current tile.
+    static constexpr int kScales = 2 * kStage;
+    static constexpr int kZeros = kScales + kMaxG128Groups * kBlockN * 4;
+    static constexpr int kBytes = kG128 ? kZeros + kMaxG128Groups * kBlockN : 2 * kStage;
+};
+
 __device__ __forceinline__ int swz(int row, int chunk) { return row * kRowBytes + ((chunk ^ (row & 7)) << 4); }
+
+// Weight row (within the wave's 64 columns) held by MFMA row i of block bj.
+__device__ __forceinline__ int wrow(int i, int bj) { return ((i >> 2) << 4) + (bj << 2) + (i & 3); }
 
 // Four unsigned nibbles (byte j of `w`, low nibble = k j, high = k 4+j) ->
 // eight int8 (q - z), natural k order, as two dwords.
@@ -99,226 +119,365 @@ __device__ __forceinline__ v8h u4x8_to_h(uint32_t w, v2h zz, v2h ss) {
     return out;
 }
 
+__device__ __forceinline__ v4i as_v4i(const uint4& u) { return v4i{(int)u.x, (int)u.y, (int)u.z, (int)u.w}; }
+
+// One K-step of one 16x16 output block: w0/w1 are the weight chunks (first
+// MFMA operand), x0/x1 the activation chunks (second operand).
 template <int F>
-__device__ __forceinline__ void mfma_step(v4f& accf, v4i& acci, const uint4& a0, const uint4& a1,
-                                          const uint4& b0, const uint4& b1, float gscale) {
+__device__ __forceinline__ void mfma_step(v4f& accf, v4i& acci, const uint4& w0, const uint4& w1, const uint4& x0,
+                                          const uint4& x1, const v4f& gscale) {
     if constexpr (F == FMT_FP8) {
-        v8i A = {(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w, (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
-        v8i B = {(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w, (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
-        accf = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A, B, accf, 0, 0, 0, 0, 0, 0);
+        const v8i W = {(int)w0.x, (int)w0.y, (int)w0.z, (int)w0.w, (int)w1.x, (int)w1.y, (int)w1.z, (int)w1.w};
+        const v8i X = {(int)x0.x, (int)x0.y, (int)x0.z, (int)x0.w, (int)x1.x, (int)x1.y, (int)x1.z, (int)x1.w};
+        accf = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(W, X, accf, 0, 0, 0, 0, 0, 0);
     } else if constexpr (F == FMT_I8) {
-        v4i A0 = {(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w};
-        v4i A1 = {(int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
-        v4i B0 = {(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w};
-        v4i B1 = {(int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
-        acci = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0, B0, acci, 0, 0, 0);
-        acci = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1, B1, acci, 0, 0, 0);
+        acci = __builtin_amdgcn_mfma_i32_16x16x64_i8(as_v4i(w0), as_v4i(x0), acci, 0, 0, 0);
+        acci = __builtin_amdgcn_mfma_i32_16x16x64_i8(as_v4i(w1), as_v4i(x1), acci, 0, 0, 0);
     } else if constexpr (F == FMT_S4) {
-        uint32_t al[8], bl[8];
-        s4x8_to_s8(a0.x, al[0], al[4]); s4x8_to_s8(a0.y, al[1], al[5]);
-        s4x8_to_s8(a0.z, al[2], al[6]); s4x8_to_s8(a0.w, al[3], al[7]);
-        s4x8_to_s8(b0.x, bl[0], bl[4]); s4x8_to_s8(b0.y, bl[1], bl[5]);
-        s4x8_to_s8(b0.z, bl[2], bl[6]); s4x8_to_s8(b0.w, bl[3], bl[7]);
-        v4i A0 = {(int)al[0], (int)al[1], (int)al[2], (int)al[3]}, A1 = {(int)al[4], (int)al[5], (int)al[6], (int)al[7]};
-        v4i B0 = {(int)bl[0], (int)bl[1], (int)bl[2], (int)bl[3]}, B1 = {(int)bl[4], (int)bl[5], (int)bl[6], (int)bl[7]};
-        acci = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0, B0, acci, 0, 0, 0);
-        acci = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1, B1, acci, 0, 0, 0);
-        s4x8_to_s8(a1.x, al[0], al[4]); s4x8_to_s8(a1.y, al[1], al[5]);
-        s4x8_to_s8(a1.z, al[2], al[6]); s4x8_to_s8(a1.w, al[3], al[7]);
-        s4x8_to_s8(b1.x, bl[0], bl[4]); s4x8_to_s8(b1.y, bl[1], bl[5]);
-        s4x8_to_s8(b1.z, bl[2], bl[6]); s4x8_to_s8(b1.w, bl[3], bl[7]);
-        v4i A2 = {(int)al[0], (int)al[1], (int)al[2], (int)al[3]}, A3 = {(int)al[4], (int)al[5], (int)al[6], (int)al[7]};
-        v4i B2 = {(int)bl[0], (int)bl[1], (int)bl[2], (int)bl[3]}, B3 = {(int)bl[4], (int)bl[5], (int)bl[6], (int)bl[7]};
-        acci = __builtin_amdgcn_mfma_i32_16x16x64_i8(A2, B2, acci, 0, 0, 0);
-        acci = __builtin_amdgcn_mfma_i32_16x16x64_i8(A3, B3, acci, 0, 0, 0);
+        uint4 wl, wh, xl, xh;
+        s4x8_to_s8(w0.x, wl.x, wh.x); s4x8_to_s8(w0.y, wl.y, wh.y); s4x8_to_s8(w0.z, wl.z, wh.z); s4x8_to_s8(w0.w, wl.w, wh.w);
+        s4x8_to_s8(x0.x, xl.x, xh.x); s4x8_to_s8(x0.y, xl.y, xh.y); s4x8_to_s8(x0.z, xl.z, xh.z); s4x8_to_s8(x0.w, xl.w, xh.w);
+        acci = __builtin_amdgcn_mfma_i32_16x16x64_i8(as_v4i(wl), as_v4i(xl), acci, 0, 0, 0);
+        acci = __builtin_amdgcn_mfma_i32_16x16x64_i8(as_v4i(wh), as_v4i(xh), acci, 0, 0, 0);
+        s4x8_to_s8(w1.x, wl.x, wh.x); s4x8_to_s8(w1.y, wl.y, wh.y); s4x8_to_s8(w1.z, wl.z, wh.z); s4x8_to_s8(w1.w, wl.w, wh.w);
+        s4x8_to_s8(x1.x, xl.x, xh.x); s4x8_to_s8(x1.y, xl.y, xh.y); s4x8_to_s8(x1.z, xl.z, xh.z); s4x8_to_s8(x1.w, xl.w, xh.w);
+        acci = __builtin_amdgcn_mfma_i32_16x16x64_i8(as_v4i(wl), as_v4i(xl), acci, 0, 0, 0);
+        acci = __builtin_amdgcn_mfma_i32_16x16x64_i8(as_v4i(wh), as_v4i(xh), acci, 0, 0, 0);
     } else if constexpr (F == FMT_G128A8) {
-        // b0/b1 already hold (q - z) as int8 (decoded once per step).
-        v4i A0 = {(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w};
-        v4i A1 = {(int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
-        v4i B0 = {(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w};
-        v4i B1 = {(int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
-        v4i zero = {0, 0, 0, 0};
-        v4i g = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0, B0, zero, 0, 0, 0);
-        g = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1, B1, g, 0, 0, 0);
-        accf[0] = __builtin_fmaf((float)g[0], gscale, accf[0]);
-        accf[1] = __builtin_fmaf((float)g[1], gscale, accf[1]);
-        accf[2] = __builtin_fmaf((float)g[2], gscale, accf[2]);
-        accf[3] = __builtin_fmaf((float)g[3], gscale, accf[3]);
-    } else {  // F16 and G128A16 (B already dequantized to halves)
-        v8h A0 = __builtin_bit_cast(v8h, a0), A1 = __builtin_bit_cast(v8h, a1);
-        v8h B0 = __builtin_bit_cast(v8h, b0), B1 = __builtin_bit_cast(v8h, b1);
-        accf = __builtin_amdgcn_mfma_f32_16x16x32_f16(A0, B0, accf, 0, 0, 0);
-        accf = __builtin_amdgcn_mfma_f32_16x16x32_f16(A1, B1, accf, 0, 0, 0);
+        // w0/w1 already hold (q - z) as int8 (decoded once per step); each
+        // 128-K group's exact int32 sum is scaled by its column's fp16 scale.
+        v4i g = __builtin_amdgcn_mfma_i32_16x16x64_i8(as_v4i(w0), as_v4i(x0), v4i{0, 0, 0, 0}, 0, 0, 0);
+        g = __builtin_amdgcn_mfma_i32_16x16x64_i8(as_v4i(w1), as_v4i(x1), g, 0, 0, 0);
+        accf[0] = __builtin_fmaf((float)g[0], gscale[0], accf[0]);
+        accf[1] = __builtin_fmaf((float)g[1], gscale[1], accf[1]);
+        accf[2] = __builtin_fmaf((float)g[2], gscale[2], accf[2]);
+        accf[3] = __builtin_fmaf((float)g[3], gscale[3], accf[3]);
+    } else {  // F16 and G128A16 (weights already dequantized to halves)
+        accf = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, w0), __builtin_bit_cast(v8h, x0), accf, 0, 0, 0);
+        accf = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, w1), __builtin_bit_cast(v8h, x1), accf, 0, 0, 0);
     }
 }
 
 // 16 bytes global -> LDS per lane (global_load_lds_dwordx4): lane l writes
-// LDS bytes [lds_addr + 16 l, + 16).  lds_addr must be wave-uniform.
+// LDS bytes [lds_addr + 16 l, + 16).  lds_addr must be wave-uniform.  Issued
+// from inline asm so that the compiler does not order every later LDS read
+// behind the load (it cannot tell the DMA target from the buffer being read);
+// the step loop waits for these loads explicitly.
 __device__ __forceinline__ void dma16(const void* src, uint32_t lds_addr) {
     asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(__builtin_amdgcn_readfirstlane(lds_addr))
                  : "memory", "m0");
-}
-
-// Orders this wave's LDS writes before its later LDS reads (and the reads
-// before the next writes) when lanes exchange data through LDS.
-// A wave's LDS instructions execute in order, so only the compiler must be
-// kept from reordering them (no global-memory fence, which would also wait
-// for the wave's outstanding global stores).
-__device__ __forceinline__ void wave_lds_sync() {
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    __builtin_amdgcn_wave_barrier();
-}
-
-// Epilogue: each wave stages 8 rows x 64 columns of fp32 accumulators per
-// pass through its own LDS slab so that lane l finishes columns
-// [8(l%8), 8(l%8)+8) of row l/8 with one contiguous store.  Column scales and
-// bias and the 16 row scales of the lane are loaded once per tile.
-template <int F, int E>
-__device__ __forceinline__ void epilogue(const GemmArgs& p, v4f (&accf)[8][4], v4i (&acci)[8][4], float* stage, int m0,
-                                         int n0, int wm, int wn, int lane) {
-    using T = FmtTraits<F>;
-    const int g = lane >> 4, l16 = lane & 15;
-    const int er = lane >> 3, ec = (lane & 7) * 8;
-    const int gcol = n0 + wn * 64 + ec;
-    const int ccol = min(gcol, p.n - 8);
-    float wsv[8], bsv[8], rsv[16];
-#pragma unroll
-    for (int j = 0; j < 8; j += 4) {
-        const float4 w4 = p.w_scales ? *(const float4*)(p.w_scales + ccol + j) : float4{1.f, 1.f, 1.f, 1.f};
-        const float4 b4 = p.bias ? *(const float4*)(p.bias + ccol + j) : float4{0.f, 0.f, 0.f, 0.f};
-        wsv[j] = w4.x; wsv[j + 1] = w4.y; wsv[j + 2] = w4.z; wsv[j + 3] = w4.w;
-        bsv[j] = b4.x; bsv[j + 1] = b4.y; bsv[j + 2] = b4.z; bsv[j + 3] = b4.w;
-    }
-#pragma unroll
-    for (int ps = 0; ps < 16; ++ps) {
-        const int row = min(m0 + wm * 128 + ps * 8 + er, p.m - 1);
-        rsv[ps] = p.row_scales ? p.row_scales[row] : p.in_scale;
-    }
-#pragma unroll
-    for (int ps = 0; ps < 16; ++ps) {
-        const int ai = ps >> 1, h = ps & 1;
-        if ((g >> 1) == h) {
-#pragma unroll
-            for (int bj = 0; bj < 4; ++bj)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    float v;
-                    if constexpr (T::kInt) {
-                        const int iv = acci[ai][bj][r];
-                        v = E == EPI_I32 ? __int_as_float(iv) : (float)iv;
-                    } else {
-                        v = accf[ai][bj][r];
-                    }
-                    stage[(4 * (g & 1) + r) * 68 + bj * 16 + l16] = v;
-                }
-        }
-        wave_lds_sync();
-        float v[8];
-        {
-            const float4 q0 = *(const float4*)(stage + er * 68 + ec);
-            const float4 q1 = *(const float4*)(stage + er * 68 + ec + 4);
-            v[0] = q0.x; v[1] = q0.y; v[2] = q0.z; v[3] = q0.w;
-            v[4] = q1.x; v[5] = q1.y; v[6] = q1.z; v[7] = q1.w;
-        }
-        wave_lds_sync();
-        const int grow = m0 + wm * 128 + ps * 8 + er;
-        if (grow >= p.m || gcol >= p.n) continue;
-
-        if constexpr (E == EPI_I32) {
-            int32_t* o = (int32_t*)p.out + (size_t)grow * p.ldo + gcol;
-            *(int4*)o = __builtin_bit_cast(int4, float4{v[0], v[1], v[2], v[3]});
-            *(int4*)(o + 4) = __builtin_bit_cast(int4, float4{v[4], v[5], v[6], v[7]});
-            continue;
-        }
-        const float rs = rsv[ps];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const float fused = __builtin_fmaf(v[j], rs * wsv[j], bsv[j]);
-            const float plain = v[j] * rs * wsv[j] + bsv[j];
-            v[j] = p.fused_scale ? fused : plain;
-        }
-        if constexpr (E == EPI_F32) {
-            float* o = (float*)p.out + (size_t)grow * p.ldo + gcol;
-            *(float4*)o = float4{v[0], v[1], v[2], v[3]};
-            *(float4*)(o + 4) = float4{v[4], v[5], v[6], v[7]};
-        } else if constexpr (E == EPI_F16) {
-            uint4 res = {0, 0, 0, 0};
-            if (p.residual) res = *(const uint4*)(p.residual + (size_t)grow * p.ldo + gcol);
-            const uint32_t rw[4] = {res.x, res.y, res.z, res.w};
-            const float rsc = p.residual ? p.res_scale : 0.0f;
-            uint32_t h[4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                float x0 = __builtin_fmaf(rsc, h2f((uint16_t)(rw[j] & 0xffff)), v[2 * j] * p.out_scale);
-                float x1 = __builtin_fmaf(rsc, h2f((uint16_t)(rw[j] >> 16)), v[2 * j + 1] * p.out_scale);
-                x0 = p.act == 1 ? silu(x0) : (p.act == 2 ? __builtin_fmaxf(x0, 0.0f) : x0);
-                x1 = p.act == 1 ? silu(x1) : (p.act == 2 ? __builtin_fmaxf(x1, 0.0f) : x1);
-                h[j] = (uint32_t)f2h(x0) | ((uint32_t)f2h(x1) << 16);
-            }
-            *(uint4*)((uint16_t*)p.out + (size_t)grow * p.ldo + gcol) = uint4{h[0], h[1], h[2], h[3]};
-        } else if constexpr (E == EPI_F8 || E == EPI_F8_24) {
-            uint32_t w[2];
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const float x0 = round_f16(silu(v[4 * j])) * 16.0f, x1 = round_f16(silu(v[4 * j + 1])) * 16.0f;
-                const float x2 = round_f16(silu(v[4 * j + 2])) * 16.0f, x3 = round_f16(silu(v[4 * j + 3])) * 16.0f;
-                w[j] = e4m3x2(x0, x1) | (e4m3x2(x2, x3) << 16);
-            }
-            if constexpr (E == EPI_F8) {
-                *(uint2*)((uint8_t*)p.out + (size_t)grow * p.ldo + gcol) = uint2{w[0], w[1]};
-            } else {
-                // encoder.cu:685-704: keep the two largest |e4m3| of each
-                // quartet (ties to the lower index), metadata idx0 | idx1 << 2.
-                uint32_t data = 0, meta = 0;
-#pragma unroll
-                for (int qd = 0; qd < 2; ++qd) {
-                    const uint32_t packed = w[qd];
-                    uint32_t d = 0, md = 0;
-                    int count = 0;
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const uint32_t mi = (packed >> (8 * i)) & 127;
-                        int rank = 0;
-#pragma unroll
-                        for (int j = 0; j < 4; ++j) {
-                            const uint32_t mj = (packed >> (8 * j)) & 127;
-                            rank += (mj > mi) || (mj == mi && j < i);
-                        }
-                        if (rank < 2) {
-                            d |= ((packed >> (8 * i)) & 255u) << (8 * count);
-                            md |= (uint32_t)i << (2 * count);
-                            ++count;
-                        }
-                    }
-                    data |= d << (16 * qd);
-                    meta |= md << (4 * qd);
-                }
-                *(uint32_t*)((uint8_t*)p.out + (size_t)grow * (p.ldo / 2) + gcol / 2) = data;
-                p.out_meta[(size_t)grow * (p.ldo / 8) + gcol / 8] = (uint8_t)meta;
-            }
-        }
-    }
 }
 
 // Persistent tile schedule.  The grid is one workgroup per CU (G of them);
 // iteration i of workgroup b computes logical tile i*G + slot(b).  Workgroups
 // are dispatched round-robin over the 8 XCDs, so slot() gives each XCD a
 // contiguous run of G/8 logical tiles per iteration; tiles are numbered N
-// fastest, so an XCD's concurrent tiles share one or two A row-strips and the
-// same B columns in its L2.
+// fastest, so an XCD's concurrent tiles share one or two activation row-strips
+// and the same weight columns in its L2.
 __device__ __forceinline__ int tile_slot(int G) {
     const int b = blockIdx.x;
     return (G & 7) == 0 ? (b & 7) * (G >> 3) + (b >> 3) : b;
 }
 
-template <int F> struct Layout {
-    static constexpr int kStage = kTileBytes + kBlockN * FmtTraits<F>::bRow;
-    static constexpr int kEpi = 2 * kStage;                      // epilogue staging
-    static constexpr int kEpiBytes = 8 * 8 * 68 * 4;              // 8 waves x 8 rows x 68 floats
-    static constexpr bool kG128 = (F == FMT_G128A8 || F == FMT_G128A16);
-    static constexpr int kGsz = kEpi + kEpiBytes;                  // g128 (scale, zero) table
-    static constexpr int kBytes = kGsz + (kG128 ? kMaxG128Groups * kBlockN * 4 : 0);
-};
+// e4m3 of 16 * fp16(SiLU(v)) for four values packed in a dword (the FF
+// expand epilogue, encoder.cu:1010-1025).  SiLU is >= -0.279, so clamping at
+// 28 (= 448 / 16) before the fp16 rounding is the reference's saturation;
+// v_cvt_scalef32_pk_fp8_f16 converts two fp16 values divided by its scale
+// operand (1/16 here) with round-to-nearest-even.
+__device__ __forceinline__ uint32_t silu_fp8x4(float a, float b, float c, float d) {
+    typedef short v2s __attribute__((ext_vector_type(2)));
+    const v2h h01 = {(_Float16)__builtin_fminf(silu(a), 28.0f), (_Float16)__builtin_fminf(silu(b), 28.0f)};
+    const v2h h23 = {(_Float16)__builtin_fminf(silu(c), 28.0f), (_Float16)__builtin_fminf(silu(d), 28.0f)};
+    v2s o = __builtin_amdgcn_cvt_scalef32_pk_fp8_f16(v2s{0, 0}, h01, 0.0625f, false);
+    o = __builtin_amdgcn_cvt_scalef32_pk_fp8_f16(o, h23, 0.0625f, true);
+    return __builtin_bit_cast(uint32_t, o);
+}
+
+// encoder.cu:685-704: of one quartet of e4m3 bytes keep the two largest
+// magnitudes (bits & 127, ties to the lower index) in index order.  Returns
+// the two kept bytes in bits 0-15 and idx0 | idx1 << 2 in bits 16-19.
+__device__ __forceinline__ uint32_t compress_quartet(uint32_t packed) {
+    uint32_t d = 0, md = 0;
+    int count = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t mi = (packed >> (8 * i)) & 127;
+        int rank = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t mj = (packed >> (8 * j)) & 127;
+            rank += (mj > mi) || (mj == mi && j < i);
+        }
+        if (rank < 2) {
+            d |= ((packed >> (8 * i)) & 255u) << (8 * count);
+            md |= (uint32_t)i << (2 * count);
+            ++count;
+        }
+    }
+    return d | (md << 16);
+}
+
+// Epilogue straight from the accumulators: for each of its 8 row blocks a
+// lane finishes columns [gcol, gcol + 16) of one row (16 contiguous outputs,
+// one to four 16-byte stores).  Column scales / bias and the 8 row scales are
+// loaded once per tile; a residual row is loaded one block ahead.
+template <int F, int E>
+__device__ __forceinline__ void epilogue(const GemmArgs& p, v4f (&accf)[8][4], v4i (&acci)[8][4], int m0, int n0, int wm,
+                                         int wn, int lane) {
+    using T = FmtTraits<F>;
+    const int g = lane >> 4, l16 = lane & 15;
+    const int gcol = n0 + wn * 64 + g * 16;
+    const int ccol = min(gcol, p.n - 16);
+    const bool col_live = gcol < p.n;
+    float wsv[16], bsv[16], rsv[8];
+    if constexpr (E != EPI_I32) {
+#pragma unroll
+        for (int j = 0; j < 16; j += 4) {
+            const float4 w4 = p.w_scales ? *(const float4*)(p.w_scales + ccol + j) : float4{1.f, 1.f, 1.f, 1.f};
+            const float4 b4 = p.bias ? *(const float4*)(p.bias + ccol + j) : float4{0.f, 0.f, 0.f, 0.f};
+            wsv[j] = w4.x; wsv[j + 1] = w4.y; wsv[j + 2] = w4.z; wsv[j + 3] = w4.w;
+            bsv[j] = b4.x; bsv[j + 1] = b4.y; bsv[j + 2] = b4.z; bsv[j + 3] = b4.w;
+        }
+#pragma unroll
+        for (int ai = 0; ai < 8; ++ai) {
+            const int row = min(m0 + wm * 128 + ai * 16 + l16, p.m - 1);
+            rsv[ai] = p.row_scales ? p.row_scales[row] : p.in_scale;
+        }
+    }
+    // Retire the scale loads once here; a wait for them inside the block loop
+    // would also wait for the previous block's stores.
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+    auto row_of = [&](int ai) { return min(m0 + wm * 128 + ai * 16 + l16, p.m - 1); };
+    // Without a residual the loads read the (same-shaped) output instead and
+    // a select discards them, keeping the block loop free of branches.
+    const uint16_t* res_src = p.residual ? p.residual : (const uint16_t*)p.out;
+    const bool has_res = p.residual != nullptr;
+    uint4 rn0 = {0, 0, 0, 0}, rn1 = {0, 0, 0, 0};
+    if constexpr (E == EPI_F16) {
+        const uint4* rp = (const uint4*)(res_src + (size_t)row_of(0) * p.ldo + ccol);
+        rn0 = rp[0];
+        rn1 = rp[1];
+    }
+#pragma unroll
+    for (int ai = 0; ai < 8; ++ai) {
+        const int grow = m0 + wm * 128 + ai * 16 + l16;
+        const bool live = grow < p.m && col_live;
+        float v[16];
+        if constexpr (E == EPI_I32) {
+            if (live) {
+                int4* o = (int4*)((int32_t*)p.out + (size_t)grow * p.ldo + gcol);
+#pragma unroll
+                for (int bj = 0; bj < 4; ++bj) o[bj] = int4{acci[ai][bj][0], acci[ai][bj][1], acci[ai][bj][2], acci[ai][bj][3]};
+            }
+            continue;
+        } else {
+#pragma unroll
+            for (int bj = 0; bj < 4; ++bj)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) v[bj * 4 + r] = T::kInt ? (float)acci[ai][bj][r] : accf[ai][bj][r];
+        }
+        const float rs = rsv[ai];
+        if (p.fused_scale) {
+#pragma unroll
+            for (int j = 0; j < 16; ++j) v[j] = __builtin_fmaf(v[j], rs * wsv[j], bsv[j]);
+        } else {
+#pragma unroll
+            for (int j = 0; j < 16; ++j) v[j] = __builtin_fmaf(v[j] * rs, wsv[j], bsv[j]);
+        }
+        if constexpr (E == EPI_F32) {
+            if (live) {
+                float4* o = (float4*)((float*)p.out + (size_t)grow * p.ldo + gcol);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) o[j] = float4{v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]};
+            }
+        } else if constexpr (E == EPI_F16) {
+            const uint4 r0 = rn0, r1 = rn1;
+            if (ai + 1 < 8) {
+                const uint4* rp = (const uint4*)(res_src + (size_t)row_of(ai + 1) * p.ldo + ccol);
+                rn0 = rp[0];
+                rn1 = rp[1];
+            }
+            const uint32_t rw[8] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
+            uint32_t h[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float y0 = v[2 * j] * p.out_scale, y1 = v[2 * j + 1] * p.out_scale;
+                float x0 = has_res ? __builtin_fmaf(p.res_scale, h2f((uint16_t)(rw[j] & 0xffff)), y0) : y0;
+                float x1 = has_res ? __builtin_fmaf(p.res_scale, h2f((uint16_t)(rw[j] >> 16)), y1) : y1;
+                x0 = p.act == 1 ? silu(x0) : (p.act == 2 ? __builtin_fmaxf(x0, 0.0f) : x0);
+                x1 = p.act == 1 ? silu(x1) : (p.act == 2 ? __builtin_fmaxf(x1, 0.0f) : x1);
+                h[j] = (uint32_t)f2h(x0) | ((uint32_t)f2h(x1) << 16);
+            }
+            if (live) {
+                uint4* o = (uint4*)((uint16_t*)p.out + (size_t)grow * p.ldo + gcol);
+                o[0] = uint4{h[0], h[1], h[2], h[3]};
+                o[1] = uint4{h[4], h[5], h[6], h[7]};
+            }
+        } else {  // EPI_F8, EPI_F8_24
+            uint32_t w[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) w[j] = silu_fp8x4(v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]);
+            if constexpr (E == EPI_F8) {
+                if (live) *(uint4*)((uint8_t*)p.out + (size_t)grow * p.ldo + gcol) = uint4{w[0], w[1], w[2], w[3]};
+            } else {
+                uint32_t c[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) c[j] = compress_quartet(w[j]);
+                if (live) {
+                    const uint32_t d0 = (c[0] & 0xffff) | (c[1] << 16), d1 = (c[2] & 0xffff) | (c[3] << 16);
+                    const uint32_t meta = (c[0] >> 16) | ((c[1] >> 16) << 4) | ((c[2] >> 16) << 8) | ((c[3] >> 16) << 12);
+                    *(uint2*)((uint8_t*)p.out + (size_t)grow * (p.ldo / 2) + gcol / 2) = uint2{d0, d1};
+                    *(uint16_t*)(p.out_meta + (size_t)grow * (p.ldo / 8) + gcol / 8) = (uint16_t)meta;
+                }
+            }
+        }
+    }
+}
+
+
+// Output bytes per element of an epilogue.
+template <int E> struct EpiBytes { static constexpr int v = (E == EPI_F8 || E == EPI_F8_24) ? 1 : (E == EPI_F16 ? 2 : 4); };
+
+// Epilogue through LDS for outputs without a residual: the waves convert
+// their accumulators to output bytes and place them in the stage buffer the
+// last K-step has just released (64 KiB: the whole 256x256 tile of fp8, half
+// of fp16, a quarter of fp32 per pass); then all 512 threads store whole row
+// segments, so one wave instruction writes four rows x 256 bytes of fp8.  16-
+// byte chunks of a staged row are XOR-swizzled by (row & 15).
+template <int F, int E>
+__device__ __forceinline__ void epilogue_staged(const GemmArgs& p, v4f (&accf)[8][4], v4i (&acci)[8][4], uint8_t* sbuf, int m0,
+                                                int n0, int wm, int wn, int lane, int tid) {
+    using T = FmtTraits<F>;
+    constexpr int eb = EpiBytes<E>::v;
+    static_assert(eb <= 2, "fp32 / int32 outputs use the register epilogue");
+    constexpr int kRows = 256 / eb;          // rows staged per pass
+    constexpr int kChunks = 16 * eb;         // 16-byte chunks per staged row (full width)
+    const int g = lane >> 4, l16 = lane & 15;
+    const int lcol = wn * 64 + g * 16;       // first of the lane's 16 columns within the tile
+    const int gcol = n0 + lcol;
+    const int ccol = min(gcol, p.n - 16);
+    float wsv[16], bsv[16], rsv[8];
+    if constexpr (E != EPI_I32) {
+#pragma unroll
+        for (int j = 0; j < 16; j += 4) {
+            const float4 w4 = p.w_scales ? *(const float4*)(p.w_scales + ccol + j) : float4{1.f, 1.f, 1.f, 1.f};
+            const float4 b4 = p.bias ? *(const float4*)(p.bias + ccol + j) : float4{0.f, 0.f, 0.f, 0.f};
+            wsv[j] = w4.x; wsv[j + 1] = w4.y; wsv[j + 2] = w4.z; wsv[j + 3] = w4.w;
+            bsv[j] = b4.x; bsv[j + 1] = b4.y; bsv[j + 2] = b4.z; bsv[j + 3] = b4.w;
+        }
+#pragma unroll
+        for (int ai = 0; ai < 8; ++ai) {
+            const int row = min(m0 + wm * 128 + ai * 16 + l16, p.m - 1);
+            rsv[ai] = p.row_scales ? p.row_scales[row] : p.in_scale;
+        }
+    }
+    const int ntile_cols = min(256, p.n - n0);  // multiple of 16
+#pragma unroll
+    for (int pass = 0; pass < eb; ++pass) {
+        __syncthreads();  // the previous pass's stores have read the staging area
+        // fp8: one pass, every wave; fp16: pass 0 = waves 0-3, pass 1 = 4-7
+        if (eb == 2 && wm != pass) goto staged_store;
+#pragma unroll
+        for (int ai = 0; ai < 8; ++ai) {
+            const int srow = (eb == 2 ? 0 : wm * 128) + ai * 16 + l16;
+            uint8_t* dst = sbuf + srow * (kChunks * 16);
+            auto put = [&](int chunk, uint4 val) { *(uint4*)(dst + ((chunk ^ (srow & 15)) << 4)) = val; };
+            if constexpr (E == EPI_I32) {
+#pragma unroll
+                for (int bj = 0; bj < 4; ++bj)
+                    put(lcol / 4 + bj, uint4{(uint32_t)acci[ai][bj][0], (uint32_t)acci[ai][bj][1], (uint32_t)acci[ai][bj][2], (uint32_t)acci[ai][bj][3]});
+                continue;
+            } else {
+                float v[16];
+#pragma unroll
+                for (int bj = 0; bj < 4; ++bj)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) v[bj * 4 + r] = T::kInt ? (float)acci[ai][bj][r] : accf[ai][bj][r];
+                const float rs = rsv[ai];
+                if (p.fused_scale) {
+#pragma unroll
+                    for (int j = 0; j < 16; ++j) v[j] = __builtin_fmaf(v[j], rs * wsv[j], bsv[j]);
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 16; ++j) v[j] = __builtin_fmaf(v[j] * rs, wsv[j], bsv[j]);
+                }
+                if constexpr (E == EPI_F32) {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        put(lcol / 4 + j, __builtin_bit_cast(uint4, float4{v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]}));
+                } else if constexpr (E == EPI_F16) {
+                    uint32_t h[8];
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        float x0 = v[2 * j] * p.out_scale, x1 = v[2 * j + 1] * p.out_scale;
+                        x0 = p.act == 1 ? silu(x0) : (p.act == 2 ? __builtin_fmaxf(x0, 0.0f) : x0);
+                        x1 = p.act == 1 ? silu(x1) : (p.act == 2 ? __builtin_fmaxf(x1, 0.0f) : x1);
+                        h[j] = (uint32_t)f2h(x0) | ((uint32_t)f2h(x1) << 16);
+                    }
+                    put(lcol / 8, uint4{h[0], h[1], h[2], h[3]});
+                    put(lcol / 8 + 1, uint4{h[4], h[5], h[6], h[7]});
+                } else {
+                    uint32_t w[4];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) w[j] = silu_fp8x4(v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]);
+                    if constexpr (E == EPI_F8) {
+                        put(lcol / 16, uint4{w[0], w[1], w[2], w[3]});
+                    } else {
+                        // 2:4 compressed: 8 data bytes at lcol/2 of a 128-byte
+                        // data row, 2 metadata bytes at lcol/8 of a 32-byte row
+                        // placed after the 32 KiB of data rows.
+                        uint32_t c[4];
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) c[j] = compress_quartet(w[j]);
+                        const uint32_t d0 = (c[0] & 0xffff) | (c[1] << 16), d1 = (c[2] & 0xffff) | (c[3] << 16);
+                        const uint32_t meta = (c[0] >> 16) | ((c[1] >> 16) << 4) | ((c[2] >> 16) << 8) | ((c[3] >> 16) << 12);
+                        uint8_t* drow = sbuf + srow * 128;
+                        const int dchunk = lcol >> 5, dhalf = (lcol >> 4) & 1;
+                        *(uint2*)(drow + ((dchunk ^ (srow & 7)) << 4) + dhalf * 8) = uint2{d0, d1};
+                        *(uint16_t*)(sbuf + 32768 + srow * 32 + lcol / 8) = (uint16_t)meta;
+                    }
+                }
+            }
+        }
+    staged_store:
+        __syncthreads();
+        // Store phase: chunk q of the pass is row q / row_chunks, 16-byte
+        // column chunk q % row_chunks; rows past M and columns past N drop.
+        if constexpr (E == EPI_F8_24) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int q = i * kThreads + tid, row = q >> 3, c = q & 7;
+                const int grow = m0 + row;
+                if (grow < p.m && c * 32 < ntile_cols)
+                    *(uint4*)((uint8_t*)p.out + (size_t)grow * (p.ldo / 2) + n0 / 2 + c * 16) =
+                        *(const uint4*)(sbuf + row * 128 + ((c ^ (row & 7)) << 4));
+            }
+            {
+                const int row = tid >> 1, c = tid & 1;
+                const int grow = m0 + row;
+                if (grow < p.m && c * 128 < ntile_cols) {
+                    const uint4 mv = *(const uint4*)(sbuf + 32768 + row * 32 + c * 16);
+                    uint8_t* md = p.out_meta + (size_t)grow * (p.ldo / 8) + n0 / 8 + c * 16;
+                    if (ntile_cols - c * 128 >= 128) *(uint4*)md = mv;
+                    else {
+                        const uint8_t* mb = (const uint8_t*)&mv;
+                        for (int j = 0; j < (ntile_cols - c * 128) / 8; ++j) md[j] = mb[j];
+                    }
+                }
+            }
+        } else {
+            constexpr int kIters = kRows * kChunks / kThreads;
+#pragma unroll
+            for (int i = 0; i < kIters; ++i) {
+                const int q = i * kThreads + tid, row = q / kChunks, c = q % kChunks;
+                const int grow = m0 + pass * kRows + row;
+                if (grow < p.m && c * (16 / eb) < ntile_cols)
+                    *(uint4*)((uint8_t*)p.out + ((size_t)grow * p.ldo + n0) * eb + c * 16) =
+                        *(const uint4*)(sbuf + row * (kChunks * 16) + ((c ^ (row & 15)) << 4));
+            }
+        }
+    }
+}
 
 template <int F, int E>
 __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs p) {
@@ -332,19 +491,19 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs p) {
     const int tiles_n = (p.n + kBlockN - 1) / kBlockN;
     const int ntiles = ((p.m + kBlockM - 1) / kBlockM) * tiles_n;
     const int G = gridDim.x;
-    const int slot = tile_slot(G);
-    const size_t lda = (size_t)p.k * T::aElemNum / T::aElemDen;  // bytes per A row
-    const size_t ldb = (size_t)p.k * T::bNum / T::bDen;          // bytes per B row
+    const size_t lda = (size_t)p.k * T::aElemNum / T::aElemDen;  // bytes per activation row
+    const size_t ldb = (size_t)p.k * T::bNum / T::bDen;          // bytes per weight row
     const int steps = p.k / T::kStep;
     const int groups = p.k >> 7;
     const uint8_t* __restrict__ pa = p.a;
     const uint8_t* __restrict__ pb = p.b;
     const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)lds;
-    uint32_t* gsz = (uint32_t*)(lds + L::kGsz);
+    float* g_scale = (float*)(lds + L::kScales);
+    uint8_t* g_zero = lds + L::kZeros;
 
-    // Direct-to-LDS operand loads (global_load_lds_dwordx4): one wave
-    // instruction fills 1 KiB of LDS, lane l writing bytes [16l, 16l+16), so
-    // each lane loads the global chunk the swizzled layout puts there.
+    // Direct-to-LDS loads: one wave instruction fills 1 KiB of LDS, lane l
+    // writing bytes [16l, 16l+16), so each lane loads the global chunk the
+    // swizzled layout puts there.
     constexpr int kBLoadsPerWave = (kBlockN * T::bRow) / 1024 / 8;
     uint32_t a_off[4], b_off[kBLoadsPerWave];
     auto set_tile = [&](int t, int& m0, int& n0) {
@@ -371,9 +530,6 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs p) {
             b_off[i] = (uint32_t)((size_t)min(n0 + row, p.n - 1) * ldb + c * 16);
         }
     };
-    // The loads are issued from inline asm so that the compiler does not order
-    // every later LDS read behind them (it cannot tell the DMA target from the
-    // buffer being read); the step loop waits for them explicitly.
     auto issue = [&](int step, int buf) {
         const uint32_t base = lds_base + buf * L::kStage;
 #pragma unroll
@@ -383,7 +539,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs p) {
             dma16(pb + b_off[i] + (size_t)step * T::bRow, base + kTileBytes + (wave * kBLoadsPerWave + i) * 1024);
     };
 
-    int t = slot;
+    int t = tile_slot(G);
     if (t >= ntiles) return;
     int m0, n0;
     set_tile(t, m0, n0);
@@ -392,7 +548,6 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs p) {
 
     v4f accf[8][4];
     v4i acci[8][4];
-    float* stage = (float*)(lds + L::kEpi + wave * (8 * 68 * 4));
 
     while (true) {
         const int t_next = t + G;
@@ -414,9 +569,10 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs p) {
             if constexpr (L::kG128) {
                 if (step == 0) {
                     for (int idx = tid; idx < kBlockN * groups; idx += kThreads) {
-                        const int col = idx / groups, grp = idx - col * groups;
+                        const int grp = idx >> 8, col = idx & 255;
                         const size_t gi = (size_t)min(cur_n0 + col, p.n - 1) * groups + grp;
-                        gsz[idx] = (uint32_t)p.g_scales[gi] | ((uint32_t)p.g_zeros[gi] << 16);
+                        g_scale[idx] = h2f(p.g_scales[gi]);
+                        g_zero[idx] = (uint8_t)(int)h2f(p.g_zeros[gi]);
                     }
                     __syncthreads();
                 }
@@ -429,54 +585,58 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs p) {
             }
             const uint8_t* As = lds + buf * L::kStage;
             const uint8_t* Bs = As + kTileBytes;
-            const int n0 = cur_n0;
-            (void)n0;
 
-            // Decode this wave's four B fragments.
-            uint4 b0[4], b1[4];
-            float gs[4] = {1.f, 1.f, 1.f, 1.f};
-    #pragma unroll
+            // This wave's four weight fragments for the step.
+            uint4 w0[4], w1[4];
+            v4f gs[4];
+#pragma unroll
             for (int bj = 0; bj < 4; ++bj) {
-                const int row = wn * 64 + bj * 16 + l16;
+                const int row = wn * 64 + wrow(l16, bj);
+                gs[bj] = v4f{1.f, 1.f, 1.f, 1.f};
                 if constexpr (T::bRow == 128) {
-                    b0[bj] = *(const uint4*)(Bs + swz(row, g));
-                    b1[bj] = *(const uint4*)(Bs + swz(row, 4 + g));
+                    w0[bj] = *(const uint4*)(Bs + swz(row, g));
+                    w1[bj] = *(const uint4*)(Bs + swz(row, 4 + g));
                 } else {
                     const int kg = (step * T::kStep) >> 7;
-                    const uint32_t sz = gsz[row * groups + kg];
-                    const float z = h2f((uint16_t)(sz >> 16));
+                    const int z = g_zero[kg * kBlockN + row];
                     if constexpr (F == FMT_G128A8) {
-                        gs[bj] = h2f((uint16_t)(sz & 0xffff));
-                        const uint32_t zz = (uint32_t)(int)z * 0x01010101u;
-                        const uint2 w0 = *(const uint2*)(Bs + row * 64 + 8 * g);
-                        const uint2 w1 = *(const uint2*)(Bs + row * 64 + 32 + 8 * g);
-                        u4x8_minus_z(w0.x, zz, b0[bj].x, b0[bj].y);
-                        u4x8_minus_z(w0.y, zz, b0[bj].z, b0[bj].w);
-                        u4x8_minus_z(w1.x, zz, b1[bj].x, b1[bj].y);
-                        u4x8_minus_z(w1.y, zz, b1[bj].z, b1[bj].w);
+                        // the accumulators of block bj hold columns 16g + 4bj + r
+                        gs[bj] = *(const v4f*)(g_scale + kg * kBlockN + wn * 64 + g * 16 + bj * 4);
+                        const uint32_t zz = (uint32_t)z * 0x01010101u;
+                        const uint2 q0 = *(const uint2*)(Bs + row * 64 + 8 * g);
+                        const uint2 q1 = *(const uint2*)(Bs + row * 64 + 32 + 8 * g);
+                        u4x8_minus_z(q0.x, zz, w0[bj].x, w0[bj].y);
+                        u4x8_minus_z(q0.y, zz, w0[bj].z, w0[bj].w);
+                        u4x8_minus_z(q1.x, zz, w1[bj].x, w1[bj].y);
+                        u4x8_minus_z(q1.y, zz, w1[bj].z, w1[bj].w);
                     } else {  // G128A16
-                        const _Float16 s = __builtin_bit_cast(_Float16, (uint16_t)(sz & 0xffff));
-                        const _Float16 zh = (_Float16)(1024.0f + z);
+                        const _Float16 s = (_Float16)g_scale[kg * kBlockN + row];
+                        const _Float16 zh = (_Float16)(1024 + z);
                         const v2h ss = {s, s}, zz = {zh, zh};
-                        const uint32_t w0 = *(const uint32_t*)(Bs + row * 32 + 4 * g);
-                        const uint32_t w1 = *(const uint32_t*)(Bs + row * 32 + 16 + 4 * g);
-                        b0[bj] = __builtin_bit_cast(uint4, u4x8_to_h(w0, zz, ss));
-                        b1[bj] = __builtin_bit_cast(uint4, u4x8_to_h(w1, zz, ss));
+                        const uint32_t q0 = *(const uint32_t*)(Bs + row * 32 + 4 * g);
+                        const uint32_t q1 = *(const uint32_t*)(Bs + row * 32 + 16 + 4 * g);
+                        w0[bj] = __builtin_bit_cast(uint4, u4x8_to_h(q0, zz, ss));
+                        w1[bj] = __builtin_bit_cast(uint4, u4x8_to_h(q1, zz, ss));
                     }
                 }
             }
 #pragma unroll
             for (int ai = 0; ai < 8; ++ai) {
                 const int row = wm * 128 + ai * 16 + l16;
-                const uint4 a0 = *(const uint4*)(As + swz(row, g));
-                const uint4 a1 = *(const uint4*)(As + swz(row, 4 + g));
+                const uint4 x0 = *(const uint4*)(As + swz(row, g));
+                const uint4 x1 = *(const uint4*)(As + swz(row, 4 + g));
 #pragma unroll
-                for (int bj = 0; bj < 4; ++bj) mfma_step<F>(accf[ai][bj], acci[ai][bj], a0, a1, b0[bj], b1[bj], gs[bj]);
+                for (int bj = 0; bj < 4; ++bj) mfma_step<F>(accf[ai][bj], acci[ai][bj], w0[bj], w1[bj], x0, x1, gs[bj]);
             }
             buf ^= 1;
         }
 
-        epilogue<F, E>(p, accf, acci, stage, cur_m0, cur_n0, wm, wn, lane);
+        // Outputs without a residual go through the stage buffer the last
+        // K-step has released (buf ^ 1 after the final flip); the next tile's
+        // first step is already loading into the other buffer.
+        if constexpr (E == EPI_F16_RES) epilogue<F, EPI_F16>(p, accf, acci, cur_m0, cur_n0, wm, wn, lane);
+        else if constexpr (E == EPI_F32 || E == EPI_I32) epilogue<F, E>(p, accf, acci, cur_m0, cur_n0, wm, wn, lane);
+        else epilogue_staged<F, E>(p, accf, acci, lds + (buf ^ 1) * L::kStage, cur_m0, cur_n0, wm, wn, lane, tid);
         if (t_next >= ntiles) break;
         t = t_next;
     }

@@ -14,7 +14,7 @@ import ctypes
 import os
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(os.path.dirname(HERE), "build", "libpk_linear.so")
+LIB_PATH = os.environ.get("PK_LINEAR_LIB") or os.path.join(os.path.dirname(HERE), "build", "libpk_linear.so")
 
 P = ctypes.c_void_p
 I = ctypes.c_int32
