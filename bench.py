@@ -255,6 +255,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--frames", type=int, default=T)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only-dominant", action="store_true",
+                    help="run only the dominant kernel (20 launches) and a 256 MiB device copy, "
+                         "for rocprofv3 counter passes")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -268,6 +271,16 @@ def main():
 
     torch.cuda.set_device(0)
     stream = torch.cuda.current_stream()
+    if args.only_dominant:
+        k_ms, _, k_bytes = dominant_kernel(pk, torch, args.frames, stream)
+        src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"dominant_avg_ms": k_ms, "algorithmic_bytes": k_bytes,
+                          "copy_bytes": 256 << 20}), flush=True)
+        return
     plan = format_plan()
     print(f"[bench] building stack T={args.frames}", file=sys.stderr, flush=True)
     stack = Stack(pk, torch, args.frames, plan)

@@ -171,12 +171,18 @@ __device__ __forceinline__ void dma16(const void* src, uint32_t lds_addr) {
 // Persistent tile schedule.  The grid is one workgroup per CU (G of them);
 // iteration i of workgroup b computes logical tile i*G + slot(b).  Workgroups
 // are dispatched round-robin over the 8 XCDs, so slot() gives each XCD a
-// contiguous run of G/8 logical tiles per iteration; tiles are numbered N
-// fastest, so an XCD's concurrent tiles share one or two activation row-strips
-// and the same weight columns in its L2.
+// contiguous run of G/8 logical tiles per iteration.  Logical tiles are
+// ordered by groups of GW weight column-tiles, then by activation row-strip,
+// then by column-tile within the group, so one XCD's run covers G/8/GW row
+// strips of one column group, and its next runs keep the same weight columns
+// (L2-resident) while sweeping new rows.
 __device__ __forceinline__ int tile_slot(int G) {
     const int b = blockIdx.x;
     return (G & 7) == 0 ? (b & 7) * (G >> 3) + (b >> 3) : b;
+}
+
+__device__ __forceinline__ int group_width(int tiles_n) {
+    return (tiles_n & 7) == 0 ? 8 : ((tiles_n & 3) == 0 ? 4 : ((tiles_n & 1) == 0 ? 2 : 1));
 }
 
 // e4m3 of 16 * fp16(SiLU(v)) for four values packed in a dword (the FF
@@ -506,10 +512,14 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs p) {
     // swizzled layout puts there.
     constexpr int kBLoadsPerWave = (kBlockN * T::bRow) / 1024 / 8;
     uint32_t a_off[4], b_off[kBLoadsPerWave];
+    const int tiles_m = (p.m + kBlockM - 1) / kBlockM;
+    const int gw = group_width(tiles_n);
     auto set_tile = [&](int t, int& m0, int& n0) {
-        const int tm = t / tiles_n;
+        const int ng = t / (tiles_m * gw);
+        const int r = t - ng * tiles_m * gw;
+        const int tm = r / gw;
         m0 = tm * kBlockM;
-        n0 = (t - tm * tiles_n) * kBlockN;
+        n0 = (ng * gw + (r - tm * gw)) * kBlockN;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int o = (wave * 4 + i) * 1024 + lane * 16;
