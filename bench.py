@@ -156,6 +156,18 @@ def dominant_kernel(pk, torch, t, stream, reps=20):
     return ms, flops, nbytes
 
 
+def measured_traffic():
+    """HBM bytes per launch of the dominant kernel from the committed rocprofv3
+    counter summary (FETCH_SIZE + WRITE_SIZE, copy-calibrated), or None."""
+    path = os.path.join(ROOT, "profiles", "gemm_fp8_ff1_expand_T45000_traffic.txt")
+    try:
+        with open(path) as f:
+            kv = dict(line.strip().split("=", 1) for line in f if "=" in line and not line.startswith("#"))
+        return int(kv["traffic_bytes"])
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def joint_bench(pk, torch, stream, reps=2000):
     """Batch-1 INT8 joint GEMV 640 -> 1030 (+ decision), one launch per frame."""
     dev = "cuda"
@@ -327,7 +339,7 @@ def main():
                        "bytes_per_step": j_bytes, "pct_hbm": round(100.0 * j_gbs / 8000.0, 3)},
         "roofline": {"kernel": "gemm_kernel<FP8, EPI_F8> (FF1 expand 1024->4096, T=45000)",
                      "bound": "mfma", "achieved": round(k_tflops, 2), "peak": PEAK["fp8"],
-                     "unit": "TFLOP/s", "frac": round(k_tflops / PEAK["fp8"], 4), "traffic": None,
+                     "unit": "TFLOP/s", "frac": round(k_tflops / PEAK["fp8"], 4), "traffic": measured_traffic(),
                      "avg_ms": round(k_ms, 4), "algorithmic_bytes": k_bytes},
         "cpu_baseline": cpu,
         "wall_s_timed": round(wall, 3),
