@@ -199,6 +199,35 @@ int32_t pk_conv_residual_fp8(const uint8_t* input, const uint8_t* weight, const 
 int32_t pk_attention_output_fp8(const uint8_t* input, const uint8_t* weight, const float* weight_scales,
                                 uint16_t* output, int32_t rows, void* stream);
 
+/* encoder.cu:1121-1127 pk_sm89_conv_glu_fp8: pointwise1 1024 -> 2048 (weight
+ * [2048 x 1024] natural row order, scales [2048]) with dynamic per-row input
+ * scales, then GLU: out[r, c] = fp16(v) / (1 + exp(-fp16(g))) with v, g the
+ * scaled fp16-rounded outputs c and c + 1024; rows >= valid_rows are written
+ * as 0.  output is fp16 [rows x 1024]. */
+int32_t pk_conv_glu_fp8(const uint8_t* input, const uint8_t* weight, const float* weight_scales,
+                        const float* input_scales, uint16_t* output, int32_t rows, int32_t valid_rows, void* stream);
+/* encoder.cu:1105-1111 pk_sm89_subsample_projection_fp8: 4096 -> 1024 + bias,
+ * dynamic per-row input scales, fp16 out (subsampling.rs:436-806 caller). */
+int32_t pk_subsample_projection_fp8(const uint8_t* input, const uint8_t* weight, const float* weight_scales,
+                                    const float* input_scales, const float* bias, uint16_t* output, int32_t rows,
+                                    void* stream);
+/* encoder.cu:1113-1119 pk_sm89_subsample_pointwise_fp8: 256 -> 256 + bias, ReLU. */
+int32_t pk_subsample_pointwise_fp8(const uint8_t* input, const uint8_t* weight, const float* weight_scales,
+                                   const float* input_scales, const float* bias, uint16_t* output, int32_t rows,
+                                   void* stream);
+
+/* Activation-sparse FF2 contract (the reference's sparse
+ * FF2 is the 2:4 path, encoder.cu:1087-1095): INT8 activations [rows x 4096]
+ * with per-row scales (zeros where the frame's activations were dropped) x
+ * per-row INT8 weights [1024 x 4096] -> fp32 [rows x 1024],
+ * out = (acc * input_scale[r]) * weight_scale[n].  Every 16-row x 128-K
+ * activation block whose bytes are all zero skips its MFMAs (wave ballot),
+ * which is exact.  skip_counts (device uint32[2], may be NULL) accumulates
+ * {skipped blocks, total blocks}; the caller clears it. */
+int32_t pk_ffn_contract_int8_rowskip(const int8_t* input, const float* input_scales, const int8_t* weight,
+                                     const float* weight_scales, float* output, int32_t rows, uint32_t* skip_counts,
+                                     void* stream);
+
 /* ---- generic fused GEMM ------------------------------------------------------
  * format: 0 FP8, 1 INT8, 2 INT4 (s4 x s4), 3 INT4-g128 x INT8, 4 FP16,
  * 5 INT4-g128 x FP16.  epilogue: 0 fp16 (act(v [+bias]) * out_scale

@@ -346,6 +346,48 @@ int32_t pk_attention_output_fp8(const uint8_t* in, const uint8_t* w, const float
     return scaled_linear(FMT_FP8, EPI_F16, in, nullptr, 1.0f / 28.0f, 0, w, ws, nullptr, out, 1.0f, 0, out, rows, 1024, 1024, stream);
 }
 
+int32_t pk_conv_glu_fp8(const uint8_t* in, const uint8_t* w, const float* ws, const float* in_scales, uint16_t* out, int32_t rows,
+                        int32_t valid_rows, void* stream) {
+    if (!need(in, "input") || !need(w, "weight") || !need(ws, "weight_scales") || !need(in_scales, "input_scales") ||
+        !need(out, "output"))
+        return PK_E_ARG;
+    if (rows < 0 || valid_rows < 0 || valid_rows > rows) { set_error("need 0 <= valid_rows <= rows"); return PK_E_SHAPE; }
+    GemmArgs g = base_args(in, w, rows, 2048, 1024, out, 1024);
+    g.w_scales = ws;
+    g.row_scales = in_scales;
+    g.valid_rows = valid_rows;
+    return launch_gemm(FMT_FP8, EPI_GLU, g, STREAM);
+}
+
+static int32_t subsample_linear(const uint8_t* in, const uint8_t* w, const float* ws, const float* in_scales, const float* bias,
+                                uint16_t* out, int32_t rows, int32_t n, int32_t k, int32_t act, void* stream) {
+    if (!need(ws, "weight_scales") || !need(in_scales, "input_scales") || !need(bias, "bias")) return PK_E_ARG;
+    return scaled_linear(FMT_FP8, EPI_F16, in, in_scales, 1.0f, 0, w, ws, bias, nullptr, 1.0f, act, out, rows, n, k, stream);
+}
+
+int32_t pk_subsample_projection_fp8(const uint8_t* in, const uint8_t* w, const float* ws, const float* in_scales, const float* bias,
+                                    uint16_t* out, int32_t rows, void* stream) {
+    return subsample_linear(in, w, ws, in_scales, bias, out, rows, 1024, 4096, 0, stream);
+}
+
+int32_t pk_subsample_pointwise_fp8(const uint8_t* in, const uint8_t* w, const float* ws, const float* in_scales, const float* bias,
+                                   uint16_t* out, int32_t rows, void* stream) {
+    return subsample_linear(in, w, ws, in_scales, bias, out, rows, 256, 256, 2, stream);
+}
+
+int32_t pk_ffn_contract_int8_rowskip(const int8_t* in, const float* in_scales, const int8_t* w, const float* ws, float* out,
+                                     int32_t rows, uint32_t* skip_counts, void* stream) {
+    if (!need(in, "input") || !need(in_scales, "input_scales") || !need(w, "weight") || !need(ws, "weight_scales") ||
+        !need(out, "output"))
+        return PK_E_ARG;
+    if (rows < 0) { set_error("negative rows"); return PK_E_SHAPE; }
+    GemmArgs g = base_args(in, w, rows, 1024, 4096, out, 1024);
+    g.w_scales = ws;
+    g.row_scales = in_scales;
+    g.skip_count = skip_counts;
+    return launch_gemm(FMT_I8_SKIP, EPI_F32, g, STREAM);
+}
+
 // ---- joint ------------------------------------------------------------------------
 
 int32_t pk_joint_gemv(const void* w, int32_t w_int8, const float* w_scales, const float* bias, const uint16_t* enc, const float* pred,

@@ -47,7 +47,16 @@ static int by_epi(int epi, const GemmArgs& a, hipStream_t s) {
     case EPI_F8: return launch_one<F, EPI_F8>(a, s);
     case EPI_F8_24: return launch_one<F, EPI_F8_24>(a, s);
     case EPI_I32:
-        if constexpr (F == FMT_I8 || F == FMT_S4) return launch_one<F, EPI_I32>(a, s);
+        if constexpr (F == FMT_I8 || F == FMT_S4 || F == FMT_I8_SKIP) return launch_one<F, EPI_I32>(a, s);
+        break;
+    case EPI_GLU:
+        if constexpr (F == FMT_FP8) {
+            if (a.n % 256 != 0 || a.ldo != a.n / 2 || !a.w_scales) {
+                set_error("GLU needs n %% 256 == 0 weight rows, ldo == n/2 and weight scales");
+                return -1;
+            }
+            return launch_one<F, EPI_GLU>(a, s);
+        }
         break;
     default: break;
     }
@@ -57,7 +66,7 @@ static int by_epi(int epi, const GemmArgs& a, hipStream_t s) {
 
 static int k_step(int fmt) {
     switch (fmt) {
-    case FMT_FP8: case FMT_I8: case FMT_G128A8: return 128;
+    case FMT_FP8: case FMT_I8: case FMT_G128A8: case FMT_I8_SKIP: return 128;
     case FMT_S4: return 256;
     default: return 64;
     }
@@ -76,7 +85,7 @@ int launch_gemm(int fmt, int epi, const GemmArgs& a, hipStream_t s) {
         set_error("k=%d must be a multiple of %d for format %d", a.k, k_step(fmt), fmt);
         return -1;
     }
-    if (a.n % 16 != 0 || a.ldo % 16 != 0 || a.ldo < a.n) {
+    if (a.n % 16 != 0 || a.ldo % 8 != 0 || (epi != EPI_GLU && (a.ldo % 16 != 0 || a.ldo < a.n))) {
         set_error("n=%d and ldo=%d must be multiples of 16 with ldo >= n", a.n, a.ldo);
         return -1;
     }
@@ -92,6 +101,7 @@ int launch_gemm(int fmt, int epi, const GemmArgs& a, hipStream_t s) {
     case FMT_G128A8: return by_epi<FMT_G128A8>(epi, a, s);
     case FMT_F16: return by_epi<FMT_F16>(epi, a, s);
     case FMT_G128A16: return by_epi<FMT_G128A16>(epi, a, s);
+    case FMT_I8_SKIP: return by_epi<FMT_I8_SKIP>(epi, a, s);
     default: break;
     }
     set_error("unknown format %d", fmt);

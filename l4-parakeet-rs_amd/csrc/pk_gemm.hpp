@@ -33,7 +33,7 @@
 
 namespace pk {
 
-enum Fmt { FMT_FP8 = 0, FMT_I8 = 1, FMT_S4 = 2, FMT_G128A8 = 3, FMT_F16 = 4, FMT_G128A16 = 5 };
+enum Fmt { FMT_FP8 = 0, FMT_I8 = 1, FMT_S4 = 2, FMT_G128A8 = 3, FMT_F16 = 4, FMT_G128A16 = 5, FMT_I8_SKIP = 6 };
 
 enum Epi {
     EPI_F16 = 0,     // fp16 out: act(scale(acc) [+bias]) * out_scale [+ res_scale * residual]
@@ -42,6 +42,7 @@ enum Epi {
     EPI_F32 = 3,     // fp32 out: scale(acc) [+bias]
     EPI_I32 = 4,     // raw int32 accumulators (integer formats only)
     EPI_F16_RES = 5, // EPI_F16 with a residual (chosen by the launcher when one is given)
+    EPI_GLU = 6,     // fp16 out [M x N/2]: fp16(v) / (1 + exp(-fp16(g))), v = column c, g = column c + N/2
 };
 
 struct GemmArgs {
@@ -64,6 +65,7 @@ struct GemmArgs {
     uint8_t* out_meta;          // EPI_F8_24: [M x ldo/8] metadata bytes
     int ldo;                    // output row stride in elements (of the output type)
     int valid_rows;
+    uint32_t* skip_count;       // FMT_I8_SKIP: {skipped, total} 16x128 activation blocks, or null
 };
 
 constexpr int kBlockM = 256;
@@ -75,6 +77,7 @@ constexpr int kMaxG128Groups = 32;               // K <= 4096 for the group-wise
 
 template <int F> struct FmtTraits;
 template <> struct FmtTraits<FMT_FP8> { static constexpr int kStep = 128, bRow = 128, aElemNum = 1, aElemDen = 1, bNum = 1, bDen = 1; static constexpr bool kInt = false; };
+template <> struct FmtTraits<FMT_I8_SKIP> { static constexpr int kStep = 128, bRow = 128, aElemNum = 1, aElemDen = 1, bNum = 1, bDen = 1; static constexpr bool kInt = true; };
 template <> struct FmtTraits<FMT_I8> { static constexpr int kStep = 128, bRow = 128, aElemNum = 1, aElemDen = 1, bNum = 1, bDen = 1; static constexpr bool kInt = true; };
 template <> struct FmtTraits<FMT_S4> { static constexpr int kStep = 256, bRow = 128, aElemNum = 1, aElemDen = 2, bNum = 1, bDen = 2; static constexpr bool kInt = true; };
 template <> struct FmtTraits<FMT_G128A8> { static constexpr int kStep = 128, bRow = 64, aElemNum = 1, aElemDen = 1, bNum = 1, bDen = 2; static constexpr bool kInt = false; };
@@ -130,7 +133,7 @@ __device__ __forceinline__ void mfma_step(v4f& accf, v4i& acci, const uint4& w0,
         const v8i W = {(int)w0.x, (int)w0.y, (int)w0.z, (int)w0.w, (int)w1.x, (int)w1.y, (int)w1.z, (int)w1.w};
         const v8i X = {(int)x0.x, (int)x0.y, (int)x0.z, (int)x0.w, (int)x1.x, (int)x1.y, (int)x1.z, (int)x1.w};
         accf = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(W, X, accf, 0, 0, 0, 0, 0, 0);
-    } else if constexpr (F == FMT_I8) {
+    } else if constexpr (F == FMT_I8 || F == FMT_I8_SKIP) {
         acci = __builtin_amdgcn_mfma_i32_16x16x64_i8(as_v4i(w0), as_v4i(x0), acci, 0, 0, 0);
         acci = __builtin_amdgcn_mfma_i32_16x16x64_i8(as_v4i(w1), as_v4i(x1), acci, 0, 0, 0);
     } else if constexpr (F == FMT_S4) {
@@ -485,6 +488,60 @@ __device__ __forceinline__ void epilogue_staged(const GemmArgs& p, v4f (&accf)[8
     }
 }
 
+// GLU tiles (pointwise1 + GLU, encoder.cu:911-947): a 256-row weight tile
+// starting at n0 serves output columns [n0/2, n0/2 + 128).  Tile row L holds
+// value row c + (L & 7) for L % 16 < 8 and the matching gate row (+ N/2) for
+// L % 16 >= 8, c = n0/2 + 8 (L / 16), so each lane's 16 accumulators are 8
+// values and their 8 gates.
+__device__ __forceinline__ int glu_row(int n0, int L, int n) {
+    const int half = n >> 1;
+    const int col = min((n0 >> 1) + ((L >> 4) << 3) + (L & 7), half - 1);
+    return col + ((L & 8) ? half : 0);
+}
+
+// GLU epilogue: out[row, c + j] = fp16(fp16(v_j) / (1 + exp(-fp16(g_j)))),
+// rows >= valid_rows written as zero (encoder.cu:936-947).
+__device__ __forceinline__ void epilogue_glu(const GemmArgs& p, v4f (&accf)[8][4], int m0, int n0, int wm, int wn, int lane) {
+    const int g = lane >> 4, l16 = lane & 15;
+    const int half = p.n >> 1;
+    const int oc = (n0 >> 1) + ((wn * 4 + g) << 3);  // first of the lane's 8 output columns
+    const bool col_live = oc < half;
+    const int cc = min(oc, half - 8);
+    float wv[8], wg[8], rsv[8];
+#pragma unroll
+    for (int j = 0; j < 8; j += 4) {
+        const float4 a = *(const float4*)(p.w_scales + cc + j);
+        const float4 b = *(const float4*)(p.w_scales + half + cc + j);
+        wv[j] = a.x; wv[j + 1] = a.y; wv[j + 2] = a.z; wv[j + 3] = a.w;
+        wg[j] = b.x; wg[j + 1] = b.y; wg[j + 2] = b.z; wg[j + 3] = b.w;
+    }
+#pragma unroll
+    for (int ai = 0; ai < 8; ++ai) {
+        const int row = min(m0 + wm * 128 + ai * 16 + l16, p.m - 1);
+        rsv[ai] = p.row_scales ? p.row_scales[row] : p.in_scale;
+    }
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+#pragma unroll
+    for (int ai = 0; ai < 8; ++ai) {
+        const int grow = m0 + wm * 128 + ai * 16 + l16;
+        const float rs = rsv[ai];
+        uint32_t h[4];
+#pragma unroll
+        for (int j = 0; j < 8; j += 2) {
+            float o[2];
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const int jj = j + u;
+                const float val = round_f16(accf[ai][jj >> 2][jj & 3] * rs * wv[jj]);
+                const float gate = round_f16(accf[ai][(jj + 8) >> 2][(jj + 8) & 3] * rs * wg[jj]);
+                o[u] = grow < p.valid_rows ? val * __builtin_amdgcn_rcpf(1.0f + __expf(-gate)) : 0.0f;
+            }
+            h[j >> 1] = (uint32_t)f2h(o[0]) | ((uint32_t)f2h(o[1]) << 16);
+        }
+        if (grow < p.m && col_live) *(uint4*)((uint16_t*)p.out + (size_t)grow * p.ldo + oc) = uint4{h[0], h[1], h[2], h[3]};
+    }
+}
+
 template <int F, int E>
 __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs p) {
     using T = FmtTraits<F>;
@@ -537,7 +594,10 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs p) {
                 row = o / T::bRow;
                 c = (o % T::bRow) / 16;
             }
-            b_off[i] = (uint32_t)((size_t)min(n0 + row, p.n - 1) * ldb + c * 16);
+            int wr;
+            if constexpr (E == EPI_GLU) wr = glu_row(n0, row, p.n);
+            else wr = min(n0 + row, p.n - 1);
+            b_off[i] = (uint32_t)((size_t)wr * ldb + c * 16);
         }
     };
     auto issue = [&](int step, int buf) {
@@ -558,6 +618,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs p) {
 
     v4f accf[8][4];
     v4i acci[8][4];
+    uint32_t skipped = 0, blocks = 0;
 
     while (true) {
         const int t_next = t + G;
@@ -635,20 +696,38 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs p) {
                 const int row = wm * 128 + ai * 16 + l16;
                 const uint4 x0 = *(const uint4*)(As + swz(row, g));
                 const uint4 x1 = *(const uint4*)(As + swz(row, 4 + g));
+                if constexpr (F == FMT_I8_SKIP) {
+                    // Activation-sparse FF2: the wave's 64 lanes hold this
+                    // 16-row x 128-K activation block; when every byte is zero
+                    // its products are exactly zero and the MFMAs are skipped.
+                    const bool nz = (x0.x | x0.y | x0.z | x0.w | x1.x | x1.y | x1.z | x1.w) != 0u;
+                    if (__builtin_amdgcn_ballot_w64(nz) == 0) {
+                        ++skipped;
+                        continue;
+                    }
+                }
 #pragma unroll
                 for (int bj = 0; bj < 4; ++bj) mfma_step<F>(accf[ai][bj], acci[ai][bj], w0[bj], w1[bj], x0, x1, gs[bj]);
             }
             buf ^= 1;
         }
+        blocks += 8 * steps;
 
         // Outputs without a residual go through the stage buffer the last
         // K-step has released (buf ^ 1 after the final flip); the next tile's
         // first step is already loading into the other buffer.
-        if constexpr (E == EPI_F16_RES) epilogue<F, EPI_F16>(p, accf, acci, cur_m0, cur_n0, wm, wn, lane);
+        if constexpr (E == EPI_GLU) epilogue_glu(p, accf, cur_m0, cur_n0, wm, wn, lane);
+        else if constexpr (E == EPI_F16_RES) epilogue<F, EPI_F16>(p, accf, acci, cur_m0, cur_n0, wm, wn, lane);
         else if constexpr (E == EPI_F32 || E == EPI_I32) epilogue<F, E>(p, accf, acci, cur_m0, cur_n0, wm, wn, lane);
         else epilogue_staged<F, E>(p, accf, acci, lds + (buf ^ 1) * L::kStage, cur_m0, cur_n0, wm, wn, lane, tid);
         if (t_next >= ntiles) break;
         t = t_next;
+    }
+    if constexpr (F == FMT_I8_SKIP) {
+        if (p.skip_count && lane == 0) {
+            atomicAdd(p.skip_count, skipped);
+            atomicAdd(p.skip_count + 1, blocks);
+        }
     }
 }
 

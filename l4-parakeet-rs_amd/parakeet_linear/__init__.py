@@ -56,6 +56,10 @@ SIGNATURES = {
     "pk_ffn_contract_fp8": (I, [P, P, P, P, I, P]),
     "pk_conv_residual_fp8": (I, [P, P, P, P, P, I, P]),
     "pk_attention_output_fp8": (I, [P, P, P, P, I, P]),
+    "pk_conv_glu_fp8": (I, [P, P, P, P, P, I, I, P]),
+    "pk_subsample_projection_fp8": (I, [P, P, P, P, P, P, I, P]),
+    "pk_subsample_pointwise_fp8": (I, [P, P, P, P, P, P, I, P]),
+    "pk_ffn_contract_int8_rowskip": (I, [P, P, P, P, P, I, P, P]),
     "pk_gemm": (I, [I, I, P, P, I, I, I, P, P, F, P, P, F, F, I, P, P, P, P, I, P]),
     "pk_joint_gemv": (I, [P, I, P, P, P, P, P, P, I, I, I, I, I, I, P]),
 }
@@ -153,5 +157,5 @@ def gemm(fmt, epi, a, b, m, n, k, out, *, w_scales=None, row_scales=None, in_sca
          stream=stream)
 
 
-FMT_FP8, FMT_I8, FMT_S4, FMT_G128A8, FMT_F16, FMT_G128A16 = range(6)
+FMT_FP8, FMT_I8, FMT_S4, FMT_G128A8, FMT_F16, FMT_G128A16, FMT_I8_SKIP = range(7)
 EPI_F16, EPI_F8, EPI_F8_24, EPI_F32, EPI_I32 = range(5)

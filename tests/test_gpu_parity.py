@@ -410,3 +410,74 @@ def test_joint_gemv(pk, orc, int8):
             ref = orc.joint_scores_f16(w16, bias, enc[t], pred)
         assert_close(got[t], ref, tol=1e-4)
         assert tuple(dec[t]) == orc.joint_decide(got[t])
+
+
+# ---- conv GLU and subsampling linears ---------------------------------------------
+
+def test_conv_glu_fp8(pk, orc):
+    note("conv_glu_fp8")
+    rows, valid = 300, 290
+    x = acts(rows, 1024, 131)
+    w = weights(2048, 1024, 132)
+    xq, xs = orc.quantize_fp8_rows(x)
+    wq, ws = orc.pack_fp8_rows(w)
+    out = empty((rows, 1024), torch.float16)
+    pk.call("pk_conv_glu_fp8", dev(xq), dev(wq), dev(ws), dev(xs), out, rows, valid)
+    ref = orc.epilogue(orc.gemm_e4m3(xq, wq), 5, ws, row_scales=xs, valid_rows=valid)
+    got = host(out)
+    assert not got[valid:].astype(np.float32).any()
+    assert_close(got[:valid], ref[:valid].astype(np.float32))
+
+
+@pytest.mark.parametrize("name,n,k,mode", [("pk_subsample_projection_fp8", 1024, 4096, 3),
+                                           ("pk_subsample_pointwise_fp8", 256, 256, 4)])
+def test_subsample_linears(pk, orc, name, n, k, mode):
+    note(name)
+    rows = 333
+    x = acts(rows, k, 141)
+    w = weights(n, k, 142)
+    bias = (np.random.default_rng(143).standard_normal(n) * 0.1).astype(np.float32)
+    xq, xs = orc.quantize_fp8_rows(x)
+    wq, ws = orc.pack_fp8_rows(w)
+    out = empty((rows, n), torch.float16)
+    pk.call(name, dev(xq), dev(wq), dev(ws), dev(xs), dev(bias), out, rows)
+    ref = orc.epilogue(orc.gemm_e4m3(xq, wq), mode, ws, row_scales=xs, bias=bias)
+    assert_close(host(out), ref.astype(np.float32))
+
+
+# ---- activation-sparse FF2 (INT8, row skip) -------------------------------------
+
+def sparse_acts(rows, k, keep, seed, dead_blocks=0):
+    """SiLU-like fp16 activations keeping each frame's top `keep` fraction of
+    magnitudes (the rest exactly 0); the last `dead_blocks` 16-row blocks are all
+    zero (padding frames), which the kernel must skip."""
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((rows, k)).astype(np.float32)
+    x = x / (1 + np.exp(-x))
+    kth = int(round(k * (1 - keep)))
+    thresh = np.partition(np.abs(x), kth, axis=1)[:, kth:kth + 1]
+    x[np.abs(x) < thresh] = 0
+    if dead_blocks:
+        x[rows - 16 * dead_blocks:] = 0
+    return x.astype(np.float16)
+
+
+@pytest.mark.parametrize("sparsity", [0.5, 0.8, 0.9, 0.95])
+def test_ffn_contract_int8_rowskip_exact(pk, orc, sparsity):
+    note(f"int8 rowskip sparsity={sparsity}")
+    rows = 512
+    x = sparse_acts(rows, 4096, 1 - sparsity, 151, dead_blocks=3)
+    w = weights(1024, 4096, 152)
+    xq, xs = orc.quantize_int8_rows(x)
+    wq, ws = orc.pack_int8_rows(w)
+    out = empty((rows, 1024), torch.float32)
+    counts = torch.zeros(2, dtype=torch.int32, device="cuda")
+    pk.call("pk_ffn_contract_int8_rowskip", dev(xq), dev(xs), dev(wq), dev(ws), out, rows, counts)
+    acc = orc.gemm_i8(xq, wq).astype(np.float32)
+    ref = (acc * xs[:, None]).astype(np.float32) * ws[None, :]
+    assert np.array_equal(host(out), ref.astype(np.float32))
+    skipped, total = (int(v) for v in host(counts))
+    tiles = ((rows + 255) // 256) * (1024 // 256)
+    assert total == tiles * 8 * 8 * (4096 // 128)  # tiles x waves x row blocks x K-steps
+    # the three dead 16-row blocks, every K-step, seen by the 4 column waves of each of 4 column tiles
+    assert skipped >= 3 * 32 * 4 * 4
