@@ -190,6 +190,14 @@ int32_t pk_ffn_expand_int4_sparse(const uint8_t* input, const uint8_t* weight, c
  * FP8 input at scale 1/16; output (fp16 [rows x 1024]) += 0.5 * Y in place. */
 int32_t pk_ffn_contract_fp8(const uint8_t* input, const uint8_t* weight, const float* weight_scales,
                             uint16_t* output, int32_t rows, void* stream);
+/* encoder.cu:1087-1093 pk_sm89_ffn_contract_fp8_sparse: FF2 contract on 2:4
+ * compressed FP8 activations on the sparse MFMA (v_smfmac_f32_16x16x128_fp8_fp8).
+ * `input` holds [rows x inner_width/2] data bytes followed by [rows x
+ * inner_width/8] metadata bytes (the layout pk_ffn_expand_int4_sparse writes);
+ * weight FP8 [1024 x inner_width]; output (fp16 [rows x 1024]) += 0.5 * Y at
+ * input scale 1/16.  The metadata block must be 16-byte aligned. */
+int32_t pk_ffn_contract_fp8_sparse(const uint8_t* input, const uint8_t* weight, const float* weight_scales,
+                                   uint16_t* output, int32_t rows, int32_t inner_width, void* stream);
 /* encoder.cu:1313-1319 pk_sm89_conv_residual_fp8: pointwise2 1024 -> 1024,
  * dynamic per-row input scales, output += Y in place. */
 int32_t pk_conv_residual_fp8(const uint8_t* input, const uint8_t* weight, const float* weight_scales,

@@ -335,6 +335,19 @@ int32_t pk_ffn_contract_fp8(const uint8_t* in, const uint8_t* w, const float* ws
     return scaled_linear(FMT_FP8, EPI_F16, in, nullptr, 1.0f / 16.0f, 0, w, ws, nullptr, out, 0.5f, 0, out, rows, 1024, 4096, stream);
 }
 
+int32_t pk_ffn_contract_fp8_sparse(const uint8_t* in, const uint8_t* w, const float* ws, uint16_t* out, int32_t rows,
+                                   int32_t inner_width, void* stream) {
+    if (!need(in, "input") || !need(w, "weight") || !need(ws, "weight_scales") || !need(out, "output")) return PK_E_ARG;
+    if (rows < 0 || inner_width <= 0 || inner_width % 128) {
+        set_error("sparse contract needs rows >= 0 and inner_width %% 128 == 0 (got %d)", inner_width);
+        return PK_E_SHAPE;
+    }
+    if (((uintptr_t)in | (uintptr_t)w | (uintptr_t)out) & 15) { set_error("pointers must be 16-byte aligned"); return PK_E_ALIGN; }
+    const uint8_t* meta = in + (size_t)rows * (inner_width / 2);
+    if (((uintptr_t)meta) & 15) { set_error("metadata (input + rows * inner_width / 2) must be 16-byte aligned"); return PK_E_ALIGN; }
+    return launch_sparse24_contract(in, meta, w, ws, 1.0f / 16.0f, out, rows, 1024, inner_width, STREAM);
+}
+
 int32_t pk_conv_residual_fp8(const uint8_t* in, const uint8_t* w, const float* ws, const float* in_scales, uint16_t* out, int32_t rows,
                              void* stream) {
     if (!need(ws, "weight_scales") || !need(in_scales, "input_scales")) return PK_E_ARG;

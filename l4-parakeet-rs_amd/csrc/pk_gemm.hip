@@ -5,7 +5,7 @@
 
 namespace pk {
 
-static int cu_count() {
+int cu_count() {
     static int cus = 0;
     if (cus == 0) {
         int dev = 0;

@@ -4,6 +4,8 @@
 
 #include <stddef.h>
 
+#include <mutex>
+
 #include "pk_gemm.hpp"
 
 namespace pk {
@@ -20,5 +22,8 @@ int launch_joint(const void* w, int w_int8, const float* w_scales, const float* 
                  int enc_stride, hipStream_t s);
 
 void set_error(const char* fmt, ...);
+int cu_count();
+int launch_sparse24_contract(const uint8_t* data, const uint8_t* meta, const uint8_t* w, const float* w_scales, float in_scale,
+                             uint16_t* out, int m, int n, int k, hipStream_t s);
 
 }  // namespace pk

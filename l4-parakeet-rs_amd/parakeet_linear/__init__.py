@@ -54,6 +54,7 @@ SIGNATURES = {
     "pk_ffn_expand_fp8_packed": (I, [P, P, P, P, P, I, F, I, P]),
     "pk_ffn_expand_int4_sparse": (I, [P, P, P, P, P, I, F, I, P]),
     "pk_ffn_contract_fp8": (I, [P, P, P, P, I, P]),
+    "pk_ffn_contract_fp8_sparse": (I, [P, P, P, P, I, I, P]),
     "pk_conv_residual_fp8": (I, [P, P, P, P, P, I, P]),
     "pk_attention_output_fp8": (I, [P, P, P, P, I, P]),
     "pk_conv_glu_fp8": (I, [P, P, P, P, P, I, I, P]),

@@ -481,3 +481,25 @@ def test_ffn_contract_int8_rowskip_exact(pk, orc, sparsity):
     assert total == tiles * 8 * 8 * (4096 // 128)  # tiles x waves x row blocks x K-steps
     # the three dead 16-row blocks, every K-step, seen by the 4 column waves of each of 4 column tiles
     assert skipped >= 3 * 32 * 4 * 4
+
+
+# ---- 2:4 sparse FF2 contract (SMFMAC) ----------------------------------------------
+
+def test_ffn_contract_fp8_sparse(pk, orc):
+    """The expand epilogue 7 output (2:4 compressed e4m3) feeds the sparse contract."""
+    note("ffn_contract_fp8_sparse")
+    rows = 272
+    rng = np.random.default_rng(161)
+    dense = orc.quantize_fp8_static((rng.standard_normal((rows, 4096)) * 2).astype(np.float16), 16.0)
+    data, meta = orc.compress_24(dense)
+    w = weights(1024, 4096, 162)
+    wq, ws = orc.pack_fp8_rows(w)
+    residual = acts(rows, 1024, 163, outliers=False)
+    buf = np.concatenate([data.ravel(), meta.ravel()])
+    out = dev(residual.copy())
+    pk.call("pk_ffn_contract_fp8_sparse", dev(buf), dev(wq), dev(ws), out, rows, 4096)
+    ref = orc.epilogue(orc.gemm_e4m3(orc.decompress_24(data, meta), wq), 8, ws, in_scale=1.0 / 16.0,
+                       residual=residual)
+    delta_ref = ref.astype(np.float32) - residual.astype(np.float32)
+    delta_got = host(out).astype(np.float32) - residual.astype(np.float32)
+    assert_close(delta_got, delta_ref, tol=2e-2)
