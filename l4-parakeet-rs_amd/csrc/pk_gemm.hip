@@ -89,6 +89,11 @@ int launch_gemm(int fmt, int epi, const GemmArgs& a, hipStream_t s) {
         set_error("n=%d and ldo=%d must be multiples of 16 with ldo >= n", a.n, a.ldo);
         return -1;
     }
+    // Operand loads address rows with 32-bit byte offsets from the base.
+    if ((uint64_t)a.m * a.k * 2 > 0xffffffffull || (uint64_t)a.n * a.k * 2 > 0xffffffffull) {
+        set_error("operands of m=%d n=%d k=%d exceed the 4 GiB a launch addresses", a.m, a.n, a.k);
+        return -1;
+    }
     if (((uintptr_t)a.a | (uintptr_t)a.b | (uintptr_t)a.out) & 15) {
         set_error("operand pointers must be 16-byte aligned");
         return -2;

@@ -6,8 +6,8 @@
 // 128 bytes of each of its 256 weight rows global -> LDS with direct-to-LDS
 // loads (double buffered, one barrier per step, the next tile's first step
 // prefetched while the current tile finishes).  The 16-byte chunks of each
-// 128-byte LDS row are XOR-swizzled by (row & 7) so that the 16 lanes reading
-// one chunk column hit distinct banks.
+// 128-byte LDS row are XOR-swizzled (swz_key) so that the 16 lanes reading one
+// chunk column hit distinct banks.
 //
 // The weights are the MFMA's first operand and the activations its second,
 // so accumulator register r of lane l holds output column 4*(l/16)+r of row
@@ -94,7 +94,14 @@ template <int F> struct Layout {
     static constexpr int kBytes = kG128 ? kZeros + kMaxG128Groups * kBlockN : 2 * kStage;
 };
 
-__device__ __forceinline__ int swz(int row, int chunk) { return row * kRowBytes + ((chunk ^ (row & 7)) << 4); }
+// XOR key of a 128-byte LDS row's 16-byte chunks (bits: k0 = r1, k1 = r2^r4,
+// k2 = r0^r3^r5).  One chunk column read by 8 (or 16) lanes then touches
+// distinct banks both for 8 (16) consecutive rows and for the weight rows
+// wrow(0..7 (15), bj), with 32 banks per 128 bytes as with 64 per 256 bytes.
+__device__ __forceinline__ int swz_key(int row) {
+    return ((row >> 1) & 1) | (((row >> 2) ^ (row >> 4)) & 1) << 1 | ((row ^ (row >> 3) ^ (row >> 5)) & 1) << 2;
+}
+__device__ __forceinline__ int swz(int row, int chunk) { return row * kRowBytes + ((chunk ^ swz_key(row)) << 4); }
 
 // Weight row (within the wave's 64 columns) held by MFMA row i of block bj.
 __device__ __forceinline__ int wrow(int i, int bj) { return ((i >> 2) << 4) + (bj << 2) + (i & 3); }
@@ -168,6 +175,11 @@ __device__ __forceinline__ void mfma_step(v4f& accf, v4i& acci, const uint4& w0,
 // the step loop waits for these loads explicitly.
 __device__ __forceinline__ void dma16(const void* src, uint32_t lds_addr) {
     asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(__builtin_amdgcn_readfirstlane(lds_addr))
+                 : "memory", "m0");
+}
+// Same with a wave-uniform 64-bit base (SGPR pair) and a 32-bit lane offset.
+__device__ __forceinline__ void dma16(const uint8_t* base, uint32_t off, uint32_t lds_addr) {
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(__builtin_amdgcn_readfirstlane(lds_addr))
                  : "memory", "m0");
 }
 
@@ -580,7 +592,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs p) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int o = (wave * 4 + i) * 1024 + lane * 16;
-            const int row = o >> 7, c = ((o >> 4) & 7) ^ (row & 7);
+            const int row = o >> 7, c = ((o >> 4) & 7) ^ swz_key(row);
             a_off[i] = (uint32_t)((size_t)min(m0 + row, p.m - 1) * lda + c * 16);
         }
 #pragma unroll
@@ -589,7 +601,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs p) {
             int row, c;
             if constexpr (T::bRow == 128) {
                 row = o >> 7;
-                c = ((o >> 4) & 7) ^ (row & 7);
+                c = ((o >> 4) & 7) ^ swz_key(row);
             } else {
                 row = o / T::bRow;
                 c = (o % T::bRow) / 16;
@@ -603,10 +615,10 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs p) {
     auto issue = [&](int step, int buf) {
         const uint32_t base = lds_base + buf * L::kStage;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) dma16(pa + a_off[i] + (size_t)step * kRowBytes, base + (wave * 4 + i) * 1024);
+        for (int i = 0; i < 4; ++i) dma16(pa + (size_t)step * kRowBytes, a_off[i], base + (wave * 4 + i) * 1024);
 #pragma unroll
         for (int i = 0; i < kBLoadsPerWave; ++i)
-            dma16(pb + b_off[i] + (size_t)step * T::bRow, base + kTileBytes + (wave * kBLoadsPerWave + i) * 1024);
+            dma16(pb + (size_t)step * T::bRow, b_off[i], base + kTileBytes + (wave * kBLoadsPerWave + i) * 1024);
     };
 
     int t = tile_slot(G);
@@ -691,23 +703,56 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs p) {
                     }
                 }
             }
+            // Activation fragments are read one 16-row block ahead of the
+            // MFMAs that consume them where the step's weight decode leaves the
+            // registers for it (FP8, INT8, FP16).
+            constexpr bool kAhead = F == FMT_FP8 || F == FMT_I8 || F == FMT_I8_SKIP || F == FMT_F16;
+            uint4 x0, x1, y0, y1;
+            if constexpr (kAhead) {
+                const int row = wm * 128 + l16;
+                x0 = *(const uint4*)(As + swz(row, g));
+                x1 = *(const uint4*)(As + swz(row, 4 + g));
+            }
 #pragma unroll
             for (int ai = 0; ai < 8; ++ai) {
-                const int row = wm * 128 + ai * 16 + l16;
-                const uint4 x0 = *(const uint4*)(As + swz(row, g));
-                const uint4 x1 = *(const uint4*)(As + swz(row, 4 + g));
+                if (!kAhead || ai + 1 < 8) {
+                    const int row = wm * 128 + (kAhead ? ai + 1 : ai) * 16 + l16;
+                    y0 = *(const uint4*)(As + swz(row, g));
+                    y1 = *(const uint4*)(As + swz(row, 4 + g));
+                }
+                if constexpr (!kAhead) {
+                    x0 = y0;
+                    x1 = y1;
+                }
+                bool live = true;
                 if constexpr (F == FMT_I8_SKIP) {
                     // Activation-sparse FF2: the wave's 64 lanes hold this
                     // 16-row x 128-K activation block; when every byte is zero
                     // its products are exactly zero and the MFMAs are skipped.
                     const bool nz = (x0.x | x0.y | x0.z | x0.w | x1.x | x1.y | x1.z | x1.w) != 0u;
-                    if (__builtin_amdgcn_ballot_w64(nz) == 0) {
-                        ++skipped;
-                        continue;
-                    }
+                    live = __builtin_amdgcn_ballot_w64(nz) != 0;
+                    skipped += live ? 0u : 1u;
                 }
+                if (live) {
 #pragma unroll
-                for (int bj = 0; bj < 4; ++bj) mfma_step<F>(accf[ai][bj], acci[ai][bj], w0[bj], w1[bj], x0, x1, gs[bj]);
+                    for (int bj = 0; bj < 4; ++bj) mfma_step<F>(accf[ai][bj], acci[ai][bj], w0[bj], w1[bj], x0, x1, gs[bj]);
+                }
+                if constexpr (kAhead) {
+                    x0 = y0;
+                    x1 = y1;
+                }
+            }
+            if constexpr (F == FMT_FP8 || F == FMT_I8) {
+                // Scheduling order: the 8 weight reads and the first block's 2
+                // activation reads, then per block the next block's 2 reads
+                // ahead of this block's MFMAs.
+                constexpr int kMfma = F == FMT_FP8 ? 4 : 8;
+                __builtin_amdgcn_sched_group_barrier(0x100, 10, 0);
+#pragma unroll
+                for (int ai = 0; ai < 8; ++ai) {
+                    if (ai + 1 < 8) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x008, kMfma, 0);
+                }
             }
             buf ^= 1;
         }

@@ -24,6 +24,14 @@ constexpr int kSpMeta = 256 * 16;     // metadata bytes per stage
 constexpr int kSpW = 256 * 128;       // weight bytes per stage
 constexpr int kSpStage = kSpData + kSpMeta + kSpW;
 
+// XOR key of a 64-byte compressed row's 16-byte chunks: 8 (16) consecutive
+// rows reading one chunk column touch distinct banks of 128 (256) bytes.
+__device__ __forceinline__ int sp_key(int row) { return ((row >> 1) & 2) | (((row >> 1) ^ (row >> 3)) & 1); }
+// XOR key of a 128-byte weight row's chunks for the rows 4i + bj that lanes
+// i = 0..15 read: distinct for every 8 lanes (16 lanes share each bank pair).
+__device__ __forceinline__ int spw_key(int row) { return (row >> 2) & 7; }
+__device__ __forceinline__ int spw(int row, int chunk) { return row * 128 + ((chunk ^ spw_key(row)) << 4); }
+
 struct SparseArgs {
     const uint8_t* data;    // [M x K/2]
     const uint8_t* meta;    // [M x K/8]
@@ -48,9 +56,9 @@ __global__ __launch_bounds__(kThreads, 1) void sparse24_contract_kernel(SparseAr
     const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)lds;
 
     // Per-lane source offsets of this wave's direct-to-LDS loads: compressed
-    // data (2 KiB per wave, 64-byte rows, 16-byte chunks swizzled by (row/2)&3),
+    // data (2 KiB per wave, 64-byte rows, 16-byte chunks swizzled by sp_key),
     // metadata (waves 0-3, 1 KiB each, 16-byte rows), weights (4 KiB per wave,
-    // 128-byte rows swizzled by row & 7).
+    // 128-byte rows swizzled by spw_key).
     uint32_t d_off[2], m_off = 0, w_off[4];
     const int gw = group_width(tiles_n);
     auto set_tile = [&](int t, int& m0, int& n0) {
@@ -62,7 +70,7 @@ __global__ __launch_bounds__(kThreads, 1) void sparse24_contract_kernel(SparseAr
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             const int o = (wave * 2 + i) * 1024 + lane * 16;
-            const int row = o >> 6, c = ((o >> 4) & 3) ^ ((row >> 1) & 3);
+            const int row = o >> 6, c = ((o >> 4) & 3) ^ sp_key(row);
             d_off[i] = (uint32_t)((size_t)min(m0 + row, p.m - 1) * ld_data + c * 16);
         }
         {
@@ -72,7 +80,7 @@ __global__ __launch_bounds__(kThreads, 1) void sparse24_contract_kernel(SparseAr
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int o = (wave * 4 + i) * 1024 + lane * 16;
-            const int row = o >> 7, c = ((o >> 4) & 7) ^ (row & 7);
+            const int row = o >> 7, c = ((o >> 4) & 7) ^ spw_key(row);
             w_off[i] = (uint32_t)((size_t)min(n0 + row, p.n - 1) * ld_w + c * 16);
         }
     };
@@ -117,14 +125,14 @@ __global__ __launch_bounds__(kThreads, 1) void sparse24_contract_kernel(SparseAr
 #pragma unroll
             for (int bj = 0; bj < 4; ++bj) {
                 const int row = wn * 64 + 4 * l16 + bj;
-                const uint4 w0 = *(const uint4*)(Ws + swz(row, g));
-                const uint4 w1 = *(const uint4*)(Ws + swz(row, 4 + g));
+                const uint4 w0 = *(const uint4*)(Ws + spw(row, g));
+                const uint4 w1 = *(const uint4*)(Ws + spw(row, 4 + g));
                 wf[bj] = v8i{(int)w0.x, (int)w0.y, (int)w0.z, (int)w0.w, (int)w1.x, (int)w1.y, (int)w1.z, (int)w1.w};
             }
 #pragma unroll
             for (int ai = 0; ai < 8; ++ai) {
                 const int row = wm * 128 + ai * 16 + l16;
-                const uint4 d = *(const uint4*)(Ds + row * 64 + ((g ^ ((row >> 1) & 3)) << 4));
+                const uint4 d = *(const uint4*)(Ds + row * 64 + ((g ^ sp_key(row)) << 4));
                 const int idx = *(const int*)(Ms + row * 16 + g * 4);
                 const v4i dv = {(int)d.x, (int)d.y, (int)d.z, (int)d.w};
 #pragma unroll
