@@ -74,6 +74,10 @@ int32_t pk_pack_int4_rows(const uint16_t* weight, int32_t n, int32_t k, uint8_t*
  * fp16 zero-points ([n x k/128]); dequant (q - z) * s. */
 int32_t pk_pack_int4_g128(const uint16_t* weight, int32_t n, int32_t k, uint32_t* packed,
                           uint16_t* scales, uint16_t* zeros, void* stream);
+/* linear.cu:459-472 pk_sm89_q4_k_dequantize: GGUF Q4_K superblocks (144 bytes
+ * per 256 values: fp16 d, fp16 dmin, 12 bytes of 6-bit scales/mins, 128 quant
+ * bytes) [n x k/256] -> fp16 [n x k], value = f16(d*sc*q - dmin*mn). */
+int32_t pk_q4_k_dequantize(const uint8_t* input, uint16_t* output, int32_t n, int32_t k, void* stream);
 
 /* ---- activation quantizers ------------------------------------------------ */
 
@@ -157,6 +161,11 @@ int32_t pk_linear_int4_accumulate(const uint8_t* input, const uint8_t* weight_oi
 int32_t pk_linear_int4g128(const uint16_t* input, const uint32_t* weight_q, const uint16_t* weight_scales,
                            const uint16_t* weight_zeros, const float* bias, void* output, int32_t output_fp32,
                            int32_t m, int32_t n, int32_t k, void* stream);
+/* linear.cu:478-535 pk_sm89_q4_k_linear_epilogue: fp16 input [m x k] x Q4_K
+ * weights [n x k/256 blocks] dequantized to fp16 in registers, fp32
+ * accumulate, out = f16(act(acc + bias[n])); bias may be NULL; k % 256 == 0. */
+int32_t pk_q4_k_linear_epilogue(const uint16_t* input, const uint8_t* weight_oi, const float* bias, uint16_t* output,
+                                int32_t m, int32_t n, int32_t k, int32_t activation, void* stream);
 /* Mixed variant: per-token dynamic INT8 activations x group-wise INT4 weights
  * on the INT8 MFMA; each 128-K group's int32 sum (exact) is scaled by its fp16
  * scale in fp32, then by the row scale. */
@@ -238,7 +247,8 @@ int32_t pk_ffn_contract_int8_rowskip(const int8_t* input, const float* input_sca
 
 /* ---- generic fused GEMM ------------------------------------------------------
  * format: 0 FP8, 1 INT8, 2 INT4 (s4 x s4), 3 INT4-g128 x INT8, 4 FP16,
- * 5 INT4-g128 x FP16.  epilogue: 0 fp16 (act(v [+bias]) * out_scale
+ * 5 INT4-g128 x FP16, 6 INT8 with zero-block skip, 7 Q4_K x FP16 (epilogues
+ * 0 and 3 only).  epilogue: 0 fp16 (act(v [+bias]) * out_scale
  * [+ res_scale * residual]), 1 e4m3(fp16(SiLU(v)) * 16), 2 as 1 + 2:4
  * compression (metadata to out_meta), 3 fp32 v [+bias], 4 raw int32.
  * v = acc * row_scale * w_scale with row_scale = row_scales[r] or in_scale. */

@@ -136,6 +136,14 @@ int32_t pk_pack_int4_g128(const uint16_t* w, int32_t n, int32_t k, uint32_t* q, 
     return check_launch("pack_int4_g128");
 }
 
+int32_t pk_q4_k_dequantize(const uint8_t* input, uint16_t* output, int32_t n, int32_t k, void* stream) {
+    if (n < 0 || k <= 0 || k % 256) { set_error("Q4_K needs k %% 256 == 0 (k=%d)", k); return PK_E_SHAPE; }
+    if (!need(input, "input") || !need(output, "output")) return PK_E_ARG;
+    if (((uintptr_t)input | (uintptr_t)output) & 15) { set_error("Q4_K blocks and output must be 16-byte aligned"); return PK_E_ALIGN; }
+    launch_q4k_dequant(input, output, n, k, STREAM);
+    return check_launch("q4_k_dequantize");
+}
+
 // ---- activation quantizers ------------------------------------------------------
 
 int32_t pk_quantize_fp8(const uint16_t* in, uint8_t* out, float inverse_scale, int32_t elements, void* stream) {
@@ -223,6 +231,19 @@ int32_t pk_linear_fp16_epilogue(const uint16_t* in, const uint16_t* w, const flo
                                 int32_t m, int32_t n, int32_t k, float out_scale, float res_scale, int32_t act, void* stream) {
     return pk_gemm(FMT_F16, EPI_F16, in, w, m, n, k, nullptr, nullptr, 1.0f, bias, residual, out_scale, res_scale, act, nullptr,
                    nullptr, out, nullptr, n, stream);
+}
+
+int32_t pk_q4_k_linear_epilogue(const uint16_t* in, const uint8_t* w, const float* bias, uint16_t* out, int32_t m, int32_t n, int32_t k,
+                                int32_t act, void* stream) {
+    if (!need(in, "input") || !need(w, "weight_oi") || !need(out, "output")) return PK_E_ARG;
+    if (act < 0 || act > 2) { set_error("activation must be 0, 1 or 2"); return PK_E_ARG; }
+    GemmArgs g = base_args(in, w, m, n, k, out, n);
+    g.in_scale = 1.0f;
+    g.bias = bias;
+    g.out_scale = 1.0f;
+    g.res_scale = 0.0f;
+    g.act = act;
+    return launch_gemm(FMT_Q4K, EPI_F16, g, STREAM);
 }
 
 int32_t pk_linear_fp16_qkv(const uint16_t* in, const uint16_t* wq, const uint16_t* wk, const uint16_t* wv, uint16_t* out, int32_t m,

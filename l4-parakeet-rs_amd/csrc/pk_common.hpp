@@ -72,4 +72,32 @@ __device__ __forceinline__ float wave_max(float v) {
 // SiLU with the hardware reciprocal (<= 1 ulp) instead of an IEEE division.
 __device__ __forceinline__ float silu(float v) { return v * __builtin_amdgcn_rcpf(1.0f + __expf(-v)); }
 
+// Q4_K group g (0..7) of a superblock header: d * scale and dmin * min
+// (linear.cu:431-457; 6-bit scale/min pairs, groups 4..7 split over bytes).
+__device__ __forceinline__ void q4k_coeffs(const uint4& h, int g, float& a, float& b) {
+    auto byte = [&](int i) { return ((i < 4 ? h.y : (i < 8 ? h.z : h.w)) >> ((i & 3) * 8)) & 0xffu; };
+    uint32_t sc, mn;
+    if (g < 4) {
+        sc = byte(g) & 63u;
+        mn = byte(g + 4) & 63u;
+    } else {
+        sc = (byte(g + 4) & 15u) | ((byte(g - 4) >> 6) << 4);
+        mn = (byte(g + 4) >> 4) | ((byte(g) >> 6) << 4);
+    }
+    a = h2f((uint16_t)(h.x & 0xffffu)) * (float)sc;
+    b = h2f((uint16_t)(h.x >> 16)) * (float)mn;
+}
+
+// Eight nibbles (byte j of lo / hi, j = 0..3) -> f16(a * q - b), in k order.
+__device__ __forceinline__ uint4 q4k_decode8(uint32_t lo, uint32_t hi, float a, float b) {
+    uint32_t r[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t w = j < 2 ? lo : hi;
+        const float q0 = (float)((w >> (16 * (j & 1))) & 0xffu), q1 = (float)((w >> (16 * (j & 1) + 8)) & 0xffu);
+        r[j] = (uint32_t)f2h(a * q0 - b) | ((uint32_t)f2h(a * q1 - b) << 16);
+    }
+    return uint4{r[0], r[1], r[2], r[3]};
+}
+
 }  // namespace pk

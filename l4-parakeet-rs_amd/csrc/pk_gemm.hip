@@ -41,6 +41,12 @@ static int launch_one(const GemmArgs& a, hipStream_t s) {
 
 template <int F>
 static int by_epi(int epi, const GemmArgs& a, hipStream_t s) {
+    if constexpr (F == FMT_Q4K) {
+        if (epi == EPI_F16) return a.residual ? launch_one<F, EPI_F16_RES>(a, s) : launch_one<F, EPI_F16>(a, s);
+        if (epi == EPI_F32) return launch_one<F, EPI_F32>(a, s);
+        set_error("unsupported epilogue %d for format %d", epi, F);
+        return -4;
+    } else {
     switch (epi) {
     case EPI_F16: return a.residual ? launch_one<F, EPI_F16_RES>(a, s) : launch_one<F, EPI_F16>(a, s);
     case EPI_F32: return launch_one<F, EPI_F32>(a, s);
@@ -62,12 +68,13 @@ static int by_epi(int epi, const GemmArgs& a, hipStream_t s) {
     }
     set_error("unsupported epilogue %d for format %d", epi, F);
     return -4;
+    }
 }
 
 static int k_step(int fmt) {
     switch (fmt) {
     case FMT_FP8: case FMT_I8: case FMT_G128A8: case FMT_I8_SKIP: return 128;
-    case FMT_S4: return 256;
+    case FMT_S4: case FMT_Q4K: return 256;
     default: return 64;
     }
 }
@@ -107,6 +114,7 @@ int launch_gemm(int fmt, int epi, const GemmArgs& a, hipStream_t s) {
     case FMT_F16: return by_epi<FMT_F16>(epi, a, s);
     case FMT_G128A16: return by_epi<FMT_G128A16>(epi, a, s);
     case FMT_I8_SKIP: return by_epi<FMT_I8_SKIP>(epi, a, s);
+    case FMT_Q4K: return by_epi<FMT_Q4K>(epi, a, s);
     default: break;
     }
     set_error("unknown format %d", fmt);

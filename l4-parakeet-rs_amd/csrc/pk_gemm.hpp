@@ -27,13 +27,15 @@
 //                         fp32 fma of each group sum with its fp16 scale
 //   F16     f16 x f16     2 x v_mfma_f32_16x16x32_f16      K/step 64
 //   G128A16 f16((q-z)*s) x f16, INT4 weights dequantized in registers
+//   Q4K     f16(d*sc*q - dmin*mn) x f16, GGUF Q4_K superblocks (144 bytes
+//           per 256 K) dequantized in registers, K/step 64 = one group pair
 #pragma once
 
 #include "pk_common.hpp"
 
 namespace pk {
 
-enum Fmt { FMT_FP8 = 0, FMT_I8 = 1, FMT_S4 = 2, FMT_G128A8 = 3, FMT_F16 = 4, FMT_G128A16 = 5, FMT_I8_SKIP = 6 };
+enum Fmt { FMT_FP8 = 0, FMT_I8 = 1, FMT_S4 = 2, FMT_G128A8 = 3, FMT_F16 = 4, FMT_G128A16 = 5, FMT_I8_SKIP = 6, FMT_Q4K = 7 };
 
 enum Epi {
     EPI_F16 = 0,     // fp16 out: act(scale(acc) [+bias]) * out_scale [+ res_scale * residual]
@@ -83,15 +85,29 @@ template <> struct FmtTraits<FMT_S4> { static constexpr int kStep = 256, bRow = 
 template <> struct FmtTraits<FMT_G128A8> { static constexpr int kStep = 128, bRow = 64, aElemNum = 1, aElemDen = 1, bNum = 1, bDen = 2; static constexpr bool kInt = false; };
 template <> struct FmtTraits<FMT_F16> { static constexpr int kStep = 64, bRow = 128, aElemNum = 2, aElemDen = 1, bNum = 2, bDen = 1; static constexpr bool kInt = false; };
 template <> struct FmtTraits<FMT_G128A16> { static constexpr int kStep = 64, bRow = 32, aElemNum = 2, aElemDen = 1, bNum = 1, bDen = 2; static constexpr bool kInt = false; };
+// Q4_K: per column and 64-K step the superblock's 16-byte header (d, dmin,
+// 12 bytes of 6-bit scales/mins) and the step's 32 quant bytes.
+template <> struct FmtTraits<FMT_Q4K> { static constexpr int kStep = 64, bRow = 48, aElemNum = 2, aElemDen = 1, bNum = 9, bDen = 16; static constexpr bool kInt = false; };
 
+// LDS of one workgroup.  A stage holds one K-step of the activation and
+// weight tiles.  The staged epilogue writes up to 64 KiB (256 rows x 256 fp8,
+// or 128 rows x 256 fp16) starting at the stage the last K-step released
+// (offset kStage * that buffer) while the next tile's first step is loading
+// into the other buffer, so the 64 KiB from either start must miss the other
+// buffer: stages are padded to 64 KiB, except for the G128 formats, whose
+// per-tile group tables (fp32 scales [group][256 columns], u8 zero-points
+// [group][256 columns]; refilled at each tile's first step) sit between the
+// two stages and are free during the epilogue.
 template <int F> struct Layout {
-    static constexpr int kStage = kTileBytes + kBlockN * FmtTraits<F>::bRow;
     static constexpr bool kG128 = (F == FMT_G128A8 || F == FMT_G128A16);
-    // G128 tables after the two stages: fp32 scales [group][256 columns] and
-    // u8 zero-points [group][256 columns] of the current tile.
-    static constexpr int kScales = 2 * kStage;
+    static constexpr int kNatural = kTileBytes + kBlockN * FmtTraits<F>::bRow;
+    static constexpr int kTables = kG128 ? kMaxG128Groups * kBlockN * 5 : 0;
+    static constexpr int kStage = kG128 ? kNatural : (kNatural > 65536 ? kNatural : 65536);
+    static constexpr int kBufStride = kStage + kTables;  // buffer b starts at b * kBufStride
+    static constexpr int kScales = kStage;
     static constexpr int kZeros = kScales + kMaxG128Groups * kBlockN * 4;
-    static constexpr int kBytes = kG128 ? kZeros + kMaxG128Groups * kBlockN : 2 * kStage;
+    static constexpr int kBytes = 2 * kStage + kTables;
+    static_assert(kStage + kTables >= 65536, "staged epilogue window");
 };
 
 // XOR key of a 128-byte LDS row's 16-byte chunks (bits: k0 = r1, k1 = r2^r4,
@@ -162,7 +178,7 @@ __device__ __forceinline__ void mfma_step(v4f& accf, v4i& acci, const uint4& w0,
         accf[1] = __builtin_fmaf((float)g[1], gscale[1], accf[1]);
         accf[2] = __builtin_fmaf((float)g[2], gscale[2], accf[2]);
         accf[3] = __builtin_fmaf((float)g[3], gscale[3], accf[3]);
-    } else {  // F16 and G128A16 (weights already dequantized to halves)
+    } else {  // F16, G128A16 and Q4K (weights already dequantized to halves)
         accf = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, w0), __builtin_bit_cast(v8h, x0), accf, 0, 0, 0);
         accf = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, w1), __builtin_bit_cast(v8h, x1), accf, 0, 0, 0);
     }
@@ -579,7 +595,12 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs p) {
     // Direct-to-LDS loads: one wave instruction fills 1 KiB of LDS, lane l
     // writing bytes [16l, 16l+16), so each lane loads the global chunk the
     // swizzled layout puts there.
-    constexpr int kBLoadsPerWave = (kBlockN * T::bRow) / 1024 / 8;
+    // Weight loads: wave w issues instructions bj(w, i) of the stage's kBLoads
+    // (a contiguous run per wave; interleaved when kBLoads is not a multiple of 8).
+    constexpr int kBLoads = (kBlockN * T::bRow) / 1024;
+    constexpr int kBLoadsPerWave = (kBLoads + 7) / 8;
+    auto bj_index = [&](int i) { return kBLoads % 8 == 0 ? wave * kBLoadsPerWave + i : i * 8 + wave; };
+    uint32_t b_q4k = 0;  // Q4K: bit i set when load i carries quant bytes
     uint32_t a_off[4], b_off[kBLoadsPerWave];
     const int tiles_m = (p.m + kBlockM - 1) / kBlockM;
     const int gw = group_width(tiles_n);
@@ -597,7 +618,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs p) {
         }
 #pragma unroll
         for (int i = 0; i < kBLoadsPerWave; ++i) {
-            const int o = (wave * kBLoadsPerWave + i) * 1024 + lane * 16;
+            const int o = bj_index(i) * 1024 + lane * 16;
             int row, c;
             if constexpr (T::bRow == 128) {
                 row = o >> 7;
@@ -610,15 +631,24 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs p) {
             if constexpr (E == EPI_GLU) wr = glu_row(n0, row, p.n);
             else wr = min(n0 + row, p.n - 1);
             b_off[i] = (uint32_t)((size_t)wr * ldb + c * 16);
+            if constexpr (F == FMT_Q4K) b_q4k = c > 0 ? b_q4k | (1u << i) : b_q4k & ~(1u << i);
         }
     };
     auto issue = [&](int step, int buf) {
-        const uint32_t base = lds_base + buf * L::kStage;
+        const uint32_t base = lds_base + buf * L::kBufStride;
 #pragma unroll
         for (int i = 0; i < 4; ++i) dma16(pa + (size_t)step * kRowBytes, a_off[i], base + (wave * 4 + i) * 1024);
 #pragma unroll
-        for (int i = 0; i < kBLoadsPerWave; ++i)
-            dma16(pb + (size_t)step * T::bRow, b_off[i], base + kTileBytes + (wave * kBLoadsPerWave + i) * 1024);
+        for (int i = 0; i < kBLoadsPerWave; ++i) {
+            if (kBLoads % 8 != 0 && bj_index(i) >= kBLoads) continue;
+            if constexpr (F == FMT_Q4K) {
+                // superblock step >> 2; quant chunks advance 32 bytes per step
+                const uint32_t qa = (b_q4k >> i) & 1u ? (uint32_t)(step & 3) * 32u : 0u;
+                dma16(pb + (size_t)(step >> 2) * 144, b_off[i] + qa, base + kTileBytes + bj_index(i) * 1024);
+            } else {
+                dma16(pb + (size_t)step * T::bRow, b_off[i], base + kTileBytes + bj_index(i) * 1024);
+            }
+        }
     };
 
     int t = tile_slot(G);
@@ -666,7 +696,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs p) {
                 set_tile(t_next, m0, n0);
                 issue(0, buf ^ 1);
             }
-            const uint8_t* As = lds + buf * L::kStage;
+            const uint8_t* As = lds + buf * L::kBufStride;
             const uint8_t* Bs = As + kTileBytes;
 
             // This wave's four weight fragments for the step.
@@ -679,6 +709,17 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs p) {
                 if constexpr (T::bRow == 128) {
                     w0[bj] = *(const uint4*)(Bs + swz(row, g));
                     w1[bj] = *(const uint4*)(Bs + swz(row, 4 + g));
+                } else if constexpr (F == FMT_Q4K) {
+                    // K slots 8g..8g+7 are the low nibbles of quant bytes
+                    // 8g..8g+7 (group 2*(step&3)), K slots 32+8g.. the high
+                    // nibbles (group 2*(step&3)+1).
+                    const uint4 h = *(const uint4*)(Bs + row * 48);
+                    const uint2 q = *(const uint2*)(Bs + row * 48 + 16 + 8 * g);
+                    float al, bl, ah, bh;
+                    q4k_coeffs(h, 2 * (step & 3), al, bl);
+                    q4k_coeffs(h, 2 * (step & 3) + 1, ah, bh);
+                    w0[bj] = q4k_decode8(q.x & 0x0f0f0f0fu, q.y & 0x0f0f0f0fu, al, bl);
+                    w1[bj] = q4k_decode8((q.x >> 4) & 0x0f0f0f0fu, (q.y >> 4) & 0x0f0f0f0fu, ah, bh);
                 } else {
                     const int kg = (step * T::kStep) >> 7;
                     const int z = g_zero[kg * kBlockN + row];

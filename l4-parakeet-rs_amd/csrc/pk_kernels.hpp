@@ -14,6 +14,7 @@ int launch_gemm(int fmt, int epi, const GemmArgs& args, hipStream_t stream);
 int launch_quantize_static(const void* in, void* out, float inverse_scale, size_t elements, bool int8, hipStream_t s);
 int launch_quantize_rows(int kind, const void* in, void* out, float* scales, int rows, int valid_rows, int k, hipStream_t s);
 int launch_pack_rows(int kind, const void* w, void* out, float* scales, int n, int k, hipStream_t s);
+int launch_q4k_dequant(const uint8_t* blocks, uint16_t* out, int n, int k, hipStream_t s);
 int launch_pack_g128(const void* w, uint32_t* q, uint16_t* scales, uint16_t* zeros, int n, int k, hipStream_t s);
 int launch_layer_norm_quantize(bool int4, const void* in, const void* gamma, const void* beta, void* out, float* scales,
                                void* normalized, int rows, int padded_rows, float epsilon, hipStream_t s);

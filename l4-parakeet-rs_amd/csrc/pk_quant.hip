@@ -260,6 +260,25 @@ __global__ __launch_bounds__(256) void layer_norm_quantize_kernel(const uint16_t
 
 // ---- launchers -------------------------------------------------------------
 
+// Q4_K superblocks -> fp16 [n x k] (linear.cu:459-472): one thread per 8
+// consecutive values of one 32-value group.
+__global__ __launch_bounds__(256) void q4k_dequant_kernel(const uint8_t* __restrict__ blocks, uint16_t* __restrict__ out, int n,
+                                                          int k) {
+    const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+    const size_t per_row = (size_t)k / 8;
+    if (idx >= (size_t)n * per_row) return;
+    const size_t row = idx / per_row;
+    const int t = (int)(idx - row * per_row) * 8;
+    const uint8_t* blk = blocks + (row * (size_t)(k / 256) + (size_t)(t >> 8)) * 144;
+    const int v = t & 255, group = v >> 5;
+    const uint4 h = *(const uint4*)blk;
+    const uint2 q = *(const uint2*)(blk + 16 + (group >> 1) * 32 + (v & 31));
+    float a, b;
+    q4k_coeffs(h, group, a, b);
+    const int sh = (group & 1) * 4;
+    *(uint4*)(out + row * (size_t)k + t) = q4k_decode8((q.x >> sh) & 0x0f0f0f0fu, (q.y >> sh) & 0x0f0f0f0fu, a, b);
+}
+
 int launch_quantize_static(const void* in, void* out, float inverse_scale, size_t elements, bool int8, hipStream_t s) {
     if (elements == 0) return 0;
     const size_t threads = (elements + 7) / 8;
@@ -301,6 +320,13 @@ int launch_layer_norm_quantize(bool int4, const void* in, const void* gamma, con
     else
         layer_norm_quantize_kernel<false><<<padded_rows, 256, 0, s>>>((const uint16_t*)in, (const uint16_t*)gamma, (const uint16_t*)beta,
                                                                        (uint8_t*)out, scales, (uint16_t*)normalized, rows, epsilon);
+    return 0;
+}
+
+int launch_q4k_dequant(const uint8_t* blocks, uint16_t* out, int n, int k, hipStream_t s) {
+    const size_t threads = (size_t)n * (k / 8);
+    if (threads == 0) return 0;
+    hipLaunchKernelGGL(q4k_dequant_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, blocks, out, n, k);
     return 0;
 }
 

@@ -31,6 +31,7 @@ SIGNATURES = {
     "pk_pack_int8_rows": (I, [P, I, I, P, P, P]),
     "pk_pack_int4_rows": (I, [P, I, I, P, P, P]),
     "pk_pack_int4_g128": (I, [P, I, I, P, P, P, P]),
+    "pk_q4_k_dequantize": (I, [P, P, I, I, P]),
     "pk_quantize_fp8": (I, [P, P, F, I, P]),
     "pk_quantize_int8": (I, [P, P, F, I, P]),
     "pk_quantize_fp8_fixed": (I, [P, P, I, F, P]),
@@ -50,6 +51,7 @@ SIGNATURES = {
     "pk_linear_int4_accumulate": (I, [P, P, P, I, I, I, P]),
     "pk_linear_int4g128": (I, [P, P, P, P, P, P, I, I, I, I, P]),
     "pk_linear_int4g128_a8": (I, [P, P, P, P, P, P, P, I, I, I, I, P]),
+    "pk_q4_k_linear_epilogue": (I, [P, P, P, P, I, I, I, I, P]),
     "pk_ffn_expand_fp8": (I, [P, P, P, P, P, I, F, I, P]),
     "pk_ffn_expand_fp8_packed": (I, [P, P, P, P, P, I, F, I, P]),
     "pk_ffn_expand_int4_sparse": (I, [P, P, P, P, P, I, F, I, P]),
@@ -158,5 +160,5 @@ def gemm(fmt, epi, a, b, m, n, k, out, *, w_scales=None, row_scales=None, in_sca
          stream=stream)
 
 
-FMT_FP8, FMT_I8, FMT_S4, FMT_G128A8, FMT_F16, FMT_G128A16, FMT_I8_SKIP = range(7)
+FMT_FP8, FMT_I8, FMT_S4, FMT_G128A8, FMT_F16, FMT_G128A16, FMT_I8_SKIP, FMT_Q4K = range(8)
 EPI_F16, EPI_F8, EPI_F8_24, EPI_F32, EPI_I32 = range(5)

@@ -381,6 +381,81 @@ def test_int4g128_a8_exact(pk, orc, m, n, k):
     assert np.array_equal(host(out), ref)
 
 
+# ---- Q4_K ----------------------------------------------------------------------------------
+
+def q4k_random_blocks(n, k, seed):
+    """Raw Q4_K blocks with arbitrary scale/min/quant bytes and finite d, dmin."""
+    rng = np.random.default_rng(seed)
+    blocks = rng.integers(0, 256, (n, k // 256, 144), dtype=np.uint8)
+    d = (rng.random((n, k // 256, 2)) * 2e-3).astype(np.float16)
+    blocks[..., 0:4] = d.view(np.uint8).reshape(n, k // 256, 4)
+    return blocks
+
+
+@pytest.mark.parametrize("source", ["encoded", "random"])
+def test_q4k_dequantize_exact(pk, orc, source):
+    n, k = 40, 1024
+    note(f"q4k dequantize {source} n={n} k={k}")
+    blocks = orc.q4k_encode(weights(n, k, 130)) if source == "encoded" else q4k_random_blocks(n, k, 131)
+    out = empty((n, k), torch.float16)
+    pk.call("pk_q4_k_dequantize", dev(blocks), out, n, k)
+    ref = orc.q4k_dequant(blocks).astype(np.float16)
+    assert np.array_equal(host(out).view(np.uint16), ref.view(np.uint16))
+
+
+@pytest.mark.parametrize("m,n,k,act", [(300, 272, 512, 0), (97, 1024, 1024, 2), (130, 256, 768, 1)])
+def test_q4k_linear_epilogue(pk, orc, m, n, k, act):
+    note(f"q4k linear m={m} n={n} k={k} act={act}")
+    x = acts(m, k, 132, outliers=False)
+    blocks = orc.q4k_encode(weights(n, k, 133))
+    bias = (np.random.default_rng(134).standard_normal(n) * 0.1).astype(np.float32)
+    out = empty((m, n), torch.float16)
+    pk.call("pk_q4_k_linear_epilogue", dev(x), dev(blocks), dev(bias), out, m, n, k, act)
+    ref = orc.epilogue_linear(orc.gemm_q4k(x, blocks), bias=bias, activation=act)
+    assert_close(host(out), ref)
+
+
+def test_q4k_linear_multi_tile(pk):
+    """More 256x256 tiles than workgroups (each runs several): fp16 output of
+    the fused kernel against the device dequantization (pinned bit-exact
+    above) followed by an fp32 torch matmul."""
+    m, n, k = 10240, 2048, 512
+    note(f"q4k linear multi-tile m={m} n={n} k={k}")
+    gen = torch.Generator(device="cuda").manual_seed(135)
+    x = torch.randn((m, k), device="cuda", generator=gen).half()
+    blocks = torch.from_numpy(q4k_random_blocks(n, k, 136)).cuda()
+    deq = empty((n, k), torch.float16)
+    pk.call("pk_q4_k_dequantize", blocks, deq, n, k)
+    out = empty((m, n), torch.float16)
+    pk.call("pk_q4_k_linear_epilogue", x, blocks, None, out, m, n, k, 0)
+    torch.backends.cuda.matmul.allow_tf32 = False
+    ref = (x.float() @ deq.float().t()).half().float()
+    assert_close(host(out).astype(np.float32), ref.cpu().numpy())
+
+
+@pytest.mark.parametrize("fmt", ["g128a16", "g128a8"])
+def test_g128_staged_fp16_multi_tile(pk, orc, fmt):
+    """fp16 outputs leave through the LDS staging area while the next tile's
+    first K-step loads; with more tiles than workgroups they must equal the
+    fp32 outputs (register epilogue) rounded to fp16, bit for bit."""
+    m, n, k = 10240, 2048, 512
+    note(f"g128 staged fp16 {fmt} m={m} n={n} k={k}")
+    w = weights(n, k, 137)
+    q, s, z = orc.pack_int4_g128(w)
+    rng = np.random.default_rng(138)
+    if fmt == "g128a16":
+        a = dev(acts(m, k, 139, outliers=False))
+        f, rs = pk.FMT_G128A16, None
+    else:
+        a = torch.from_numpy(rng.integers(-127, 128, (m, k), dtype=np.int8)).cuda()
+        f, rs = pk.FMT_G128A8, dev((rng.random(m) * 1e-2 + 1e-3).astype(np.float32))
+    o16 = empty((m, n), torch.float16)
+    o32 = empty((m, n), torch.float32)
+    for epi, o in ((pk.EPI_F16, o16), (pk.EPI_F32, o32)):
+        pk.gemm(f, epi, a, dev(q), m, n, k, o, row_scales=rs, g_scales=dev(s), g_zeros=dev(z))
+    assert np.array_equal(host(o16).view(np.uint16), host(o32).astype(np.float16).view(np.uint16))
+
+
 # ---- joint ---------------------------------------------------------------------------------
 
 @pytest.mark.parametrize("int8", [False, True])
