@@ -273,6 +273,24 @@ int32_t pk_joint_gemv(const void* weight, int32_t weight_int8, const float* w_sc
                       int32_t outputs, int32_t hidden, int32_t token_outputs, int32_t durations,
                       int32_t steps, int32_t enc_stride, void* stream);
 
+/* The greedy TDT loop's joint steps between two emitted tokens
+ * (decoder.cu:690-783 with the prediction vector fixed), in one persistent
+ * launch: from frame state[0] with state[1] symbols already added at it,
+ * repeat { scores of frame t; token / duration decision as pk_joint_gemv;
+ * symbols += 1; t += duration; if duration != 0 or symbols == max_symbols
+ * { if duration == 0, t += 1; symbols = 0 } } until a token other than the
+ * blank (id token_outputs - 1) is chosen or t >= frames.  state (device
+ * int32[4]) returns {t, symbols, token or -1 when the frames ran out, joint
+ * steps run}; state[2] = -2 if the workgroups failed to meet at a barrier
+ * (not co-resident).  The weights stay in registers for the whole scan:
+ * hidden % 128 == 0, hidden <= 1024, durations <= 8, token_outputs +
+ * durations <= 2048.  workspace is a device uint32[512] the call overwrites
+ * (the per-step decision words the workgroups exchange). */
+int32_t pk_joint_scan(const void* weight, int32_t weight_int8, const float* w_scales, const float* bias,
+                      const uint16_t* enc, const float* pred, int32_t outputs, int32_t hidden,
+                      int32_t token_outputs, int32_t durations, int32_t frames, int32_t enc_stride,
+                      int32_t max_symbols, int32_t* state, uint32_t* workspace, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -441,4 +441,26 @@ int32_t pk_joint_gemv(const void* w, int32_t w_int8, const float* w_scales, cons
     return check_launch("joint_gemv");
 }
 
+int32_t pk_joint_scan(const void* w, int32_t w_int8, const float* w_scales, const float* bias, const uint16_t* enc, const float* pred,
+                      int32_t outputs, int32_t hidden, int32_t token_outputs, int32_t durations, int32_t frames, int32_t enc_stride,
+                      int32_t max_symbols, int32_t* state, uint32_t* workspace, void* stream) {
+    if (outputs <= 0 || hidden <= 0 || hidden > 1024 || hidden % 128 || token_outputs <= 0 || durations <= 0 || durations > 8 ||
+        token_outputs + durations > outputs || token_outputs + durations > 2048 || token_outputs > 65535 || frames < 0 ||
+        enc_stride < hidden || max_symbols <= 0) {
+        set_error("invalid joint scan shape outputs=%d hidden=%d tokens=%d durations=%d frames=%d stride=%d max_symbols=%d", outputs,
+                  hidden, token_outputs, durations, frames, enc_stride, max_symbols);
+        return PK_E_SHAPE;
+    }
+    if (!need(w, "weight") || !need(enc, "enc") || !need(pred, "pred") || !need(state, "state") || !need(workspace, "workspace"))
+        return PK_E_ARG;
+    if (w_int8 && !need(w_scales, "w_scales")) return PK_E_ARG;
+    if (((uintptr_t)w | (uintptr_t)enc | (uintptr_t)workspace) & 7 || enc_stride % 2) {
+        set_error("joint scan weight, enc and workspace must be 8-byte aligned, enc_stride even");
+        return PK_E_ALIGN;
+    }
+    launch_joint_scan(w, w_int8, w_scales, bias, enc, pred, outputs, hidden, token_outputs, durations, frames, enc_stride, max_symbols,
+                      state, workspace, STREAM);
+    return check_launch("joint_scan");
+}
+
 }  // extern "C"

@@ -80,6 +80,234 @@ __global__ __launch_bounds__(256) void joint_decide_kernel(const float* __restri
     }
 }
 
+// ---- persistent blank scan (decoder.cu:690-783) ---------------------------------
+//
+// Between two emitted tokens the prediction vector is fixed, so the greedy TDT
+// loop is a sequence of joint steps that only move the frame index.  One
+// persistent launch runs those steps.  Every active workgroup keeps its slice
+// of W in registers for the whole scan (8 rows per wave; lane l holds
+// k = 2l + 128j, j < hidden/128).  Per step it scores its rows for the current
+// frame and publishes ONE 64-bit word: its best token as an order-preserving
+// key (score bits, then 0xffff - id), the duration decision when it owns the
+// duration rows, and the step's tag.  The words double as the grid barrier:
+// each workgroup polls all of them in parallel (one lane per workgroup) until
+// every tag is the current one, then takes the maximum.  So a step costs about
+// one memory round trip; the encoder rows of every frame the decision can move
+// to are loaded while the poll waits.  The scan stops after the first
+// non-blank token (the prediction network must run before the next step) or
+// when the frames run out.
+//
+// Logical row i of the scan is joint row T + i for i < D (the durations, all
+// in workgroup 0's wave 0) and row i - D for the tokens.  Workgroups are
+// dispatched round-robin over the 8 XCDs; only those with blockIdx % 8 == 0
+// work, so the active ones share one XCD's L2.
+
+constexpr int kScanRows = 8;      // joint rows per wave
+constexpr int kScanCand = 8;      // frames the decision can move to: +0 .. +7
+constexpr int kScanMaxBlocks = 64;
+constexpr uint32_t kScanSpinLimit = 1u << 22;
+
+struct ScanArgs {
+    const void* w;
+    const float* w_scales;
+    const float* bias;
+    const uint16_t* enc;
+    const float* pred;
+    int* state;
+    uint32_t* ws;  // [0] abort flag; words 8.. : 2 x kScanMaxBlocks published u64 (by step parity)
+    int outputs, hidden, token_outputs, durations, frames, enc_stride, max_symbols;
+};
+
+__device__ __forceinline__ uint32_t ordered_bits(float score) {
+    if (score == 0.0f) score = 0.0f;  // -0 and +0 tie on the id
+    const uint32_t bits = __float_as_uint(score);
+    return (bits & 0x80000000u) ? ~bits : (bits ^ 0x80000000u);
+}
+
+// KP = hidden / 128 pairs of k per lane.
+template <bool kInt8, int KP>
+__global__ __launch_bounds__(256) void joint_scan_kernel(ScanArgs p) {
+    if (blockIdx.x & 7) return;
+    __shared__ float best_s[4];
+    __shared__ int best_i[4];
+    __shared__ int dur_s;
+    const int blk = blockIdx.x >> 3;
+    const int nblocks = gridDim.x >> 3;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int T = p.token_outputs, D = p.durations;
+    unsigned long long* const pub = (unsigned long long*)(p.ws + 8) + blk;
+    const unsigned long long* const watch = (const unsigned long long*)(p.ws + 8) + (lane < nblocks ? lane : 0);
+    const bool watcher = lane < nblocks;
+
+    uint32_t w[kScanRows][KP];
+    float wsc[kScanRows], wb[kScanRows];
+    int rid[kScanRows];
+#pragma unroll
+    for (int r = 0; r < kScanRows; ++r) {
+        const int i = (blk * 4 + wave) * kScanRows + r;
+        rid[r] = i < D ? T + i : (i < T + D ? i - D : -1);
+        const int row = rid[r] < 0 ? p.outputs - 1 : rid[r];
+#pragma unroll
+        for (int j = 0; j < KP; ++j) {
+            const int k = 2 * lane + 128 * j;
+            if constexpr (kInt8) w[r][j] = *(const uint16_t*)((const int8_t*)p.w + (size_t)row * p.hidden + k);
+            else w[r][j] = *(const uint32_t*)((const uint16_t*)p.w + (size_t)row * p.hidden + k);
+        }
+        wsc[r] = kInt8 ? p.w_scales[row] : 1.0f;
+        wb[r] = p.bias ? p.bias[row] : 0.0f;
+    }
+    float pv[2 * KP];
+#pragma unroll
+    for (int j = 0; j < KP; ++j) {
+        pv[2 * j] = p.pred[2 * lane + 128 * j];
+        pv[2 * j + 1] = p.pred[2 * lane + 128 * j + 1];
+    }
+    auto enc_pairs = [&](int f, uint32_t (&e)[KP]) {
+        const uint16_t* row = p.enc + (size_t)min(f, p.frames - 1) * p.enc_stride + 2 * lane;
+#pragma unroll
+        for (int j = 0; j < KP; ++j) e[j] = *(const uint32_t*)(row + 128 * j);
+    };
+
+    int frame = p.state[0], symbols = p.state[1];
+    int token = -1, steps = 0;
+    bool failed = false;
+    const int blank = T - 1;
+    uint32_t ev[KP];  // the current frame's encoder pairs
+    enc_pairs(frame, ev);
+
+    while (frame < p.frames) {
+        float bs = -__builtin_huge_valf(), dbest = 0.0f;
+        int bi = 0x7fffffff, dur = 0;
+        {
+            float x[2 * KP];
+#pragma unroll
+            for (int j = 0; j < KP; ++j) {
+                x[2 * j] = __builtin_fmaxf(h2f((uint16_t)(ev[j] & 0xffffu)) + pv[2 * j], 0.0f);
+                x[2 * j + 1] = __builtin_fmaxf(h2f((uint16_t)(ev[j] >> 16)) + pv[2 * j + 1], 0.0f);
+            }
+#pragma unroll
+            for (int r = 0; r < kScanRows; ++r) {
+                float sum = 0.0f;
+#pragma unroll
+                for (int j = 0; j < KP; ++j) {
+                    float w0, w1;
+                    if constexpr (kInt8) {
+                        w0 = (float)(int8_t)(w[r][j] & 0xffu);
+                        w1 = (float)(int8_t)((w[r][j] >> 8) & 0xffu);
+                    } else {
+                        w0 = h2f((uint16_t)(w[r][j] & 0xffffu));
+                        w1 = h2f((uint16_t)(w[r][j] >> 16));
+                    }
+                    sum = __builtin_fmaf(w0, x[2 * j], sum);
+                    sum = __builtin_fmaf(w1, x[2 * j + 1], sum);
+                }
+#pragma unroll
+                for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
+                const float score = __builtin_fmaf(wsc[r], sum, wb[r]);
+                const int id = rid[r];
+                if (id >= T) {  // duration id - T, first maximum wins
+                    if (id == T || score > dbest) { dbest = score; dur = id - T; }
+                } else if (id >= 0) {
+                    if (score > bs || (score == bs && id < bi)) { bs = score; bi = id; }
+                }
+            }
+        }
+        if (lane == 0) {
+            best_s[wave] = bs;
+            best_i[wave] = bi;
+            if (blk == 0 && wave == 0) dur_s = dur;
+        }
+        __syncthreads();
+        const int par = (steps & 1) * kScanMaxBlocks;
+        const uint32_t tag = (uint32_t)(steps + 1) & 0x1fffu;
+        if (threadIdx.x == 0) {
+            for (int i = 1; i < 4; ++i)
+                if (best_s[i] > bs || (best_s[i] == bs && best_i[i] < bi)) { bs = best_s[i]; bi = best_i[i]; }
+            const bool any = bi != 0x7fffffff;
+            const uint32_t lo = ((any ? 0xffffu - (uint32_t)bi : 0u) << 16) | ((uint32_t)(blk == 0 ? dur_s : 0) << 13) | tag;
+            const unsigned long long word = any ? ((unsigned long long)ordered_bits(bs) << 32) | lo : (unsigned long long)lo;
+            __hip_atomic_store(pub + par, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        // Encoder rows of every frame the decision can move to, while polling.
+        uint32_t cand[kScanCand][KP];
+#pragma unroll
+        for (int c = 0; c < kScanCand; ++c) enc_pairs(frame + c, cand[c]);
+        // Poll: lane b watches workgroup b's word for this step's tag.
+        unsigned long long mine = 0;
+        uint32_t spins = 0;
+        while (true) {
+            mine = __hip_atomic_load(watch + par, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const bool ready = !watcher || ((uint32_t)mine & 0x1fffu) == tag;
+            if (__builtin_amdgcn_ballot_w64(!ready) == 0) break;
+            if ((++spins & 63) == 0 &&
+                (spins > kScanSpinLimit || __hip_atomic_load(&p.ws[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u)) {
+                __hip_atomic_store(&p.ws[0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                failed = true;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+        if (failed) break;
+        // Workgroup 0's word carries the duration; the maximum word the token.
+        dur = (int)(((uint32_t)__shfl(mine, 0, 64) >> 13) & 7u);
+        unsigned long long best = watcher ? mine : 0ull;
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+            const unsigned long long o = __shfl_xor(best, off, 64);
+            best = o > best ? o : best;
+        }
+        token = (int)(0xffffu - (((uint32_t)best) >> 16));
+        // the LDS reduction slots are reused next step
+        __syncthreads();
+        ++steps;
+        ++symbols;
+        const int prev = frame;
+        frame += dur;
+        if (dur != 0 || symbols == p.max_symbols) {
+            if (dur == 0) ++frame;
+            symbols = 0;
+        }
+        if (token != blank) break;
+        token = -1;
+        const int c = frame - prev;
+#pragma unroll
+        for (int cc = 0; cc < kScanCand; ++cc)
+            if (cc == c) {
+#pragma unroll
+                for (int j = 0; j < KP; ++j) ev[j] = cand[cc][j];
+            }
+    }
+    if (blk == 0 && threadIdx.x == 0) {
+        p.state[0] = frame;
+        p.state[1] = symbols;
+        p.state[2] = failed ? -2 : token;
+        p.state[3] = steps;
+    }
+}
+
+__global__ void scan_clear_kernel(uint32_t* ws) { ws[threadIdx.x] = 0u; }
+
+int launch_joint_scan(const void* w, int w_int8, const float* w_scales, const float* bias, const uint16_t* enc, const float* pred,
+                      int outputs, int hidden, int token_outputs, int durations, int frames, int enc_stride, int max_symbols,
+                      int* state, uint32_t* workspace, hipStream_t s) {
+    const int active = (token_outputs + durations + 4 * kScanRows - 1) / (4 * kScanRows);
+    ScanArgs a{w, w_scales, bias, enc, pred, state, workspace, outputs, hidden, token_outputs, durations, frames, enc_stride, max_symbols};
+    scan_clear_kernel<<<1, kJointScanWorkspaceWords, 0, s>>>(workspace);
+    const dim3 grid(8 * active);
+    switch (hidden >> 7) {
+#define PK_SCAN_CASE(KP)                                                              \
+    case KP:                                                                          \
+        if (w_int8) joint_scan_kernel<true, KP><<<grid, 256, 0, s>>>(a);             \
+        else joint_scan_kernel<false, KP><<<grid, 256, 0, s>>>(a);                   \
+        break;
+        PK_SCAN_CASE(1) PK_SCAN_CASE(2) PK_SCAN_CASE(3) PK_SCAN_CASE(4)
+        PK_SCAN_CASE(5) PK_SCAN_CASE(6) PK_SCAN_CASE(7) PK_SCAN_CASE(8)
+#undef PK_SCAN_CASE
+    default: break;
+    }
+    return 0;
+}
+
 int launch_joint(const void* w, int w_int8, const float* w_scales, const float* bias, const void* enc, const float* pred,
                  float* scores, int* decision, int outputs, int hidden, int token_outputs, int durations, int steps,
                  int enc_stride, hipStream_t s) {

@@ -22,6 +22,11 @@ int launch_joint(const void* w, int w_int8, const float* w_scales, const float* 
                  float* scores, int* decision, int outputs, int hidden, int token_outputs, int durations, int steps,
                  int enc_stride, hipStream_t s);
 
+constexpr int kJointScanWorkspaceWords = 512;
+int launch_joint_scan(const void* w, int w_int8, const float* w_scales, const float* bias, const uint16_t* enc, const float* pred,
+                      int outputs, int hidden, int token_outputs, int durations, int frames, int enc_stride, int max_symbols,
+                      int* state, uint32_t* workspace, hipStream_t s);
+
 void set_error(const char* fmt, ...);
 int cu_count();
 int launch_sparse24_contract(const uint8_t* data, const uint8_t* meta, const uint8_t* w, const float* w_scales, float in_scale,

@@ -65,6 +65,7 @@ SIGNATURES = {
     "pk_ffn_contract_int8_rowskip": (I, [P, P, P, P, P, I, P, P]),
     "pk_gemm": (I, [I, I, P, P, I, I, I, P, P, F, P, P, F, F, I, P, P, P, P, I, P]),
     "pk_joint_gemv": (I, [P, I, P, P, P, P, P, P, I, I, I, I, I, I, P]),
+    "pk_joint_scan": (I, [P, I, P, P, P, P, I, I, I, I, I, I, I, P, P, P]),
 }
 
 

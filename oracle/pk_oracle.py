@@ -472,3 +472,25 @@ def joint_decide(scores, token_outputs=1025, durations=5):
     lib().orc_joint_decide(_p(scores), token_outputs, durations, ctypes.byref(tok),
                            ctypes.byref(dur))
     return tok.value, dur.value
+
+
+def joint_scan(scores_of_frame, frames, frame=0, symbols=0, token_outputs=1025, durations=5,
+               max_symbols=10):
+    """decoder.cu:733-783 with the prediction vector fixed: greedy TDT joint
+    steps from (frame, symbols) until a non-blank token (id token_outputs-1 is
+    the blank) or the frames run out.  scores_of_frame(t) returns the fp32
+    scores of frame t.  Returns (frame, symbols, token or -1, steps)."""
+    blank = token_outputs - 1
+    steps = 0
+    while frame < frames:
+        tok, dur = joint_decide(scores_of_frame(frame), token_outputs, durations)
+        steps += 1
+        symbols += 1
+        frame += dur
+        if dur != 0 or symbols == max_symbols:
+            if dur == 0:
+                frame += 1
+            symbols = 0
+        if tok != blank:
+            return frame, symbols, tok, steps
+    return frame, symbols, -1, steps

@@ -578,3 +578,45 @@ def test_ffn_contract_fp8_sparse(pk, orc):
     delta_ref = ref.astype(np.float32) - residual.astype(np.float32)
     delta_got = host(out).astype(np.float32) - residual.astype(np.float32)
     assert_close(delta_got, delta_ref, tol=2e-2)
+
+
+@pytest.mark.parametrize("int8", [False, True])
+def test_joint_scan(pk, orc, int8):
+    """Whole utterance through repeated scans (the prediction vector redrawn
+    after each token, as the prediction network would) against the oracle loop
+    over the oracle's per-frame scores."""
+    note(f"joint scan int8={int8}")
+    T, D, hidden, frames = 1025, 5, 640, 160
+    outputs = T + D
+    rng = np.random.default_rng(150 + int8)
+    w = (rng.standard_normal((outputs, hidden)) * 0.05).astype(np.float16)
+    bias = (rng.standard_normal(outputs) * 0.1).astype(np.float32)
+    bias[T - 1] += 2.2  # blank-dominated frames, as in real audio
+    enc = (rng.standard_normal((frames, hidden)) * 0.5).astype(np.float16)
+    if int8:
+        wq, ws = orc.quantize_int8_rows(w)
+        d_w, d_ws = dev(wq), dev(ws)
+        score = lambda t, pred: orc.joint_scores_i8(wq, ws, bias, enc[t], pred)
+    else:
+        d_w, d_ws = dev(w), None
+        score = lambda t, pred: orc.joint_scores_f16(w, bias, enc[t], pred)
+    d_bias, d_enc = dev(bias), dev(enc)
+    state = torch.zeros(4, dtype=torch.int32, device="cuda")
+    work = torch.zeros(512, dtype=torch.int32, device="cuda")
+    frame = symbols = 0
+    tokens, scans = [], 0
+    while True:
+        pred = (rng.standard_normal(hidden) * 0.3).astype(np.float32)
+        ref = orc.joint_scan(lambda t: score(t, pred), frames, frame, symbols)
+        state[0], state[1] = frame, symbols
+        pk.call("pk_joint_scan", d_w, int(int8), d_ws, d_bias, d_enc, dev(pred), outputs, hidden, T, D,
+                frames, hidden, 10, state, work)
+        got = tuple(int(v) for v in host(state))
+        assert got == ref, f"scan {scans}: {got} != {ref}"
+        scans += 1
+        frame, symbols, tok, _ = got
+        if tok < 0:
+            break
+        tokens.append(tok)
+    note(f"joint scan: {scans} scans, {len(tokens)} tokens")
+    assert 3 <= len(tokens) < frames

@@ -341,3 +341,31 @@ def test_joint_matches_numpy(oracle):
     tie[[7, 9]] = 5.0
     tie[[1027, 1028]] = 1.0
     assert oracle.joint_decide(tie) == (7, 2)
+
+
+def _scores(token_outputs, durations, token, dur, margin=1.0):
+    s = np.zeros(token_outputs + durations, np.float32)
+    s[token] = margin
+    s[token_outputs + dur] = margin
+    return s
+
+
+def test_joint_scan_frame_rules(oracle):
+    """decoder.cu:773-783 closed forms: blank with duration d advances d frames
+    per step; blank with duration 0 advances one frame every max_symbols
+    steps; a token stops the scan after its own advance."""
+    T, D, F = 11, 5, 17
+    blank = T - 1
+    for d in range(1, D):
+        out = oracle.joint_scan(lambda t: _scores(T, D, blank, d), F, token_outputs=T, durations=D)
+        assert out == (F + (-F) % d, 0, -1, -(-F // d))
+    out = oracle.joint_scan(lambda t: _scores(T, D, blank, 0), F, token_outputs=T, durations=D,
+                            max_symbols=3)
+    assert out == (F, 0, -1, 3 * F)
+    # token 4 at frame 6 with duration 0: stays on frame 6, one symbol added
+    f = lambda t: _scores(T, D, 4, 0) if t == 6 else _scores(T, D, blank, 2)
+    assert oracle.joint_scan(f, F, token_outputs=T, durations=D) == (6, 1, 4, 4)
+    # resuming at frame 6 with 9 symbols: the tenth symbol forces the advance
+    assert oracle.joint_scan(f, F, frame=6, symbols=9, token_outputs=T, durations=D) == (7, 0, 4, 1)
+    # ties: lower token id and first duration maximum win
+    assert oracle.joint_decide(np.zeros(T + D, np.float32), T, D) == (0, 0)
