@@ -229,6 +229,159 @@ def joint_bench(pk, torch, stream, reps=2000):
     return out
 
 
+def joint_streaming(pk, torch, stream, copies=512, reps=5):
+    """The joint GEMV kernel streaming INT8 weights from HBM: `copies` joint
+    matrices stacked as one [copies*1030 x 640] weight (337 MB, beyond the
+    256 MB MALL), one frame, one launch.  Bytes = weights + scales + bias +
+    scores written."""
+    outputs, hidden = 1030 * copies, 640
+    g = torch.Generator(device="cuda")
+    g.manual_seed(8)
+    w = torch.randint(-127, 128, (outputs, hidden), generator=g, device="cuda", dtype=torch.int8)
+    ws = torch.rand(outputs, generator=g, device="cuda") * 0.01
+    bias = torch.randn(outputs, generator=g, device="cuda")
+    enc = torch.randn((1, hidden), generator=g, device="cuda").half()
+    pred = torch.randn(hidden, generator=g, device="cuda")
+    scores = torch.empty(outputs, dtype=torch.float32, device="cuda")
+    run = lambda: pk.call("pk_joint_gemv", w, 1, ws, bias, enc, pred, scores, None, outputs, hidden, 1025, 5, 1,
+                          hidden, stream=stream)
+    run()
+    ms = time_events(torch, run, reps, stream)
+    nbytes = outputs * hidden + outputs * 12
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"rows": outputs, "bytes": nbytes, "us": round(ms * 1e3, 2), "GBps": round(gbs, 1),
+            "pct_hbm": round(100.0 * gbs / 8000.0, 2)}
+
+
+def roof(flops, nbytes, peak_tops):
+    """Roofline bound of one launch: min(MFMA peak, arithmetic intensity x 8 TB/s)."""
+    return min(peak_tops, flops / nbytes * 8.0)  # TFLOP/s
+
+
+def config_results(pk, torch, stream, reps=10):
+    """BASELINE configs 1-4 on the GPU: per GEMM TOPS, GB/s (algorithmic bytes)
+    and the fraction of its roofline min(5.0 PF, AI x 8 TB/s)."""
+    dev = "cuda"
+    g = torch.Generator(device=dev)
+    g.manual_seed(99)
+
+    def timed(fn):
+        fn()
+        return time_events(torch, fn, reps, stream)
+
+    def entry(ms, flops, nbytes, useful=None):
+        tops = flops / (ms * 1e-3) / 1e12
+        r = roof(flops, nbytes, PEAK["fp8"])
+        e = {"us": round(ms * 1e3, 1), "TOPS": round(tops, 1), "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1),
+             "roofline_TOPS": round(r, 1), "frac": round(tops / r, 3)}
+        if useful is not None:
+            e["useful_TOPS"] = round(useful / (ms * 1e-3) / 1e12, 1)
+        return e
+
+    def packed(kind, n, k):
+        w16 = (torch.randn((n, k), generator=g, device=dev) * 0.02).half()
+        if kind == "fp8":
+            q, s = torch.empty((n, k), dtype=torch.uint8, device=dev), torch.empty(n, device=dev)
+            pk.call("pk_pack_fp8_rows", w16, n, k, q, s)
+            return q, s, None
+        if kind == "int8":
+            q, s = torch.empty((n, k), dtype=torch.int8, device=dev), torch.empty(n, device=dev)
+            pk.call("pk_pack_int8_rows", w16, n, k, q, s)
+            return q, s, None
+        q = torch.empty((n, k // 8), dtype=torch.int32, device=dev)
+        s = torch.empty((n, k // 128), dtype=torch.float16, device=dev)
+        z = torch.empty((n, k // 128), dtype=torch.float16, device=dev)
+        pk.call("pk_pack_int4_g128", w16, n, k, q, s, z)
+        return q, s, z
+
+    def rows_q(kind, t, k, src=None):
+        x = torch.randn((t, k), generator=g, device=dev).half() if src is None else src
+        q = torch.empty((t, k), dtype=torch.uint8 if kind == 0 else torch.int8, device=dev)
+        sc = torch.empty(t, device=dev)
+        pk.call("pk_quantize_rows", kind, x, q, sc, t, t, k)
+        return q, sc
+
+    out = {}
+    # C1: INT8 FF1 1024 -> 4096 over 750 frames, per-token dynamic scales, fp32 out
+    t, n, k = 750, 4096, 1024
+    xq, xs = rows_q(1, t, k)
+    wq, ws, _ = packed("int8", n, k)
+    y = torch.empty((t, n), device=dev)
+    ms = timed(lambda: pk.call("pk_linear_int8_dyn", xq, xs, wq, ws, None, y, 1, t, n, k, stream=stream))
+    out["c1_int8_750x1024x4096_f32"] = entry(ms, 2 * t * n * k, t * k + n * k + 4 * (n + t) + 4 * t * n)
+    # C2: one layer at T=7500, FP8 weights, per-row FP8 activations
+    t = 7500
+    x8, xs8 = rows_q(0, t, 4096)
+    x8d = x8[:, :1024].contiguous()
+    o8 = torch.empty((t, 4096), dtype=torch.uint8, device=dev)
+    o16 = torch.empty((t, 3072), dtype=torch.float16, device=dev)
+    st = torch.randn((t, 1024), generator=g, device=dev).half()
+    c2 = {}
+    tot_ms = tot_f = 0.0
+    for name, n, k, kind in (("qkv", 3072, 1024, "f16"), ("attn_out", 1024, 1024, "res"), ("ff1", 4096, 1024, "f8"),
+                             ("ff2", 1024, 4096, "res_half"), ("pw1", 2048, 1024, "f16")):
+        q, s, _ = packed("fp8", n, k)
+        a = x8 if k == 4096 else x8d
+        if kind == "f8":
+            fn = lambda: pk.gemm(pk.FMT_FP8, pk.EPI_F8, a, q, t, n, k, o8, w_scales=s, row_scales=xs8, stream=stream)
+            ob = t * n
+        elif kind == "f16":
+            fn = lambda: pk.gemm(pk.FMT_FP8, pk.EPI_F16, a, q, t, n, k, o16, w_scales=s, row_scales=xs8, stream=stream)
+            ob = 2 * t * n
+        else:
+            fn = lambda: pk.gemm(pk.FMT_FP8, pk.EPI_F16, a, q, t, n, k, st, w_scales=s, row_scales=xs8, residual=st,
+                                 out_scale=0.5 if kind == "res_half" else 1.0, res_scale=1.0, stream=stream)
+            ob = 4 * t * n
+        ms = timed(fn)
+        f = 2 * t * n * k
+        c2[name] = entry(ms, f, t * k + n * k + 4 * (n + t) + ob)
+        tot_ms += ms
+        tot_f += f
+    c2["layer_TOPS"] = round(tot_f / (tot_ms * 1e-3) / 1e12, 1)
+    out["c2_fp8_layer_T7500"] = c2
+    # C3: INT4 g128 FF1 / FF2, fp16 activations (and the INT8 x INT4 mixed variant), fp16 out
+    c3 = {}
+    for t in (750, 7500, 45000):
+        for name, n, k in (("ff1", 4096, 1024), ("ff2", 1024, 4096)):
+            q, s, z = packed("int4g128", n, k)
+            x = torch.randn((t, k), generator=g, device=dev).half()
+            o = torch.empty((t, n), dtype=torch.float16, device=dev)
+            wb = n * k // 2 + 4 * n * (k // 128)
+            ms = timed(lambda: pk.gemm(pk.FMT_G128A16, pk.EPI_F16, x, q, t, n, k, o, g_scales=s, g_zeros=z,
+                                       stream=stream))
+            c3[f"{name}_a16_T{t}"] = entry(ms, 2 * t * n * k, 2 * t * k + wb + 2 * t * n)
+            xq, xs = rows_q(1, t, k, x)
+            ms = timed(lambda: pk.gemm(pk.FMT_G128A8, pk.EPI_F16, xq, q, t, n, k, o, row_scales=xs, g_scales=s,
+                                       g_zeros=z, stream=stream))
+            c3[f"{name}_a8_T{t}"] = entry(ms, 2 * t * n * k, t * k + 4 * t + wb + 2 * t * n)
+            del x, xq, o
+    out["c3_int4_g128"] = c3
+    # C4: activation-sparse FF2 (INT8 rows, exact zero blocks skipped), fp32 out
+    t, n, k = 7500, 1024, 4096
+    wq, ws, _ = packed("int8", n, k)
+    y = torch.empty((t, n), device=dev)
+    counts = torch.zeros(2, dtype=torch.int32, device=dev)
+    c4 = {}
+    for sp in (0.5, 0.8, 0.9, 0.95):
+        a = torch.randn((t, k), generator=g, device=dev).half()
+        keep = max(1, int(round(k * (1.0 - sp))))
+        thr = a.abs().float().kthvalue(k - keep + 1, dim=1, keepdim=True).values
+        a = torch.where(a.abs().float() >= thr, a, torch.zeros_like(a))
+        xq, xs = rows_q(1, t, k, a)
+        counts.zero_()
+        pk.call("pk_ffn_contract_int8_rowskip", xq, xs, wq, ws, y, t, counts, stream=stream)
+        torch.cuda.synchronize()
+        skipped, total = (int(v) for v in counts.cpu().tolist())
+        ms = timed(lambda: pk.call("pk_ffn_contract_int8_rowskip", xq, xs, wq, ws, y, t, None, stream=stream))
+        f = 2 * t * n * k
+        e = entry(ms, f, t * k + 4 * t + n * k + 4 * n + 4 * t * n, useful=(1.0 - sp) * f)
+        e["skip_rate"] = round(skipped / max(total, 1), 4)
+        c4[f"sparsity_{int(sp * 100)}"] = e
+        del a, xq
+    out["c4_sparse_ff2_int8_T7500"] = c4
+    return out
+
+
 def cpu_baseline(plan, budget_s=20.0):
     """The oracle (a C restatement of the reference's CPU dequantize-then-
     matmul path) on a bounded sample: layer 0's eight linears over `rows`
@@ -349,6 +502,8 @@ def main():
     k_ms, k_flops, k_bytes = dominant_kernel(pk, torch, args.frames, stream)
     k_tflops = k_flops / (k_ms * 1e-3) / 1e12
     joint = joint_bench(pk, torch, stream)
+    joint["hbm_streaming"] = joint_streaming(pk, torch, stream)
+    configs = config_results(pk, torch, stream)
     cpu = None if args.no_cpu else cpu_baseline(plan)
 
     audio_min = args.frames * 0.08 / 60.0
@@ -376,6 +531,7 @@ def main():
                      "unit": "TFLOP/s", "frac": round(k_tflops / PEAK["fp8"], 4), "traffic": measured_traffic(),
                      "avg_ms": round(k_ms, 4), "algorithmic_bytes": k_bytes},
         "cpu_baseline": cpu,
+        "configs": configs,
         "wall_s_timed": round(wall, 3),
     }
     print(json.dumps(line), flush=True)

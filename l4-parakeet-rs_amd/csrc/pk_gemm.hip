@@ -1,6 +1,7 @@
 // Instantiations and the launcher of the byte-tile GEMM engine.
 #include <mutex>
 
+#include "pk_gemm3.hpp"
 #include "pk_kernels.hpp"
 
 namespace pk {
@@ -39,8 +40,45 @@ static int launch_one(const GemmArgs& a, hipStream_t s) {
     return 0;
 }
 
+// FP8 / INT8 on the occupancy-2 engine: two 256x128-tile workgroups per CU.
+template <int F, int E>
+static int launch_two(const GemmArgs& a, hipStream_t s) {
+    static std::once_flag once;
+    static hipError_t attr = hipSuccess;
+    std::call_once(once, [] {
+        attr = hipFuncSetAttribute((const void*)g3::gemm3_kernel<F, E>, hipFuncAttributeMaxDynamicSharedMemorySize, g3::kLds);
+    });
+    if (attr != hipSuccess) {
+        set_error("hipFuncSetAttribute(LDS %d bytes) failed: %s", g3::kLds, hipGetErrorString(attr));
+        return -3;
+    }
+    const int tiles = ((a.m + g3::kBM - 1) / g3::kBM) * ((a.n + g3::kBN - 1) / g3::kBN);
+    const int slots = 2 * cu_count();
+    // two persistent workgroups per CU; a multiple of 8 keeps the XCD mapping
+    const int grid = tiles < slots ? tiles : slots - slots % 8;
+    hipLaunchKernelGGL((g3::gemm3_kernel<F, E>), dim3(grid), dim3(g3::kThreads), g3::kLds, s, a);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        set_error("gemm launch (fmt %d, epi %d) failed: %s", F, E, hipGetErrorString(e));
+        return -3;
+    }
+    return 0;
+}
+
 template <int F>
 static int by_epi(int epi, const GemmArgs& a, hipStream_t s) {
+    if constexpr (F == FMT_FP8 || F == FMT_I8 || F == FMT_I8_SKIP) {
+        switch (epi) {
+        case EPI_F16: return a.residual ? launch_two<F, EPI_F16_RES>(a, s) : launch_two<F, EPI_F16>(a, s);
+        case EPI_F32: return launch_two<F, EPI_F32>(a, s);
+        case EPI_F8: return launch_two<F, EPI_F8>(a, s);
+        case EPI_F8_24: return launch_two<F, EPI_F8_24>(a, s);
+        case EPI_I32:
+            if constexpr (F != FMT_FP8) return launch_two<F, EPI_I32>(a, s);
+            break;
+        default: break;
+        }
+    }
     if constexpr (F == FMT_Q4K) {
         if (epi == EPI_F16) return a.residual ? launch_one<F, EPI_F16_RES>(a, s) : launch_one<F, EPI_F16>(a, s);
         if (epi == EPI_F32) return launch_one<F, EPI_F32>(a, s);

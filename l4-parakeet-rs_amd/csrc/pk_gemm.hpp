@@ -257,8 +257,8 @@ __device__ __forceinline__ uint32_t compress_quartet(uint32_t packed) {
 // Epilogue straight from the accumulators: for each of its 8 row blocks a
 // lane finishes columns [gcol, gcol + 16) of one row (16 contiguous outputs,
 // one to four 16-byte stores).  Column scales / bias and the 8 row scales are
-// loaded once per tile; a residual row is loaded one block ahead.
-template <int F, int E>
+// loaded once per tile; a residual row (kRes) is loaded one block ahead.
+template <int F, int E, bool kRes = true>
 __device__ __forceinline__ void epilogue(const GemmArgs& p, v4f (&accf)[8][4], v4i (&acci)[8][4], int m0, int n0, int wm,
                                          int wn, int lane) {
     using T = FmtTraits<F>;
@@ -288,9 +288,9 @@ __device__ __forceinline__ void epilogue(const GemmArgs& p, v4f (&accf)[8][4], v
     // Without a residual the loads read the (same-shaped) output instead and
     // a select discards them, keeping the block loop free of branches.
     const uint16_t* res_src = p.residual ? p.residual : (const uint16_t*)p.out;
-    const bool has_res = p.residual != nullptr;
+    const bool has_res = kRes && p.residual != nullptr;
     uint4 rn0 = {0, 0, 0, 0}, rn1 = {0, 0, 0, 0};
-    if constexpr (E == EPI_F16) {
+    if constexpr (E == EPI_F16 && kRes) {
         const uint4* rp = (const uint4*)(res_src + (size_t)row_of(0) * p.ldo + ccol);
         rn0 = rp[0];
         rn1 = rp[1];
@@ -329,7 +329,7 @@ __device__ __forceinline__ void epilogue(const GemmArgs& p, v4f (&accf)[8][4], v
             }
         } else if constexpr (E == EPI_F16) {
             const uint4 r0 = rn0, r1 = rn1;
-            if (ai + 1 < 8) {
+            if (kRes && ai + 1 < 8) {
                 const uint4* rp = (const uint4*)(res_src + (size_t)row_of(ai + 1) * p.ldo + ccol);
                 rn0 = rp[0];
                 rn1 = rp[1];
