@@ -40,23 +40,23 @@ static int launch_one(const GemmArgs& a, hipStream_t s) {
     return 0;
 }
 
-// FP8 / INT8 on the occupancy-2 engine: two 256x128-tile workgroups per CU.
+// The occupancy-2 engine: two 256x128-tile workgroups per CU.
 template <int F, int E>
 static int launch_two(const GemmArgs& a, hipStream_t s) {
     static std::once_flag once;
     static hipError_t attr = hipSuccess;
     std::call_once(once, [] {
-        attr = hipFuncSetAttribute((const void*)g3::gemm3_kernel<F, E>, hipFuncAttributeMaxDynamicSharedMemorySize, g3::kLds);
+        attr = hipFuncSetAttribute((const void*)g3::gemm3_kernel<F, E>, hipFuncAttributeMaxDynamicSharedMemorySize, g3::L3<F>::kBytes);
     });
     if (attr != hipSuccess) {
-        set_error("hipFuncSetAttribute(LDS %d bytes) failed: %s", g3::kLds, hipGetErrorString(attr));
+        set_error("hipFuncSetAttribute(LDS %d bytes) failed: %s", g3::L3<F>::kBytes, hipGetErrorString(attr));
         return -3;
     }
     const int tiles = ((a.m + g3::kBM - 1) / g3::kBM) * ((a.n + g3::kBN - 1) / g3::kBN);
     const int slots = 2 * cu_count();
     // two persistent workgroups per CU; a multiple of 8 keeps the XCD mapping
     const int grid = tiles < slots ? tiles : slots - slots % 8;
-    hipLaunchKernelGGL((g3::gemm3_kernel<F, E>), dim3(grid), dim3(g3::kThreads), g3::kLds, s, a);
+    hipLaunchKernelGGL((g3::gemm3_kernel<F, E>), dim3(grid), dim3(g3::kThreads), g3::L3<F>::kBytes, s, a);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
         set_error("gemm launch (fmt %d, epi %d) failed: %s", F, E, hipGetErrorString(e));
@@ -65,35 +65,37 @@ static int launch_two(const GemmArgs& a, hipStream_t s) {
     return 0;
 }
 
+// Engine per format, by measurement on MI355X: the occupancy-2 engine for the
+// byte formats, the 256x256 engine for fp16 activations (FP16, G128A16, Q4K),
+// whose 64-K steps make its per-step barriers relatively more costly.
+template <int F, int E>
+static int launch_fmt(const GemmArgs& a, hipStream_t s) {
+    if constexpr (F == FMT_F16 || F == FMT_G128A16 || F == FMT_Q4K) return launch_one<F, E>(a, s);
+    else return launch_two<F, E>(a, s);
+}
+
 template <int F>
 static int by_epi(int epi, const GemmArgs& a, hipStream_t s) {
-    if constexpr (F == FMT_FP8 || F == FMT_I8 || F == FMT_I8_SKIP) {
-        switch (epi) {
-        case EPI_F16: return a.residual ? launch_two<F, EPI_F16_RES>(a, s) : launch_two<F, EPI_F16>(a, s);
-        case EPI_F32: return launch_two<F, EPI_F32>(a, s);
-        case EPI_F8: return launch_two<F, EPI_F8>(a, s);
-        case EPI_F8_24: return launch_two<F, EPI_F8_24>(a, s);
-        case EPI_I32:
-            if constexpr (F != FMT_FP8) return launch_two<F, EPI_I32>(a, s);
-            break;
-        default: break;
+    if constexpr (F == FMT_Q4K) {
+        if (epi != EPI_F16 && epi != EPI_F32) {
+            set_error("unsupported epilogue %d for format %d", epi, F);
+            return -4;
         }
     }
-    if constexpr (F == FMT_Q4K) {
-        if (epi == EPI_F16) return a.residual ? launch_one<F, EPI_F16_RES>(a, s) : launch_one<F, EPI_F16>(a, s);
-        if (epi == EPI_F32) return launch_one<F, EPI_F32>(a, s);
-        set_error("unsupported epilogue %d for format %d", epi, F);
-        return -4;
-    } else {
     switch (epi) {
-    case EPI_F16: return a.residual ? launch_one<F, EPI_F16_RES>(a, s) : launch_one<F, EPI_F16>(a, s);
-    case EPI_F32: return launch_one<F, EPI_F32>(a, s);
-    case EPI_F8: return launch_one<F, EPI_F8>(a, s);
-    case EPI_F8_24: return launch_one<F, EPI_F8_24>(a, s);
+    case EPI_F16: return a.residual ? launch_fmt<F, EPI_F16_RES>(a, s) : launch_fmt<F, EPI_F16>(a, s);
+    case EPI_F32: return launch_fmt<F, EPI_F32>(a, s);
+    case EPI_F8:
+        if constexpr (F != FMT_Q4K) return launch_fmt<F, EPI_F8>(a, s);
+        break;
+    case EPI_F8_24:
+        if constexpr (F != FMT_Q4K) return launch_fmt<F, EPI_F8_24>(a, s);
+        break;
     case EPI_I32:
-        if constexpr (F == FMT_I8 || F == FMT_S4 || F == FMT_I8_SKIP) return launch_one<F, EPI_I32>(a, s);
+        if constexpr (F == FMT_I8 || F == FMT_S4 || F == FMT_I8_SKIP) return launch_fmt<F, EPI_I32>(a, s);
         break;
     case EPI_GLU:
+        // the paired value / gate weight rows need the 256-column tiles
         if constexpr (F == FMT_FP8) {
             if (a.n % 256 != 0 || a.ldo != a.n / 2 || !a.w_scales) {
                 set_error("GLU needs n %% 256 == 0 weight rows, ldo == n/2 and weight scales");
@@ -106,7 +108,6 @@ static int by_epi(int epi, const GemmArgs& a, hipStream_t s) {
     }
     set_error("unsupported epilogue %d for format %d", epi, F);
     return -4;
-    }
 }
 
 static int k_step(int fmt) {

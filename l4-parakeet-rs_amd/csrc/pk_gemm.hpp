@@ -372,6 +372,52 @@ __device__ __forceinline__ void epilogue(const GemmArgs& p, v4f (&accf)[8][4], v
 }
 
 
+// Weight fragment of tile-local weight row `row` for one K-step: the lane's
+// two 16-byte operand chunks (lane group g), decoded to the MFMA input type.
+// sc / zr are the step's 128-K group scales / zero-points indexed by
+// tile-local column (G128 formats); gs returns the group scales of the 4
+// columns block bj's accumulators hold (G128A8: 16g + 4bj + r of the wave's 64).
+template <int F>
+__device__ __forceinline__ void weight_frag(const uint8_t* Bs, int row, int g, int bj, int wn, int step, const float* sc,
+                                            const uint8_t* zr, uint4& w0, uint4& w1, v4f& gs) {
+    using T = FmtTraits<F>;
+    gs = v4f{1.f, 1.f, 1.f, 1.f};
+    if constexpr (T::bRow == 128) {
+        w0 = *(const uint4*)(Bs + swz(row, g));
+        w1 = *(const uint4*)(Bs + swz(row, 4 + g));
+    } else if constexpr (F == FMT_Q4K) {
+        // K slots 8g..8g+7 are the low nibbles of quant bytes 8g..8g+7 (group
+        // 2*(step&3)), K slots 32+8g.. the high nibbles (group 2*(step&3)+1).
+        const uint4 h = *(const uint4*)(Bs + row * 48);
+        const uint2 q = *(const uint2*)(Bs + row * 48 + 16 + 8 * g);
+        float al, bl, ah, bh;
+        q4k_coeffs(h, 2 * (step & 3), al, bl);
+        q4k_coeffs(h, 2 * (step & 3) + 1, ah, bh);
+        w0 = q4k_decode8(q.x & 0x0f0f0f0fu, q.y & 0x0f0f0f0fu, al, bl);
+        w1 = q4k_decode8((q.x >> 4) & 0x0f0f0f0fu, (q.y >> 4) & 0x0f0f0f0fu, ah, bh);
+    } else {
+        const int z = zr[row];
+        if constexpr (F == FMT_G128A8) {
+            gs = *(const v4f*)(sc + wn * 64 + g * 16 + bj * 4);
+            const uint32_t zz = (uint32_t)z * 0x01010101u;
+            const uint2 q0 = *(const uint2*)(Bs + row * 64 + 8 * g);
+            const uint2 q1 = *(const uint2*)(Bs + row * 64 + 32 + 8 * g);
+            u4x8_minus_z(q0.x, zz, w0.x, w0.y);
+            u4x8_minus_z(q0.y, zz, w0.z, w0.w);
+            u4x8_minus_z(q1.x, zz, w1.x, w1.y);
+            u4x8_minus_z(q1.y, zz, w1.z, w1.w);
+        } else {  // G128A16
+            const _Float16 s = (_Float16)sc[row];
+            const _Float16 zh = (_Float16)(1024 + z);
+            const v2h ss = {s, s}, zz = {zh, zh};
+            const uint32_t q0 = *(const uint32_t*)(Bs + row * 32 + 4 * g);
+            const uint32_t q1 = *(const uint32_t*)(Bs + row * 32 + 16 + 4 * g);
+            w0 = __builtin_bit_cast(uint4, u4x8_to_h(q0, zz, ss));
+            w1 = __builtin_bit_cast(uint4, u4x8_to_h(q1, zz, ss));
+        }
+    }
+}
+
 // Output bytes per element of an epilogue.
 template <int E> struct EpiBytes { static constexpr int v = (E == EPI_F8 || E == EPI_F8_24) ? 1 : (E == EPI_F16 ? 2 : 4); };
 
@@ -702,48 +748,11 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs p) {
             // This wave's four weight fragments for the step.
             uint4 w0[4], w1[4];
             v4f gs[4];
+            const int kg = (step * T::kStep) >> 7;
 #pragma unroll
-            for (int bj = 0; bj < 4; ++bj) {
-                const int row = wn * 64 + wrow(l16, bj);
-                gs[bj] = v4f{1.f, 1.f, 1.f, 1.f};
-                if constexpr (T::bRow == 128) {
-                    w0[bj] = *(const uint4*)(Bs + swz(row, g));
-                    w1[bj] = *(const uint4*)(Bs + swz(row, 4 + g));
-                } else if constexpr (F == FMT_Q4K) {
-                    // K slots 8g..8g+7 are the low nibbles of quant bytes
-                    // 8g..8g+7 (group 2*(step&3)), K slots 32+8g.. the high
-                    // nibbles (group 2*(step&3)+1).
-                    const uint4 h = *(const uint4*)(Bs + row * 48);
-                    const uint2 q = *(const uint2*)(Bs + row * 48 + 16 + 8 * g);
-                    float al, bl, ah, bh;
-                    q4k_coeffs(h, 2 * (step & 3), al, bl);
-                    q4k_coeffs(h, 2 * (step & 3) + 1, ah, bh);
-                    w0[bj] = q4k_decode8(q.x & 0x0f0f0f0fu, q.y & 0x0f0f0f0fu, al, bl);
-                    w1[bj] = q4k_decode8((q.x >> 4) & 0x0f0f0f0fu, (q.y >> 4) & 0x0f0f0f0fu, ah, bh);
-                } else {
-                    const int kg = (step * T::kStep) >> 7;
-                    const int z = g_zero[kg * kBlockN + row];
-                    if constexpr (F == FMT_G128A8) {
-                        // the accumulators of block bj hold columns 16g + 4bj + r
-                        gs[bj] = *(const v4f*)(g_scale + kg * kBlockN + wn * 64 + g * 16 + bj * 4);
-                        const uint32_t zz = (uint32_t)z * 0x01010101u;
-                        const uint2 q0 = *(const uint2*)(Bs + row * 64 + 8 * g);
-                        const uint2 q1 = *(const uint2*)(Bs + row * 64 + 32 + 8 * g);
-                        u4x8_minus_z(q0.x, zz, w0[bj].x, w0[bj].y);
-                        u4x8_minus_z(q0.y, zz, w0[bj].z, w0[bj].w);
-                        u4x8_minus_z(q1.x, zz, w1[bj].x, w1[bj].y);
-                        u4x8_minus_z(q1.y, zz, w1[bj].z, w1[bj].w);
-                    } else {  // G128A16
-                        const _Float16 s = (_Float16)g_scale[kg * kBlockN + row];
-                        const _Float16 zh = (_Float16)(1024 + z);
-                        const v2h ss = {s, s}, zz = {zh, zh};
-                        const uint32_t q0 = *(const uint32_t*)(Bs + row * 32 + 4 * g);
-                        const uint32_t q1 = *(const uint32_t*)(Bs + row * 32 + 16 + 4 * g);
-                        w0[bj] = __builtin_bit_cast(uint4, u4x8_to_h(q0, zz, ss));
-                        w1[bj] = __builtin_bit_cast(uint4, u4x8_to_h(q1, zz, ss));
-                    }
-                }
-            }
+            for (int bj = 0; bj < 4; ++bj)
+                weight_frag<F>(Bs, wn * 64 + wrow(l16, bj), g, bj, wn, step, g_scale + kg * kBlockN, g_zero + kg * kBlockN, w0[bj],
+                               w1[bj], gs[bj]);
             // Activation fragments are read one 16-row block ahead of the
             // MFMAs that consume them where the step's weight decode leaves the
             // registers for it (FP8, INT8, FP16).

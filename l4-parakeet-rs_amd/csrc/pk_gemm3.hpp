@@ -1,4 +1,4 @@
-// Occupancy-2 GEMM engine for the 128-byte-row formats (FP8, INT8) on gfx950.
+// Occupancy-2 GEMM engine (gfx950) for every format but the GLU epilogue.
 //
 // Two independent workgroups share each CU, so one workgroup's epilogue
 // (VALU: scaling, SiLU, conversions, stores) and its barrier waits run while
@@ -14,7 +14,9 @@
 // tiles are complete); every wave copies its four weight fragments into
 // registers and the next activation tile starts loading; a second barrier
 // (all weight fragments copied) lets the next weight tile load into the same
-// buffer while the MFMAs run.  Loads are direct-to-LDS, whole 128-byte rows.
+// buffer while the MFMAs run.  Loads are direct-to-LDS.  The G128 formats
+// stream each step's group scales / zero-points (tile columns) through a
+// two-slot LDS table written alongside the next weight tile.
 #pragma once
 
 #include "pk_gemm.hpp"
@@ -24,14 +26,24 @@ namespace g3 {
 
 constexpr int kBM = 256, kBN = 128, kThreads = 256;
 constexpr int kATile = kBM * kRowBytes;  // 32 KiB
-constexpr int kBTile = kBN * kRowBytes;  // 16 KiB
 constexpr int kB = 2 * kATile;           // weight buffer offset
-constexpr int kLds = 2 * kATile + kBTile;  // 80 KiB
+
+// Weight tile bytes of one step, and the LDS of one workgroup: two activation
+// tiles, one weight tile and (G128 formats) a 2-entry ring of the step's
+// group scales (fp32) and zero-points (u8) for the tile's 128 columns.
+template <int F> struct L3 {
+    static constexpr bool kG128 = (F == FMT_G128A8 || F == FMT_G128A16);
+    static constexpr int kBTile = kBN * FmtTraits<F>::bRow;
+    static constexpr int kTab = kB + kBTile;
+    static constexpr int kBytes = kTab + (kG128 ? 2 * kBN * 5 : 0);
+    static constexpr int kBLoads = kBTile / 1024;  // direct-to-LDS weight loads per step
+    static constexpr int kBPerWave = (kBLoads + 3) / 4;
+};
 
 template <int F, int E>
 __global__ __launch_bounds__(kThreads, 2) void gemm3_kernel(GemmArgs p) {
     using T = FmtTraits<F>;
-    static_assert(T::bRow == 128 && T::kStep == 128, "128-byte rows, one MFMA K per step");
+    using L = L3<F>;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
@@ -40,41 +52,117 @@ __global__ __launch_bounds__(kThreads, 2) void gemm3_kernel(GemmArgs p) {
     const int tiles_m = (p.m + kBM - 1) / kBM;
     const int ntiles = tiles_m * tiles_n;
     const int G = gridDim.x;
-    const size_t ld = (size_t)p.k;  // bytes per row (1-byte elements)
+    const size_t lda = (size_t)p.k * T::aElemNum / T::aElemDen;  // bytes per activation row
+    const size_t ldb = (size_t)p.k * T::bNum / T::bDen;          // bytes per weight row
     const int steps = p.k / T::kStep;
+    const int groups = p.k >> 7;
     const uint8_t* __restrict__ pa = p.a;
     const uint8_t* __restrict__ pb = p.b;
     const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)lds;
     const int gw = group_width(tiles_n);
+    float* tab_s = (float*)(lds + L::kTab);                  // [2][128] group scales
+    uint8_t* tab_z = lds + L::kTab + 2 * kBN * 4;            // [2][128] zero-points
 
-    uint32_t a_off[8], b_off[4];
-    auto set_tile = [&](int tt, int& m0, int& n0) {
+    // Activation load i of this wave covers tile rows wave*64 + 8i + q,
+    // q = lane / 8, 16-byte chunk position lane % 8.  swz_key of that row is
+    // kq(q) ^ ki(i), so a lane keeps only its first row and (lane % 8) ^ kq.
+    const int q = lane >> 3;
+    const uint32_t a_cq = (uint32_t)((lane & 7) ^ ((q >> 1) & 1) ^ (((q >> 2) & 1) << 1) ^ ((q & 1) << 2));
+    int a_row = 0;  // m0 + wave*64 + q of the issue tile
+    // Formats whose decode leaves the registers keep the 8 offsets instead.
+    constexpr bool kPreOff = F == FMT_FP8 || F == FMT_I8 || F == FMT_I8_SKIP || F == FMT_F16;
+    uint32_t a_off[kPreOff ? 8 : 1];
+    uint32_t b_off[L::kBPerWave];
+    uint32_t b_q4k = 0;  // Q4K: bit i set when weight load i carries quant bytes
+    auto tile_origin = [&](int tt, int& m0, int& n0) {
         const int ng = tt / (tiles_m * gw);
         const int r = tt - ng * tiles_m * gw;
         const int tm = r / gw;
         m0 = tm * kBM;
         n0 = (ng * gw + (r - tm * gw)) * kBN;
+    };
+    auto set_tile = [&](int tt, int& m0, int& n0) {
+        tile_origin(tt, m0, n0);
+        a_row = m0 + wave * 64 + q;
+        if constexpr (kPreOff) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int o = (wave * 8 + i) * 1024 + lane * 16;
-            const int row = o >> 7, c = ((o >> 4) & 7) ^ swz_key(row);
-            a_off[i] = (uint32_t)((size_t)min(m0 + row, p.m - 1) * ld + c * 16);
+            for (int i = 0; i < 8; ++i) {
+                const uint32_t ki = (uint32_t)((((i >> 1) & 1) << 1) | (((i ^ (i >> 2)) & 1) << 2));
+                a_off[i] = (uint32_t)min(a_row + 8 * i, p.m - 1) * (uint32_t)lda + ((a_cq ^ ki) << 4);
+            }
         }
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int o = (wave * 4 + i) * 1024 + lane * 16;
-            const int row = o >> 7, c = ((o >> 4) & 7) ^ swz_key(row);
-            b_off[i] = (uint32_t)((size_t)min(n0 + row, p.n - 1) * ld + c * 16);
+        for (int i = 0; i < L::kBPerWave; ++i) {
+            const int o = (i * 4 + wave) * 1024 + lane * 16;
+            int row, c;
+            if constexpr (T::bRow == 128) {
+                row = o >> 7;
+                c = ((o >> 4) & 7) ^ swz_key(row);
+            } else {
+                row = o / T::bRow;
+                c = (o % T::bRow) / 16;
+            }
+            b_off[i] = (uint32_t)min(n0 + row, p.n - 1) * (uint32_t)ldb + (uint32_t)(c * 16);
+            if constexpr (F == FMT_Q4K) b_q4k = c > 0 ? b_q4k | (1u << i) : b_q4k & ~(1u << i);
         }
     };
     auto issue_a = [&](int step, int buf) {
         const uint32_t base = lds_base + buf * kATile;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) dma16(pa + (size_t)step * kRowBytes, a_off[i], base + (wave * 8 + i) * 1024);
+        for (int i = 0; i < 8; ++i) {
+            uint32_t off;
+            if constexpr (kPreOff) {
+                off = a_off[i];
+            } else {
+                const uint32_t ki = (uint32_t)((((i >> 1) & 1) << 1) | (((i ^ (i >> 2)) & 1) << 2));
+                off = (uint32_t)min(a_row + 8 * i, p.m - 1) * (uint32_t)lda + ((a_cq ^ ki) << 4);
+            }
+            dma16(pa + (size_t)step * kRowBytes, off, base + (wave * 8 + i) * 1024);
+        }
     };
     auto issue_b = [&](int step) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) dma16(pb + (size_t)step * kRowBytes, b_off[i], lds_base + kB + (wave * 4 + i) * 1024);
+        for (int i = 0; i < L::kBPerWave; ++i) {
+            if (L::kBLoads % 4 != 0 && i * 4 + wave >= L::kBLoads) continue;
+            const uint32_t dst = lds_base + kB + (i * 4 + wave) * 1024;
+            if constexpr (F == FMT_Q4K) {
+                // superblock step >> 2; quant chunks advance 32 bytes per step
+                const uint32_t qa = (b_q4k >> i) & 1u ? (uint32_t)(step & 3) * 32u : 0u;
+                dma16(pb + (size_t)(step >> 2) * 144, b_off[i] + qa, dst);
+            } else {
+                dma16(pb + (size_t)step * T::bRow, b_off[i], dst);
+            }
+        }
+    };
+    // G128: the scale and zero-point of a step's 128-K group for the tile's
+    // columns are fetched two steps ahead (a cursor over this workgroup's
+    // (tile, step) sequence) and written into table slot `step & 1` at the
+    // step before their use.
+    float tv_s = 0.0f;
+    uint32_t tv_z = 0;
+    int f_t = 0, f_step = 0, f_n0 = 0;
+    auto fetch_tab = [&]() {
+        if constexpr (L::kG128) {
+            if (tid < kBN && f_t < ntiles) {
+                const size_t gi = (size_t)min(f_n0 + tid, p.n - 1) * groups + ((f_step * T::kStep) >> 7);
+                tv_s = h2f(p.g_scales[gi]);
+                tv_z = (uint32_t)(int)h2f(p.g_zeros[gi]);
+            }
+            if (++f_step == steps) {
+                f_step = 0;
+                f_t += G;
+                int fm0;
+                if (f_t < ntiles) tile_origin(f_t, fm0, f_n0);
+            }
+        }
+    };
+    auto store_tab = [&](int step) {
+        if constexpr (L::kG128) {
+            if (tid < kBN) {
+                tab_s[(step & 1) * kBN + tid] = tv_s;
+                tab_z[(step & 1) * kBN + tid] = (uint8_t)tv_z;
+            }
+        }
     };
 
     int t = tile_slot(G);
@@ -83,6 +171,14 @@ __global__ __launch_bounds__(kThreads, 2) void gemm3_kernel(GemmArgs p) {
     set_tile(t, m0, n0);
     issue_a(0, 0);
     issue_b(0);
+    if constexpr (L::kG128) {
+        f_t = t;
+        f_n0 = n0;
+        fetch_tab();  // step 0
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        store_tab(0);
+        fetch_tab();  // the second step
+    }
     int buf = 0;
 
     v4f accf[8][4];
@@ -115,21 +211,25 @@ __global__ __launch_bounds__(kThreads, 2) void gemm3_kernel(GemmArgs p) {
             const uint8_t* As = lds + buf * kATile;
             const uint8_t* Bs = lds + kB;
             uint4 w0[4], w1[4];
+            v4f gs[4];
 #pragma unroll
-            for (int bj = 0; bj < 4; ++bj) {
-                const int row = wn * 64 + wrow(l16, bj);
-                w0[bj] = *(const uint4*)(Bs + swz(row, g));
-                w1[bj] = *(const uint4*)(Bs + swz(row, 4 + g));
-            }
+            for (int bj = 0; bj < 4; ++bj)
+                weight_frag<F>(Bs, wn * 64 + wrow(l16, bj), g, bj, wn, step, tab_s + (step & 1) * kBN, tab_z + (step & 1) * kBN,
+                               w0[bj], w1[bj], gs[bj]);
             uint4 x0, x1, y0, y1;
             {
                 const int row = wm * 128 + l16;
                 x0 = *(const uint4*)(As + swz(row, g));
                 x1 = *(const uint4*)(As + swz(row, 4 + g));
             }
-            // every wave holds its weight fragments: the weight buffer is free
+            // every wave holds its weight fragments: the weight buffer (and the
+            // group table slot of the step before) are free
             __syncthreads();
-            if (nstep >= 0) issue_b(nstep);
+            if (nstep >= 0) {
+                issue_b(nstep);
+                store_tab(nstep);  // fetched a step ago
+                fetch_tab();       // for the step after nstep
+            }
 #pragma unroll
             for (int ai = 0; ai < 8; ++ai) {
                 if (ai + 1 < 8) {
@@ -139,13 +239,16 @@ __global__ __launch_bounds__(kThreads, 2) void gemm3_kernel(GemmArgs p) {
                 }
                 bool live = true;
                 if constexpr (F == FMT_I8_SKIP) {
+                    // Activation-sparse FF2: the wave's 64 lanes hold this
+                    // 16-row x 128-K activation block; when every byte is zero
+                    // its products are exactly zero and the MFMAs are skipped.
                     const bool nz = (x0.x | x0.y | x0.z | x0.w | x1.x | x1.y | x1.z | x1.w) != 0u;
                     live = __builtin_amdgcn_ballot_w64(nz) != 0;
                     skipped += live ? 0u : 1u;
                 }
                 if (live) {
 #pragma unroll
-                    for (int bj = 0; bj < 4; ++bj) mfma_step<F>(accf[ai][bj], acci[ai][bj], w0[bj], w1[bj], x0, x1, v4f{1.f, 1.f, 1.f, 1.f});
+                    for (int bj = 0; bj < 4; ++bj) mfma_step<F>(accf[ai][bj], acci[ai][bj], w0[bj], w1[bj], x0, x1, gs[bj]);
                 }
                 x0 = y0;
                 x1 = y1;
