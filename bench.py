@@ -526,7 +526,7 @@ def main():
         "pct_mfma_peak": round(100.0 * tops / PEAK["fp8"], 2),
         "ms_per_audio_min": round(ms_step / audio_min, 4),
         "joint_gemv": joint,
-        "roofline": {"kernel": "gemm_kernel<FP8, EPI_F8> (FF1 expand 1024->4096, T=45000)",
+        "roofline": {"kernel": "g3::gemm3_kernel<FP8, EPI_F8> (FF1 expand 1024->4096, T=45000)",
                      "bound": "mfma", "achieved": round(k_tflops, 2), "peak": PEAK["fp8"],
                      "unit": "TFLOP/s", "frac": round(k_tflops / PEAK["fp8"], 4), "traffic": measured_traffic(),
                      "avg_ms": round(k_ms, 4), "algorithmic_bytes": k_bytes},
