@@ -38,6 +38,8 @@ extern "C" {
 #define PK_E_ALIGN (-2)
 #define PK_E_LAUNCH (-3)
 #define PK_E_ARG (-4)
+#define PK_E_FORMAT (-5) /* invalid .pkl4 artifact */
+#define PK_E_IO (-6)     /* artifact file could not be read */
 
 const char* pk_last_error(void);
 /* Version of this ABI (bumped on any signature change). */
@@ -55,6 +57,72 @@ int32_t pk_estimate_linear(int32_t format, size_t logical_in, size_t logical_out
 /* exl3.rs:37-75 (Exl3Layout).  out7 = {padded_in, padded_out, trellis_shape[3],
  * trellis_bytes, scale_bytes}.  Returns 0, PK_E_SHAPE or PK_E_ARG. */
 int32_t pk_exl3_layout(size_t logical_in, size_t logical_out, int32_t qbits, size_t* out7);
+
+/* ---- .pkl4 artifact and load-time derivation (host code) -------------------
+ * artifact.rs:11-157 (AotArtifactIndex::open) with the checks of
+ * artifact.rs:514-650: prefix "PKL4AOT\0", schema 2, flags 0, JSON header,
+ * payload at the first 4096-byte boundary, 256-byte aligned tensors, linear
+ * weights as fp16 [ceil128(N) x ceil128(K)] and their biases as fp32
+ * [ceil128(N)] zero padded.  Invalid files return PK_E_FORMAT with the
+ * reference's message in pk_last_error(). */
+
+typedef struct pk_artifact pk_artifact;
+
+#define PK_STORAGE_FP16 0        /* AotStorage::Fp16 */
+#define PK_STORAGE_FP32 1        /* AotStorage::Fp32 */
+#define PK_STORAGE_FP16_LINEAR 2 /* AotStorage::Sm89Fp16Linear */
+#define PK_STORAGE_FP32_BIAS 3   /* AotStorage::Sm89Fp32Bias */
+
+typedef struct {
+    const char* name;          /* owned by the artifact */
+    int32_t storage;           /* PK_STORAGE_* */
+    int32_t rank;
+    uint64_t logical_shape[4];
+    uint64_t physical_shape[4];
+    uint64_t offset;           /* payload offset */
+    uint64_t bytes;
+} pk_tensor_info;
+
+typedef struct {
+    int32_t profile;           /* 0 v2-english, 1 v3-multilingual (config.rs:14-17) */
+    int32_t blank_token_id;    /* 1024 or 8192 */
+    int32_t tensor_count;
+    int32_t vocabulary_size;
+    uint64_t data_start;       /* file offset of the payload */
+    uint64_t payload_bytes;
+    uint64_t file_bytes;
+} pk_artifact_summary;
+
+/* Opens and validates an artifact; *out is NULL on failure. */
+int32_t pk_artifact_open(const char* path, pk_artifact** out);
+void pk_artifact_close(pk_artifact* artifact);
+int32_t pk_artifact_info(const pk_artifact* artifact, pk_artifact_summary* out);
+/* Tensor `index` (header order). */
+int32_t pk_artifact_tensor(const pk_artifact* artifact, int32_t index, pk_tensor_info* out);
+/* Index of the tensor called `name`, or PK_E_ARG (artifact.rs:160-167's missing tensor). */
+int32_t pk_artifact_find(const pk_artifact* artifact, const char* name);
+/* Vocabulary piece `index` (< blank_token_id), or NULL. */
+const char* pk_artifact_vocabulary(const pk_artifact* artifact, int32_t index);
+/* Copies tensor `index`'s stored bytes into host memory (capacity >= bytes). */
+int32_t pk_artifact_read(const pk_artifact* artifact, int32_t index, void* host_dst, uint64_t capacity);
+
+#define PK_DERIVE_FP16 0      /* upload only */
+#define PK_DERIVE_FP8_ROWS 1  /* pk_pack_fp8_rows: packed u8 [N x K], fp32 scales [N] */
+#define PK_DERIVE_INT8_ROWS 2 /* pk_pack_int8_rows: packed s8 [N x K], fp32 scales [N] */
+#define PK_DERIVE_INT4_ROWS 3 /* pk_pack_int4_rows: packed [N x K/2], fp32 scales [N] */
+#define PK_DERIVE_INT4_G128 4 /* pk_pack_int4_g128: u32 [N x K/8], fp16 scales and zeros [N x K/128] */
+
+/* Load-time derivation of one sm89_fp16_linear tensor (the job of
+ * QuantizedFfnWeights::load_for, encoder.rs:361-422, and of upload_aot,
+ * cuda.rs:375-412, for one tensor): reads its padded fp16 [N x K] (physical
+ * shape) into host_staging (staging_bytes >= its bytes; pinned memory makes the
+ * copy asynchronous), uploads it to device_fp16 on `stream` and packs it on the
+ * GPU into `format` (packed / scales / zeros as the packer it names; zeros only
+ * for PK_DERIVE_INT4_G128).  All-zero padding rows pack with scale 1.  The
+ * staging buffer must stay untouched until the stream has run the upload. */
+int32_t pk_artifact_derive_linear(const pk_artifact* artifact, int32_t index, int32_t format, void* host_staging,
+                                  uint64_t staging_bytes, uint16_t* device_fp16, void* packed, void* scales,
+                                  uint16_t* zeros, void* stream);
 
 /* ---- load-time weight packers (fp16 [n x k] -> packed) -------------------- */
 

@@ -21,8 +21,33 @@ I = ctypes.c_int32
 F = ctypes.c_float
 S = ctypes.c_size_t
 
+U64 = ctypes.c_uint64
+
+
+class TensorInfo(ctypes.Structure):
+    """pk_tensor_info."""
+    _fields_ = [("name", ctypes.c_char_p), ("storage", I), ("rank", I),
+                ("logical_shape", U64 * 4), ("physical_shape", U64 * 4),
+                ("offset", U64), ("bytes", U64)]
+
+
+class ArtifactSummary(ctypes.Structure):
+    """pk_artifact_summary."""
+    _fields_ = [("profile", I), ("blank_token_id", I), ("tensor_count", I),
+                ("vocabulary_size", I), ("data_start", U64), ("payload_bytes", U64),
+                ("file_bytes", U64)]
+
+
 # name -> argument types (the trailing stream argument included)
 SIGNATURES = {
+    "pk_artifact_open": (I, [ctypes.c_char_p, ctypes.POINTER(P)]),
+    "pk_artifact_close": (None, [P]),
+    "pk_artifact_info": (I, [P, ctypes.POINTER(ArtifactSummary)]),
+    "pk_artifact_tensor": (I, [P, I, ctypes.POINTER(TensorInfo)]),
+    "pk_artifact_find": (I, [P, ctypes.c_char_p]),
+    "pk_artifact_vocabulary": (ctypes.c_char_p, [P, I]),
+    "pk_artifact_read": (I, [P, I, P, U64]),
+    "pk_artifact_derive_linear": (I, [P, I, I, P, U64, P, P, P, P, P]),
     "pk_last_error": (ctypes.c_char_p, []),
     "pk_abi_version": (I, []),
     "pk_estimate_linear": (I, [I, S, S, I, P]),
@@ -163,3 +188,71 @@ def gemm(fmt, epi, a, b, m, n, k, out, *, w_scales=None, row_scales=None, in_sca
 
 FMT_FP8, FMT_I8, FMT_S4, FMT_G128A8, FMT_F16, FMT_G128A16, FMT_I8_SKIP, FMT_Q4K = range(8)
 EPI_F16, EPI_F8, EPI_F8_24, EPI_F32, EPI_I32 = range(5)
+
+
+# ---- .pkl4 artifact (host) ------------------------------------------------------
+
+STORAGE = {0: "fp16", 1: "fp32", 2: "sm89_fp16_linear", 3: "sm89_fp32_bias"}
+DERIVE_FP16, DERIVE_FP8_ROWS, DERIVE_INT8_ROWS, DERIVE_INT4_ROWS, DERIVE_INT4_G128 = range(5)
+
+
+class Artifact:
+    """An opened, validated .pkl4 artifact (artifact.rs AotArtifactIndex)."""
+
+    def __init__(self, path: str):
+        handle = P()
+        status = lib.pk_artifact_open(os.fsencode(path), ctypes.byref(handle))
+        if status < 0:
+            raise PkError(f"pk_artifact_open: status {status}: {last_error()}")
+        self.handle = handle.value
+
+    def close(self):
+        if getattr(self, "handle", None):
+            lib.pk_artifact_close(self.handle)
+            self.handle = None
+
+    __del__ = close
+
+    def _check(self, name, status):
+        if status < 0:
+            raise PkError(f"{name}: status {status}: {last_error()}")
+        return status
+
+    def info(self) -> dict:
+        out = ArtifactSummary()
+        self._check("pk_artifact_info", lib.pk_artifact_info(self.handle, ctypes.byref(out)))
+        return {f: getattr(out, f) for f, _ in ArtifactSummary._fields_}
+
+    def tensor(self, index: int) -> dict:
+        out = TensorInfo()
+        self._check("pk_artifact_tensor", lib.pk_artifact_tensor(self.handle, index, ctypes.byref(out)))
+        return {"name": out.name.decode(), "storage": STORAGE[out.storage],
+                "logical_shape": list(out.logical_shape[:out.rank]),
+                "physical_shape": list(out.physical_shape[:out.rank]),
+                "offset": out.offset, "bytes": out.bytes}
+
+    def tensors(self) -> list:
+        return [self.tensor(i) for i in range(self.info()["tensor_count"])]
+
+    def find(self, name: str) -> int:
+        return self._check("pk_artifact_find", lib.pk_artifact_find(self.handle, name.encode()))
+
+    def vocabulary(self, index: int):
+        piece = lib.pk_artifact_vocabulary(self.handle, index)
+        return None if piece is None else piece.decode()
+
+    def read(self, index: int):
+        import numpy as np
+
+        out = np.empty(self.tensor(index)["bytes"], np.uint8)
+        self._check("pk_artifact_read", lib.pk_artifact_read(self.handle, index, out.ctypes.data, out.nbytes))
+        return out
+
+    def derive_linear(self, index, fmt, host_staging, device_fp16, packed=None, scales=None, zeros=None,
+                      stream=None):
+        """Upload tensor `index` (fp16 linear) through `host_staging` (a numpy
+        uint8 buffer) into `device_fp16` and pack it on the GPU into `fmt`."""
+        fn = lib.pk_artifact_derive_linear
+        status = fn(self.handle, index, fmt, host_staging.ctypes.data, host_staging.nbytes,
+                    _ptr(device_fp16), _ptr(packed), _ptr(scales), _ptr(zeros), _stream(stream))
+        self._check("pk_artifact_derive_linear", status)

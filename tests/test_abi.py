@@ -17,7 +17,7 @@ GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "reference_known_answ
 
 def declared_symbols():
     text = open(HEADER).read()
-    return sorted(set(re.findall(r"^\s*(?:const char\*|int32_t)\s+(pk_\w+)\s*\(", text, re.M)))
+    return sorted(set(re.findall(r"^\s*(?:const char\*|int32_t|void)\s+(pk_\w+)\s*\(", text, re.M)))
 
 
 @pytest.fixture(scope="module")

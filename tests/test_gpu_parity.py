@@ -620,3 +620,51 @@ def test_joint_scan(pk, orc, int8):
         tokens.append(tok)
     note(f"joint scan: {scans} scans, {len(tokens)} tokens")
     assert 3 <= len(tokens) < frames
+
+
+# ---- .pkl4 load-time derivation ----------------------------------------------------------
+
+@pytest.mark.parametrize("fmt", ["fp16", "fp8", "int8", "int4", "g128"])
+def test_artifact_derive_linear(pk, orc, fmt, tmp_path):
+    """A linear read from a .pkl4 artifact, uploaded and packed on the GPU,
+    equals the oracle's packer applied to the artifact's padded fp16 matrix."""
+    sys.path.insert(0, __import__("os").path.dirname(__file__))
+    import pkl4_writer
+
+    note(f"artifact derive {fmt}")
+    rng = np.random.default_rng(160)
+    wsrc = rng.standard_normal((300, 200)) * 0.02
+    path = pkl4_writer.write(tmp_path / "d.pkl4", [("encoder.layers.3.feed_forward2.linear1.weight", "linear", wsrc)])
+    art = pk.Artifact(str(path))
+    idx = art.find("encoder.layers.3.feed_forward2.linear1.weight")
+    n, k = art.tensor(idx)["physical_shape"]
+    padded = np.zeros((n, k), np.float16)
+    padded[:300, :200] = wsrc.astype(np.float16)
+    staging = np.empty(n * k * 2, np.uint8)
+    d16 = empty((n, k), torch.float16)
+    if fmt == "fp16":
+        art.derive_linear(idx, pk.DERIVE_FP16, staging, d16)
+        assert np.array_equal(host(d16).view(np.uint16), padded.view(np.uint16))
+    elif fmt in ("fp8", "int8"):
+        q = empty((n, k), torch.uint8 if fmt == "fp8" else torch.int8)
+        sc = empty((n,), torch.float32)
+        art.derive_linear(idx, pk.DERIVE_FP8_ROWS if fmt == "fp8" else pk.DERIVE_INT8_ROWS, staging, d16, q, sc)
+        rq, rs = orc.pack_fp8_rows(padded) if fmt == "fp8" else orc.pack_int8_rows(padded)
+        assert np.array_equal(host(q).view(np.uint8), np.asarray(rq).view(np.uint8))
+        assert np.array_equal(host(sc), rs)
+    elif fmt == "int4":
+        q = empty((n, k // 2), torch.uint8)
+        sc = empty((n,), torch.float32)
+        art.derive_linear(idx, pk.DERIVE_INT4_ROWS, staging, d16, q, sc)
+        rq, rs = orc.pack_int4_rows(padded)
+        assert np.array_equal(host(q), rq) and np.array_equal(host(sc), rs)
+    else:
+        q = empty((n, k // 8), torch.int32)
+        sc = empty((n, k // 128), torch.float16)
+        z = empty((n, k // 128), torch.float16)
+        art.derive_linear(idx, pk.DERIVE_INT4_G128, staging, d16, q, sc, z)
+        rq, rs, rz = orc.pack_int4_g128(padded)
+        assert np.array_equal(host(q).view(np.uint32), rq)
+        assert np.array_equal(host(sc).view(np.uint16), rs.view(np.uint16))
+        assert np.array_equal(host(z).view(np.uint16), rz.view(np.uint16))
+    art.close()
