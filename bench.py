@@ -229,6 +229,48 @@ def joint_bench(pk, torch, stream, reps=2000):
     return out
 
 
+def decode_bench(pk, torch, stream, frames=45000):
+    """BASELINE configs[4]'s decoder: batch-1 greedy TDT decode of T frames in
+    one persistent launch (2-layer LSTM, 640 hidden, fp16 weights; INT8 joint
+    640 -> 1030), synthetic random weights and encoder rows, the joint bias
+    favouring the blank and duration 1 so tokens come about every 5 frames,
+    roughly the rate of speech at 80 ms per frame."""
+    H, T, D = 640, 1025, 5
+    g = torch.Generator(device="cuda")
+    g.manual_seed(21)
+    r = lambda *shape, sc: (torch.randn(shape, generator=g, device="cuda") * sc)
+    lstm = [r(4 * H, H, sc=0.05).half(), r(4 * H, H, sc=0.05).half(), r(4 * H, sc=0.1), r(4 * H, sc=0.1),
+            r(4 * H, H, sc=0.05).half(), r(4 * H, H, sc=0.05).half(), r(4 * H, sc=0.1), r(4 * H, sc=0.1)]
+    w_proj, b_proj = r(H, H, sc=0.1).half(), r(H, sc=0.1)
+    wj16 = r(T + D, H, sc=0.08).half()
+    wj = torch.empty((T + D, H), dtype=torch.int8, device="cuda")
+    sj = torch.empty(T + D, device="cuda")
+    pk.call("pk_pack_int8_rows", wj16, T + D, H, wj, sj, stream=stream)
+    bj = r(T + D, sc=0.1)
+    bj[T - 1] += 2.3  # blank favoured, duration 0 rare and 1 preferred, as in speech
+    bj[T] -= 3.0
+    bj[T + 1] += 0.5
+    enc = r(frames, H, sc=0.5).half()
+    emb = r(T - 1, H, sc=0.5).half()
+    cap = frames * 10
+    toks = torch.empty(cap, dtype=torch.int32, device="cuda")
+    res = torch.zeros(4, dtype=torch.int32, device="cuda")
+    wbytes = pk.lib.pk_tdt_decode_workspace_bytes(H)
+    work = torch.empty(wbytes // 4, dtype=torch.int32, device="cuda")
+
+    def run(n):
+        pk.call("pk_tdt_decode", enc, n, H, emb, *lstm, w_proj, b_proj, wj, 1, sj, bj, H, T, D, 10, toks, cap, res,
+                work, wbytes, stream=stream)
+
+    run(256)
+    ms = time_events(torch, lambda: run(frames), 1, stream)
+    count, frame, status, steps = (int(v) for v in res.cpu().tolist())
+    audio_min = frames * 0.08 / 60.0
+    return {"frames": frames, "tokens": count, "joint_steps": steps, "status": status, "ms": round(ms, 2),
+            "us_per_joint_step": round(1e3 * ms / max(steps, 1), 3), "ms_per_audio_min": round(ms / audio_min, 4),
+            "note": "one persistent launch; every weight register-resident; LSTM fp16, joint INT8"}
+
+
 def joint_streaming(pk, torch, stream, copies=512, reps=5):
     """The joint GEMV kernel streaming INT8 weights from HBM: `copies` joint
     matrices stacked as one [copies*1030 x 640] weight (337 MB, beyond the
@@ -503,6 +545,7 @@ def main():
     k_tflops = k_flops / (k_ms * 1e-3) / 1e12
     joint = joint_bench(pk, torch, stream)
     joint["hbm_streaming"] = joint_streaming(pk, torch, stream)
+    decode = decode_bench(pk, torch, stream, args.frames)
     configs = config_results(pk, torch, stream)
     cpu = None if args.no_cpu else cpu_baseline(plan)
 
@@ -526,6 +569,7 @@ def main():
         "pct_mfma_peak": round(100.0 * tops / PEAK["fp8"], 2),
         "ms_per_audio_min": round(ms_step / audio_min, 4),
         "joint_gemv": joint,
+        "tdt_decode": decode,
         "roofline": {"kernel": "g3::gemm3_kernel<FP8, EPI_F8> (FF1 expand 1024->4096, T=45000)",
                      "bound": "mfma", "achieved": round(k_tflops, 2), "peak": PEAK["fp8"],
                      "unit": "TFLOP/s", "frac": round(k_tflops / PEAK["fp8"], 4), "traffic": measured_traffic(),

@@ -359,6 +359,28 @@ int32_t pk_joint_scan(const void* weight, int32_t weight_int8, const float* w_sc
                       int32_t token_outputs, int32_t durations, int32_t frames, int32_t enc_stride,
                       int32_t max_symbols, int32_t* state, uint32_t* workspace, void* stream);
 
+/* ---- TDT greedy decode (decoder.cu:146-445, fp16 prediction network) --------
+ * The whole batch-1 greedy decode of one utterance in one persistent launch:
+ * 2-layer LSTM prediction network (weights [4H x H] fp16 with gate rows
+ * i, f, g, o; fp32 biases [4H]) on the last emitted token's embedding (zeros
+ * before the first token), projection [H x H] fp16 + fp32 bias, joint as
+ * pk_joint_gemv (fp16 weights, or INT8 with per-row scales), token / duration
+ * decision and the frame / symbol rules (decoder.cu:773-783).  The prediction
+ * is recomputed, and its LSTM state committed, after each emitted token.
+ * tokens (device int32[capacity]) receive the emitted ids; result (device
+ * int32[4]) = {tokens emitted (may exceed capacity), final frame, status
+ * (0, or -2 if the persistent workgroups failed to meet), joint steps}.
+ * hidden % 128 == 0, hidden <= 1024, durations <= 8; workspace = device
+ * memory of pk_tdt_decode_workspace_bytes(hidden) bytes, overwritten. */
+int32_t pk_tdt_decode_workspace_bytes(int32_t hidden);
+int32_t pk_tdt_decode(const uint16_t* enc, int32_t frames, int32_t enc_stride, const uint16_t* embedding,
+                      const uint16_t* w_ih0, const uint16_t* w_hh0, const float* b_ih0, const float* b_hh0,
+                      const uint16_t* w_ih1, const uint16_t* w_hh1, const float* b_ih1, const float* b_hh1,
+                      const uint16_t* w_proj, const float* b_proj, const void* w_joint, int32_t joint_int8,
+                      const float* joint_scales, const float* b_joint, int32_t hidden, int32_t token_outputs,
+                      int32_t durations, int32_t max_symbols, int32_t* tokens, int32_t capacity, int32_t* result,
+                      void* workspace, uint64_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

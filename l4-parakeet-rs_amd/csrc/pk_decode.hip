@@ -1,0 +1,400 @@
+// Batch-1 greedy TDT decode in one persistent launch (decoder.cu:146-445,
+// the fp16 prediction-network path): 2-layer LSTM prediction network (gate
+// rows i, f, g, o of 4H), projection + bias, joint, token / duration decision
+// and the frame / symbol rules, for all frames of one utterance.
+//
+// Every weight stays in registers for the whole decode: the grid is one
+// workgroup per CU (up to 256, 4 wave64 each) and wave w owns LSTM hidden unit
+// w of both layers (4 gates x (W_ih, W_hh) rows), projection row w and joint
+// rows 2w, 2w+1 (logical order: the duration rows first, so workgroup 0 holds
+// them all).  Lane l holds k = 2l + 128j (j < H/128) of every row it owns.
+// The phases (layer 0, layer 1, projection, joint) are separated by a grid
+// barrier made of per-workgroup published 64-bit words (a step tag and, for
+// the joint, the workgroup's best token key and workgroup 0's duration): every
+// workgroup polls all words in parallel, so one barrier costs about one memory
+// round trip, and the joint's decision comes with its barrier.  State vectors
+// (h, c of both layers, double buffered as committed / candidate, and the
+// prediction) move through agent-scope atomic stores and loads in a caller
+// workspace.  Blank steps run only the joint; an emitted token commits the
+// candidate state and re-runs the prediction network on its embedding.
+#include "pk_kernels.hpp"
+
+namespace pk {
+
+namespace {
+
+constexpr int kDecThreads = 256;
+constexpr int kDecMaxBlocks = 256;
+constexpr uint32_t kDecSpinLimit = 1u << 22;
+constexpr int kDecWords = 8;                                // u32 offset of the barrier words
+constexpr int kDecState = kDecWords + 2 * kDecMaxBlocks * 2;  // u32 offset of the state vectors, after the words
+static_assert(kDecState == 1032, "workspace layout");
+
+struct DecodeArgs {
+    const uint16_t* enc;  // [frames x enc_stride] fp16
+    const uint16_t* emb;  // [token_outputs - 1 x H] fp16
+    const uint16_t* w_ih[2];
+    const uint16_t* w_hh[2];
+    const float* b_ih[2];
+    const float* b_hh[2];
+    const uint16_t* w_proj;
+    const float* b_proj;
+    const void* w_joint;  // fp16 or int8 [outputs x H]
+    const float* joint_scales;
+    const float* b_joint;
+    int32_t* tokens;
+    int32_t* result;  // {tokens emitted, final frame, status, joint steps}
+    uint32_t* ws;     // [0] abort; words at kDecWords (2 x 256 u64 = 1024 u32); state floats at kDecState
+    int frames, enc_stride, outputs, token_outputs, durations, max_symbols, capacity;
+};
+
+__device__ __forceinline__ uint32_t key_bits(float score) {
+    if (score == 0.0f) score = 0.0f;
+    const uint32_t bits = __float_as_uint(score);
+    return (bits & 0x80000000u) ? ~bits : (bits ^ 0x80000000u);
+}
+
+__device__ __forceinline__ float sigmoid(float v) { return 1.0f / (1.0f + expf(-v)); }
+
+__device__ __forceinline__ float2 ld2(const float* p) {
+    const unsigned long long v = __hip_atomic_load((const unsigned long long*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return make_float2(__uint_as_float((uint32_t)v), __uint_as_float((uint32_t)(v >> 32)));
+}
+__device__ __forceinline__ float ld1(const float* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+__device__ __forceinline__ void st1(float* p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+// fp16 pair -> two floats
+__device__ __forceinline__ float lo16(uint32_t w) { return h2f((uint16_t)(w & 0xffffu)); }
+__device__ __forceinline__ float hi16(uint32_t w) { return h2f((uint16_t)(w >> 16)); }
+
+template <bool kInt8, int KP>
+__global__ __launch_bounds__(kDecThreads, 1) void tdt_decode_kernel(DecodeArgs p) {
+    constexpr int H = 128 * KP;
+    __shared__ unsigned long long best_w[4];
+    __shared__ unsigned long long payload_s;
+    __shared__ float dur_sc[8];
+    __shared__ int dur_s;
+    __shared__ int stop_s;
+    const int blk = blockIdx.x, nblocks = gridDim.x;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int gw = blk * 4 + wave;
+    const int T = p.token_outputs, D = p.durations, blank = T - 1;
+    unsigned long long* words = (unsigned long long*)(p.ws + kDecWords);
+    float* st = (float*)(p.ws + kDecState);
+    // state: h[buf][layer][H], c[buf][layer][H], pred[H]
+    auto hp = [&](int buf, int layer) { return st + (buf * 2 + layer) * H; };
+    auto cp = [&](int buf, int layer) { return st + 4 * H + (buf * 2 + layer) * H; };
+    float* pred = st + 8 * H;
+
+    // ---- weights into registers --------------------------------------------------
+    const bool owns_unit = gw < H;
+    const int u = owns_unit ? gw : 0;
+    uint32_t wih[2][4][KP], whh[2][4][KP], wpj[KP];
+    float bias[2][4];
+#pragma unroll
+    for (int l = 0; l < 2; ++l)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const size_t row = (size_t)(g * H + u) * H;
+#pragma unroll
+            for (int j = 0; j < KP; ++j) {
+                const int k = 2 * lane + 128 * j;
+                wih[l][g][j] = *(const uint32_t*)(p.w_ih[l] + row + k);
+                whh[l][g][j] = *(const uint32_t*)(p.w_hh[l] + row + k);
+            }
+            bias[l][g] = p.b_ih[l][g * H + u] + p.b_hh[l][g * H + u];
+        }
+#pragma unroll
+    for (int j = 0; j < KP; ++j) wpj[j] = *(const uint32_t*)(p.w_proj + (size_t)u * H + 2 * lane + 128 * j);
+    const float bpj = p.b_proj[u];
+    uint32_t wj[2][KP];
+    float wjs[2], wjb[2];
+    int jid[2];
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+        const int i = 2 * gw + r;
+        jid[r] = i < D ? T + i : (i < T + D ? i - D : -1);
+        const int row = jid[r] < 0 ? p.outputs - 1 : jid[r];
+#pragma unroll
+        for (int j = 0; j < KP; ++j) {
+            const int k = 2 * lane + 128 * j;
+            if constexpr (kInt8) wj[r][j] = *(const uint16_t*)((const int8_t*)p.w_joint + (size_t)row * H + k);
+            else wj[r][j] = *(const uint32_t*)((const uint16_t*)p.w_joint + (size_t)row * H + k);
+        }
+        wjs[r] = kInt8 ? p.joint_scales[row] : 1.0f;
+        wjb[r] = p.b_joint[row];
+    }
+
+    // ---- grid barrier: publish this workgroup's word, wait for every tag ---------
+    uint32_t epoch = 0;
+    bool failed = false;
+    auto barrier = [&](unsigned long long payload) -> unsigned long long {
+        // this wave's state stores have completed before the word goes out
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        const uint32_t tag = (epoch + 1) & 0x1fffu;
+        unsigned long long* slot = words + (epoch & 1) * kDecMaxBlocks;
+        if (tid == 0) __hip_atomic_store(slot + blk, payload | tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        unsigned long long mine = 0;
+        uint32_t spins = 0;
+        while (true) {
+            bool ready = true;
+            if (tid < nblocks) {
+                mine = __hip_atomic_load(slot + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                ready = ((uint32_t)mine & 0x1fffu) == tag;
+            }
+            if (__syncthreads_and(ready)) break;
+            if ((++spins & 63) == 0) {
+                // one thread decides, so the whole workgroup leaves together
+                if (tid == 0)
+                    stop_s = spins > kDecSpinLimit || __hip_atomic_load(&p.ws[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u;
+                __syncthreads();
+                if (stop_s) {
+                    if (tid == 0) __hip_atomic_store(&p.ws[0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    failed = true;
+                    break;
+                }
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+        ++epoch;
+        return mine;  // thread t holds workgroup t's word
+    };
+
+    int frame = 0, symbols = 0, last = blank, count = 0, steps = 0, alt = 0;
+    bool emitted = false, valid = false;
+    float pv[2 * KP];
+    while (frame < p.frames && !failed) {
+        if (!valid) {
+            // ---- two LSTM layers on the last token's embedding (zeros before any)
+#pragma unroll
+            for (int l = 0; l < 2; ++l) {
+                if (owns_unit) {
+                    float x[2 * KP], hv[2 * KP];
+#pragma unroll
+                    for (int j = 0; j < KP; ++j) {
+                        const int k = 2 * lane + 128 * j;
+                        if (l == 0) {
+                            if (emitted) {
+                                const uint32_t e = *(const uint32_t*)(p.emb + (size_t)last * H + k);
+                                x[2 * j] = lo16(e);
+                                x[2 * j + 1] = hi16(e);
+                            } else {
+                                x[2 * j] = x[2 * j + 1] = 0.0f;
+                            }
+                        } else {
+                            const float2 v = ld2(hp(alt ^ 1, 0) + k);  // this update's layer-0 output
+                            x[2 * j] = v.x;
+                            x[2 * j + 1] = v.y;
+                        }
+                        const float2 hh = ld2(hp(alt, l) + k);
+                        hv[2 * j] = hh.x;
+                        hv[2 * j + 1] = hh.y;
+                    }
+                    float s[4];
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        float a = 0.0f;
+#pragma unroll
+                        for (int j = 0; j < KP; ++j) {
+                            a = __builtin_fmaf(lo16(wih[l][g][j]), x[2 * j], a);
+                            a = __builtin_fmaf(hi16(wih[l][g][j]), x[2 * j + 1], a);
+                            a = __builtin_fmaf(lo16(whh[l][g][j]), hv[2 * j], a);
+                            a = __builtin_fmaf(hi16(whh[l][g][j]), hv[2 * j + 1], a);
+                        }
+                        s[g] = wave_sum(a) + bias[l][g];
+                    }
+                    if (lane == 0) {
+                        const float ig = sigmoid(s[0]), fg = sigmoid(s[1]), cg = tanhf(s[2]), og = sigmoid(s[3]);
+                        const float cell = fg * ld1(cp(alt, l) + u) + ig * cg;
+                        st1(cp(alt ^ 1, l) + u, cell);
+                        st1(hp(alt ^ 1, l) + u, og * tanhf(cell));
+                    }
+                }
+                barrier(0);
+                if (failed) break;
+            }
+            if (failed) break;
+            // ---- projection of the new layer-1 output
+            if (owns_unit) {
+                float a = 0.0f;
+#pragma unroll
+                for (int j = 0; j < KP; ++j) {
+                    const float2 v = ld2(hp(alt ^ 1, 1) + 2 * lane + 128 * j);
+                    a = __builtin_fmaf(lo16(wpj[j]), v.x, a);
+                    a = __builtin_fmaf(hi16(wpj[j]), v.y, a);
+                }
+                a = wave_sum(a) + bpj;
+                if (lane == 0) st1(pred + u, a);
+            }
+            barrier(0);
+            if (failed) break;
+#pragma unroll
+            for (int j = 0; j < KP; ++j) {
+                const float2 v = ld2(pred + 2 * lane + 128 * j);
+                pv[2 * j] = v.x;
+                pv[2 * j + 1] = v.y;
+            }
+            valid = true;
+        }
+        // ---- joint step at `frame`
+        {
+            float bs = -__builtin_huge_valf();
+            int bi = 0x7fffffff;
+            float x[2 * KP];
+            const uint16_t* e = p.enc + (size_t)frame * p.enc_stride + 2 * lane;
+#pragma unroll
+            for (int j = 0; j < KP; ++j) {
+                const uint32_t ev = *(const uint32_t*)(e + 128 * j);
+                x[2 * j] = __builtin_fmaxf(lo16(ev) + pv[2 * j], 0.0f);
+                x[2 * j + 1] = __builtin_fmaxf(hi16(ev) + pv[2 * j + 1], 0.0f);
+            }
+#pragma unroll
+            for (int r = 0; r < 2; ++r) {
+                float a = 0.0f;
+#pragma unroll
+                for (int j = 0; j < KP; ++j) {
+                    float w0, w1;
+                    if constexpr (kInt8) {
+                        w0 = (float)(int8_t)(wj[r][j] & 0xffu);
+                        w1 = (float)(int8_t)((wj[r][j] >> 8) & 0xffu);
+                    } else {
+                        w0 = lo16(wj[r][j]);
+                        w1 = hi16(wj[r][j]);
+                    }
+                    a = __builtin_fmaf(w0, x[2 * j], a);
+                    a = __builtin_fmaf(w1, x[2 * j + 1], a);
+                }
+                const float score = __builtin_fmaf(wjs[r], wave_sum(a), wjb[r]);
+                const int id = jid[r];
+                if (id >= T) {
+                    if (lane == 0) dur_sc[id - T] = score;  // workgroup 0 only
+                } else if (id >= 0) {
+                    if (score > bs || (score == bs && id < bi)) { bs = score; bi = id; }
+                }
+            }
+            if (lane == 0)
+                best_w[wave] = bi == 0x7fffffff ? 0ull
+                                                : (((unsigned long long)key_bits(bs) << 32) | ((unsigned long long)(0xffffu - (uint32_t)bi) << 16));
+        }
+        __syncthreads();
+        if (tid == 0) {
+            unsigned long long b = best_w[0];
+            for (int i = 1; i < 4; ++i) b = best_w[i] > b ? best_w[i] : b;
+            if (blk == 0) {  // first maximum of the duration scores
+                int d = 0;
+                for (int i = 1; i < D; ++i)
+                    if (dur_sc[i] > dur_sc[d]) d = i;
+                b |= (unsigned long long)d << 13;
+            }
+            payload_s = b;
+        }
+        __syncthreads();
+        const unsigned long long word = barrier(payload_s);
+        if (failed) break;
+        // decision: the largest word is the best token; workgroup 0's carries the duration
+        {
+            unsigned long long b = tid < nblocks ? word : 0ull;
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) {
+                const unsigned long long o = __shfl_xor(b, off, 64);
+                b = o > b ? o : b;
+            }
+            if (lane == 0) best_w[wave] = b;
+            if (tid == 0) dur_s = (int)(((uint32_t)word >> 13) & 7u);
+            __syncthreads();
+            b = best_w[0];
+            for (int i = 1; i < 4; ++i) b = best_w[i] > b ? best_w[i] : b;
+            const int token = (int)(0xffffu - (((uint32_t)b) >> 16));
+            const int dur = dur_s;
+            __syncthreads();  // best_w / dur_s are reused next step
+            ++steps;
+            if (token != blank) {
+                if (blk == 0 && tid == 0 && count < p.capacity) p.tokens[count] = token;
+                ++count;
+                last = token;
+                emitted = true;
+                valid = false;
+                alt ^= 1;  // the candidate state becomes the committed one
+            }
+            ++symbols;
+            frame += dur;
+            if (dur != 0 || symbols == p.max_symbols) {
+                if (dur == 0) ++frame;
+                symbols = 0;
+            }
+        }
+    }
+    if (blk == 0 && tid == 0) {
+        p.result[0] = count;
+        p.result[1] = frame;
+        p.result[2] = failed ? -2 : 0;
+        p.result[3] = steps;
+    }
+}
+
+__global__ void decode_clear_kernel(uint32_t* ws, int words) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < words; i += gridDim.x * blockDim.x) ws[i] = 0u;
+}
+
+}  // namespace
+
+int decode_workspace_words(int hidden) { return kDecState + 9 * hidden; }
+
+int launch_tdt_decode(const uint16_t* enc, int frames, int enc_stride, const uint16_t* emb, const uint16_t* const* w_ih,
+                      const uint16_t* const* w_hh, const float* const* b_ih, const float* const* b_hh, const uint16_t* w_proj,
+                      const float* b_proj, const void* w_joint, int joint_int8, const float* joint_scales, const float* b_joint,
+                      int hidden, int token_outputs, int durations, int max_symbols, int32_t* tokens, int capacity, int32_t* result,
+                      uint32_t* workspace, hipStream_t s) {
+    int blocks = cu_count();
+    if (blocks > kDecMaxBlocks) blocks = kDecMaxBlocks;
+    const int outputs = token_outputs + durations;
+    if (hidden > 4 * blocks || outputs > 8 * blocks) {
+        set_error("decode needs hidden <= %d and outputs <= %d on this GPU", 4 * blocks, 8 * blocks);
+        return -1;
+    }
+    DecodeArgs a{};
+    a.enc = enc;
+    a.emb = emb;
+    for (int l = 0; l < 2; ++l) {
+        a.w_ih[l] = w_ih[l];
+        a.w_hh[l] = w_hh[l];
+        a.b_ih[l] = b_ih[l];
+        a.b_hh[l] = b_hh[l];
+    }
+    a.w_proj = w_proj;
+    a.b_proj = b_proj;
+    a.w_joint = w_joint;
+    a.joint_scales = joint_scales;
+    a.b_joint = b_joint;
+    a.tokens = tokens;
+    a.result = result;
+    a.ws = workspace;
+    a.frames = frames;
+    a.enc_stride = enc_stride;
+    a.outputs = outputs;
+    a.token_outputs = token_outputs;
+    a.durations = durations;
+    a.max_symbols = max_symbols;
+    a.capacity = capacity;
+    decode_clear_kernel<<<16, 256, 0, s>>>(workspace, decode_workspace_words(hidden));
+    switch (hidden >> 7) {
+#define PK_DEC_CASE(KP)                                                                   \
+    case KP:                                                                              \
+        if (joint_int8) tdt_decode_kernel<true, KP><<<blocks, kDecThreads, 0, s>>>(a);   \
+        else tdt_decode_kernel<false, KP><<<blocks, kDecThreads, 0, s>>>(a);             \
+        break;
+        PK_DEC_CASE(1) PK_DEC_CASE(2) PK_DEC_CASE(3) PK_DEC_CASE(4) PK_DEC_CASE(5) PK_DEC_CASE(6) PK_DEC_CASE(7) PK_DEC_CASE(8)
+#undef PK_DEC_CASE
+    default: break;
+    }
+    return 0;
+}
+
+}  // namespace pk

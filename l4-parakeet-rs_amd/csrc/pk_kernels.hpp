@@ -27,6 +27,13 @@ int launch_joint_scan(const void* w, int w_int8, const float* w_scales, const fl
                       int outputs, int hidden, int token_outputs, int durations, int frames, int enc_stride, int max_symbols,
                       int* state, uint32_t* workspace, hipStream_t s);
 
+int decode_workspace_words(int hidden);
+int launch_tdt_decode(const uint16_t* enc, int frames, int enc_stride, const uint16_t* emb, const uint16_t* const* w_ih,
+                      const uint16_t* const* w_hh, const float* const* b_ih, const float* const* b_hh, const uint16_t* w_proj,
+                      const float* b_proj, const void* w_joint, int joint_int8, const float* joint_scales, const float* b_joint,
+                      int hidden, int token_outputs, int durations, int max_symbols, int32_t* tokens, int capacity, int32_t* result,
+                      uint32_t* workspace, hipStream_t s);
+
 void set_error(const char* fmt, ...);
 int cu_count();
 int launch_sparse24_contract(const uint8_t* data, const uint8_t* meta, const uint8_t* w, const float* w_scales, float in_scale,

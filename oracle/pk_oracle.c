@@ -1013,3 +1013,99 @@ void orc_joint_decide(const float* scores, int token_outputs, int durations, int
     *token = best;
     *duration = d;
 }
+
+/* ---- TDT greedy decode (prediction network + joint) ------------------------ */
+
+/* One LSTM layer step (decoder.cu:116-129 lstm_cell, gate rows i, f, g, o of
+ * 4*hidden): gates = b_ih + b_hh + W_ih x + W_hh h (x NULL = zeros),
+ * c' = sigmoid(f) c + sigmoid(i) tanh(g), h' = sigmoid(o) tanh(c'). */
+void orc_lstm_step(const uint16_t* w_ih, const uint16_t* w_hh, const float* b_ih, const float* b_hh,
+                   const float* x, const float* h, const float* c, int hidden, float* h_out, float* c_out) {
+    for (int u = 0; u < hidden; ++u) {
+        float g[4];
+        for (int gate = 0; gate < 4; ++gate) {
+            const size_t row = (size_t)(gate * hidden + u);
+            double s = (double)b_ih[row] + (double)b_hh[row];
+            for (int k = 0; k < hidden; ++k) {
+                if (x) s += (double)orc_f16_to_f32(w_ih[row * hidden + k]) * (double)x[k];
+                s += (double)orc_f16_to_f32(w_hh[row * hidden + k]) * (double)h[k];
+            }
+            g[gate] = (float)s;
+        }
+        const float ig = 1.0f / (1.0f + expf(-g[0]));
+        const float fg = 1.0f / (1.0f + expf(-g[1]));
+        const float cg = tanhf(g[2]);
+        const float og = 1.0f / (1.0f + expf(-g[3]));
+        const float cell = fg * c[u] + ig * cg;
+        c_out[u] = cell;
+        h_out[u] = og * tanhf(cell);
+    }
+}
+
+/* decoder.cu:146-445 (tdt_persistent_fp16): greedy TDT decode.  The prediction
+ * (2-layer LSTM on the last emitted token's embedding, zero input before the
+ * first token, then projection + bias) is recomputed after each emitted token
+ * and its state committed; blanks leave it unchanged.  Joint and frame rules
+ * as orc_joint_scores_* / orc_joint_decide and decoder.cu:773-783.  Returns
+ * the number of tokens (at most capacity are stored); pred_out = the final
+ * prediction vector, *frame_out = the final frame index. */
+int orc_tdt_decode(const uint16_t* enc, int frames, int enc_stride, const uint16_t* emb, const uint16_t* w_ih0,
+                   const uint16_t* w_hh0, const float* b_ih0, const float* b_hh0, const uint16_t* w_ih1,
+                   const uint16_t* w_hh1, const float* b_ih1, const float* b_hh1, const uint16_t* w_proj,
+                   const float* b_proj, const void* w_joint, int joint_int8, const float* joint_scales,
+                   const float* b_joint, int hidden, int token_outputs, int durations, int max_symbols,
+                   int32_t* tokens, int capacity, float* pred_out, int* frame_out) {
+    const int outputs = token_outputs + durations, blank = token_outputs - 1;
+    float* h = (float*)calloc((size_t)4 * hidden, sizeof(float));  /* committed h0, h1, c0, c1 */
+    float* cand = (float*)calloc((size_t)4 * hidden, sizeof(float));
+    float* x = (float*)malloc((size_t)hidden * sizeof(float));
+    float* pred = (float*)calloc((size_t)hidden, sizeof(float));
+    float* scores = (float*)malloc((size_t)outputs * sizeof(float));
+    int frame = 0, symbols = 0, last = blank, emitted = 0, valid = 0, count = 0;
+    while (frame < frames) {
+        if (!valid) {
+            if (emitted)
+                for (int k = 0; k < hidden; ++k) x[k] = orc_f16_to_f32(emb[(size_t)last * hidden + k]);
+            orc_lstm_step(w_ih0, w_hh0, b_ih0, b_hh0, emitted ? x : NULL, h, h + 2 * hidden, hidden, cand,
+                          cand + 2 * hidden);
+            orc_lstm_step(w_ih1, w_hh1, b_ih1, b_hh1, cand, h + hidden, h + 3 * hidden, hidden, cand + hidden,
+                          cand + 3 * hidden);
+            for (int o = 0; o < hidden; ++o) {
+                double s = (double)b_proj[o];
+                for (int k = 0; k < hidden; ++k)
+                    s += (double)orc_f16_to_f32(w_proj[(size_t)o * hidden + k]) * (double)cand[hidden + k];
+                pred[o] = (float)s;
+            }
+            valid = 1;
+        }
+        const uint16_t* e = enc + (size_t)frame * enc_stride;
+        if (joint_int8)
+            orc_joint_scores_i8((const int8_t*)w_joint, joint_scales, b_joint, e, pred, outputs, hidden, scores);
+        else
+            orc_joint_scores_f16((const uint16_t*)w_joint, b_joint, e, pred, outputs, hidden, scores);
+        int tok, dur;
+        orc_joint_decide(scores, token_outputs, durations, &tok, &dur);
+        if (tok != blank) {
+            if (count < capacity) tokens[count] = tok;
+            ++count;
+            last = tok;
+            emitted = 1;
+            valid = 0;
+            memcpy(h, cand, (size_t)4 * hidden * sizeof(float));
+        }
+        ++symbols;
+        frame += dur;
+        if (dur != 0 || symbols == max_symbols) {
+            if (dur == 0) ++frame;
+            symbols = 0;
+        }
+    }
+    memcpy(pred_out, pred, (size_t)hidden * sizeof(float));
+    *frame_out = frame;
+    free(h);
+    free(cand);
+    free(x);
+    free(pred);
+    free(scores);
+    return count;
+}

@@ -98,6 +98,16 @@ void orc_joint_decide(const float* scores, int token_outputs, int durations, int
 int orc_threads(void);
 void orc_set_threads(int threads);
 
+/* ---- TDT decode ------------------------------------------------------------- */
+void orc_lstm_step(const uint16_t* w_ih, const uint16_t* w_hh, const float* b_ih, const float* b_hh,
+                   const float* x, const float* h, const float* c, int hidden, float* h_out, float* c_out);
+int orc_tdt_decode(const uint16_t* enc, int frames, int enc_stride, const uint16_t* emb, const uint16_t* w_ih0,
+                   const uint16_t* w_hh0, const float* b_ih0, const float* b_hh0, const uint16_t* w_ih1,
+                   const uint16_t* w_hh1, const float* b_ih1, const float* b_hh1, const uint16_t* w_proj,
+                   const float* b_proj, const void* w_joint, int joint_int8, const float* joint_scales,
+                   const float* b_joint, int hidden, int token_outputs, int durations, int max_symbols,
+                   int32_t* tokens, int capacity, float* pred_out, int* frame_out);
+
 #ifdef __cplusplus
 }
 #endif

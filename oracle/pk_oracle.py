@@ -81,6 +81,8 @@ def _declare(l):
         "orc_joint_scores_f16": (None, [P, P, P, P, I, I, P]),
         "orc_joint_scores_i8": (None, [P, P, P, P, P, I, I, P]),
         "orc_joint_decide": (None, [P, I, I, P, P]),
+        "orc_lstm_step": (None, [P, P, P, P, P, P, P, I, P, P]),
+        "orc_tdt_decode": (I, [P, I, I, P, P, P, P, P, P, P, P, P, P, P, P, I, P, P, I, I, I, I, P, I, P, P]),
         "orc_threads": (I, []),
         "orc_set_threads": (None, [I]),
     }
@@ -494,3 +496,41 @@ def joint_scan(scores_of_frame, frames, frame=0, symbols=0, token_outputs=1025, 
         if tok != blank:
             return frame, symbols, tok, steps
     return frame, symbols, -1, steps
+
+
+def lstm_step(w_ih, w_hh, b_ih, b_hh, x, h, c):
+    """decoder.cu:116-129: one LSTM layer step; x None = zero input."""
+    w_ih, w_hh = _h(w_ih), _h(w_hh)
+    hidden = w_ih.shape[1]
+    f32 = lambda a: np.ascontiguousarray(a, np.float32)
+    ho = np.empty(hidden, np.float32)
+    co = np.empty(hidden, np.float32)
+    lib().orc_lstm_step(_p(w_ih), _p(w_hh), _p(f32(b_ih)), _p(f32(b_hh)), None if x is None else _p(f32(x)),
+                        _p(f32(h)), _p(f32(c)), hidden, _p(ho), _p(co))
+    return ho, co
+
+
+def tdt_decode(enc, emb, lstm, proj, joint, token_outputs=1025, durations=5, max_symbols=10, capacity=None):
+    """decoder.cu:146-445 greedy TDT decode.  lstm = (w_ih0, w_hh0, b_ih0, b_hh0,
+    w_ih1, w_hh1, b_ih1, b_hh1) (fp16 weights [4H x H], fp32 biases); proj =
+    (w fp16 [H x H], b fp32 [H]); joint = (w fp16 or int8 [O x H], scales or
+    None, b fp32 [O]).  Returns (tokens, final frame, final prediction)."""
+    enc = _h(enc)
+    frames, hidden = enc.shape
+    f32 = lambda a: np.ascontiguousarray(a, np.float32)
+    w_ih0, w_hh0, b_ih0, b_hh0, w_ih1, w_hh1, b_ih1, b_hh1 = lstm
+    wj, sj, bj = joint
+    int8 = np.asarray(wj).dtype == np.int8
+    wj = np.ascontiguousarray(wj)
+    capacity = capacity or frames * max_symbols
+    toks = np.empty(capacity, np.int32)
+    pred = np.empty(hidden, np.float32)
+    frame = ctypes.c_int()
+    keep = [f32(b_ih0), f32(b_hh0), f32(b_ih1), f32(b_hh1), f32(proj[1]), f32(bj),
+            None if sj is None else f32(sj)]
+    n = lib().orc_tdt_decode(_p(enc), frames, hidden, _p(_h(emb)), _p(_h(w_ih0)), _p(_h(w_hh0)), _p(keep[0]),
+                             _p(keep[1]), _p(_h(w_ih1)), _p(_h(w_hh1)), _p(keep[2]), _p(keep[3]),
+                             _p(_h(proj[0])), _p(keep[4]), _p(wj), int(int8), _p(keep[6]) if int8 else None,
+                             _p(keep[5]), hidden, token_outputs, durations, max_symbols, _p(toks), capacity,
+                             _p(pred), ctypes.byref(frame))
+    return toks[:min(n, capacity)].copy(), frame.value, pred

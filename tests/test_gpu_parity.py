@@ -668,3 +668,51 @@ def test_artifact_derive_linear(pk, orc, fmt, tmp_path):
         assert np.array_equal(host(sc).view(np.uint16), rs.view(np.uint16))
         assert np.array_equal(host(z).view(np.uint16), rz.view(np.uint16))
     art.close()
+
+
+# ---- TDT greedy decode ---------------------------------------------------------------------
+
+def decode_case(H, T, D, frames, seed, int8):
+    rng = np.random.default_rng(seed)
+    f16 = lambda *s, sc=0.05: (rng.standard_normal(s) * sc).astype(np.float16)
+    f32 = lambda *s, sc=0.1: (rng.standard_normal(s) * sc).astype(np.float32)
+    lstm = (f16(4 * H, H), f16(4 * H, H), f32(4 * H), f32(4 * H), f16(4 * H, H), f16(4 * H, H), f32(4 * H), f32(4 * H))
+    proj = (f16(H, H, sc=0.1), f32(H))
+    wj = f16(T + D, H, sc=0.08)
+    bj = f32(T + D)
+    bj[T - 1] += 2.0 * np.sqrt(H / 640)  # blank-dominated frames, as in real audio
+    enc = f16(frames, H, sc=0.5)
+    emb = f16(T - 1, H, sc=0.5)
+    return lstm, proj, wj, bj, enc, emb
+
+
+@pytest.mark.parametrize("H,int8", [(640, False), (640, True), (128, False)])
+def test_tdt_decode(pk, orc, H, int8):
+    """The whole utterance decoded in one persistent launch: tokens, final
+    frame and final prediction vector against the oracle's decode loop."""
+    T, D, frames = 1025, 5, 96
+    note(f"tdt decode H={H} int8={int8}")
+    lstm, proj, wj, bj, enc, emb = decode_case(H, T, D, frames, 180 + H + int8, int8)
+    if int8:
+        wq, ws = orc.quantize_int8_rows(wj)
+        joint = (wq, ws, bj)
+    else:
+        joint = (wj, None, bj)
+    ref_toks, ref_frame, ref_pred = orc.tdt_decode(enc, emb, lstm, proj, joint, T, D)
+    assert 3 <= len(ref_toks) <= 10 * frames, len(ref_toks)
+    d = [dev(a) for a in lstm]
+    cap = frames * 10
+    toks = torch.zeros(cap, dtype=torch.int32, device="cuda")
+    res = torch.zeros(4, dtype=torch.int32, device="cuda")
+    wbytes = pk.lib.pk_tdt_decode_workspace_bytes(H)
+    work = torch.zeros(wbytes // 4, dtype=torch.int32, device="cuda")
+    pk.call("pk_tdt_decode", dev(enc), frames, H, dev(emb), d[0], d[1], d[2], d[3], d[4], d[5], d[6], d[7],
+            dev(proj[0]), dev(proj[1]), dev(joint[0]), int(int8), None if joint[1] is None else dev(joint[1]),
+            dev(bj), H, T, D, 10, toks, cap, res, work, wbytes)
+    count, frame, status, steps = (int(v) for v in host(res))
+    note(f"tdt decode: {count} tokens, {steps} joint steps, status {status}")
+    assert status == 0
+    assert count == len(ref_toks) and frame == ref_frame
+    assert np.array_equal(host(toks)[:count], ref_toks)
+    pred = host(work).view(np.float32)[1032 + 8 * H:1032 + 9 * H]  # state after the 1032-word barrier area
+    assert np.max(np.abs(pred - ref_pred)) <= 1e-4 * max(1.0, float(np.max(np.abs(ref_pred))))

@@ -369,3 +369,53 @@ def test_joint_scan_frame_rules(oracle):
     assert oracle.joint_scan(f, F, frame=6, symbols=9, token_outputs=T, durations=D) == (7, 0, 4, 1)
     # ties: lower token id and first duration maximum win
     assert oracle.joint_decide(np.zeros(T + D, np.float32), T, D) == (0, 0)
+
+
+def test_lstm_step_matches_torch_lstm_cell(oracle):
+    """The oracle's LSTM cell (gate order i, f, g, o; decoder.cu:116-129)
+    against torch.nn.LSTMCell with the same fp16-valued weights."""
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(170)
+    H = 64
+    w_ih = (rng.standard_normal((4 * H, H)) * 0.2).astype(np.float16)
+    w_hh = (rng.standard_normal((4 * H, H)) * 0.2).astype(np.float16)
+    b_ih, b_hh = rng.standard_normal(4 * H).astype(np.float32), rng.standard_normal(4 * H).astype(np.float32)
+    x, h, c = (rng.standard_normal(H).astype(np.float32) for _ in range(3))
+    cell = torch.nn.LSTMCell(H, H).double()
+    with torch.no_grad():
+        cell.weight_ih.copy_(torch.from_numpy(w_ih.astype(np.float64)))
+        cell.weight_hh.copy_(torch.from_numpy(w_hh.astype(np.float64)))
+        cell.bias_ih.copy_(torch.from_numpy(b_ih.astype(np.float64)))
+        cell.bias_hh.copy_(torch.from_numpy(b_hh.astype(np.float64)))
+        th, tc = cell(torch.from_numpy(x.astype(np.float64))[None], (torch.from_numpy(h.astype(np.float64))[None],
+                                                                      torch.from_numpy(c.astype(np.float64))[None]))
+    oh, oc = oracle.lstm_step(w_ih, w_hh, b_ih, b_hh, x, h, c)
+    assert np.allclose(oh, th[0].numpy(), atol=2e-6) and np.allclose(oc, tc[0].numpy(), atol=2e-6)
+    zh, zc = oracle.lstm_step(w_ih, w_hh, b_ih, b_hh, None, h, c)
+    with torch.no_grad():
+        th, tc = cell(torch.zeros(1, H, dtype=torch.float64), (torch.from_numpy(h.astype(np.float64))[None],
+                                                                torch.from_numpy(c.astype(np.float64))[None]))
+    assert np.allclose(zh, th[0].numpy(), atol=2e-6) and np.allclose(zc, tc[0].numpy(), atol=2e-6)
+
+
+def test_tdt_decode_composition(oracle):
+    """The decode loop is the joint scan between tokens with the prediction
+    network re-run after each token (decoder.cu:733-783 and 616-688): with
+    every joint step forced to blank / duration 1, nothing is emitted and the
+    prediction is the projection of the zero-input LSTM from the zero state."""
+    rng = np.random.default_rng(171)
+    H, T, D, frames = 128, 33, 5, 19
+    f16 = lambda *s: (rng.standard_normal(s) * 0.1).astype(np.float16)
+    f32 = lambda *s: (rng.standard_normal(s) * 0.1).astype(np.float32)
+    lstm = (f16(4 * H, H), f16(4 * H, H), f32(4 * H), f32(4 * H), f16(4 * H, H), f16(4 * H, H), f32(4 * H), f32(4 * H))
+    proj = (f16(H, H), f32(H))
+    bj = f32(T + D)
+    bj[T - 1] = 100.0
+    bj[T + 1] = 100.0
+    toks, frame, pred = oracle.tdt_decode(f16(frames, H), f16(T, H), lstm, proj, (f16(T + D, H), None, bj), T, D)
+    assert len(toks) == 0 and frame == frames
+    z = np.zeros(H, np.float32)
+    h0, c0 = oracle.lstm_step(lstm[0], lstm[1], lstm[2], lstm[3], None, z, z)
+    h1, _ = oracle.lstm_step(lstm[4], lstm[5], lstm[6], lstm[7], h0, z, z)
+    ref = proj[0].astype(np.float64) @ h1.astype(np.float64) + proj[1]
+    assert np.allclose(pred, ref, atol=1e-5)
