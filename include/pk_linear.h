@@ -381,6 +381,58 @@ int32_t pk_tdt_decode(const uint16_t* enc, int32_t frames, int32_t enc_stride, c
                       int32_t durations, int32_t max_symbols, int32_t* tokens, int32_t capacity, int32_t* result,
                       void* workspace, uint64_t workspace_bytes, void* stream);
 
+/* ---- long-form local relative-position attention (encoder.cu:1476-2097) ----
+ * Model constants: width 1024 = 8 heads x 128, window 128 left / 128 right,
+ * position table [8 x 272 x 128] fp16 (rows 257..271 padding).  Query and
+ * key are [padded_rows x 1024] fp16 row-major.  value_fp8 is the buffer
+ * written by pk_quantize_value_int4{,_register} with value_stride =
+ * padded_rows: FP8 V [1024 x stride] (v * 56), S4 V [1024 x stride / 2],
+ * 1024 float per-feature scales.  Tiles of 16 queries whose window lies in
+ * [0, valid_rows) take the quantized tile path; all other queries the FP32
+ * per-query path; rows >= min(rows, valid_rows) are written as zero.
+ * Requirements: padded_rows % 16 == 0, rows and valid_rows in (0, padded_rows],
+ * value_stride >= padded_rows and % 16 == 0, attention_left = attention_right
+ * = 128, 16-byte aligned operands.  `value` (fp16 V) is not read. */
+
+/* encoder.cu:2054-2074 pk_sm89_pack_score_vectors: per 128-value fp16 vector,
+ * scale = max|v|/127 (1 if zero), bytes rn(v/scale) in MMA fragment order. */
+int32_t pk_pack_score_vectors(const uint16_t* input, uint8_t* output, float* scales, int32_t vectors,
+                              void* stream);
+/* encoder.cu:2076-2097 pk_sm89_pack_key_int4: scale = max|v|/7, 64 bytes of
+ * nibbles rn(v/scale) & 15 per vector in MMA fragment order. */
+int32_t pk_pack_key_int4(const uint16_t* input, uint8_t* output, float* scales, int32_t vectors, void* stream);
+/* encoder.cu:561-595 pk_sm89_quantize_value_int4: feature-major fp16 V
+ * [1024 x elements/1024] -> FP8 V, S4 V (clamp +-7, per-feature max/7),
+ * scales.  elements % (1024*16) == 0. */
+int32_t pk_quantize_value_int4(const uint16_t* input, uint8_t* output, int32_t elements, float inverse_scale,
+                               void* stream);
+/* encoder.cu:597-634 pk_sm89_quantize_value_int4_register: as above, but FP8 V
+ * is written only for row pairs (2i, 2i+1) with 2i < 272 or 2i + 1 >=
+ * valid_rows - 272 (the keys the per-query boundary path reads). */
+int32_t pk_quantize_value_int4_register(const uint16_t* input, uint8_t* output, int32_t elements,
+                                        float inverse_scale, int32_t valid_rows, void* stream);
+/* encoder.cu:2024-2036 pk_sm89_local_relpos_attention_tc_scores: fp16 scores,
+ * e4m3 probabilities and V, fp16 output [padded_rows x 1024]. */
+int32_t pk_local_relpos_attention_tc_scores(const uint16_t* query, const uint16_t* key, const uint16_t* value,
+                                            const uint8_t* value_fp8, const uint16_t* position,
+                                            const uint16_t* bias_u, const uint16_t* bias_v, uint16_t* output,
+                                            int32_t rows, int32_t padded_rows, int32_t valid_rows,
+                                            int32_t attention_left, int32_t attention_right,
+                                            int32_t value_stride, void* stream);
+/* encoder.cu:2038-2052 pk_sm89_local_relpos_attention_packed: INT4 content
+ * scores against pk_pack_key_int4 keys (vectors row*8 + head), INT8 position
+ * scores against pk_pack_score_vectors of the position table (vectors
+ * head*272 + row), U4 probabilities x S4 V; output e4m3(fp16(context) * 28)
+ * bytes [padded_rows x 1024], the input of pk_attention_output_fp8. */
+int32_t pk_local_relpos_attention_packed(const uint16_t* query, const uint16_t* key, const uint16_t* value,
+                                         const uint8_t* value_fp8, const uint16_t* position,
+                                         const uint16_t* bias_u, const uint16_t* bias_v, uint8_t* output,
+                                         int32_t rows, int32_t padded_rows, int32_t valid_rows,
+                                         int32_t attention_left, int32_t attention_right, int32_t value_stride,
+                                         const uint8_t* packed_key, const float* key_scales,
+                                         const uint8_t* packed_position, const float* position_scales,
+                                         void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -505,4 +505,104 @@ int32_t pk_tdt_decode(const uint16_t* enc, int32_t frames, int32_t enc_stride, c
     return check_launch("tdt_decode");
 }
 
+// ---- local attention and its producers ---------------------------------------
+
+static bool misaligned(const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) != 0; }
+
+static int32_t pack_vectors(bool int4, const uint16_t* input, uint8_t* output, float* scales, int32_t vectors, void* stream) {
+    if (vectors < 0) { set_error("vectors must be >= 0, got %d", vectors); return PK_E_SHAPE; }
+    if (vectors == 0) return PK_OK;
+    if (!need(input, "input") || !need(output, "output") || !need(scales, "scales")) return PK_E_ARG;
+    if (misaligned(input, 16) || misaligned(output, 4)) { set_error("input must be 16-byte, output 4-byte aligned"); return PK_E_ALIGN; }
+    launch_pack_vectors(int4, input, output, scales, vectors, STREAM);
+    return check_launch(int4 ? "pack_key_int4" : "pack_score_vectors");
+}
+
+int32_t pk_pack_score_vectors(const uint16_t* input, uint8_t* output, float* scales, int32_t vectors, void* stream) {
+    return pack_vectors(false, input, output, scales, vectors, stream);
+}
+
+int32_t pk_pack_key_int4(const uint16_t* input, uint8_t* output, float* scales, int32_t vectors, void* stream) {
+    return pack_vectors(true, input, output, scales, vectors, stream);
+}
+
+static int32_t quantize_value(const uint16_t* input, uint8_t* output, int32_t elements, float inverse_scale, bool edge_only,
+                              int32_t valid_rows, void* stream) {
+    if (elements <= 0 || elements % (1024 * 16)) {
+        set_error("value elements must be a positive multiple of 1024*16, got %d", elements);
+        return PK_E_SHAPE;
+    }
+    if (edge_only && (valid_rows < 0 || valid_rows > elements / 1024)) {
+        set_error("valid_rows %d outside [0, %d]", valid_rows, elements / 1024);
+        return PK_E_SHAPE;
+    }
+    if (!need(input, "input") || !need(output, "output")) return PK_E_ARG;
+    if (misaligned(input, 16) || misaligned(output, 8)) { set_error("input must be 16-byte, output 8-byte aligned"); return PK_E_ALIGN; }
+    launch_quantize_value_int4(input, output, elements / 1024, inverse_scale, edge_only, valid_rows, STREAM);
+    return check_launch("quantize_value_int4");
+}
+
+int32_t pk_quantize_value_int4(const uint16_t* input, uint8_t* output, int32_t elements, float inverse_scale, void* stream) {
+    return quantize_value(input, output, elements, inverse_scale, false, 0, stream);
+}
+
+int32_t pk_quantize_value_int4_register(const uint16_t* input, uint8_t* output, int32_t elements, float inverse_scale,
+                                        int32_t valid_rows, void* stream) {
+    return quantize_value(input, output, elements, inverse_scale, true, valid_rows, stream);
+}
+
+static int32_t local_attention(bool packed, const uint16_t* query, const uint16_t* key, const uint8_t* value_fp8,
+                               const uint16_t* position, const uint16_t* bias_u, const uint16_t* bias_v, void* output,
+                               int32_t rows, int32_t padded_rows, int32_t valid_rows, int32_t attention_left,
+                               int32_t attention_right, int32_t value_stride, const uint8_t* packed_key, const float* key_scales,
+                               const uint8_t* packed_position, const float* position_scales, void* stream) {
+    if (padded_rows <= 0 || padded_rows % 16 || padded_rows > (1 << 21) || rows <= 0 || rows > padded_rows || valid_rows <= 0 ||
+        valid_rows > padded_rows || value_stride < padded_rows || value_stride % 16) {
+        set_error("invalid attention shape rows=%d padded_rows=%d valid_rows=%d value_stride=%d", rows, padded_rows, valid_rows,
+                  value_stride);
+        return PK_E_SHAPE;
+    }
+    if (attention_left != 128 || attention_right != 128) {
+        set_error("the long-form attention kernels are built for a 128/128 window, got %d/%d", attention_left, attention_right);
+        return PK_E_SHAPE;
+    }
+    if (!need(query, "query") || !need(key, "key") || !need(value_fp8, "value_fp8") || !need(position, "position") ||
+        !need(bias_u, "bias_u") || !need(bias_v, "bias_v") || !need(output, "output"))
+        return PK_E_ARG;
+    if (packed && (!need(packed_key, "packed_key") || !need(key_scales, "key_scales") || !need(packed_position, "packed_position") ||
+                   !need(position_scales, "position_scales")))
+        return PK_E_ARG;
+    if (misaligned(query, 16) || misaligned(key, 16) || misaligned(position, 16) || misaligned(bias_u, 16) ||
+        misaligned(bias_v, 16) || misaligned(value_fp8, 16) || misaligned(output, 16) || misaligned(packed_key, 8) ||
+        misaligned(packed_position, 16) || misaligned(key_scales, 4) || misaligned(position_scales, 4)) {
+        set_error("attention operands must be 16-byte aligned (packed keys 8-byte, scales 4-byte)");
+        return PK_E_ALIGN;
+    }
+    launch_local_attention(packed, query, key, value_fp8, position, bias_u, bias_v, output, rows, padded_rows, valid_rows,
+                           attention_left, attention_right, value_stride, packed_key, key_scales, packed_position, position_scales,
+                           STREAM);
+    return check_launch(packed ? "local_relpos_attention_packed" : "local_relpos_attention_tc_scores");
+}
+
+int32_t pk_local_relpos_attention_tc_scores(const uint16_t* query, const uint16_t* key, const uint16_t* value, const uint8_t* value_fp8,
+                                            const uint16_t* position, const uint16_t* bias_u, const uint16_t* bias_v,
+                                            uint16_t* output, int32_t rows, int32_t padded_rows, int32_t valid_rows,
+                                            int32_t attention_left, int32_t attention_right, int32_t value_stride, void* stream) {
+    (void)value;
+    return local_attention(false, query, key, value_fp8, position, bias_u, bias_v, output, rows, padded_rows, valid_rows,
+                           attention_left, attention_right, value_stride, nullptr, nullptr, nullptr, nullptr, stream);
+}
+
+int32_t pk_local_relpos_attention_packed(const uint16_t* query, const uint16_t* key, const uint16_t* value, const uint8_t* value_fp8,
+                                         const uint16_t* position, const uint16_t* bias_u, const uint16_t* bias_v, uint8_t* output,
+                                         int32_t rows, int32_t padded_rows, int32_t valid_rows, int32_t attention_left,
+                                         int32_t attention_right, int32_t value_stride, const uint8_t* packed_key,
+                                         const float* key_scales, const uint8_t* packed_position, const float* position_scales,
+                                         void* stream) {
+    (void)value;
+    return local_attention(true, query, key, value_fp8, position, bias_u, bias_v, output, rows, padded_rows, valid_rows,
+                           attention_left, attention_right, value_stride, packed_key, key_scales, packed_position,
+                           position_scales, stream);
+}
+
 }  // extern "C"

@@ -34,6 +34,14 @@ int launch_tdt_decode(const uint16_t* enc, int frames, int enc_stride, const uin
                       int hidden, int token_outputs, int durations, int max_symbols, int32_t* tokens, int capacity, int32_t* result,
                       uint32_t* workspace, hipStream_t s);
 
+int launch_pack_vectors(bool int4, const uint16_t* in, uint8_t* out, float* scales, int vectors, hipStream_t s);
+int launch_quantize_value_int4(const uint16_t* vt, uint8_t* out, int rows, float inverse_scale, bool edge_only, int valid_rows,
+                               hipStream_t s);
+int launch_local_attention(bool packed, const uint16_t* query, const uint16_t* key, const uint8_t* value_fp8,
+                           const uint16_t* position, const uint16_t* bias_u, const uint16_t* bias_v, void* output, int rows,
+                           int padded_rows, int valid_rows, int left, int right, int value_stride, const uint8_t* packed_key,
+                           const float* key_scales, const uint8_t* packed_position, const float* position_scales, hipStream_t s);
+
 void set_error(const char* fmt, ...);
 int cu_count();
 int launch_sparse24_contract(const uint8_t* data, const uint8_t* meta, const uint8_t* w, const float* w_scales, float in_scale,

@@ -94,6 +94,12 @@ SIGNATURES = {
     "pk_tdt_decode_workspace_bytes": (I, [I]),
     "pk_tdt_decode": (I, [P, I, I, P, P, P, P, P, P, P, P, P, P, P, P, I, P, P, I, I, I, I, P, I, P, P,
                           ctypes.c_uint64, P]),
+    "pk_pack_score_vectors": (I, [P, P, P, I, P]),
+    "pk_pack_key_int4": (I, [P, P, P, I, P]),
+    "pk_quantize_value_int4": (I, [P, P, I, F, P]),
+    "pk_quantize_value_int4_register": (I, [P, P, I, F, I, P]),
+    "pk_local_relpos_attention_tc_scores": (I, [P, P, P, P, P, P, P, P, I, I, I, I, I, I, P]),
+    "pk_local_relpos_attention_packed": (I, [P, P, P, P, P, P, P, P, I, I, I, I, I, I, P, P, P, P, P]),
 }
 
 
@@ -259,3 +265,29 @@ class Artifact:
         status = fn(self.handle, index, fmt, host_staging.ctypes.data, host_staging.nbytes,
                     _ptr(device_fp16), _ptr(packed), _ptr(scales), _ptr(zeros), _stream(stream))
         self._check("pk_artifact_derive_linear", status)
+
+
+# ---- long-form local attention (encoder.rs:1839-1968 launch_attention_arena) ----
+
+ATTENTION_LEFT = ATTENTION_RIGHT = 128
+POSITION_ROWS_PADDED = 272
+
+
+def launch_attention_arena(query, key, value_fp8, position, bias_u, bias_v, output, rows, padded_rows,
+                           valid_rows, value_stride, packed=None, stream=None):
+    """Mirror of encoder.rs:1839-1968.  With `packed` (padded_rows >= 1040 in
+    the reference) it is a dict of caller-owned buffers {key: u8 [padded_rows
+    * 512], key_scales: f32 [padded_rows * 8], position: u8 [8 * 272 * 128],
+    position_scales: f32 [8 * 272]} that receives the INT4 keys and INT8
+    position vectors before pk_local_relpos_attention_packed runs (output e4m3
+    bytes); without it pk_local_relpos_attention_tc_scores runs (output fp16)."""
+    if packed is not None:
+        call("pk_pack_key_int4", key, packed["key"], packed["key_scales"], padded_rows * 8, stream=stream)
+        call("pk_pack_score_vectors", position, packed["position"], packed["position_scales"], 8 * POSITION_ROWS_PADDED,
+             stream=stream)
+        call("pk_local_relpos_attention_packed", query, key, None, value_fp8, position, bias_u, bias_v, output, rows,
+             padded_rows, valid_rows, ATTENTION_LEFT, ATTENTION_RIGHT, value_stride, packed["key"],
+             packed["key_scales"], packed["position"], packed["position_scales"], stream=stream)
+    else:
+        call("pk_local_relpos_attention_tc_scores", query, key, None, value_fp8, position, bias_u, bias_v, output,
+             rows, padded_rows, valid_rows, ATTENTION_LEFT, ATTENTION_RIGHT, value_stride, stream=stream)

@@ -13,6 +13,7 @@
  */
 #include "pk_oracle.h"
 
+#include <float.h>
 #include <math.h>
 #include <stdlib.h>
 #include <string.h>
@@ -1108,4 +1109,374 @@ int orc_tdt_decode(const uint16_t* enc, int frames, int enc_stride, const uint16
     free(pred);
     free(scores);
     return count;
+}
+
+/* ======================================================================== */
+/* Local relative-position attention and its packers                        */
+/* (encoder.cu:1476-2097, launch_attention_arena encoder.rs:1839-1968).      */
+/* Model constants: width 1024, 8 heads of 128, position rows padded to 272 */
+/* (encoder.cu:12-17), window 128 left / 128 right (encoder.rs:24-26).       */
+/* ======================================================================== */
+
+#define ORC_MODEL 1024
+#define ORC_HEAD 128
+#define ORC_HEADS 8
+#define ORC_MAXATT 257
+#define ORC_POSROWS 272
+#define ORC_FP8ROWS 288
+
+/* bf16 round to nearest even of a finite float (__float2bfloat16_rn). */
+static float round_bf16(float v) {
+    uint32_t b;
+    memcpy(&b, &v, 4);
+    b = (b + 0x7fffu + ((b >> 16) & 1u)) & 0xffff0000u;
+    float r;
+    memcpy(&r, &b, 4);
+    return r;
+}
+
+/* Storage byte of dimension d in an INT8 score vector: the byte written by
+ * pk_sm89_pack_score_vectors (encoder.cu:2054-2074), lane = d / 4 stores its
+ * four bytes at (lane/8)*32 + (lane%4)*8 + (lane&4). */
+int orc_score_vector_byte(int d) {
+    const int lane = d / 4;
+    return (lane / 8) * 32 + (lane % 4) * 8 + (lane & 4) + d % 4;
+}
+
+/* Storage nibble of dimension d in an INT4 key vector: lane = d / 4 stores a
+ * u16 of four nibbles at byte (lane/16)*32 + ((lane/2)%4)*8 + ((lane/2)&4) +
+ * (lane&1)*2 (pk_sm89_pack_key_int4, encoder.cu:2076-2097). */
+int orc_key_int4_nibble(int d) {
+    const int lane = d / 4;
+    const int byte = (lane / 16) * 32 + ((lane / 2) % 4) * 8 + ((lane / 2) & 4) + (lane & 1) * 2;
+    return 2 * byte + d % 4;
+}
+
+/* encoder.cu:2054-2074: per 128-value vector, scale = max|v|/127 (1 if the
+ * vector is zero), byte = (uint8)rn(v/scale), stored in the MMA byte order. */
+void orc_pack_score_vectors(const uint16_t* in, int vectors, uint8_t* out, float* scales) {
+    for (int vec = 0; vec < vectors; ++vec) {
+        const uint16_t* x = in + (size_t)vec * 128;
+        float m = 0.0f;
+        for (int d = 0; d < 128; ++d) m = fmaxf(m, fabsf(orc_f16_to_f32(x[d])));
+        const float scale = m > 0.0f ? m / 127.0f : 1.0f;
+        scales[vec] = scale;
+        for (int d = 0; d < 128; ++d)
+            out[(size_t)vec * 128 + orc_score_vector_byte(d)] = (uint8_t)(int)rintf(orc_f16_to_f32(x[d]) / scale);
+    }
+}
+
+/* encoder.cu:2076-2097: per vector, scale = max|v|/7, nibble = rn(v/scale)&15,
+ * 64 bytes per vector in the MMA nibble order. */
+void orc_pack_key_int4(const uint16_t* in, int vectors, uint8_t* out, float* scales) {
+    for (int vec = 0; vec < vectors; ++vec) {
+        const uint16_t* x = in + (size_t)vec * 128;
+        uint8_t* o = out + (size_t)vec * 64;
+        float m = 0.0f;
+        for (int d = 0; d < 128; ++d) m = fmaxf(m, fabsf(orc_f16_to_f32(x[d])));
+        const float scale = m > 0.0f ? m / 7.0f : 1.0f;
+        scales[vec] = scale;
+        memset(o, 0, 64);
+        for (int d = 0; d < 128; ++d) {
+            const int q = (int)rintf(orc_f16_to_f32(x[d]) / scale) & 15;
+            const int s = orc_key_int4_nibble(d);
+            o[s / 2] |= (uint8_t)(q << (4 * (s & 1)));
+        }
+    }
+}
+
+/* encoder.cu:561-634 pk_sm89_quantize_value_int4{,_register}.  Input V is
+ * feature-major [1024 x rows] fp16.  Output: FP8 V (e4m3(v*inverse_scale))
+ * [1024 x rows], then S4 V (clamp(rn(v/s_f), -7, 7), two keys per byte, even
+ * key in the low nibble), then 1024 float scales s_f = max|V_f|/7 (1 when
+ * zero).  With edge_only the FP8 copy is written only for row pairs with
+ * row < 272 or row + 1 >= valid_rows - 272 (the register variant). */
+void orc_quantize_value_int4(const uint16_t* vt, int rows, float inverse_scale, int edge_only, int valid_rows,
+                             uint8_t* out) {
+    const size_t elements = (size_t)rows * ORC_MODEL;
+    float* scales = (float*)(out + elements + elements / 2);
+    for (int f = 0; f < ORC_MODEL; ++f) {
+        const uint16_t* x = vt + (size_t)f * rows;
+        float m = 0.0f;
+        for (int r = 0; r < rows; ++r) m = fmaxf(m, fabsf(orc_f16_to_f32(x[r])));
+        const float scale = m > 0.0f ? m / 7.0f : 1.0f;
+        scales[f] = scale;
+        for (int r = 0; r + 1 < rows; r += 2) {
+            const float a = orc_f16_to_f32(x[r]), b = orc_f16_to_f32(x[r + 1]);
+            if (!edge_only || r < 272 || r + 1 >= valid_rows - 272) {
+                out[(size_t)f * rows + r] = orc_f32_to_e4m3(a * inverse_scale);
+                out[(size_t)f * rows + r + 1] = orc_f32_to_e4m3(b * inverse_scale);
+            }
+            int qa = (int)rintf(a / scale), qb = (int)rintf(b / scale);
+            qa = qa < -7 ? -7 : (qa > 7 ? 7 : qa);
+            qb = qb < -7 ? -7 : (qb > 7 ? 7 : qb);
+            out[elements + ((size_t)f * rows + r) / 2] = (uint8_t)((qa & 15) | ((qb & 15) << 4));
+        }
+    }
+}
+
+static int sext4(int v) { return (v & 8) ? (v & 15) - 16 : (v & 15); }
+
+/* Output store of the attention kernels (encoder.cu:1463-1474): the context is
+ * rounded to fp16; the packed form stores e4m3(fp16 * 28). */
+static void store_context(int packed, void* output, size_t index, float value) {
+    const uint16_t h = orc_f32_to_f16(value);
+    if (packed)
+        ((uint8_t*)output)[index] = orc_f32_to_e4m3(orc_f16_to_f32(h) * 28.0f);
+    else
+        ((uint16_t*)output)[index] = h;
+}
+
+/* The per-query FP32 path every boundary tile takes (encoder.cu:1548-1684).
+ * Reduction orders follow the 32-lane warp: lane pairs of 16 accumulate a
+ * score over dimensions 2*l + 32*quarter with interleaved content/position
+ * FMAs, then a shuffle-down tree over 16 lanes; denominators sum slots
+ * l, l+32, ... per lane, then a shuffle-down tree over 32 lanes. */
+static void attention_scalar_row(int packed, const uint16_t* query, const uint16_t* key, const uint8_t* value_fp8,
+                                 const uint16_t* position, const uint16_t* bias_u, const uint16_t* bias_v, void* output,
+                                 int head, int qr, int rows, int padded_rows, int valid_rows, int left, int right,
+                                 int value_stride, float* scores) {
+    if (qr >= rows || qr >= valid_rows) {
+        if (qr < padded_rows)
+            for (int d = 0; d < ORC_HEAD; ++d) store_context(packed, output, (size_t)qr * ORC_MODEL + head * ORC_HEAD + d, 0.0f);
+        return;
+    }
+    const int first = qr - left > 0 ? qr - left : 0;
+    const int last = qr + right < valid_rows - 1 ? qr + right : valid_rows - 1;
+    const int count = last - first + 1;
+    const size_t qh = (size_t)qr * ORC_MODEL + head * ORC_HEAD;
+    float su[ORC_HEAD], sv[ORC_HEAD];
+    for (int d = 0; d < ORC_HEAD; ++d) {
+        const float q = orc_f16_to_f32(query[qh + d]);
+        su[d] = q + orc_f16_to_f32(bias_u[head * ORC_HEAD + d]);
+        sv[d] = q + orc_f16_to_f32(bias_v[head * ORC_HEAD + d]);
+    }
+    for (int slot = 0; slot < count; ++slot) {
+        const int key_row = first + slot;
+        const int prow = left - qr + key_row;
+        const uint16_t* k = key + (size_t)key_row * ORC_MODEL + head * ORC_HEAD;
+        const uint16_t* p = position + ((size_t)head * ORC_POSROWS + prow) * ORC_HEAD;
+        float part[16];
+        for (int l = 0; l < 16; ++l) {
+            float s = 0.0f;
+            for (int quarter = 0; quarter < 4; ++quarter) {
+                const int d = 2 * l + 32 * quarter;
+                s = fmaf(su[d], orc_f16_to_f32(k[d]), s);
+                s = fmaf(sv[d], orc_f16_to_f32(p[d]), s);
+                s = fmaf(su[d + 1], orc_f16_to_f32(k[d + 1]), s);
+                s = fmaf(sv[d + 1], orc_f16_to_f32(p[d + 1]), s);
+            }
+            part[l] = s;
+        }
+        for (int off = 8; off > 0; off /= 2)
+            for (int l = 0; l < off; ++l) part[l] = part[l] + part[l + off];
+        scores[slot] = part[0] * 0.08838834764831845f;
+    }
+    float maximum = -FLT_MAX;
+    for (int slot = 0; slot < count; ++slot) maximum = fmaxf(maximum, scores[slot]);
+    float lane_sum[32];
+    for (int l = 0; l < 32; ++l) lane_sum[l] = 0.0f;
+    for (int slot = 0; slot < count; ++slot) {
+        scores[slot] = expf(scores[slot] - maximum);
+        lane_sum[slot % 32] += scores[slot];
+    }
+    for (int off = 16; off > 0; off /= 2)
+        for (int l = 0; l < off; ++l) lane_sum[l] = lane_sum[l] + lane_sum[l + off];
+    const float denominator = lane_sum[0];
+    const float value_scale = 8.0f / 448.0f;
+    for (int d = 0; d < ORC_HEAD; ++d) {
+        const int feature = head * ORC_HEAD + d;
+        float context = 0.0f;
+        for (int key_row = first; key_row <= last; ++key_row) {
+            const float weight = scores[key_row - first] / denominator;
+            const float value = orc_e4m3_to_f32(value_fp8[(size_t)feature * value_stride + key_row]) * value_scale;
+            context = fmaf(weight, value, context);
+        }
+        store_context(packed, output, qh + d, context);
+    }
+}
+
+/* Interior tile of pk_sm89_local_relpos_attention_packed (encoder.cu:1687-1966):
+ * 16 queries qb..qb+15 share keys qb-128 .. qb+143.  q+u is quantized per
+ * query to INT4 (max/7) against the INT4 keys, q+v to INT8 (max/127) against
+ * the INT8 position vectors; each integer score is scaled by both scales and
+ * rounded to bf16; softmax in FP32; probabilities quantized to U4 (rn(e*15),
+ * scale 1/(15*denominator)); context = sum U4 * S4(V) times the probability
+ * and per-feature value scales, rounded to fp16 and stored as e4m3(x*28). */
+static void attention_packed_tile(const uint16_t* query, const uint8_t* value_fp8, const uint16_t* bias_u,
+                                  const uint16_t* bias_v, uint8_t* output, int head, int qb, int value_stride,
+                                  const uint8_t* packed_key, const float* key_scales, const uint8_t* packed_position,
+                                  const float* position_scales) {
+    const int first_key = qb - 128;
+    int qu[16][ORC_HEAD], qv[16][ORC_HEAD];
+    float su[16], sv[16];
+    for (int r = 0; r < 16; ++r) {
+        float vals[2][ORC_HEAD], mx[2] = {0.0f, 0.0f};
+        for (int d = 0; d < ORC_HEAD; ++d) {
+            const float q = orc_f16_to_f32(query[(size_t)(qb + r) * ORC_MODEL + head * ORC_HEAD + d]);
+            vals[0][d] = round_f16(q + orc_f16_to_f32(bias_u[head * ORC_HEAD + d]));
+            vals[1][d] = round_f16(q + orc_f16_to_f32(bias_v[head * ORC_HEAD + d]));
+            mx[0] = fmaxf(mx[0], fabsf(vals[0][d]));
+            mx[1] = fmaxf(mx[1], fabsf(vals[1][d]));
+        }
+        su[r] = mx[0] > 0.0f ? mx[0] / 7.0f : 1.0f;
+        sv[r] = mx[1] > 0.0f ? mx[1] / 127.0f : 1.0f;
+        for (int d = 0; d < ORC_HEAD; ++d) {
+            qu[r][d] = sext4((int)rintf(vals[0][d] / su[r]));
+            qv[r][d] = (int8_t)(uint8_t)(int)rintf(vals[1][d] / sv[r]);
+        }
+    }
+    static float content[16][ORC_POSROWS], pos[16][ORC_POSROWS];
+#pragma omp threadprivate(content, pos)
+    for (int col = 0; col < ORC_POSROWS; ++col) {
+        const int kvec = (first_key + col) * ORC_HEADS + head;
+        const int pvec = head * ORC_POSROWS + col;
+        int kd[ORC_HEAD], pd[ORC_HEAD];
+        for (int d = 0; d < ORC_HEAD; ++d) {
+            const int s = orc_key_int4_nibble(d);
+            kd[d] = sext4(packed_key[(size_t)kvec * 64 + s / 2] >> (4 * (s & 1)));
+            pd[d] = (int8_t)packed_position[(size_t)pvec * 128 + orc_score_vector_byte(d)];
+        }
+        for (int r = 0; r < 16; ++r) {
+            int32_t a = 0, b = 0;
+            for (int d = 0; d < ORC_HEAD; ++d) {
+                a += qu[r][d] * kd[d];
+                b += qv[r][d] * pd[d];
+            }
+            content[r][col] = round_bf16((float)a * (su[r] * key_scales[kvec]));
+            pos[r][col] = round_bf16((float)b * (sv[r] * position_scales[pvec]));
+        }
+    }
+    int prob[16][ORC_POSROWS];
+    float prob_scale[16];
+    for (int r = 0; r < 16; ++r) {
+        float e[ORC_MAXATT], maximum = -FLT_MAX;
+        for (int slot = 0; slot < ORC_MAXATT; ++slot) {
+            e[slot] = (content[r][r + slot] + pos[r][slot]) * 0.08838834764831845f;
+            maximum = fmaxf(maximum, e[slot]);
+        }
+        float lane_sum[32];
+        for (int l = 0; l < 32; ++l) lane_sum[l] = 0.0f;
+        for (int slot = 0; slot < ORC_MAXATT; ++slot) {
+            e[slot] = expf(e[slot] - maximum);
+            lane_sum[slot % 32] += e[slot];
+        }
+        for (int off = 16; off > 0; off /= 2)
+            for (int l = 0; l < off; ++l) lane_sum[l] = lane_sum[l] + lane_sum[l + off];
+        prob_scale[r] = 1.0f / (15.0f * lane_sum[0]);
+        for (int k = 0; k < ORC_POSROWS; ++k) prob[r][k] = 0;
+        for (int slot = 0; slot < ORC_MAXATT; ++slot) prob[r][r + slot] = (int)rintf(e[slot] * 15.0f);
+    }
+    const uint8_t* s4 = value_fp8 + (size_t)ORC_MODEL * value_stride;
+    const float* vscales = (const float*)(value_fp8 + (size_t)ORC_MODEL * value_stride * 3 / 2);
+    for (int d = 0; d < ORC_HEAD; ++d) {
+        const int feature = head * ORC_HEAD + d;
+        int v[ORC_POSROWS];
+        for (int k = 0; k < ORC_POSROWS; ++k) {
+            const size_t nib = (size_t)feature * value_stride + first_key + k;
+            v[k] = sext4(s4[nib / 2] >> (4 * (nib & 1)));
+        }
+        for (int r = 0; r < 16; ++r) {
+            int32_t acc = 0;
+            for (int k = 0; k < ORC_POSROWS; ++k) acc += prob[r][k] * v[k];
+            const float out = (float)acc * (prob_scale[r] * vscales[feature]);
+            store_context(1, output, (size_t)(qb + r) * ORC_MODEL + feature, out);
+        }
+    }
+}
+
+/* Interior tile of pk_sm89_local_relpos_attention_tc_scores (encoder.cu:
+ * 1768-2018): q+u and q+v rounded to fp16; FP32 dot products with fp16 K and
+ * position rows; softmax; probabilities e4m3(p*448); context = sum e4m3(p) *
+ * e4m3(V) over keys qb-128 .. qb+143, times (1/448)*(8/448), stored as fp16.
+ * The tensor-core accumulation order is unspecified; this sums in k order. */
+static void attention_tc_tile(const uint16_t* query, const uint16_t* key, const uint8_t* value_fp8,
+                              const uint16_t* position, const uint16_t* bias_u, const uint16_t* bias_v, uint16_t* output,
+                              int head, int qb, int value_stride) {
+    const int first_key = qb - 128;
+    static float qu[16][ORC_HEAD], qv[16][ORC_HEAD], content[16][ORC_POSROWS], pos[16][ORC_POSROWS];
+#pragma omp threadprivate(qu, qv, content, pos)
+    for (int r = 0; r < 16; ++r)
+        for (int d = 0; d < ORC_HEAD; ++d) {
+            const float q = orc_f16_to_f32(query[(size_t)(qb + r) * ORC_MODEL + head * ORC_HEAD + d]);
+            qu[r][d] = round_f16(q + orc_f16_to_f32(bias_u[head * ORC_HEAD + d]));
+            qv[r][d] = round_f16(q + orc_f16_to_f32(bias_v[head * ORC_HEAD + d]));
+        }
+    for (int col = 0; col < ORC_POSROWS; ++col) {
+        const uint16_t* k = key + (size_t)(first_key + col) * ORC_MODEL + head * ORC_HEAD;
+        const uint16_t* p = position + ((size_t)head * ORC_POSROWS + col) * ORC_HEAD;
+        for (int r = 0; r < 16; ++r) {
+            float a = 0.0f, b = 0.0f;
+            for (int d = 0; d < ORC_HEAD; ++d) {
+                a += qu[r][d] * orc_f16_to_f32(k[d]);
+                b += qv[r][d] * orc_f16_to_f32(p[d]);
+            }
+            content[r][col] = a;
+            pos[r][col] = b;
+        }
+    }
+    uint8_t prob[16][ORC_FP8ROWS];
+    for (int r = 0; r < 16; ++r) {
+        float e[ORC_MAXATT], maximum = -FLT_MAX;
+        for (int slot = 0; slot < ORC_MAXATT; ++slot) {
+            e[slot] = (content[r][r + slot] + pos[r][slot]) * 0.08838834764831845f;
+            maximum = fmaxf(maximum, e[slot]);
+        }
+        float lane_sum[32];
+        for (int l = 0; l < 32; ++l) lane_sum[l] = 0.0f;
+        for (int slot = 0; slot < ORC_MAXATT; ++slot) {
+            e[slot] = expf(e[slot] - maximum);
+            lane_sum[slot % 32] += e[slot];
+        }
+        for (int off = 16; off > 0; off /= 2)
+            for (int l = 0; l < off; ++l) lane_sum[l] = lane_sum[l] + lane_sum[l + off];
+        const float denominator = lane_sum[0];
+        for (int u = 0; u < ORC_FP8ROWS; ++u) {
+            const int in_window = u >= r && u < r + ORC_MAXATT;
+            prob[r][u] = orc_f32_to_e4m3((in_window ? e[u - r] / denominator : 0.0f) * 448.0f);
+        }
+    }
+    const float context_scale = (1.0f / 448.0f) * (8.0f / 448.0f);
+    for (int d = 0; d < ORC_HEAD; ++d) {
+        const int feature = head * ORC_HEAD + d;
+        float v[ORC_POSROWS];
+        for (int k = 0; k < ORC_POSROWS; ++k)
+            v[k] = orc_e4m3_to_f32(value_fp8[(size_t)feature * value_stride + first_key + k]);
+        for (int r = 0; r < 16; ++r) {
+            float acc = 0.0f;
+            for (int k = 0; k < ORC_POSROWS; ++k) acc += orc_e4m3_to_f32(prob[r][k]) * v[k];
+            output[(size_t)(qb + r) * ORC_MODEL + feature] = orc_f32_to_f16(acc * context_scale);
+        }
+    }
+}
+
+/* Both long-form attention kernels over query tiles [tile_begin, tile_end) of
+ * 16 rows and all 8 heads.  packed != 0: pk_sm89_local_relpos_attention_packed
+ * (output e4m3 bytes); packed == 0: pk_sm89_local_relpos_attention_tc_scores
+ * (output fp16).  Tiles with qb >= left, qb + 15 + right < valid_rows and
+ * qb + 16 <= rows take the tile path; all others the per-query path. */
+void orc_local_attention(int packed, const uint16_t* query, const uint16_t* key, const uint8_t* value_fp8,
+                         const uint16_t* position, const uint16_t* bias_u, const uint16_t* bias_v, void* output, int rows,
+                         int padded_rows, int valid_rows, int left, int right, int value_stride,
+                         const uint8_t* packed_key, const float* key_scales, const uint8_t* packed_position,
+                         const float* position_scales, int tile_begin, int tile_end) {
+#pragma omp parallel for collapse(2) schedule(dynamic)
+    for (int tile = tile_begin; tile < tile_end; ++tile)
+        for (int head = 0; head < ORC_HEADS; ++head) {
+            const int qb = 16 * tile;
+            if (qb >= padded_rows) continue;
+            const int interior = qb >= left && qb + 15 + right < valid_rows && qb + 16 <= rows;
+            if (!interior) {
+                float scores[1024];
+                for (int r = 0; r < 16; ++r)
+                    attention_scalar_row(packed, query, key, value_fp8, position, bias_u, bias_v, output, head, qb + r,
+                                         rows, padded_rows, valid_rows, left, right, value_stride, scores);
+            } else if (packed) {
+                attention_packed_tile(query, value_fp8, bias_u, bias_v, (uint8_t*)output, head, qb, value_stride,
+                                      packed_key, key_scales, packed_position, position_scales);
+            } else {
+                attention_tc_tile(query, key, value_fp8, position, bias_u, bias_v, (uint16_t*)output, head, qb,
+                                  value_stride);
+            }
+        }
 }

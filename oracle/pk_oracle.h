@@ -108,6 +108,19 @@ int orc_tdt_decode(const uint16_t* enc, int frames, int enc_stride, const uint16
                    const float* b_joint, int hidden, int token_outputs, int durations, int max_symbols,
                    int32_t* tokens, int capacity, float* pred_out, int* frame_out);
 
+/* ---- local relative-position attention (encoder.cu:1476-2097) ----------- */
+int orc_score_vector_byte(int d);
+int orc_key_int4_nibble(int d);
+void orc_pack_score_vectors(const uint16_t* in, int vectors, uint8_t* out, float* scales);
+void orc_pack_key_int4(const uint16_t* in, int vectors, uint8_t* out, float* scales);
+void orc_quantize_value_int4(const uint16_t* vt, int rows, float inverse_scale, int edge_only, int valid_rows,
+                             uint8_t* out);
+void orc_local_attention(int packed, const uint16_t* query, const uint16_t* key, const uint8_t* value_fp8,
+                         const uint16_t* position, const uint16_t* bias_u, const uint16_t* bias_v, void* output, int rows,
+                         int padded_rows, int valid_rows, int left, int right, int value_stride,
+                         const uint8_t* packed_key, const float* key_scales, const uint8_t* packed_position,
+                         const float* position_scales, int tile_begin, int tile_end);
+
 #ifdef __cplusplus
 }
 #endif

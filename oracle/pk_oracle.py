@@ -83,6 +83,12 @@ def _declare(l):
         "orc_joint_decide": (None, [P, I, I, P, P]),
         "orc_lstm_step": (None, [P, P, P, P, P, P, P, I, P, P]),
         "orc_tdt_decode": (I, [P, I, I, P, P, P, P, P, P, P, P, P, P, P, P, I, P, P, I, I, I, I, P, I, P, P]),
+        "orc_score_vector_byte": (I, [I]),
+        "orc_key_int4_nibble": (I, [I]),
+        "orc_pack_score_vectors": (None, [P, I, P, P]),
+        "orc_pack_key_int4": (None, [P, I, P, P]),
+        "orc_quantize_value_int4": (None, [P, I, F, I, I, P]),
+        "orc_local_attention": (None, [I, P, P, P, P, P, P, P, I, I, I, I, I, I, P, P, P, P, I, I]),
         "orc_threads": (I, []),
         "orc_set_threads": (None, [I]),
     }
@@ -534,3 +540,62 @@ def tdt_decode(enc, emb, lstm, proj, joint, token_outputs=1025, durations=5, max
                              _p(keep[5]), hidden, token_outputs, durations, max_symbols, _p(toks), capacity,
                              _p(pred), ctypes.byref(frame))
     return toks[:min(n, capacity)].copy(), frame.value, pred
+
+
+# ---- local relative-position attention (encoder.cu:1476-2097) -----------------
+
+MODEL_WIDTH, HEAD_WIDTH, HEADS, POSITION_ROWS = 1024, 128, 8, 272
+
+
+def pack_score_vectors(x16: np.ndarray):
+    """encoder.cu:2054-2074: INT8 per-128-vector packing in MMA byte order."""
+    x16 = _h(x16)
+    vectors = x16.size // 128
+    out = np.empty(vectors * 128, np.uint8)
+    sc = np.empty(vectors, np.float32)
+    lib().orc_pack_score_vectors(_p(x16), vectors, _p(out), _p(sc))
+    return out, sc
+
+
+def pack_key_int4(x16: np.ndarray):
+    """encoder.cu:2076-2097: INT4 per-128-vector packing, 64 bytes per vector."""
+    x16 = _h(x16)
+    vectors = x16.size // 128
+    out = np.empty(vectors * 64, np.uint8)
+    sc = np.empty(vectors, np.float32)
+    lib().orc_pack_key_int4(_p(x16), vectors, _p(out), _p(sc))
+    return out, sc
+
+
+def quantize_value_int4(vt16: np.ndarray, inverse_scale: float = 56.0, edge_only: bool = False,
+                        valid_rows: int | None = None, fill: int = 0) -> np.ndarray:
+    """encoder.cu:561-634: feature-major V [1024 x rows] -> FP8 V, S4 V, scales.
+    Bytes the edge-only form does not write keep the value `fill`."""
+    vt16 = _h(vt16)
+    rows = vt16.shape[1]
+    elements = rows * MODEL_WIDTH
+    out = np.full(elements + elements // 2 + 4 * MODEL_WIDTH, fill, np.uint8)
+    lib().orc_quantize_value_int4(_p(vt16), rows, inverse_scale, int(edge_only),
+                                  rows if valid_rows is None else valid_rows, _p(out))
+    return out
+
+
+def local_attention(packed, query, key, value_fp8, position, bias_u, bias_v, rows, valid_rows=None,
+                    value_stride=None, packed_key=None, key_scales=None, packed_position=None,
+                    position_scales=None, tiles=None, left=128, right=128, out=None):
+    """encoder.cu:1476-2052 long-form local attention over query tiles `tiles`
+    (range of 16-row tiles; default all).  Returns the output [padded_rows x
+    1024]: e4m3 bytes when packed, fp16 bits otherwise."""
+    query, key, position = _h(query), _h(key), _h(position)
+    padded_rows = query.shape[0]
+    valid_rows = rows if valid_rows is None else valid_rows
+    value_stride = padded_rows if value_stride is None else value_stride
+    if out is None:
+        out = np.zeros((padded_rows, MODEL_WIDTH), np.uint8 if packed else np.uint16)
+    t0, t1 = (0, (padded_rows + 15) // 16) if tiles is None else tiles
+    f32 = lambda a: None if a is None else np.ascontiguousarray(a, np.float32)
+    ks, ps = f32(key_scales), f32(position_scales)
+    lib().orc_local_attention(int(bool(packed)), _p(query), _p(key), _p(np.ascontiguousarray(value_fp8)),
+                              _p(position), _p(_h(bias_u)), _p(_h(bias_v)), _p(out), rows, padded_rows, valid_rows,
+                              left, right, value_stride, _p(packed_key), _p(ks), _p(packed_position), _p(ps), t0, t1)
+    return out
