@@ -295,6 +295,69 @@ def joint_streaming(pk, torch, stream, copies=512, reps=5):
             "pct_hbm": round(100.0 * gbs / 8000.0, 2)}
 
 
+def attention_bench(pk, torch, stream, frames=45000, reps=20):
+    """Long-form local attention of one encoder layer at T frames (encoder.rs
+    :1839-1968): the INT4 key and INT8 position packers, the feature-major
+    value quantizer (register variant) and both attention kernels, each timed
+    over `reps` launches with HIP events on the launch stream.  Algorithmic
+    bytes per packed launch: q fp16 (2048 B/row), INT4 keys + scales (544
+    B/row), S4 V (512 B/row), e4m3 output (1024 B/row), plus the 8 x 272 packed
+    position vectors and the 4 KB of value scales once; per tc launch: q and
+    k fp16, FP8 V, fp16 output (7168 B/row) plus the fp16 position table.
+    Integer ops of the packed tile path: per 16-query tile and head, 2 x 16 x
+    272 x 128 score MACs and 16 x 320 x 128 context MACs (boundary tiles run
+    the per-query FP32 path and are not counted)."""
+    padded = (frames + 15) // 16 * 16
+    g = torch.Generator(device="cuda")
+    g.manual_seed(77)
+    q = torch.randn((padded, 1024), generator=g, device="cuda").half()
+    k = torch.randn((padded, 1024), generator=g, device="cuda").half()
+    vt = torch.randn((1024, padded), generator=g, device="cuda").half()
+    pos = torch.randn((8 * 272, 128), generator=g, device="cuda").half()
+    bu = (0.1 * torch.randn(1024, generator=g, device="cuda")).half()
+    bv = (0.1 * torch.randn(1024, generator=g, device="cuda")).half()
+    el = padded * 1024
+    vf = torch.empty(el + el // 2 + 4096, dtype=torch.uint8, device="cuda")
+    pk_key = torch.empty(padded * 512, dtype=torch.uint8, device="cuda")
+    k_sc = torch.empty(padded * 8, dtype=torch.float32, device="cuda")
+    pk_pos = torch.empty(8 * 272 * 128, dtype=torch.uint8, device="cuda")
+    p_sc = torch.empty(8 * 272, dtype=torch.float32, device="cuda")
+    out8 = torch.empty((padded, 1024), dtype=torch.uint8, device="cuda")
+    out16 = torch.empty((padded, 1024), dtype=torch.float16, device="cuda")
+    runs = {
+        "pack_key_int4": lambda: pk.call("pk_pack_key_int4", k, pk_key, k_sc, padded * 8, stream=stream),
+        "pack_score_vectors": lambda: pk.call("pk_pack_score_vectors", pos, pk_pos, p_sc, 8 * 272, stream=stream),
+        "quantize_value_int4": lambda: pk.call("pk_quantize_value_int4_register", vt, vf, el, 56.0, frames, stream=stream),
+        "attention_packed": lambda: pk.call("pk_local_relpos_attention_packed", q, k, None, vf, pos, bu, bv, out8, frames,
+                                            padded, frames, 128, 128, padded, pk_key, k_sc, pk_pos, p_sc, stream=stream),
+        "attention_tc": lambda: pk.call("pk_local_relpos_attention_tc_scores", q, k, None, vf, pos, bu, bv, out16, frames,
+                                        padded, frames, 128, 128, padded, stream=stream),
+    }
+    nbytes = {
+        "pack_key_int4": padded * (2048 + 512 + 32),
+        "pack_score_vectors": 8 * 272 * (256 + 128 + 4),
+        "quantize_value_int4": padded * (2048 + 512) + 4096 + 2 * 272 * 1024,
+        "attention_packed": padded * (2048 + 544 + 512 + 1024) + 8 * 272 * 132 + 4096,
+        "attention_tc": padded * (2048 + 2048 + 1024 + 2048) + 8 * 272 * 256,
+    }
+    for f in runs.values():
+        f()
+    torch.cuda.synchronize()
+    interior_tiles = max(0, (frames - 144) // 16 - 7)  # qb in [128, frames - 144]
+    ops = 2 * interior_tiles * 8 * (2 * 16 * 272 * 128 + 16 * 320 * 128)
+    out = {"frames": frames}
+    for name, f in runs.items():
+        ms = time_events(torch, f, reps, stream)
+        gbs = nbytes[name] / (ms * 1e-3) / 1e9
+        out[name] = {"us": round(ms * 1e3, 2), "bytes": nbytes[name], "GBps": round(gbs, 1),
+                     "pct_hbm": round(100.0 * gbs / 8000.0, 2)}
+    out["attention_packed"]["int8_tops"] = round(ops / (out["attention_packed"]["us"] * 1e-6) / 1e12, 2)
+    layer_us = sum(out[n]["us"] for n in ("pack_key_int4", "pack_score_vectors", "quantize_value_int4", "attention_packed"))
+    out["packed_layer_us"] = round(layer_us, 2)
+    out["packed_24_layers_ms_per_audio_min"] = round(24 * layer_us * 1e-3 / (frames * 0.08 / 60.0), 4)
+    return out
+
+
 def roof(flops, nbytes, peak_tops):
     """Roofline bound of one launch: min(MFMA peak, arithmetic intensity x 8 TB/s)."""
     return min(peak_tops, flops / nbytes * 8.0)  # TFLOP/s
@@ -501,6 +564,8 @@ def main():
     ap.add_argument("--only-dominant", action="store_true",
                     help="run only the dominant kernel (20 launches) and a 256 MiB device copy, "
                          "for rocprofv3 counter passes")
+    ap.add_argument("--only-attention", action="store_true",
+                    help="run only the attention measurements and a 256 MiB device copy, for rocprofv3 passes")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -514,6 +579,15 @@ def main():
 
     torch.cuda.set_device(0)
     stream = torch.cuda.current_stream()
+    if args.only_attention:
+        res = attention_bench(pk, torch, stream, args.frames)
+        src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps(res), flush=True)
+        return
     if args.only_dominant:
         k_ms, _, k_bytes = dominant_kernel(pk, torch, args.frames, stream)
         src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
@@ -546,6 +620,7 @@ def main():
     joint = joint_bench(pk, torch, stream)
     joint["hbm_streaming"] = joint_streaming(pk, torch, stream)
     decode = decode_bench(pk, torch, stream, args.frames)
+    attention = attention_bench(pk, torch, stream, args.frames)
     configs = config_results(pk, torch, stream)
     cpu = None if args.no_cpu else cpu_baseline(plan)
 
@@ -570,6 +645,7 @@ def main():
         "ms_per_audio_min": round(ms_step / audio_min, 4),
         "joint_gemv": joint,
         "tdt_decode": decode,
+        "local_attention": attention,
         "roofline": {"kernel": "g3::gemm3_kernel<FP8, EPI_F8> (FF1 expand 1024->4096, T=45000)",
                      "bound": "mfma", "achieved": round(k_tflops, 2), "peak": PEAK["fp8"],
                      "unit": "TFLOP/s", "frac": round(k_tflops / PEAK["fp8"], 4), "traffic": measured_traffic(),

@@ -49,6 +49,72 @@ __device__ __forceinline__ uint16_t bf16_rn(float v) {  // finite inputs only
 }
 __device__ __forceinline__ float bf16_f32(uint16_t h) { return __builtin_bit_cast(float, (uint32_t)h << 16); }
 
+// Two floats -> two bf16 (round to nearest even) in one v_cvt_pk_bf16_f32.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t bf16x2_rn(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, bf16x2_t));
+}
+
+// rint(v / s) for the IEEE quotient with |v / s| <= 127.5, from v * rcp(s):
+// v_rcp_f32 is within 1 ulp of 1/s, so the product is within 3.1e-5 of the
+// rounded quotient and both round to the same integer unless the product
+// lies within 5e-5 of a half-integer.  quant8 returns rint(v * rcp(s)) and
+// flags the lanes that must divide instead.
+__device__ __forceinline__ float quant_fast(float v, float inv_s, bool& tie) {
+    const float r = v * inv_s;
+    const float t = __builtin_rintf(r);
+    tie = tie || __builtin_fabsf(r - t) > 0.49995f;
+    return t;
+}
+// Four integer-valued floats in [-128, 127] -> four int8 bytes.
+__device__ __forceinline__ uint32_t pack_i8x4(float a, float b, float c, float d) {
+    return ((uint32_t)(int)a & 255u) | (((uint32_t)(int)b & 255u) << 8) | (((uint32_t)(int)c & 255u) << 16) |
+           ((uint32_t)(int)d << 24);
+}
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+
+// Byte `b` of w as OCP e4m3 -> float (v_cvt_f32_fp8, exact); b folds to a
+// constant in unrolled loops.
+__device__ __forceinline__ float fp8_byte(uint32_t w, int b) {
+    switch (b) {
+        case 0: return __builtin_amdgcn_cvt_f32_fp8((int)w, 0);
+        case 1: return __builtin_amdgcn_cvt_f32_fp8((int)w, 1);
+        case 2: return __builtin_amdgcn_cvt_f32_fp8((int)w, 2);
+        default: return __builtin_amdgcn_cvt_f32_fp8((int)w, 3);
+    }
+}
+
+// e4m3 of two finite values (saturating), without the NaN handling of e4m3x2.
+__device__ __forceinline__ uint32_t e4m3x2_finite(float a, float b) {
+    return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(__builtin_fminf(__builtin_fmaxf(a, -448.0f), 448.0f),
+                                                     __builtin_fminf(__builtin_fmaxf(b, -448.0f), 448.0f), 0, false) & 0xffffu;
+}
+
+// Lane moves within rows of 16 lanes (DPP, no LDS round trip).  row_shl(v, n)
+// gives lane i the value of lane i + n of its row (lanes past the row's end
+// get 0): in a reduction tree v += row_shl(v, n), n = 8, 4, 2, 1, the row's
+// lane 0 adds exactly the operands of a shuffle-down tree.  row_ror rotates
+// the row, so a max over rotations 8, 4, 2, 1 reaches every lane.
+template <int kCtrl>
+__device__ __forceinline__ float dpp(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), kCtrl, 0xf, 0xf, true));
+}
+template <int N>
+__device__ __forceinline__ float row_shl(float v) { return dpp<0x100 + N>(v); }
+__device__ __forceinline__ float row_max16(float v) {
+    v = __builtin_fmaxf(v, dpp<0x128>(v));
+    v = __builtin_fmaxf(v, dpp<0x124>(v));
+    v = __builtin_fmaxf(v, dpp<0x122>(v));
+    return __builtin_fmaxf(v, dpp<0x121>(v));
+}
+__device__ __forceinline__ float row_sum_tree16(float v) {  // exact shuffle-down tree, valid in the row's lane 0
+    v += row_shl<8>(v);
+    v += row_shl<4>(v);
+    v += row_shl<2>(v);
+    return v + row_shl<1>(v);
+}
+
 // Eight signed nibbles -> two words of four bytes, each nibble in the high
 // half of its byte (value * 16): lo takes the even nibbles, hi the odd ones.
 __device__ __forceinline__ uint32_t nib_lo16(uint32_t w) { return (w << 4) & 0xf0f0f0f0u; }
@@ -177,12 +243,20 @@ __global__ __launch_bounds__(1024) void quantize_value_int4_kernel(const uint16_
 
 // ---- attention -----------------------------------------------------------
 
-struct ScalarShared {
-    float scores[8][264];
+struct QueryShared {
+    float scores[4][264];  // one row per wave: scores, then exp, then weights
 };
-struct PackedShared {
-    uint8_t qa_u[16][144];  // INT4 (q+u) as int8, MFMA operand order, rows padded
-    uint8_t qa_v[16][144];  // INT8 (q+v), reference score-vector byte order
+// Interior tiles of one head streamed through one workgroup: the keys and
+// S4 values of the current window live in rings indexed by key % 288 (the
+// 272-key window plus the 16 keys of the next tile), so each tile fetches only
+// its 16 new keys.
+constexpr int kRing = 288;
+struct StreamShared {
+    uint8_t ring_k[kRing][72];  // INT4 key vectors (64 bytes, row padded)
+    float ring_ks[kRing];
+    uint8_t ring_v[kHead][144];  // S4 V of the head's 128 features, ring key / 2
+    uint8_t qa_u[16][144];       // INT4 (q+u) as int8, MFMA operand order, rows padded
+    uint8_t qa_v[16][144];       // INT8 (q+v), reference score-vector byte order
     uint16_t cs[16][kPosRows];
     uint16_t ps[16][kPosRows];
     uint8_t prob[16][336];  // U4 probabilities as bytes, prob_pos order
@@ -197,74 +271,72 @@ struct TcShared {
     uint8_t prob[16][400];  // e4m3 probabilities for keys 0..383 (zero past the window)
     uint16_t out[16][128];
 };
-// Each kernel instantiation declares only the union it uses, so the packed
-// kernel's LDS (and occupancy) does not pay for the fp32 score planes.
-union PackedAttnShared {
-    ScalarShared s;
-    PackedShared p;
-};
-union TcAttnShared {
-    ScalarShared s;
-    TcShared t;
-};
 
-// Context store (encoder.cu:1463-1474): fp16 round, packed form e4m3(x * 28).
+// Context store (encoder.cu:1463-1474) of two adjacent features: fp16 round,
+// packed form e4m3(x * 28).
 template <bool kPacked>
-__device__ __forceinline__ void store4(void* output, size_t index, const float (&c)[4]) {
-    if constexpr (kPacked) {
-        const uint32_t lo = e4m3x2(round_f16(c[0]) * 28.0f, round_f16(c[1]) * 28.0f);
-        const uint32_t hi = e4m3x2(round_f16(c[2]) * 28.0f, round_f16(c[3]) * 28.0f);
-        *(uint32_t*)((uint8_t*)output + index) = lo | (hi << 16);
-    } else {
-        const uint32_t lo = (uint32_t)f2h(c[0]) | ((uint32_t)f2h(c[1]) << 16);
-        const uint32_t hi = (uint32_t)f2h(c[2]) | ((uint32_t)f2h(c[3]) << 16);
-        *(uint2*)((uint16_t*)output + index) = uint2{lo, hi};
-    }
+__device__ __forceinline__ void store2(void* output, size_t index, float c0, float c1) {
+    if constexpr (kPacked)
+        *(uint16_t*)((uint8_t*)output + index) = (uint16_t)e4m3x2(round_f16(c0) * 28.0f, round_f16(c1) * 28.0f);
+    else
+        *(uint32_t*)((uint16_t*)output + index) = (uint32_t)f2h(c0) | ((uint32_t)f2h(c1) << 16);
 }
 
-// encoder.cu:1548-1684: per-query FP32 path, one half wave per query.
+// encoder.cu:1548-1684: the per-query FP32 path of boundary tiles, one wave
+// per query.  The arithmetic is the reference's, in its 32-lane warp order:
+// a slot's score is 16 partial sums (lane h of 16 accumulates dimensions
+// 2h + 32q, q = 0..3, interleaving content and position FMAs) reduced by a
+// shuffle tree; the denominator is 32 partial sums (partial l adds slots l,
+// l + 32, ... in order) reduced by a shuffle tree; each output feature's
+// context is one FMA chain over the keys in order.  Which lane runs which of
+// these chains is free, so a wave evaluates four slots per step, keeps eight
+// steps of loads in flight, and owns two features per lane.
 template <bool kPacked>
-__device__ void attention_scalar(ScalarShared& sh, const uint16_t* __restrict__ query, const uint16_t* __restrict__ key,
-                                 const uint8_t* __restrict__ value_fp8, const uint16_t* __restrict__ position,
-                                 const uint16_t* __restrict__ bias_u, const uint16_t* __restrict__ bias_v, void* output,
-                                 int qb, int head, int rows, int padded_rows, int valid_rows, int left, int right,
-                                 int value_stride) {
-    const int hw = threadIdx.x >> 5, ln = threadIdx.x & 31;
-    float* scores = sh.scores[hw];
-    for (int lq = hw; lq < 16; lq += 8) {
-        const int qr = qb + lq;
-        const size_t oidx = (size_t)qr * kModel + head * kHead + 4 * ln;
-        if (qr >= rows || qr >= valid_rows) {
-            if (qr < padded_rows) {
-                const float z[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-                store4<kPacked>(output, oidx, z);
-            }
-            continue;
-        }
-        const int first = max(0, qr - left), last = min(valid_rows - 1, qr + right);
-        const int count = last - first + 1;
-        const int half = ln >> 4, hl = ln & 15;
-        float2 su[4], sv[4];
+__device__ void attention_query(float* scores, const uint16_t* __restrict__ query, const uint16_t* __restrict__ key,
+                                const uint8_t* __restrict__ value_fp8, const uint16_t* __restrict__ position,
+                                const uint16_t* __restrict__ bias_u, const uint16_t* __restrict__ bias_v, void* output, int qr,
+                                int head, int rows, int padded_rows, int valid_rows, int left, int right, int value_stride) {
+    const int lane = threadIdx.x & 63;
+    const size_t oidx = (size_t)qr * kModel + head * kHead + 2 * lane;
+    if (qr >= rows || qr >= valid_rows) {
+        if (qr < padded_rows) store2<kPacked>(output, oidx, 0.0f, 0.0f);
+        return;
+    }
+    const int first = max(0, qr - left), last = min(valid_rows - 1, qr + right);
+    const int count = last - first + 1;
+    const int grp = lane >> 4, hl = lane & 15;
+    float2 su[4], sv[4];
 #pragma unroll
-        for (int quarter = 0; quarter < 4; ++quarter) {
-            const int d = head * kHead + 2 * hl + 32 * quarter;
-            const uint32_t q = *(const uint32_t*)(query + (size_t)qr * kModel + d);
-            const uint32_t u = *(const uint32_t*)(bias_u + d);
-            const uint32_t v = *(const uint32_t*)(bias_v + d);
-            const float q0 = h2f((uint16_t)q), q1 = h2f((uint16_t)(q >> 16));
-            su[quarter] = make_float2(q0 + h2f((uint16_t)u), q1 + h2f((uint16_t)(u >> 16)));
-            sv[quarter] = make_float2(q0 + h2f((uint16_t)v), q1 + h2f((uint16_t)(v >> 16)));
-        }
-        for (int sp = 0; sp < count; sp += 2) {
-            const int slot = sp + half;
-            const int key_row = first + min(slot, count - 1);
+    for (int quarter = 0; quarter < 4; ++quarter) {
+        const int d = head * kHead + 2 * hl + 32 * quarter;
+        const uint32_t q = *(const uint32_t*)(query + (size_t)qr * kModel + d);
+        const uint32_t u = *(const uint32_t*)(bias_u + d);
+        const uint32_t v = *(const uint32_t*)(bias_v + d);
+        const float q0 = h2f((uint16_t)q), q1 = h2f((uint16_t)(q >> 16));
+        su[quarter] = make_float2(q0 + h2f((uint16_t)u), q1 + h2f((uint16_t)(u >> 16)));
+        sv[quarter] = make_float2(q0 + h2f((uint16_t)v), q1 + h2f((uint16_t)(v >> 16)));
+    }
+    constexpr int kU = 8;
+    for (int sp0 = 0; sp0 < count; sp0 += 4 * kU) {
+        uint32_t kw[kU][4], pw[kU][4];
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+            const int key_row = first + min(sp0 + 4 * u + grp, count - 1);
             const int prow = left - qr + key_row;
-            float s = 0.0f;
 #pragma unroll
             for (int quarter = 0; quarter < 4; ++quarter) {
                 const int d = 2 * hl + 32 * quarter;
-                const uint32_t k = *(const uint32_t*)(key + (size_t)key_row * kModel + head * kHead + d);
-                const uint32_t p = *(const uint32_t*)(position + ((size_t)head * kPosRows + prow) * kHead + d);
+                kw[u][quarter] = *(const uint32_t*)(key + (size_t)key_row * kModel + head * kHead + d);
+                pw[u][quarter] = *(const uint32_t*)(position + ((size_t)head * kPosRows + prow) * kHead + d);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+            const int slot = sp0 + 4 * u + grp;
+            float s = 0.0f;
+#pragma unroll
+            for (int quarter = 0; quarter < 4; ++quarter) {
+                const uint32_t k = kw[u][quarter], p = pw[u][quarter];
                 s = __builtin_fmaf(su[quarter].x, h2f((uint16_t)k), s);
                 s = __builtin_fmaf(sv[quarter].x, h2f((uint16_t)p), s);
                 s = __builtin_fmaf(su[quarter].y, h2f((uint16_t)(k >> 16)), s);
@@ -274,40 +346,47 @@ __device__ void attention_scalar(ScalarShared& sh, const uint16_t* __restrict__ 
             for (int off = 8; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
             if (hl == 0 && slot < count) scores[slot] = s * kScoreScale;
         }
-        wave_sync();
-        float mx = -FLT_MAX;
-        for (int slot = ln; slot < count; slot += 32) mx = __builtin_fmaxf(mx, scores[slot]);
+    }
+    wave_sync();
+    float mx = -FLT_MAX;
+    for (int slot = lane; slot < count; slot += 64) mx = __builtin_fmaxf(mx, scores[slot]);
 #pragma unroll
-        for (int off = 16; off > 0; off >>= 1) mx = __builtin_fmaxf(mx, __shfl_xor(mx, off, 64));
-        float den = 0.0f;
-        for (int slot = ln; slot < count; slot += 32) {
-            const float e = expf(scores[slot] - mx);
-            scores[slot] = e;
-            den += e;
+    for (int off = 32; off > 0; off >>= 1) mx = __builtin_fmaxf(mx, __shfl_xor(mx, off, 64));
+    for (int slot = lane; slot < count; slot += 64) scores[slot] = expf(scores[slot] - mx);
+    wave_sync();
+    float den = 0.0f;
+    if (lane < 32)
+        for (int slot = lane; slot < count; slot += 32) den += scores[slot];
+#pragma unroll
+    for (int off = 16; off > 0; off >>= 1) den += __shfl_xor(den, off, 64);
+    den = __shfl(den, 0, 64);
+    wave_sync();
+    for (int slot = lane; slot < count; slot += 64) scores[slot] = scores[slot] / den;
+    wave_sync();
+    float c0 = 0.0f, c1 = 0.0f;
+    const int feature = head * kHead + 2 * lane;
+    constexpr int kC = 16;  // chunks of four keys in flight per batch
+    for (int chunk0 = first & ~3; chunk0 <= last; chunk0 += 4 * kC) {
+        uint32_t words[kC][2];
+#pragma unroll
+        for (int b = 0; b < kC; ++b) {
+            const int chunk = min(chunk0 + 4 * b, last & ~3);
+            words[b][0] = *(const uint32_t*)(value_fp8 + (size_t)feature * value_stride + chunk);
+            words[b][1] = *(const uint32_t*)(value_fp8 + (size_t)(feature + 1) * value_stride + chunk);
         }
 #pragma unroll
-        for (int off = 16; off > 0; off >>= 1) den += __shfl_xor(den, off, 64);
-        den = __shfl(den, 0, 32);
-        wave_sync();
-        float c[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        const int feature = head * kHead + 4 * ln;
-        for (int chunk = first & ~3; chunk <= last; chunk += 4) {
-            uint32_t words[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) words[i] = *(const uint32_t*)(value_fp8 + (size_t)(feature + i) * value_stride + chunk);
+        for (int b = 0; b < kC; ++b) {
 #pragma unroll
             for (int item = 0; item < 4; ++item) {
-                const int kr = chunk + item;
+                const int kr = chunk0 + 4 * b + item;
                 if (kr < first || kr > last) continue;
-                const float weight = scores[kr - first] / den;
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    c[i] = __builtin_fmaf(weight, e4m3_to_f32((words[i] >> (8 * item)) & 0xffu) * kValueScale, c[i]);
+                const float weight = scores[kr - first];
+                c0 = __builtin_fmaf(weight, fp8_byte(words[b][0], item) * kValueScale, c0);
+                c1 = __builtin_fmaf(weight, fp8_byte(words[b][1], item) * kValueScale, c1);
             }
         }
-        store4<kPacked>(output, oidx, c);
-        wave_sync();
     }
+    store2<kPacked>(output, oidx, c0, c1);
 }
 
 // Softmax of query lq over its 257 slots from the combined logits held by a
@@ -332,157 +411,239 @@ __device__ __forceinline__ float softmax_half(float (&l)[9], int ln) {
     return __shfl(den, 0, 32);
 }
 
-// encoder.cu:1687-1966: INT4/INT8 scores, U4 x S4 context, e4m3(x*28) out.
-__device__ void attention_packed_tile(PackedShared& sh, const uint16_t* __restrict__ query, const uint8_t* __restrict__ value_fp8,
-                                      const uint16_t* __restrict__ bias_u, const uint16_t* __restrict__ bias_v,
-                                      uint8_t* __restrict__ output, int qb, int head, int value_stride,
-                                      const uint8_t* __restrict__ packed_key, const float* __restrict__ key_scales,
-                                      const uint8_t* __restrict__ packed_position, const float* __restrict__ position_scales) {
+// encoder.cu:1687-1966 for the interior tiles [t0, t1) of one head: INT4
+// content and INT8 position scores, U4 probabilities x S4 V, e4m3(x*28) out.
+// The position operands (the same for every tile of a head) stay in
+// registers; keys and values stream through the LDS rings; the next tile's
+// queries and 16 new keys are loaded while the current tile computes.
+__device__ void attention_packed_stream(StreamShared& sh, const uint16_t* __restrict__ query, const uint8_t* __restrict__ value_fp8,
+                                        const uint16_t* __restrict__ bias_u, const uint16_t* __restrict__ bias_v,
+                                        uint8_t* __restrict__ output, int t0, int t1, int head, int value_stride,
+                                        const uint8_t* __restrict__ packed_key, const float* __restrict__ key_scales,
+                                        const uint8_t* __restrict__ packed_position, const float* __restrict__ position_scales) {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int g = lane >> 4, l16 = lane & 15;
-    const int first_key = qb - 128;
+    const int qr16 = tid >> 4, qj = tid & 15;  // query row / 8-dimension slice this thread quantizes
+    const uint8_t* s4 = value_fp8 + (size_t)kModel * value_stride;
+    const float* vscales = (const float*)(value_fp8 + (size_t)kModel * value_stride * 3 / 2);
 
-    // Phase 1: clear the probability rows; quantize q+u and q+v.
-    for (int i = tid; i < 16 * 336 / 4; i += 256) ((uint32_t*)sh.prob)[i] = 0;
+    // Position operands of this wave's key tiles kt = wave + 4i.
+    uint4 pq[5][2];
+    float psc[5];
+#pragma unroll
+    for (int i = 0; i < 5; ++i) {
+        const int kt = min(wave + 4 * i, kPosRows / 16 - 1);
+        const int pvec = head * kPosRows + 16 * kt + l16;
+        const uint8_t* pb = packed_position + (size_t)pvec * 128;
+        pq[i][0] = *(const uint4*)(pb + 16 * g);
+        pq[i][1] = *(const uint4*)(pb + 64 + 16 * g);
+        psc[i] = position_scales[pvec];
+    }
+    const uint4 bu = *(const uint4*)(bias_u + head * kHead + 8 * qj);
+    const uint4 bv = *(const uint4*)(bias_v + head * kHead + 8 * qj);
+    float vs[2];
+#pragma unroll
+    for (int c = 0; c < 2; ++c) vs[c] = vscales[head * kHead + 16 * (2 * wave + c) + l16];
+
+    // Prologue: the first tile's whole key window into the rings.
     {
-        const int r = tid >> 4, j = tid & 15;
-        const size_t qi = (size_t)(qb + r) * kModel + head * kHead + 8 * j;
-        const uint4 q = *(const uint4*)(query + qi);
-        const uint4 u = *(const uint4*)(bias_u + head * kHead + 8 * j);
-        const uint4 v = *(const uint4*)(bias_v + head * kHead + 8 * j);
-        const uint32_t qw[4] = {q.x, q.y, q.z, q.w}, uw[4] = {u.x, u.y, u.z, u.w}, vw[4] = {v.x, v.y, v.z, v.w};
-        float vu[8], vv[8], mu = 0.0f, mv = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int sh16 = 16 * (i & 1);
-            const float qf = h2f((uint16_t)(qw[i / 2] >> sh16));
-            vu[i] = round_f16(qf + h2f((uint16_t)(uw[i / 2] >> sh16)));
-            vv[i] = round_f16(qf + h2f((uint16_t)(vw[i / 2] >> sh16)));
-            mu = __builtin_fmaxf(mu, __builtin_fabsf(vu[i]));
-            mv = __builtin_fmaxf(mv, __builtin_fabsf(vv[i]));
+        const int fk = 16 * t0 - 128;
+        for (int i = tid; i < kPosRows * 4; i += 256) {
+            const int key = fk + (i >> 2);
+            *(uint4*)&sh.ring_k[key % kRing][16 * (i & 3)] =
+                *(const uint4*)(packed_key + ((size_t)key * kHeads + head) * 64 + 16 * (i & 3));
         }
-#pragma unroll
-        for (int off = 1; off < 16; off <<= 1) {
-            mu = __builtin_fmaxf(mu, __shfl_xor(mu, off, 64));
-            mv = __builtin_fmaxf(mv, __shfl_xor(mv, off, 64));
-        }
-        const float su = mu > 0.0f ? mu / 7.0f : 1.0f, sv = mv > 0.0f ? mv / 127.0f : 1.0f;
-        if (j == 0) {
-            sh.qs_u[r] = su;
-            sh.qs_v[r] = sv;
-        }
-        uint32_t ue = 0, uo = 0, v8[2] = {0, 0};
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const uint32_t a = (uint32_t)(int)__builtin_rintf(vu[i] / su) & 255u;
-            if (i & 1) uo |= a << (8 * (i >> 1));
-            else ue |= a << (8 * (i >> 1));
-            v8[i / 4] |= ((uint32_t)(int)__builtin_rintf(vv[i] / sv) & 255u) << (8 * (i & 3));
-        }
-        // INT4 plane: dimension 8j+i sits at storage nibble 2*off_j + i of the
-        // key vectors; widen_s4x16 of the key's bytes [32m + 8g', +8) yields
-        // even nibbles then odd nibbles per word, hence this operand order.
-        const int pa = 64 * (j >> 3) + 16 * (j & 3) + 8 * ((j >> 2) & 1);
-        *(uint2*)&sh.qa_u[r][pa] = uint2{ue, uo};
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const int L = 2 * j + h;
-            *(uint32_t*)&sh.qa_v[r][(L / 8) * 32 + (L % 4) * 8 + (L & 4)] = v8[h];
+        for (int i = tid; i < kPosRows; i += 256) sh.ring_ks[(fk + i) % kRing] = key_scales[(size_t)(fk + i) * kHeads + head];
+        for (int i = tid; i < kHead * (kPosRows / 16); i += 256) {
+            const int f = i / (kPosRows / 16), seg = i % (kPosRows / 16);
+            const int key = fk + 16 * seg;
+            *(uint2*)&sh.ring_v[f][(key % kRing) / 2] = *(const uint2*)(s4 + ((size_t)(head * kHead + f) * value_stride + key) / 2);
         }
     }
-    __syncthreads();
+    uint4 qn = *(const uint4*)(query + (size_t)(16 * t0 + qr16) * kModel + head * kHead + 8 * qj);
 
-    // Phase 2: scores for the 17 key tiles of 16 columns, four waves.
-    {
-        const v4i au0 = __builtin_bit_cast(v4i, *(const uint4*)&sh.qa_u[l16][16 * g]);
-        const v4i au1 = __builtin_bit_cast(v4i, *(const uint4*)&sh.qa_u[l16][64 + 16 * g]);
-        const v4i av0 = __builtin_bit_cast(v4i, *(const uint4*)&sh.qa_v[l16][16 * g]);
-        const v4i av1 = __builtin_bit_cast(v4i, *(const uint4*)&sh.qa_v[l16][64 + 16 * g]);
-        float qsu[4], qsv[4];
+    for (int t = t0; t < t1; ++t) {
+        const int qb = 16 * t, first_key = qb - 128;
+        const bool more = t + 1 < t1;
+
+        // Phase 1: clear the probability rows; quantize q+u and q+v.
+        for (int i = tid; i < 16 * 336 / 4; i += 256) ((uint32_t*)sh.prob)[i] = 0;
+        {
+            // q+u and q+v as fp16 adds: for fp16 operands, rounding the fp32 sum
+            // to fp16 is the same as one fp16 addition (24 >= 2*11 + 2 bits).
+            const uint32_t qw[4] = {qn.x, qn.y, qn.z, qn.w}, uw[4] = {bu.x, bu.y, bu.z, bu.w}, vw[4] = {bv.x, bv.y, bv.z, bv.w};
+            h2_t au[4], av[4], mxu = h2_t{0, 0}, mxv = h2_t{0, 0};
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            qsu[r] = sh.qs_u[4 * g + r];
-            qsv[r] = sh.qs_v[4 * g + r];
+            for (int i = 0; i < 4; ++i) {
+                au[i] = __builtin_bit_cast(h2_t, qw[i]) + __builtin_bit_cast(h2_t, uw[i]);
+                av[i] = __builtin_bit_cast(h2_t, qw[i]) + __builtin_bit_cast(h2_t, vw[i]);
+                mxu = __builtin_elementwise_max(mxu, __builtin_elementwise_abs(au[i]));
+                mxv = __builtin_elementwise_max(mxv, __builtin_elementwise_abs(av[i]));
+            }
+            float mu = __builtin_fmaxf((float)mxu[0], (float)mxu[1]), mv = __builtin_fmaxf((float)mxv[0], (float)mxv[1]);
+            mu = row_max16(mu);
+            mv = row_max16(mv);
+            const float su = mu > 0.0f ? mu / 7.0f : 1.0f, sv = mv > 0.0f ? mv / 127.0f : 1.0f;
+            const float isu = __builtin_amdgcn_rcpf(su), isv = __builtin_amdgcn_rcpf(sv);
+            if (qj == 0) {
+                sh.qs_u[qr16] = su * 0.0625f;  // carries the 1/16 of the widened INT4 keys
+                sh.qs_v[qr16] = sv;
+            }
+            float fu[8], fv[8];
+            bool tie = false;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                fu[i] = quant_fast((float)au[i / 2][i & 1], isu, tie);
+                fv[i] = quant_fast((float)av[i / 2][i & 1], isv, tie);
+            }
+            if (__builtin_amdgcn_ballot_w64(tie) != 0) {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    fu[i] = __builtin_rintf((float)au[i / 2][i & 1] / su);
+                    fv[i] = __builtin_rintf((float)av[i / 2][i & 1] / sv);
+                }
+            }
+            const uint32_t ue = pack_i8x4(fu[0], fu[2], fu[4], fu[6]), uo = pack_i8x4(fu[1], fu[3], fu[5], fu[7]);
+            const uint32_t v8[2] = {pack_i8x4(fv[0], fv[1], fv[2], fv[3]), pack_i8x4(fv[4], fv[5], fv[6], fv[7])};
+            // INT4 plane: dimension 8j+i sits at storage nibble 2*off_j + i of
+            // the key vectors; widen_s4x16 of the key's bytes [32m + 8g, +8)
+            // yields even nibbles then odd nibbles per word, hence this order.
+            const int pa = 64 * (qj >> 3) + 16 * (qj & 3) + 8 * ((qj >> 2) & 1);
+            *(uint2*)&sh.qa_u[qr16][pa] = uint2{ue, uo};
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int L = 2 * qj + h;
+                *(uint32_t*)&sh.qa_v[qr16][(L / 8) * 32 + (L % 4) * 8 + (L & 4)] = v8[h];
+            }
         }
-        for (int kt = wave; kt < kPosRows / 16; kt += 4) {
-            const int col = 16 * kt + l16;
-            const int kvec = (first_key + col) * kHeads + head;
-            const int pvec = head * kPosRows + col;
-            const uint8_t* kb = packed_key + (size_t)kvec * 64;
-            const uint8_t* pb = packed_position + (size_t)pvec * 128;
-            const uint2 k0 = *(const uint2*)(kb + 8 * g), k1 = *(const uint2*)(kb + 32 + 8 * g);
-            const uint4 p0 = *(const uint4*)(pb + 16 * g), p1 = *(const uint4*)(pb + 64 + 16 * g);
-            const float ks = key_scales[kvec], pscl = position_scales[pvec];
-            v4i acu = __builtin_amdgcn_mfma_i32_16x16x64_i8(au0, widen_s4x16(k0), v4i{0, 0, 0, 0}, 0, 0, 0);
-            acu = __builtin_amdgcn_mfma_i32_16x16x64_i8(au1, widen_s4x16(k1), acu, 0, 0, 0);
-            v4i acv = __builtin_amdgcn_mfma_i32_16x16x64_i8(av0, __builtin_bit_cast(v4i, p0), v4i{0, 0, 0, 0}, 0, 0, 0);
-            acv = __builtin_amdgcn_mfma_i32_16x16x64_i8(av1, __builtin_bit_cast(v4i, p1), acv, 0, 0, 0);
+        // Next tile's queries and its 16 new keys (qb + 144 .. qb + 159).
+        uint4 nk = uint4{0, 0, 0, 0};
+        uint2 nv = uint2{0, 0};
+        float nks = 0.0f;
+        const int nkey = qb + 144;
+        if (more) {
+            qn = *(const uint4*)(query + (size_t)(qb + 16 + qr16) * kModel + head * kHead + 8 * qj);
+            if (tid < 64) nk = *(const uint4*)(packed_key + ((size_t)(nkey + (tid >> 2)) * kHeads + head) * 64 + 16 * (tid & 3));
+            else if (tid < 80) nks = key_scales[(size_t)(nkey + tid - 64) * kHeads + head];
+            else if (tid >= 128) nv = *(const uint2*)(s4 + ((size_t)(head * kHead + tid - 128) * value_stride + nkey) / 2);
+        }
+        __syncthreads();
+
+        // Phase 2: scores for the 17 key tiles of 16 columns, four waves.
+        {
+            const v4i au0 = __builtin_bit_cast(v4i, *(const uint4*)&sh.qa_u[l16][16 * g]);
+            const v4i au1 = __builtin_bit_cast(v4i, *(const uint4*)&sh.qa_u[l16][64 + 16 * g]);
+            const v4i av0 = __builtin_bit_cast(v4i, *(const uint4*)&sh.qa_v[l16][16 * g]);
+            const v4i av1 = __builtin_bit_cast(v4i, *(const uint4*)&sh.qa_v[l16][64 + 16 * g]);
+            float qsu[4], qsv[4];
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                sh.cs[4 * g + r][col] = bf16_rn((float)(acu[r] >> 4) * (qsu[r] * ks));
-                sh.ps[4 * g + r][col] = bf16_rn((float)acv[r] * (qsv[r] * pscl));
+                qsu[r] = sh.qs_u[4 * g + r];
+                qsv[r] = sh.qs_v[4 * g + r];
+            }
+            const int ring0 = first_key % kRing;
+#pragma unroll
+            for (int i = 0; i < 5; ++i) {
+                const int kt = min(wave + 4 * i, kPosRows / 16 - 1);  // wave 0 alone has a fifth tile
+                const int col = 16 * kt + l16;
+                int slot = ring0 + col;
+                slot = slot >= kRing ? slot - kRing : slot;
+                const uint2 k0 = *(const uint2*)&sh.ring_k[slot][8 * g], k1 = *(const uint2*)&sh.ring_k[slot][32 + 8 * g];
+                const float ks = sh.ring_ks[slot], pscl = psc[i];
+                v4i acu = __builtin_amdgcn_mfma_i32_16x16x64_i8(au0, widen_s4x16(k0), v4i{0, 0, 0, 0}, 0, 0, 0);
+                acu = __builtin_amdgcn_mfma_i32_16x16x64_i8(au1, widen_s4x16(k1), acu, 0, 0, 0);
+                v4i acv = __builtin_amdgcn_mfma_i32_16x16x64_i8(av0, __builtin_bit_cast(v4i, pq[i][0]), v4i{0, 0, 0, 0}, 0, 0, 0);
+                acv = __builtin_amdgcn_mfma_i32_16x16x64_i8(av1, __builtin_bit_cast(v4i, pq[i][1]), acv, 0, 0, 0);
+                if (wave + 4 * i < kPosRows / 16) {
+#pragma unroll
+                    for (int r = 0; r < 4; r += 2) {
+                        const uint32_t c2 = bf16x2_rn((float)acu[r] * (qsu[r] * ks), (float)acu[r + 1] * (qsu[r + 1] * ks));
+                        const uint32_t p2 = bf16x2_rn((float)acv[r] * (qsv[r] * pscl), (float)acv[r + 1] * (qsv[r + 1] * pscl));
+                        sh.cs[4 * g + r][col] = (uint16_t)c2;
+                        sh.cs[4 * g + r + 1][col] = (uint16_t)(c2 >> 16);
+                        sh.ps[4 * g + r][col] = (uint16_t)p2;
+                        sh.ps[4 * g + r + 1][col] = (uint16_t)(p2 >> 16);
+                    }
+                }
             }
         }
-    }
-    __syncthreads();
+        __syncthreads();
 
-    // Phase 3: softmax and U4 probabilities, one half wave per query.
-    {
-        const int hw = tid >> 5, ln = tid & 31;
+        // Phase 3: softmax and U4 probabilities, 16 lanes per query: lane j
+        // owns slots j + 16k.  The reference's 32 denominator partials (slots
+        // l, l + 32, ...) are this lane's two chains over even and odd k; its
+        // first tree step (partial l plus partial l + 16) is the lane's own
+        // add, the remaining four run over the row.
+        {
+            const int lq = tid >> 4, j = tid & 15;
+            float l[17], mx = -FLT_MAX;
 #pragma unroll
-        for (int item = 0; item < 2; ++item) {
-            const int lq = hw + 8 * item;
-            float l[9];
-#pragma unroll
-            for (int part = 0; part < 9; ++part) {
-                const int slot = ln + 32 * part;
-                l[part] = slot < kMaxAtt ? (bf16_f32(sh.cs[lq][lq + slot]) + bf16_f32(sh.ps[lq][slot])) * kScoreScale : -FLT_MAX;
+            for (int k = 0; k < 17; ++k) {
+                const int slot = j + 16 * k;
+                l[k] = slot < kMaxAtt ? (bf16_f32(sh.cs[lq][lq + slot]) + bf16_f32(sh.ps[lq][slot])) * kScoreScale : -FLT_MAX;
+                mx = __builtin_fmaxf(mx, l[k]);
             }
-            const float den = softmax_half(l, ln);
-            if (ln == 0) sh.pscale[lq] = 1.0f / (15.0f * den);
+            mx = row_max16(mx);
+            float even = 0.0f, odd = 0.0f;
 #pragma unroll
-            for (int part = 0; part < 9; ++part) {
-                const int slot = ln + 32 * part;
-                if (slot < kMaxAtt) sh.prob[lq][prob_pos(lq + slot)] = (uint8_t)(int)__builtin_rintf(l[part] * 15.0f);
+            for (int k = 0; k < 17; ++k) {
+                if (j + 16 * k < kMaxAtt) {
+                    l[k] = expf(l[k] - mx);
+                    if (k & 1) odd += l[k];
+                    else even += l[k];
+                }
             }
+            const float den = row_sum_tree16(even + odd);
+            if (j == 0) sh.pscale[lq] = 1.0f / (15.0f * den);
+            uint8_t* prow = &sh.prob[lq][prob_pos(lq + j)];  // slot j + 16k sits 16k further
+#pragma unroll
+            for (int k = 0; k < 17; ++k)
+                if (j + 16 * k < kMaxAtt) prow[16 * k] = (uint8_t)(int)__builtin_rintf(l[k] * 15.0f);
         }
-    }
-    __syncthreads();
+        __syncthreads();
 
-    // Phase 4: context = U4 probabilities x S4 V over keys 0..271 (five K=64
-    // steps; keys >= 272 contribute zero operands).
-    {
-        const uint8_t* s4 = value_fp8 + (size_t)kModel * value_stride;
-        const float* vscales = (const float*)(value_fp8 + (size_t)kModel * value_stride * 3 / 2);
-        v4i acc[2] = {v4i{0, 0, 0, 0}, v4i{0, 0, 0, 0}};
+        // Phase 4: context = U4 probabilities x S4 V over keys 0..271 (five
+        // K=64 steps; keys >= 272 contribute zero operands).
+        {
+            v4i acc[2] = {v4i{0, 0, 0, 0}, v4i{0, 0, 0, 0}};
+            const int ring0 = first_key % kRing;
 #pragma unroll
-        for (int s = 0; s < 5; ++s) {
-            const int ko = 64 * s + 16 * g;
-            const v4i a = __builtin_bit_cast(v4i, *(const uint4*)&sh.prob[l16][ko]);
+            for (int st = 0; st < 5; ++st) {
+                const int ko = 64 * st + 16 * g;
+                const v4i a = __builtin_bit_cast(v4i, *(const uint4*)&sh.prob[l16][ko]);
+                int slot = ring0 + ko;
+                slot = slot >= kRing ? slot - kRing : slot;
+#pragma unroll
+                for (int c = 0; c < 2; ++c) {
+                    const uint2 w = ko < kPosRows ? *(const uint2*)&sh.ring_v[16 * (2 * wave + c) + l16][slot / 2] : uint2{0, 0};
+                    acc[c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, widen_s4x16(w), acc[c], 0, 0, 0);
+                }
+            }
+            float ps4[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) ps4[r] = sh.pscale[4 * g + r];
 #pragma unroll
             for (int c = 0; c < 2; ++c) {
-                const int fg = head * kHead + 16 * (2 * wave + c) + l16;
-                uint2 w = uint2{0, 0};
-                if (ko < kPosRows) w = *(const uint2*)(s4 + ((size_t)fg * value_stride + first_key + ko) / 2);
-                acc[c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, widen_s4x16(w), acc[c], 0, 0, 0);
+                const int fl = 16 * (2 * wave + c) + l16;
+#pragma unroll
+                for (int r = 0; r < 4; r += 2) {
+                    const float x0 = (float)(acc[c][r] >> 4) * (ps4[r] * vs[c]);
+                    const float x1 = (float)(acc[c][r + 1] >> 4) * (ps4[r + 1] * vs[c]);
+                    const uint32_t b2 = e4m3x2_finite(round_f16(x0) * 28.0f, round_f16(x1) * 28.0f);
+                    sh.out[4 * g + r][fl] = (uint8_t)b2;
+                    sh.out[4 * g + r + 1][fl] = (uint8_t)(b2 >> 8);
+                }
             }
         }
-#pragma unroll
-        for (int c = 0; c < 2; ++c) {
-            const int fl = 16 * (2 * wave + c) + l16;
-            const float vs = vscales[head * kHead + fl];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int row = 4 * g + r;
-                const float x = (float)(acc[c][r] >> 4) * (sh.pscale[row] * vs);
-                sh.out[row][fl] = (uint8_t)e4m3x2(round_f16(x) * 28.0f, 0.0f);
-            }
+        __syncthreads();
+        *(uint2*)(output + (size_t)(qb + qr16) * kModel + head * kHead + 8 * qj) = *(const uint2*)&sh.out[qr16][8 * qj];
+        // The 16 new keys go to ring slots of keys qb-144 .. qb-129, which this
+        // tile no longer reads; the next tile's first barrier publishes them.
+        if (more) {
+            if (tid < 64) *(uint4*)&sh.ring_k[(nkey + (tid >> 2)) % kRing][16 * (tid & 3)] = nk;
+            else if (tid < 80) sh.ring_ks[(nkey + tid - 64) % kRing] = nks;
+            else if (tid >= 128) *(uint2*)&sh.ring_v[tid - 128][(nkey % kRing) / 2] = nv;
         }
-    }
-    __syncthreads();
-    {
-        const int r = tid >> 4, j = tid & 15;
-        *(uint2*)(output + (size_t)(qb + r) * kModel + head * kHead + 8 * j) = *(const uint2*)&sh.out[r][8 * j];
     }
 }
 
@@ -599,35 +760,65 @@ __device__ void attention_tc_tile(TcShared& sh, const uint16_t* __restrict__ que
     }
 }
 
+// The boundary queries: tiles [0, ib) and [ie, tiles), four queries (one
+// per wave) of one head per workgroup, small LDS.
 template <bool kPacked>
-__global__ __launch_bounds__(256) void local_attention_kernel(
+__global__ __launch_bounds__(256) void boundary_attention_kernel(
     const uint16_t* __restrict__ query, const uint16_t* __restrict__ key, const uint8_t* __restrict__ value_fp8,
     const uint16_t* __restrict__ position, const uint16_t* __restrict__ bias_u, const uint16_t* __restrict__ bias_v,
-    void* __restrict__ output, int rows, int padded_rows, int valid_rows, int left, int right, int value_stride,
-    const uint8_t* __restrict__ packed_key, const float* __restrict__ key_scales, const uint8_t* __restrict__ packed_position,
-    const float* __restrict__ position_scales) {
-    const int qb = (int)blockIdx.x * 16, head = (int)blockIdx.y;
-    if (qb >= padded_rows) return;
-    const bool interior = qb >= left && qb + 15 + right < valid_rows && qb + 16 <= rows;
+    void* __restrict__ output, int rows, int padded_rows, int valid_rows, int left, int right, int value_stride, int ib, int ie) {
+    __shared__ QueryShared sh;
+    const int L = (int)blockIdx.x;
+    const int head = L & 7, grp = L >> 3, t = grp >> 2;
+    const int tile = t < ib ? t : ie + (t - ib);
+    attention_query<kPacked>(sh.scores[threadIdx.x >> 6], query, key, value_fp8, position, bias_u, bias_v, output,
+                             16 * tile + 4 * (grp & 3) + (int)(threadIdx.x >> 6), head, rows, padded_rows, valid_rows, left, right,
+                             value_stride);
+}
+
+// The interior tiles [ib, ie): packed -> `chunks` runs of consecutive tiles
+// per head, one workgroup each; tc -> one workgroup per tile and head.
+// Workgroup L runs on XCD L % 8; the work is split into eight contiguous
+// ranges of (tile or run, head) pairs so that each XCD's L2 holds the keys
+// and values of neighbouring tiles.
+template <bool kPacked>
+__global__ __launch_bounds__(256) void interior_attention_kernel(
+    const uint16_t* __restrict__ query, const uint16_t* __restrict__ key, const uint8_t* __restrict__ value_fp8,
+    const uint16_t* __restrict__ position, const uint16_t* __restrict__ bias_u, const uint16_t* __restrict__ bias_v,
+    void* __restrict__ output, int value_stride, const uint8_t* __restrict__ packed_key, const float* __restrict__ key_scales,
+    const uint8_t* __restrict__ packed_position, const float* __restrict__ position_scales, int ib, int ie, int chunks) {
+    const int J = (int)blockIdx.x, n = ie - ib;
     if constexpr (kPacked) {
-        __shared__ PackedAttnShared sh;
-        if (!interior)
-            attention_scalar<true>(sh.s, query, key, value_fp8, position, bias_u, bias_v, output, qb, head, rows, padded_rows,
-                                   valid_rows, left, right, value_stride);
-        else
-            attention_packed_tile(sh.p, query, value_fp8, bias_u, bias_v, (uint8_t*)output, qb, head, value_stride, packed_key,
-                                  key_scales, packed_position, position_scales);
+        __shared__ StreamShared sh;
+        const int K = (J & 7) * chunks + (J >> 3);
+        const int run = K >> 3, head = K & 7;
+        const int t0 = ib + (int)((long)n * run / chunks), t1 = ib + (int)((long)n * (run + 1) / chunks);
+        if (t0 < t1)
+            attention_packed_stream(sh, query, value_fp8, bias_u, bias_v, (uint8_t*)output, t0, t1, head, value_stride, packed_key,
+                                    key_scales, packed_position, position_scales);
     } else {
-        __shared__ TcAttnShared sh;
-        if (!interior)
-            attention_scalar<false>(sh.s, query, key, value_fp8, position, bias_u, bias_v, output, qb, head, rows, padded_rows,
-                                    valid_rows, left, right, value_stride);
-        else
-            attention_tc_tile(sh.t, query, key, value_fp8, position, bias_u, bias_v, (uint16_t*)output, qb, head, value_stride);
+        __shared__ TcShared sh;
+        const int K = (J & 7) * n + (J >> 3);
+        attention_tc_tile(sh, query, key, value_fp8, position, bias_u, bias_v, (uint16_t*)output, 16 * (ib + (K >> 3)), K & 7,
+                          value_stride);
     }
 }
 
+// A second stream per device for the boundary kernel, forked from and joined
+// back into the caller's stream with events (the caller's stream order is
+// kept: everything before the call precedes both kernels, everything after
+// follows both).  Created on first use, default priority; the mutex also
+// keeps the record / wait pairs of concurrent callers apart.
+struct SideStream {
+    hipStream_t stream = nullptr;
+    hipEvent_t fork = nullptr, join = nullptr;
+    bool ok = false, tried = false;
+};
+std::mutex g_side_mu;
+SideStream g_side[64];
+
 }  // namespace
+
 
 int launch_pack_vectors(bool int4, const uint16_t* in, uint8_t* out, float* scales, int vectors, hipStream_t s) {
     if (vectors <= 0) return 0;
@@ -650,15 +841,64 @@ int launch_local_attention(bool packed, const uint16_t* query, const uint16_t* k
                            const uint16_t* position, const uint16_t* bias_u, const uint16_t* bias_v, void* output, int rows,
                            int padded_rows, int valid_rows, int left, int right, int value_stride, const uint8_t* packed_key,
                            const float* key_scales, const uint8_t* packed_position, const float* position_scales, hipStream_t s) {
-    const dim3 grid((unsigned)((padded_rows + 15) / 16), kHeads);
-    if (packed)
-        local_attention_kernel<true><<<grid, 256, 0, s>>>(query, key, value_fp8, position, bias_u, bias_v, output, rows, padded_rows,
-                                                          valid_rows, left, right, value_stride, packed_key, key_scales,
-                                                          packed_position, position_scales);
-    else
-        local_attention_kernel<false><<<grid, 256, 0, s>>>(query, key, value_fp8, position, bias_u, bias_v, output, rows,
-                                                           padded_rows, valid_rows, left, right, value_stride, nullptr, nullptr,
-                                                           nullptr, nullptr);
+    // Interior tiles t satisfy 16t >= left, 16t + 15 + right < valid_rows and
+    // 16t + 16 <= rows: a contiguous range [ib, ie).
+    const int tiles = (padded_rows + 15) / 16;
+    const int ib = min((left + 15) / 16, tiles);
+    const int hi = min(valid_rows - 16 - right, rows - 16);  // largest admissible qb
+    const int ie = hi >= 16 * ib ? min(hi / 16 + 1, tiles) : ib;
+    const int n = ie - ib;
+    const int boundary_wgs = 8 * 4 * (ib + (tiles - ie));
+    // Runs of consecutive tiles per head: two resident workgroups per CU
+    // (the rings take 70 KB of LDS) for all eight heads.
+    const int chunks = n > 0 ? max(1, min(n, 2 * cu_count() / 8)) : 1;
+    const int interior_wgs = n > 0 ? 8 * (packed ? chunks : n) : 0;
+
+    auto interior = [&](hipStream_t st) {
+        if (packed)
+            interior_attention_kernel<true><<<interior_wgs, 256, 0, st>>>(query, key, value_fp8, position, bias_u, bias_v, output,
+                                                                          value_stride, packed_key, key_scales, packed_position,
+                                                                          position_scales, ib, ie, chunks);
+        else
+            interior_attention_kernel<false><<<interior_wgs, 256, 0, st>>>(query, key, value_fp8, position, bias_u, bias_v, output,
+                                                                           value_stride, nullptr, nullptr, nullptr, nullptr, ib, ie, 1);
+    };
+    auto boundary = [&](hipStream_t st) {
+        if (packed)
+            boundary_attention_kernel<true><<<boundary_wgs, 256, 0, st>>>(query, key, value_fp8, position, bias_u, bias_v, output, rows,
+                                                                          padded_rows, valid_rows, left, right, value_stride, ib, ie);
+        else
+            boundary_attention_kernel<false><<<boundary_wgs, 256, 0, st>>>(query, key, value_fp8, position, bias_u, bias_v, output,
+                                                                           rows, padded_rows, valid_rows, left, right, value_stride, ib,
+                                                                           ie);
+    };
+    if (interior_wgs == 0 || boundary_wgs == 0) {
+        if (interior_wgs) interior(s);
+        if (boundary_wgs) boundary(s);
+        return 0;
+    }
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = -1;
+    std::lock_guard<std::mutex> lock(g_side_mu);
+    SideStream* side = dev >= 0 ? &g_side[dev] : nullptr;
+    if (side && !side->tried) {
+        side->tried = true;
+        side->ok = hipStreamCreateWithFlags(&side->stream, hipStreamNonBlocking) == hipSuccess &&
+                   hipEventCreateWithFlags(&side->fork, hipEventDisableTiming) == hipSuccess &&
+                   hipEventCreateWithFlags(&side->join, hipEventDisableTiming) == hipSuccess;
+    }
+    // The interior kernel is issued first so that its workgroups take their
+    // LDS before the boundary workgroups fill the space left beside them.
+    if (side && side->ok && hipEventRecord(side->fork, s) == hipSuccess &&
+        hipStreamWaitEvent(side->stream, side->fork, 0) == hipSuccess) {
+        interior(s);
+        boundary(side->stream);
+        if (hipEventRecord(side->join, side->stream) == hipSuccess && hipStreamWaitEvent(s, side->join, 0) == hipSuccess) return 0;
+        hipStreamSynchronize(side->stream);  // could not order the join on the stream: complete it here
+        return 0;
+    }
+    interior(s);
+    boundary(s);
     return 0;
 }
 
