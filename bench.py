@@ -295,57 +295,73 @@ def joint_streaming(pk, torch, stream, copies=512, reps=5):
             "pct_hbm": round(100.0 * gbs / 8000.0, 2)}
 
 
-def attention_bench(pk, torch, stream, frames=45000, reps=20):
-    """Long-form local attention of one encoder layer at T frames (encoder.rs
-    :1839-1968): the INT4 key and INT8 position packers, the feature-major
-    value quantizer (register variant) and both attention kernels, each timed
-    over `reps` launches with HIP events on the launch stream.  Algorithmic
-    bytes per packed launch: q fp16 (2048 B/row), INT4 keys + scales (544
-    B/row), S4 V (512 B/row), e4m3 output (1024 B/row), plus the 8 x 272 packed
-    position vectors and the 4 KB of value scales once; per tc launch: q and
-    k fp16, FP8 V, fp16 output (7168 B/row) plus the fp16 position table.
-    Integer ops of the packed tile path: per 16-query tile and head, 2 x 16 x
-    272 x 128 score MACs and 16 x 320 x 128 context MACs (boundary tiles run
-    the per-query FP32 path and are not counted)."""
+def attention_inputs(torch, frames, seed=77):
     padded = (frames + 15) // 16 * 16
     g = torch.Generator(device="cuda")
-    g.manual_seed(77)
-    q = torch.randn((padded, 1024), generator=g, device="cuda").half()
-    k = torch.randn((padded, 1024), generator=g, device="cuda").half()
-    vt = torch.randn((1024, padded), generator=g, device="cuda").half()
-    pos = torch.randn((8 * 272, 128), generator=g, device="cuda").half()
-    bu = (0.1 * torch.randn(1024, generator=g, device="cuda")).half()
-    bv = (0.1 * torch.randn(1024, generator=g, device="cuda")).half()
+    g.manual_seed(seed)
+    d = {"padded": padded,
+         "q": torch.randn((padded, 1024), generator=g, device="cuda").half(),
+         "k": torch.randn((padded, 1024), generator=g, device="cuda").half(),
+         "vt": torch.randn((1024, padded), generator=g, device="cuda").half(),
+         "pos": torch.randn((8 * 272, 128), generator=g, device="cuda").half(),
+         "bu": (0.1 * torch.randn(1024, generator=g, device="cuda")).half(),
+         "bv": (0.1 * torch.randn(1024, generator=g, device="cuda")).half()}
     el = padded * 1024
-    vf = torch.empty(el + el // 2 + 4096, dtype=torch.uint8, device="cuda")
+    d["vf"] = torch.empty(el + el // 2 + 4096, dtype=torch.uint8, device="cuda")
+    return d
+
+
+def attention_bench(pk, torch, stream, frames=45000, tc_frames=1000, reps=20):
+    """Long-form local attention of one encoder layer (encoder.rs:1839-1968).
+    At T = `frames` (padded to 16): the INT4 key and INT8 position packers,
+    the feature-major value quantizer (register variant) and the packed
+    attention kernel, which the reference runs from padded_rows >= 1040.
+    At T = `tc_frames`: the tc kernel (fp16 scores, e4m3 context), which the
+    reference runs for 512 <= padded_rows < 1040.  Each is timed over `reps`
+    launches with HIP events on the launch stream.  Algorithmic bytes per
+    packed launch: q fp16 (2048 B/row), INT4 keys + scales (544 B/row), S4 V
+    (512 B/row), e4m3 output (1024 B/row), plus the 8 x 272 packed position
+    vectors and the 4 KB of value scales once; per tc launch: q and k fp16,
+    FP8 V, fp16 output (7168 B/row) plus the fp16 position table.  Integer ops
+    of the packed tile path: per 16-query tile and head, 2 x 16 x 272 x 128
+    score MACs and 16 x 320 x 128 context MACs (boundary tiles run the
+    per-query FP32 path and are not counted)."""
+    d = attention_inputs(torch, frames)
+    padded = d["padded"]
+    el = padded * 1024
     pk_key = torch.empty(padded * 512, dtype=torch.uint8, device="cuda")
     k_sc = torch.empty(padded * 8, dtype=torch.float32, device="cuda")
     pk_pos = torch.empty(8 * 272 * 128, dtype=torch.uint8, device="cuda")
     p_sc = torch.empty(8 * 272, dtype=torch.float32, device="cuda")
     out8 = torch.empty((padded, 1024), dtype=torch.uint8, device="cuda")
-    out16 = torch.empty((padded, 1024), dtype=torch.float16, device="cuda")
+    t = attention_inputs(torch, tc_frames, seed=78)
+    out16 = torch.empty((t["padded"], 1024), dtype=torch.float16, device="cuda")
+    pk.call("pk_quantize_value_int4", t["vt"], t["vf"], t["padded"] * 1024, 56.0, stream=stream)
     runs = {
-        "pack_key_int4": lambda: pk.call("pk_pack_key_int4", k, pk_key, k_sc, padded * 8, stream=stream),
-        "pack_score_vectors": lambda: pk.call("pk_pack_score_vectors", pos, pk_pos, p_sc, 8 * 272, stream=stream),
-        "quantize_value_int4": lambda: pk.call("pk_quantize_value_int4_register", vt, vf, el, 56.0, frames, stream=stream),
-        "attention_packed": lambda: pk.call("pk_local_relpos_attention_packed", q, k, None, vf, pos, bu, bv, out8, frames,
-                                            padded, frames, 128, 128, padded, pk_key, k_sc, pk_pos, p_sc, stream=stream),
-        "attention_tc": lambda: pk.call("pk_local_relpos_attention_tc_scores", q, k, None, vf, pos, bu, bv, out16, frames,
-                                        padded, frames, 128, 128, padded, stream=stream),
+        "pack_key_int4": lambda: pk.call("pk_pack_key_int4", d["k"], pk_key, k_sc, padded * 8, stream=stream),
+        "pack_score_vectors": lambda: pk.call("pk_pack_score_vectors", d["pos"], pk_pos, p_sc, 8 * 272, stream=stream),
+        "quantize_value_int4": lambda: pk.call("pk_quantize_value_int4_register", d["vt"], d["vf"], el, 56.0, frames,
+                                               stream=stream),
+        "attention_packed": lambda: pk.call("pk_local_relpos_attention_packed", d["q"], d["k"], None, d["vf"], d["pos"],
+                                            d["bu"], d["bv"], out8, frames, padded, frames, 128, 128, padded, pk_key, k_sc,
+                                            pk_pos, p_sc, stream=stream),
+        "attention_tc": lambda: pk.call("pk_local_relpos_attention_tc_scores", t["q"], t["k"], None, t["vf"], t["pos"],
+                                        t["bu"], t["bv"], out16, tc_frames, t["padded"], tc_frames, 128, 128, t["padded"],
+                                        stream=stream),
     }
     nbytes = {
         "pack_key_int4": padded * (2048 + 512 + 32),
         "pack_score_vectors": 8 * 272 * (256 + 128 + 4),
         "quantize_value_int4": padded * (2048 + 512) + 4096 + 2 * 272 * 1024,
         "attention_packed": padded * (2048 + 544 + 512 + 1024) + 8 * 272 * 132 + 4096,
-        "attention_tc": padded * (2048 + 2048 + 1024 + 2048) + 8 * 272 * 256,
+        "attention_tc": t["padded"] * (2048 + 2048 + 1024 + 2048) + 8 * 272 * 256,
     }
     for f in runs.values():
         f()
     torch.cuda.synchronize()
     interior_tiles = max(0, (frames - 144) // 16 - 7)  # qb in [128, frames - 144]
     ops = 2 * interior_tiles * 8 * (2 * 16 * 272 * 128 + 16 * 320 * 128)
-    out = {"frames": frames}
+    out = {"frames": frames, "tc_frames": tc_frames}
     for name, f in runs.items():
         ms = time_events(torch, f, reps, stream)
         gbs = nbytes[name] / (ms * 1e-3) / 1e9
