@@ -47,6 +47,88 @@ __global__ __launch_bounds__(256) void joint_scores_kernel(const void* __restric
     }
 }
 
+// Streaming form for rows of a whole number of 128-byte lines (the model's
+// 640-wide joint): a workgroup stages relu(enc[t] + pred) once and scores a
+// run of `rows` consecutive rows.  A wave takes 8 rows at a time, 8 lanes per
+// row; load u of lane p reads bytes [128u + 16p, +16) of its row, so each
+// load instruction covers 8 whole lines, and NL = row bytes / 128 loads give
+// the row.  Memory parallelism comes from many small resident workgroups
+// (measured: 32 runs per CU with one row group in flight per wave streams a
+// 344 MB matrix at 6.7 TB/s; deeper per-wave pipelines with fewer workgroups
+// stayed below 6.2).  x is stored with 4 floats of skew per 64 (bank-distinct
+// reads).  kNT marks the weight loads non-temporal, for matrices larger than
+// the caches (one pass); a joint matrix that stays in L2 across frames is
+// loaded normally.
+template <bool kInt8, int NL, bool kNT>
+__global__ __launch_bounds__(256) void joint_stream_kernel(const void* __restrict__ weight, const float* __restrict__ w_scales,
+                                                           const float* __restrict__ bias, const uint16_t* __restrict__ enc,
+                                                           const float* __restrict__ pred, float* __restrict__ scores,
+                                                           int outputs, int enc_stride, int rows) {
+    constexpr int kEl = kInt8 ? 16 : 8;           // elements per 16-byte load
+    constexpr int kHidden = NL * (kInt8 ? 128 : 64);
+    constexpr size_t kRowBytes = (size_t)NL * 128;
+    __shared__ float x[kHidden + kHidden / 16];
+    const int t = blockIdx.y;
+    for (int k = threadIdx.x; k < kHidden; k += 256)
+        x[k + 4 * (k >> 6)] = __builtin_fmaxf(h2f(enc[(size_t)t * enc_stride + k]) + pred[k], 0.0f);
+    __syncthreads();
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int sub = lane >> 3, part = lane & 7;
+    const int row0 = blockIdx.x * rows, row_end = min(row0 + rows, outputs);
+    const uint8_t* wb = (const uint8_t*)weight + 16 * part;
+    auto load = [&](uint4 (&q)[NL], int g) {
+        const int r = min(g + sub, row_end - 1);
+#pragma unroll
+        for (int u = 0; u < NL; ++u) {
+            typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+            const u32x4_t* src = (const u32x4_t*)(wb + (size_t)r * kRowBytes + 128 * u);
+            const u32x4_t v = kNT ? __builtin_nontemporal_load(src) : *src;
+            q[u] = uint4{v.x, v.y, v.z, v.w};
+        }
+    };
+    auto dot = [&](const uint4 (&q)[NL]) -> float {
+        float s = 0.0f;
+#pragma unroll
+        for (int u = 0; u < NL; ++u) {
+            const int k = u * (128 / (kInt8 ? 1 : 2)) + part * kEl;
+            const float4* xv = (const float4*)(x + k + 4 * (k >> 6));
+            const uint32_t wd[4] = {q[u].x, q[u].y, q[u].z, q[u].w};
+#pragma unroll
+            for (int c = 0; c < kEl / 4; ++c) {
+                const float4 xx = xv[c];
+                const float xa[4] = {xx.x, xx.y, xx.z, xx.w};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int e = 4 * c + j;
+                    const float w = kInt8 ? (float)(int8_t)(wd[e >> 2] >> (8 * (e & 3))) : h2f((uint16_t)(wd[e >> 1] >> (16 * (e & 1))));
+                    s = __builtin_fmaf(w, xa[j], s);
+                }
+            }
+        }
+        // the 8 lanes of a row: quad swaps, then the other quad (DPP)
+        s += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, s), 0xb1, 0xf, 0xf, true));
+        s += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, s), 0x4e, 0xf, 0xf, true));
+        return s + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, s), 0x141, 0xf, 0xf, true));
+    };
+    // The next group's loads are issued before this group's score store:
+    // global stores count in vmcnt, so a wait for loads issued after a store
+    // would also wait for the store.
+    int g = row0 + 8 * wave;
+    if (g >= row_end) return;
+    uint4 q[NL];
+    load(q, g);
+    for (;;) {
+        const float sum = dot(q);
+        const int gn = g + 32;
+        if (gn < row_end) load(q, gn);
+        const int r = g + sub;
+        if (part == 0 && r < row_end)
+            scores[(size_t)t * outputs + r] = __builtin_fmaf(kInt8 ? w_scales[r] : 1.0f, sum, bias ? bias[r] : 0.0f);
+        if (gn >= row_end) break;
+        g = gn;
+    }
+}
+
 // decoder.cu:34-46, 728-759: token = argmax over the first token_outputs
 // scores, ties to the lower id; duration = first maximum of the next
 // `durations` scores.
@@ -312,6 +394,34 @@ int launch_joint(const void* w, int w_int8, const float* w_scales, const float* 
                  float* scores, int* decision, int outputs, int hidden, int token_outputs, int durations, int steps,
                  int enc_stride, hipStream_t s) {
     if (steps == 0) return 0;
+    const int nl = w_int8 ? hidden / 128 : hidden / 64;
+    if ((w_int8 ? hidden % 128 : hidden % 64) == 0 && nl >= 1 && nl <= 16) {
+        // Rows per workgroup: 32 for the model's 1030-row joint (enough
+        // workgroups for one frame); a large matrix is split into about 32
+        // runs per CU.
+        const int per = 32 * max(1, (outputs + 32 * 32 * cu_count() - 1) / (32 * 32 * cu_count()));
+        const dim3 grid((outputs + per - 1) / per, steps);
+        const bool nt = (size_t)outputs * hidden * (w_int8 ? 1 : 2) > ((size_t)128 << 20);
+        switch (nl + (w_int8 ? 0 : 100)) {
+#define PK_JS(I8, N)                                                                                                       \
+    case N + (I8 ? 0 : 100):                                                                                               \
+        if (nt)                                                                                                            \
+            joint_stream_kernel<I8, N, true><<<grid, 256, 0, s>>>(w, w_scales, bias, (const uint16_t*)enc, pred, scores,   \
+                                                                  outputs, enc_stride, per);                               \
+        else                                                                                                               \
+            joint_stream_kernel<I8, N, false><<<grid, 256, 0, s>>>(w, w_scales, bias, (const uint16_t*)enc, pred, scores,  \
+                                                                   outputs, enc_stride, per);                              \
+        break;
+            PK_JS(true, 1) PK_JS(true, 2) PK_JS(true, 3) PK_JS(true, 4) PK_JS(true, 5) PK_JS(true, 6) PK_JS(true, 7) PK_JS(true, 8)
+            PK_JS(false, 2) PK_JS(false, 4) PK_JS(false, 6) PK_JS(false, 8) PK_JS(false, 10) PK_JS(false, 12) PK_JS(false, 14)
+            PK_JS(false, 16)
+#undef PK_JS
+            default: goto generic;
+        }
+        if (decision) joint_decide_kernel<<<steps, 256, 0, s>>>(scores, decision, outputs, token_outputs, durations);
+        return 0;
+    }
+generic:
     const dim3 grid((outputs + 3) / 4, steps);
     if (w_int8)
         joint_scores_kernel<true><<<grid, 256, 0, s>>>(w, w_scales, bias, (const uint16_t*)enc, pred, scores, outputs, hidden, enc_stride);
