@@ -580,6 +580,8 @@ def main():
     ap.add_argument("--only-dominant", action="store_true",
                     help="run only the dominant kernel (20 launches) and a 256 MiB device copy, "
                          "for rocprofv3 counter passes")
+    ap.add_argument("--only-joint", action="store_true",
+                    help="run only the HBM-streaming joint GEMV and a 256 MiB device copy, for rocprofv3 passes")
     ap.add_argument("--only-attention", action="store_true",
                     help="run only the attention measurements and a 256 MiB device copy, for rocprofv3 passes")
     args = ap.parse_args()
@@ -595,6 +597,15 @@ def main():
 
     torch.cuda.set_device(0)
     stream = torch.cuda.current_stream()
+    if args.only_joint:
+        res = joint_streaming(pk, torch, stream, reps=20)
+        src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps(res), flush=True)
+        return
     if args.only_attention:
         res = attention_bench(pk, torch, stream, args.frames)
         src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")

@@ -254,31 +254,6 @@ __device__ __forceinline__ uint32_t compress_quartet(uint32_t packed) {
     return d | (md << 16);
 }
 
-// Output stores through a buffer resource: a dead lane's store goes to an
-// offset beyond the resource's size, which the hardware drops, so every lane
-// issues the same number of stores whatever the tile's edges (a wait for
-// loads issued before the epilogue can then count past them).
-typedef uint32_t u32x4v_t __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2v_t __attribute__((ext_vector_type(2)));
-constexpr uint32_t kDeadOff = 0xfffffff0u;
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t out_rsrc(const void* p, size_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, (int)(uint32_t)min(bytes, (size_t)kDeadOff), 0x00020000);
-}
-__device__ __forceinline__ void bstore16(__amdgpu_buffer_rsrc_t r, uint32_t off, uint4 v) {
-    __builtin_amdgcn_raw_buffer_store_b128(u32x4v_t{v.x, v.y, v.z, v.w}, r, (int)off, 0, 0);
-}
-__device__ __forceinline__ void bstore8(__amdgpu_buffer_rsrc_t r, uint32_t off, uint2 v) {
-    __builtin_amdgcn_raw_buffer_store_b64(u32x2v_t{v.x, v.y}, r, (int)off, 0, 0);
-}
-__device__ __forceinline__ void bstore2(__amdgpu_buffer_rsrc_t r, uint32_t off, uint16_t v) {
-    __builtin_amdgcn_raw_buffer_store_b16(v, r, (int)off, 0, 0);
-}
-// Global stores one register epilogue issues per lane.
-template <int E>
-constexpr int epilogue_stores() {
-    return E == EPI_F8 ? 8 : (E == EPI_F16 || E == EPI_F16_RES || E == EPI_F8_24) ? 16 : 32;
-}
-
 // Epilogue straight from the accumulators: for each of its 8 row blocks a
 // lane finishes columns [gcol, gcol + 16) of one row (16 contiguous outputs,
 // one to four 16-byte stores).  Column scales / bias and the 8 row scales are
@@ -313,9 +288,6 @@ __device__ __forceinline__ void epilogue(const GemmArgs& p, v4f (&accf)[8][4], v
     // Without a residual the loads read the (same-shaped) output instead and
     // a select discards them, keeping the block loop free of branches.
     const uint16_t* res_src = p.residual ? p.residual : (const uint16_t*)p.out;
-    constexpr size_t kOutBytes = E == EPI_F8 ? 1 : (E == EPI_F16 ? 2 : 4);
-    const __amdgpu_buffer_rsrc_t ors =
-        E == EPI_F8_24 ? out_rsrc(p.out, (size_t)p.m * (p.ldo / 2)) : out_rsrc(p.out, (size_t)p.m * p.ldo * kOutBytes);
     const bool has_res = kRes && p.residual != nullptr;
     uint4 rn0 = {0, 0, 0, 0}, rn1 = {0, 0, 0, 0};
     if constexpr (E == EPI_F16 && kRes) {
@@ -329,11 +301,11 @@ __device__ __forceinline__ void epilogue(const GemmArgs& p, v4f (&accf)[8][4], v
         const bool live = grow < p.m && col_live;
         float v[16];
         if constexpr (E == EPI_I32) {
-            const uint32_t off = live ? (uint32_t)(((size_t)grow * p.ldo + gcol) * 4) : kDeadOff;
+            if (live) {
+                int4* o = (int4*)((int32_t*)p.out + (size_t)grow * p.ldo + gcol);
 #pragma unroll
-            for (int bj = 0; bj < 4; ++bj)
-                bstore16(ors, live ? off + 16 * bj : kDeadOff,
-                         uint4{(uint32_t)acci[ai][bj][0], (uint32_t)acci[ai][bj][1], (uint32_t)acci[ai][bj][2], (uint32_t)acci[ai][bj][3]});
+                for (int bj = 0; bj < 4; ++bj) o[bj] = int4{acci[ai][bj][0], acci[ai][bj][1], acci[ai][bj][2], acci[ai][bj][3]};
+            }
             continue;
         } else {
 #pragma unroll
@@ -350,12 +322,11 @@ __device__ __forceinline__ void epilogue(const GemmArgs& p, v4f (&accf)[8][4], v
             for (int j = 0; j < 16; ++j) v[j] = __builtin_fmaf(v[j] * rs, wsv[j], bsv[j]);
         }
         if constexpr (E == EPI_F32) {
-            const uint32_t off = live ? (uint32_t)(((size_t)grow * p.ldo + gcol) * 4) : kDeadOff;
+            if (live) {
+                float4* o = (float4*)((float*)p.out + (size_t)grow * p.ldo + gcol);
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                bstore16(ors, live ? off + 16 * j : kDeadOff,
-                         uint4{__builtin_bit_cast(uint32_t, v[4 * j]), __builtin_bit_cast(uint32_t, v[4 * j + 1]),
-                               __builtin_bit_cast(uint32_t, v[4 * j + 2]), __builtin_bit_cast(uint32_t, v[4 * j + 3])});
+                for (int j = 0; j < 4; ++j) o[j] = float4{v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]};
+            }
         } else if constexpr (E == EPI_F16) {
             const uint4 r0 = rn0, r1 = rn1;
             if (kRes && ai + 1 < 8) {
@@ -374,24 +345,27 @@ __device__ __forceinline__ void epilogue(const GemmArgs& p, v4f (&accf)[8][4], v
                 x1 = p.act == 1 ? silu(x1) : (p.act == 2 ? __builtin_fmaxf(x1, 0.0f) : x1);
                 h[j] = (uint32_t)f2h(x0) | ((uint32_t)f2h(x1) << 16);
             }
-            const uint32_t off = live ? (uint32_t)(((size_t)grow * p.ldo + gcol) * 2) : kDeadOff;
-            bstore16(ors, off, uint4{h[0], h[1], h[2], h[3]});
-            bstore16(ors, live ? off + 16 : kDeadOff, uint4{h[4], h[5], h[6], h[7]});
+            if (live) {
+                uint4* o = (uint4*)((uint16_t*)p.out + (size_t)grow * p.ldo + gcol);
+                o[0] = uint4{h[0], h[1], h[2], h[3]};
+                o[1] = uint4{h[4], h[5], h[6], h[7]};
+            }
         } else {  // EPI_F8, EPI_F8_24
             uint32_t w[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j) w[j] = silu_fp8x4(v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]);
             if constexpr (E == EPI_F8) {
-                bstore16(ors, live ? (uint32_t)((size_t)grow * p.ldo + gcol) : kDeadOff, uint4{w[0], w[1], w[2], w[3]});
+                if (live) *(uint4*)((uint8_t*)p.out + (size_t)grow * p.ldo + gcol) = uint4{w[0], w[1], w[2], w[3]};
             } else {
                 uint32_t c[4];
 #pragma unroll
                 for (int j = 0; j < 4; ++j) c[j] = compress_quartet(w[j]);
-                const uint32_t d0 = (c[0] & 0xffff) | (c[1] << 16), d1 = (c[2] & 0xffff) | (c[3] << 16);
-                const uint32_t meta = (c[0] >> 16) | ((c[1] >> 16) << 4) | ((c[2] >> 16) << 8) | ((c[3] >> 16) << 12);
-                const __amdgpu_buffer_rsrc_t mrs = out_rsrc(p.out_meta, (size_t)p.m * (p.ldo / 8));
-                bstore8(ors, live ? (uint32_t)((size_t)grow * (p.ldo / 2) + gcol / 2) : kDeadOff, uint2{d0, d1});
-                bstore2(mrs, live ? (uint32_t)((size_t)grow * (p.ldo / 8) + gcol / 8) : kDeadOff, (uint16_t)meta);
+                if (live) {
+                    const uint32_t d0 = (c[0] & 0xffff) | (c[1] << 16), d1 = (c[2] & 0xffff) | (c[3] << 16);
+                    const uint32_t meta = (c[0] >> 16) | ((c[1] >> 16) << 4) | ((c[2] >> 16) << 8) | ((c[3] >> 16) << 12);
+                    *(uint2*)((uint8_t*)p.out + (size_t)grow * (p.ldo / 2) + gcol / 2) = uint2{d0, d1};
+                    *(uint16_t*)(p.out_meta + (size_t)grow * (p.ldo / 8) + gcol / 8) = (uint16_t)meta;
+                }
             }
         }
     }

@@ -185,7 +185,6 @@ __global__ __launch_bounds__(kThreads, 2) void gemm3_kernel(GemmArgs p) {
     v4i acci[8][4];
     uint32_t skipped = 0, blocks = 0;
 
-    bool first_tile = true;
     while (true) {
         const int t_next = t + G;
         const int cur_m0 = m0, cur_n0 = n0;
@@ -198,15 +197,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm3_kernel(GemmArgs p) {
             }
 
         for (int step = 0; step < steps; ++step) {
-            // The first step of a tile after an epilogue: its operands were
-            // requested before the epilogue's S stores (a fixed count, see
-            // epilogue_stores), which need not complete.
-            if (step == 0 && !first_tile) {
-                constexpr int S = epilogue_stores<E == EPI_F16_RES ? EPI_F16 : E>();
-                asm volatile("s_waitcnt vmcnt(%0)" ::"n"(S) : "memory");
-            } else {
-                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-            }
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
             __syncthreads();
             // The next step's (or next tile's first step's) activations load
             // into the other buffer, which every wave finished with last step.
@@ -278,7 +269,6 @@ __global__ __launch_bounds__(kThreads, 2) void gemm3_kernel(GemmArgs p) {
         else epilogue<F, E, false>(p, accf, acci, cur_m0, cur_n0, wm, wn, lane);
         if (t_next >= ntiles) break;
         t = t_next;
-        first_tile = false;
     }
     if constexpr (F == FMT_I8_SKIP) {
         if (p.skip_count && lane == 0) {
