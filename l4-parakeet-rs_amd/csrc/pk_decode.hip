@@ -131,6 +131,24 @@ __global__ __launch_bounds__(kDecThreads, 1) void tdt_decode_kernel(DecodeArgs p
         wjb[r] = p.b_joint[row];
     }
 
+    // Encoder rows of the frames the next joint step can land on (frame + d,
+    // d < durations, which also covers the max-symbols advance of one frame),
+    // loaded while the joint's barrier polls, so the step after a decision
+    // does not wait for its row.  pf_base = frame of candidate 0 (-1: none).
+    uint32_t cand[8][KP];
+    int pf_base = -1;
+    bool do_pf = false;
+    auto prefetch = [&]() {
+#pragma unroll
+        for (int d = 0; d < 8; ++d) {
+            const int f = pf_base + d;
+            const bool ok = d < D && f < p.frames;
+            const uint16_t* e = p.enc + (size_t)(ok ? f : 0) * p.enc_stride + 2 * lane;
+#pragma unroll
+            for (int j = 0; j < KP; ++j) cand[d][j] = ok ? *(const uint32_t*)(e + 128 * j) : 0u;
+        }
+    };
+
     // ---- grid barrier: publish this workgroup's word, wait for every tag ---------
     uint32_t epoch = 0;
     bool failed = false;
@@ -141,6 +159,8 @@ __global__ __launch_bounds__(kDecThreads, 1) void tdt_decode_kernel(DecodeArgs p
         const uint32_t tag = (epoch + 1) & 0x1fffu;
         unsigned long long* slot = words + (epoch & 1) * kDecMaxBlocks;
         if (tid == 0) __hip_atomic_store(slot + blk, payload | tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (do_pf) prefetch();  // in flight during the poll
+        do_pf = false;
         unsigned long long mine = 0;
         uint32_t spins = 0;
         while (true) {
@@ -248,10 +268,24 @@ __global__ __launch_bounds__(kDecThreads, 1) void tdt_decode_kernel(DecodeArgs p
             float bs = -__builtin_huge_valf();
             int bi = 0x7fffffff;
             float x[2 * KP];
-            const uint16_t* e = p.enc + (size_t)frame * p.enc_stride + 2 * lane;
+            uint32_t evs[KP];
+            const int sel = frame - pf_base;
+            if (pf_base >= 0 && sel >= 0 && sel < D) {
+#pragma unroll
+                for (int j = 0; j < KP; ++j) {
+                    uint32_t v = cand[0][j];
+#pragma unroll
+                    for (int d = 1; d < 8; ++d) v = sel == d ? cand[d][j] : v;
+                    evs[j] = v;
+                }
+            } else {
+                const uint16_t* e = p.enc + (size_t)frame * p.enc_stride + 2 * lane;
+#pragma unroll
+                for (int j = 0; j < KP; ++j) evs[j] = *(const uint32_t*)(e + 128 * j);
+            }
 #pragma unroll
             for (int j = 0; j < KP; ++j) {
-                const uint32_t ev = *(const uint32_t*)(e + 128 * j);
+                const uint32_t ev = evs[j];
                 x[2 * j] = __builtin_fmaxf(lo16(ev) + pv[2 * j], 0.0f);
                 x[2 * j + 1] = __builtin_fmaxf(hi16(ev) + pv[2 * j + 1], 0.0f);
             }
@@ -296,6 +330,8 @@ __global__ __launch_bounds__(kDecThreads, 1) void tdt_decode_kernel(DecodeArgs p
             payload_s = b;
         }
         __syncthreads();
+        pf_base = frame;
+        do_pf = true;
         const unsigned long long word = barrier(payload_s);
         if (failed) break;
         // decision: the largest word is the best token; workgroup 0's carries the duration
