@@ -231,10 +231,14 @@ def joint_bench(pk, torch, stream, reps=2000):
 
 def decode_bench(pk, torch, stream, frames=45000):
     """BASELINE configs[4]'s decoder: batch-1 greedy TDT decode of T frames in
-    one persistent launch (2-layer LSTM, 640 hidden, fp16 weights; INT8 joint
-    640 -> 1030), synthetic random weights and encoder rows, the joint bias
-    favouring the blank and duration 1 so tokens come about every 5 frames,
-    roughly the rate of speech at 80 ms per frame."""
+    one persistent launch (2-layer LSTM, 640 hidden; INT8 joint 640 -> 1030),
+    synthetic random weights and encoder rows, the joint bias favouring the
+    blank and duration 1 so tokens come about every 5 frames, roughly the rate
+    of speech at 80 ms per frame.  The headline figure is the form the
+    reference runs for T >= 1024 (decoder.rs:86-92): the long-request
+    prediction network (INT8 recurrent weights derived in the launch, layer-0
+    input table derived per request by the fp16 linear, both inside the timed
+    region); the fp16 form is timed beside it."""
     H, T, D = 640, 1025, 5
     g = torch.Generator(device="cuda")
     g.manual_seed(21)
@@ -258,17 +262,29 @@ def decode_bench(pk, torch, stream, frames=45000):
     wbytes = pk.lib.pk_tdt_decode_workspace_bytes(H)
     work = torch.empty(wbytes // 4, dtype=torch.int32, device="cuda")
 
-    def run(n):
+    table = torch.empty((T - 1, 4 * H), dtype=torch.float16, device="cuda")
+
+    def run_fp16(n):
         pk.call("pk_tdt_decode", enc, n, H, emb, *lstm, w_proj, b_proj, wj, 1, sj, bj, H, T, D, 10, toks, cap, res,
                 work, wbytes, stream=stream)
 
-    run(256)
-    ms = time_events(torch, lambda: run(frames), 1, stream)
-    count, frame, status, steps = (int(v) for v in res.cpu().tolist())
+    def run_long(n):
+        pk.launch_decode(enc, n, [emb] + lstm, (w_proj, b_proj), (wj, bj), toks, res, work, input_table=table,
+                         joint_int8=True, joint_scales=sj, hidden=H, token_outputs=T, durations=D, stream=stream)
+
     audio_min = frames * 0.08 / 60.0
-    return {"frames": frames, "tokens": count, "joint_steps": steps, "status": status, "ms": round(ms, 2),
-            "us_per_joint_step": round(1e3 * ms / max(steps, 1), 3), "ms_per_audio_min": round(ms / audio_min, 4),
-            "note": "one persistent launch; every weight register-resident; LSTM fp16, joint INT8"}
+    out = {}
+    for name, run in (("long", run_long), ("fp16", run_fp16)):
+        run(1024 if name == "long" else 256)
+        ms = time_events(torch, lambda: run(frames), 1, stream)
+        count, frame, status, steps = (int(v) for v in res.cpu().tolist())
+        out[name] = {"tokens": count, "joint_steps": steps, "status": status, "ms": round(ms, 2),
+                     "us_per_joint_step": round(1e3 * ms / max(steps, 1), 3),
+                     "ms_per_audio_min": round(ms / audio_min, 4)}
+    res_long = out.pop("long")
+    return dict({"frames": frames}, **res_long, fp16_form=out["fp16"],
+                note="one persistent launch, weights register-resident; long form (INT8 W_hh0/W_hh1/W_ih1 + "
+                     "input table, joint INT8), the reference's choice for T >= 1024; fp16_form = fp16 LSTM")
 
 
 def joint_streaming(pk, torch, stream, copies=512, reps=5):
@@ -584,6 +600,7 @@ def main():
                     help="run only the HBM-streaming joint GEMV and a 256 MiB device copy, for rocprofv3 passes")
     ap.add_argument("--only-attention", action="store_true",
                     help="run only the attention measurements and a 256 MiB device copy, for rocprofv3 passes")
+    ap.add_argument("--only-decode", action="store_true", help="run only the TDT decode measurements")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -605,6 +622,9 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps(res), flush=True)
+        return
+    if args.only_decode:
+        print(json.dumps(decode_bench(pk, torch, stream, args.frames)), flush=True)
         return
     if args.only_attention:
         res = attention_bench(pk, torch, stream, args.frames)

@@ -380,6 +380,27 @@ int32_t pk_tdt_decode(const uint16_t* enc, int32_t frames, int32_t enc_stride, c
                       const float* joint_scales, const float* b_joint, int32_t hidden, int32_t token_outputs,
                       int32_t durations, int32_t max_symbols, int32_t* tokens, int32_t capacity, int32_t* result,
                       void* workspace, uint64_t workspace_bytes, void* stream);
+/* decoder.cu:452-784 tdt_persistent_fp8 (kernel pk_sm89_tdt_persistent_fp8_ih,
+ * decoder.cu:805-824; chosen by decoder.rs:86-92 for frames >= 1024): the same
+ * decode with the long-request prediction network.  Inside the launch, W_hh0,
+ * W_hh1 and W_ih1 become per-tensor symmetric INT8 (scale = max|w| / 127, 1 for
+ * an all-zero matrix; q = clamp(rint(w / scale), +-127)); hidden states are
+ * also carried as INT8 at scale 1/127 (clamp(rint(127 h))), which feed the
+ * recurrent and layer-1 input products; gate = int dot * scale / 127 + b_ih + b_hh
+ * (+ layer 0's input_table[token][gate row], fp16, zero before the first
+ * token).  input_table = [token_outputs - 1 x 4H] fp16, embedding x W_ih0^T, as
+ * decoder.rs:355-377 derives it per request with the fp16 linear
+ * (pk_linear_fp16_epilogue, m = tokens, n = 4H, k = H, no bias, scale 1).
+ * Cell states, the layer-1 output feeding the projection and the projection
+ * are fp32; projection and joint as pk_tdt_decode.  Workspace as
+ * pk_tdt_decode_workspace_bytes; W_hh0, W_hh1, W_ih1 16-byte aligned. */
+int32_t pk_tdt_decode_long(const uint16_t* enc, int32_t frames, int32_t enc_stride, const uint16_t* input_table,
+                           const uint16_t* w_hh0, const float* b_ih0, const float* b_hh0, const uint16_t* w_ih1,
+                           const uint16_t* w_hh1, const float* b_ih1, const float* b_hh1, const uint16_t* w_proj,
+                           const float* b_proj, const void* w_joint, int32_t joint_int8, const float* joint_scales,
+                           const float* b_joint, int32_t hidden, int32_t token_outputs, int32_t durations,
+                           int32_t max_symbols, int32_t* tokens, int32_t capacity, int32_t* result, void* workspace,
+                           uint64_t workspace_bytes, void* stream);
 
 /* ---- long-form local relative-position attention (encoder.cu:1476-2097) ----
  * Model constants: width 1024 = 8 heads x 128, window 128 left / 128 right,

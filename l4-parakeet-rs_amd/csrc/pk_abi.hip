@@ -465,20 +465,21 @@ int32_t pk_joint_scan(const void* w, int32_t w_int8, const float* w_scales, cons
 
 int32_t pk_tdt_decode_workspace_bytes(int32_t hidden) { return hidden > 0 ? 4 * decode_workspace_words(hidden) : PK_E_SHAPE; }
 
-int32_t pk_tdt_decode(const uint16_t* enc, int32_t frames, int32_t enc_stride, const uint16_t* embedding,
-                      const uint16_t* w_ih0, const uint16_t* w_hh0, const float* b_ih0, const float* b_hh0,
-                      const uint16_t* w_ih1, const uint16_t* w_hh1, const float* b_ih1, const float* b_hh1,
-                      const uint16_t* w_proj, const float* b_proj, const void* w_joint, int32_t joint_int8,
-                      const float* joint_scales, const float* b_joint, int32_t hidden, int32_t token_outputs,
-                      int32_t durations, int32_t max_symbols, int32_t* tokens, int32_t capacity, int32_t* result,
-                      void* workspace, uint64_t workspace_bytes, void* stream) {
+static int32_t tdt_decode(bool long_form, const uint16_t* enc, int32_t frames, int32_t enc_stride, const uint16_t* embedding,
+                          const uint16_t* table, const uint16_t* w_ih0, const uint16_t* w_hh0, const float* b_ih0,
+                          const float* b_hh0, const uint16_t* w_ih1, const uint16_t* w_hh1, const float* b_ih1,
+                          const float* b_hh1, const uint16_t* w_proj, const float* b_proj, const void* w_joint,
+                          int32_t joint_int8, const float* joint_scales, const float* b_joint, int32_t hidden,
+                          int32_t token_outputs, int32_t durations, int32_t max_symbols, int32_t* tokens, int32_t capacity,
+                          int32_t* result, void* workspace, uint64_t workspace_bytes, void* stream) {
     if (frames < 0 || hidden <= 0 || hidden > 1024 || hidden % 128 || enc_stride < hidden || token_outputs <= 1 ||
         token_outputs > 65535 || durations <= 0 || durations > 8 || max_symbols <= 0 || capacity < 0) {
         set_error("invalid decode shape frames=%d hidden=%d stride=%d tokens=%d durations=%d max_symbols=%d", frames, hidden,
                   enc_stride, token_outputs, durations, max_symbols);
         return PK_E_SHAPE;
     }
-    if (!need(enc, "enc") || !need(embedding, "embedding") || !need(w_ih0, "w_ih0") || !need(w_hh0, "w_hh0") ||
+    if (!need(enc, "enc") || (long_form ? !need(table, "input_table") : (!need(embedding, "embedding") || !need(w_ih0, "w_ih0"))) ||
+        !need(w_hh0, "w_hh0") ||
         !need(b_ih0, "b_ih0") || !need(b_hh0, "b_hh0") || !need(w_ih1, "w_ih1") || !need(w_hh1, "w_hh1") ||
         !need(b_ih1, "b_ih1") || !need(b_hh1, "b_hh1") || !need(w_proj, "w_proj") || !need(b_proj, "b_proj") ||
         !need(w_joint, "w_joint") || !need(b_joint, "b_joint") || !need(result, "result") || !need(workspace, "workspace") ||
@@ -490,19 +491,45 @@ int32_t pk_tdt_decode(const uint16_t* enc, int32_t frames, int32_t enc_stride, c
         return PK_E_SHAPE;
     }
     if (((uintptr_t)enc | (uintptr_t)embedding | (uintptr_t)w_ih0 | (uintptr_t)w_hh0 | (uintptr_t)w_ih1 | (uintptr_t)w_hh1 |
-         (uintptr_t)w_proj | (uintptr_t)w_joint | (uintptr_t)workspace) & 7 || enc_stride % 2) {
-        set_error("decode weights, enc and workspace must be 8-byte aligned, enc_stride even");
+         (uintptr_t)w_proj | (uintptr_t)w_joint | (uintptr_t)workspace) & 7 || enc_stride % 2 ||
+        (long_form && ((uintptr_t)w_hh0 | (uintptr_t)w_hh1 | (uintptr_t)w_ih1) & 15)) {
+        set_error("decode weights, enc and workspace must be 8-byte aligned (long form: W_hh0, W_hh1, W_ih1 16-byte), "
+                  "enc_stride even");
         return PK_E_ALIGN;
     }
     const uint16_t* w_ih[2] = {w_ih0, w_ih1};
     const uint16_t* w_hh[2] = {w_hh0, w_hh1};
     const float* b_ih[2] = {b_ih0, b_ih1};
     const float* b_hh[2] = {b_hh0, b_hh1};
-    const int st = launch_tdt_decode(enc, frames, enc_stride, embedding, w_ih, w_hh, b_ih, b_hh, w_proj, b_proj, w_joint, joint_int8,
-                                     joint_scales, b_joint, hidden, token_outputs, durations, max_symbols, tokens, capacity, result,
-                                     (uint32_t*)workspace, STREAM);
+    const int st = launch_tdt_decode(enc, frames, enc_stride, long_form ? nullptr : embedding, long_form ? table : nullptr, w_ih, w_hh,
+                                     b_ih, b_hh, w_proj, b_proj, w_joint, joint_int8, joint_scales, b_joint, hidden, token_outputs,
+                                     durations, max_symbols, tokens, capacity, result, (uint32_t*)workspace, STREAM);
     if (st != 0) return PK_E_SHAPE;
-    return check_launch("tdt_decode");
+    return check_launch(long_form ? "tdt_decode_long" : "tdt_decode");
+}
+
+int32_t pk_tdt_decode(const uint16_t* enc, int32_t frames, int32_t enc_stride, const uint16_t* embedding,
+                      const uint16_t* w_ih0, const uint16_t* w_hh0, const float* b_ih0, const float* b_hh0,
+                      const uint16_t* w_ih1, const uint16_t* w_hh1, const float* b_ih1, const float* b_hh1,
+                      const uint16_t* w_proj, const float* b_proj, const void* w_joint, int32_t joint_int8,
+                      const float* joint_scales, const float* b_joint, int32_t hidden, int32_t token_outputs,
+                      int32_t durations, int32_t max_symbols, int32_t* tokens, int32_t capacity, int32_t* result,
+                      void* workspace, uint64_t workspace_bytes, void* stream) {
+    return tdt_decode(false, enc, frames, enc_stride, embedding, nullptr, w_ih0, w_hh0, b_ih0, b_hh0, w_ih1, w_hh1, b_ih1, b_hh1,
+                      w_proj, b_proj, w_joint, joint_int8, joint_scales, b_joint, hidden, token_outputs, durations, max_symbols,
+                      tokens, capacity, result, workspace, workspace_bytes, stream);
+}
+
+int32_t pk_tdt_decode_long(const uint16_t* enc, int32_t frames, int32_t enc_stride, const uint16_t* input_table,
+                           const uint16_t* w_hh0, const float* b_ih0, const float* b_hh0, const uint16_t* w_ih1,
+                           const uint16_t* w_hh1, const float* b_ih1, const float* b_hh1, const uint16_t* w_proj,
+                           const float* b_proj, const void* w_joint, int32_t joint_int8, const float* joint_scales,
+                           const float* b_joint, int32_t hidden, int32_t token_outputs, int32_t durations,
+                           int32_t max_symbols, int32_t* tokens, int32_t capacity, int32_t* result, void* workspace,
+                           uint64_t workspace_bytes, void* stream) {
+    return tdt_decode(true, enc, frames, enc_stride, nullptr, input_table, nullptr, w_hh0, b_ih0, b_hh0, w_ih1, w_hh1, b_ih1,
+                      b_hh1, w_proj, b_proj, w_joint, joint_int8, joint_scales, b_joint, hidden, token_outputs, durations,
+                      max_symbols, tokens, capacity, result, workspace, workspace_bytes, stream);
 }
 
 // ---- local attention and its producers ---------------------------------------

@@ -1,7 +1,15 @@
-// Batch-1 greedy TDT decode in one persistent launch (decoder.cu:146-445,
-// the fp16 prediction-network path): 2-layer LSTM prediction network (gate
-// rows i, f, g, o of 4H), projection + bias, joint, token / duration decision
-// and the frame / symbol rules, for all frames of one utterance.
+// Batch-1 greedy TDT decode in one persistent launch: 2-layer LSTM prediction
+// network (gate rows i, f, g, o of 4H), projection + bias, joint, token /
+// duration decision and the frame / symbol rules, for all frames of one
+// utterance.  Two prediction-network forms, as in the reference:
+//  - fp16 (decoder.cu:146-445, tdt_persistent_fp16): fp16 weights, fp32 state;
+//  - long (decoder.cu:452-784, tdt_persistent_fp8, used for utterances of
+//    1024 frames and more, decoder.rs:15,86-92): W_hh of both layers and W_ih
+//    of layer 1 as per-tensor symmetric INT8 derived inside the launch
+//    (scale = max|w| / 127), hidden states carried as INT8 at a fixed 1/127
+//    scale next to the fp32 ones, layer 0's input terms read from a
+//    [tokens x 4H] fp16 table (embedding x W_ih0^T), and the recurrent terms of
+//    the state the next update consumes summed as soon as that state exists.
 //
 // Every weight stays in registers for the whole decode: the grid is one
 // workgroup per CU (up to 256, 4 wave64 each) and wave w owns LSTM hidden unit
@@ -17,6 +25,15 @@
 // prediction) move through agent-scope atomic stores and loads in a caller
 // workspace.  Blank steps run only the joint; an emitted token commits the
 // candidate state and re-runs the prediction network on its embedding.
+//
+// Long form: lane l holds bytes 4l + 256j (j < ceil(H/256)) of every INT8
+// row; a gate's INT8 dot product is summed exactly as an integer over the
+// wave (|sum| <= H * 127 * 127 < 2^24), converted once and scaled by
+// scale / 127.  The cell state stays in the owning wave's registers; the INT8
+// hidden vectors (candidate / committed banks), the candidate fp32 layer-1
+// output and the prediction go through the workspace.  The recurrent sums of
+// both layers are taken in the projection phase, from the candidate state
+// that the next update will consume once a token commits it.
 #include "pk_kernels.hpp"
 
 namespace pk {
@@ -31,8 +48,9 @@ constexpr int kDecState = kDecWords + 2 * kDecMaxBlocks * 2;  // u32 offset of t
 static_assert(kDecState == 1032, "workspace layout");
 
 struct DecodeArgs {
-    const uint16_t* enc;  // [frames x enc_stride] fp16
-    const uint16_t* emb;  // [token_outputs - 1 x H] fp16
+    const uint16_t* enc;    // [frames x enc_stride] fp16
+    const uint16_t* emb;    // [token_outputs - 1 x H] fp16 (fp16 form)
+    const uint16_t* table;  // [token_outputs - 1 x 4H] fp16 layer-0 input terms (long form)
     const uint16_t* w_ih[2];
     const uint16_t* w_hh[2];
     const float* b_ih[2];
@@ -68,15 +86,72 @@ __device__ __forceinline__ float wave_sum(float v) {
     for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
     return v;
 }
+__device__ __forceinline__ int wave_isum(int v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = __builtin_fmaxf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
+// decoder.cu:95-97 quantize_i8: round to nearest even, clamp to +-127.
+__device__ __forceinline__ int quant_i8(float v) { return max(-127, min(127, (int)__builtin_rintf(v))); }
+
+// exp(x) from IEEE basic operations only, so that the long form's cell (whose
+// outputs are rounded to INT8) is reproduced bit for bit by a CPU evaluating
+// the same operations: Cody-Waite reduction x = n ln2 + r (ln2 split into a
+// 16-bit head, so n * head is exact, and a tail), e^r by its degree-7 Taylor
+// polynomial (|r| <= 0.347: truncation error 5e-9 relative), times 2^n.
+// Within 0.82 ulp of exp over [-87, 88]; expf / tanhf of the reference are
+// within about an ulp too.
+__device__ __forceinline__ float det_exp(float x) {
+    if (x != x) return x;
+    x = __builtin_fminf(__builtin_fmaxf(x, -104.0f), 89.0f);
+    const float n = __builtin_rintf(x * 1.44269504f);
+    float r = __builtin_fmaf(n, -0.693145751953125f, x);
+    r = __builtin_fmaf(n, -1.428606765330187e-06f, r);
+    float q = 1.98412698e-04f;
+    q = __builtin_fmaf(q, r, 1.38888889e-03f);
+    q = __builtin_fmaf(q, r, 8.33333333e-03f);
+    q = __builtin_fmaf(q, r, 4.16666667e-02f);
+    q = __builtin_fmaf(q, r, 1.66666667e-01f);
+    q = __builtin_fmaf(q, r, 0.5f);
+    q = __builtin_fmaf(q, r, 1.0f);
+    q = __builtin_fmaf(q, r, 1.0f);
+    return __builtin_ldexpf(q, (int)n);
+}
+__device__ __forceinline__ float det_sigmoid(float v) { return 1.0f / (1.0f + det_exp(-v)); }
+// tanh(x) = sign(x) (1 - e^-2|x|) / (1 + e^-2|x|): absolute error ~1e-7.
+__device__ __forceinline__ float det_tanh(float v) {
+    const float t = det_exp(-2.0f * __builtin_fabsf(v));
+    return __builtin_copysignf((1.0f - t) / (1.0f + t), v);
+}
+
+// decoder.cu:116-129 lstm_cell with the transcendental functions above; the
+// cell update is fma(f, c, i * g).
+__device__ __forceinline__ void lstm_cell(const float (&s)[4], float c_prev, float& c_out, float& h_out) {
+    const float ig = det_sigmoid(s[0]), fg = det_sigmoid(s[1]), cg = det_tanh(s[2]), og = det_sigmoid(s[3]);
+    c_out = __builtin_fmaf(fg, c_prev, ig * cg);
+    h_out = og * det_tanh(c_out);
+}
+
+__device__ __forceinline__ uint32_t ld_word(const uint32_t* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+__device__ __forceinline__ void st_word(uint32_t* p, uint32_t v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
 
 // fp16 pair -> two floats
 __device__ __forceinline__ float lo16(uint32_t w) { return h2f((uint16_t)(w & 0xffffu)); }
 __device__ __forceinline__ float hi16(uint32_t w) { return h2f((uint16_t)(w >> 16)); }
 
-template <bool kInt8, int KP>
+template <bool kInt8, int KP, bool kLong>
 __global__ __launch_bounds__(kDecThreads, 1) void tdt_decode_kernel(DecodeArgs p) {
     constexpr int H = 128 * KP;
+    constexpr int KD = (KP + 1) / 2;  // INT8 dwords per lane and row (long form)
     __shared__ unsigned long long best_w[4];
+    __shared__ float red_s[12];
+    __shared__ uint32_t qb_s[4];
     __shared__ unsigned long long payload_s;
     __shared__ float dur_sc[8];
     __shared__ int dur_s;
@@ -91,45 +166,12 @@ __global__ __launch_bounds__(kDecThreads, 1) void tdt_decode_kernel(DecodeArgs p
     auto hp = [&](int buf, int layer) { return st + (buf * 2 + layer) * H; };
     auto cp = [&](int buf, int layer) { return st + 4 * H + (buf * 2 + layer) * H; };
     float* pred = st + 8 * H;
-
-    // ---- weights into registers --------------------------------------------------
-    const bool owns_unit = gw < H;
-    const int u = owns_unit ? gw : 0;
-    uint32_t wih[2][4][KP], whh[2][4][KP], wpj[KP];
-    float bias[2][4];
-#pragma unroll
-    for (int l = 0; l < 2; ++l)
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            const size_t row = (size_t)(g * H + u) * H;
-#pragma unroll
-            for (int j = 0; j < KP; ++j) {
-                const int k = 2 * lane + 128 * j;
-                wih[l][g][j] = *(const uint32_t*)(p.w_ih[l] + row + k);
-                whh[l][g][j] = *(const uint32_t*)(p.w_hh[l] + row + k);
-            }
-            bias[l][g] = p.b_ih[l][g * H + u] + p.b_hh[l][g * H + u];
-        }
-#pragma unroll
-    for (int j = 0; j < KP; ++j) wpj[j] = *(const uint32_t*)(p.w_proj + (size_t)u * H + 2 * lane + 128 * j);
-    const float bpj = p.b_proj[u];
-    uint32_t wj[2][KP];
-    float wjs[2], wjb[2];
-    int jid[2];
-#pragma unroll
-    for (int r = 0; r < 2; ++r) {
-        const int i = 2 * gw + r;
-        jid[r] = i < D ? T + i : (i < T + D ? i - D : -1);
-        const int row = jid[r] < 0 ? p.outputs - 1 : jid[r];
-#pragma unroll
-        for (int j = 0; j < KP; ++j) {
-            const int k = 2 * lane + 128 * j;
-            if constexpr (kInt8) wj[r][j] = *(const uint16_t*)((const int8_t*)p.w_joint + (size_t)row * H + k);
-            else wj[r][j] = *(const uint32_t*)((const uint16_t*)p.w_joint + (size_t)row * H + k);
-        }
-        wjs[r] = kInt8 ? p.joint_scales[row] : 1.0f;
-        wjb[r] = p.b_joint[row];
-    }
+    // long form: INT8 hidden vectors [bank][layer][H] bytes, candidate fp32
+    // layer-1 output, per-workgroup weight maxima [blocks][3]
+    uint32_t* qh = p.ws + kDecState;
+    auto qbank = [&](int bank, int layer) { return qh + (bank * 2 + layer) * (H / 4); };
+    float* h1c = st + H;
+    float* maxima = st + 2 * H;
 
     // Encoder rows of the frames the next joint step can land on (frame + d,
     // d < durations, which also covers the max-symbols advance of one frame),
@@ -187,71 +229,261 @@ __global__ __launch_bounds__(kDecThreads, 1) void tdt_decode_kernel(DecodeArgs p
         return mine;  // thread t holds workgroup t's word
     };
 
+    // ---- weights into registers --------------------------------------------------
+    const bool owns_unit = gw < H;
+    const int u = owns_unit ? gw : 0;
+    uint32_t wih[kLong ? 1 : 2][4][KP], whh[kLong ? 1 : 2][4][KP], wpj[KP];
+    // long form: INT8 rows of W_hh0, W_hh1, W_ih1 and their scale / 127
+    uint32_t qw[kLong ? 3 : 1][4][KD];
+    float cq[3] = {1.0f, 1.0f, 1.0f};
+    float bias[2][4];
+#pragma unroll
+    for (int l = 0; l < 2; ++l)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) bias[l][g] = p.b_ih[l][g * H + u] + p.b_hh[l][g * H + u];
+    if constexpr (!kLong) {
+#pragma unroll
+        for (int l = 0; l < 2; ++l)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const size_t row = (size_t)(g * H + u) * H;
+#pragma unroll
+                for (int j = 0; j < KP; ++j) {
+                    const int k = 2 * lane + 128 * j;
+                    wih[l][g][j] = *(const uint32_t*)(p.w_ih[l] + row + k);
+                    whh[l][g][j] = *(const uint32_t*)(p.w_hh[l] + row + k);
+                }
+            }
+    } else {
+        // decoder.cu:520-575: per-tensor maxima over the whole grid, scale =
+        // max / 127 (1 for an all-zero matrix), q = quantize_i8(w / scale).
+        const uint16_t* src[3] = {p.w_hh[0], p.w_hh[1], p.w_ih[1]};
+        const size_t n8 = (size_t)H * H / 2;  // 16-byte chunks of a [4H x H] fp16 matrix
+        const size_t gt = (size_t)blk * kDecThreads + tid, gs = (size_t)nblocks * kDecThreads;
+        float mx[3];
+#pragma unroll
+        for (int m = 0; m < 3; ++m) {
+            float a = 0.0f;
+            for (size_t i = gt; i < n8; i += gs) {
+                const uint4 v = ((const uint4*)src[m])[i];
+                const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    a = __builtin_fmaxf(a, __builtin_fmaxf(__builtin_fabsf(lo16(w4[e])), __builtin_fabsf(hi16(w4[e]))));
+            }
+            mx[m] = wave_max(a);
+        }
+        if (lane == 0)
+#pragma unroll
+            for (int m = 0; m < 3; ++m) red_s[wave * 3 + m] = mx[m];
+        __syncthreads();
+        if (tid == 0)
+#pragma unroll
+            for (int m = 0; m < 3; ++m)
+                st1(maxima + blk * 3 + m, __builtin_fmaxf(__builtin_fmaxf(red_s[m], red_s[3 + m]), __builtin_fmaxf(red_s[6 + m], red_s[9 + m])));
+        barrier(0);
+        float r[3] = {0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int m = 0; m < 3; ++m) {
+            if (tid < nblocks) r[m] = ld1(maxima + tid * 3 + m);
+            r[m] = wave_max(r[m]);
+        }
+        if (lane == 0)
+#pragma unroll
+            for (int m = 0; m < 3; ++m) red_s[wave * 3 + m] = r[m];
+        __syncthreads();
+        float scale[3];
+#pragma unroll
+        for (int m = 0; m < 3; ++m) {
+            const float t = __builtin_fmaxf(__builtin_fmaxf(red_s[m], red_s[3 + m]), __builtin_fmaxf(red_s[6 + m], red_s[9 + m]));
+            scale[m] = t > 0.0f ? t / 127.0f : 1.0f;
+            cq[m] = scale[m] / 127.0f;
+        }
+#pragma unroll
+        for (int m = 0; m < 3; ++m)
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+#pragma unroll
+                for (int j = 0; j < KD; ++j) {
+                    const int k = 4 * lane + 256 * j;
+                    uint32_t word = 0;
+                    if (k < H) {
+                        const uint2 hv = *(const uint2*)(src[m] + (size_t)(g * H + u) * H + k);
+                        word = (uint32_t)(uint8_t)quant_i8(lo16(hv.x) / scale[m]) | ((uint32_t)(uint8_t)quant_i8(hi16(hv.x) / scale[m]) << 8) |
+                               ((uint32_t)(uint8_t)quant_i8(lo16(hv.y) / scale[m]) << 16) |
+                               ((uint32_t)(uint8_t)quant_i8(hi16(hv.y) / scale[m]) << 24);
+                    }
+                    qw[m][g][j] = word;
+                }
+    }
+#pragma unroll
+    for (int j = 0; j < KP; ++j) wpj[j] = *(const uint32_t*)(p.w_proj + (size_t)u * H + 2 * lane + 128 * j);
+    const float bpj = p.b_proj[u];
+    uint32_t wj[2][KP];
+    float wjs[2], wjb[2];
+    int jid[2];
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+        const int i = 2 * gw + r;
+        jid[r] = i < D ? T + i : (i < T + D ? i - D : -1);
+        const int row = jid[r] < 0 ? p.outputs - 1 : jid[r];
+#pragma unroll
+        for (int j = 0; j < KP; ++j) {
+            const int k = 2 * lane + 128 * j;
+            if constexpr (kInt8) wj[r][j] = *(const uint16_t*)((const int8_t*)p.w_joint + (size_t)row * H + k);
+            else wj[r][j] = *(const uint32_t*)((const uint16_t*)p.w_joint + (size_t)row * H + k);
+        }
+        wjs[r] = kInt8 ? p.joint_scales[row] : 1.0f;
+        wjb[r] = p.b_joint[row];
+    }
+
     int frame = 0, symbols = 0, last = blank, count = 0, steps = 0, alt = 0;
     bool emitted = false, valid = false;
     float pv[2 * KP];
+    // long form: integer recurrent sums [layer][gate] of the committed state
+    // (rs) and of the candidate (rs_next); the owning wave's cell states
+    int rs[2][4] = {{0, 0, 0, 0}, {0, 0, 0, 0}}, rs_next[2][4] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
+    float c_cur[2] = {0.0f, 0.0f}, c_new[2] = {0.0f, 0.0f};
     while (frame < p.frames && !failed) {
         if (!valid) {
-            // ---- two LSTM layers on the last token's embedding (zeros before any)
+            if constexpr (!kLong) {
+                // ---- two LSTM layers on the last token's embedding (zeros before any)
 #pragma unroll
-            for (int l = 0; l < 2; ++l) {
+                for (int l = 0; l < 2; ++l) {
+                    if (owns_unit) {
+                        float x[2 * KP], hv[2 * KP];
+#pragma unroll
+                        for (int j = 0; j < KP; ++j) {
+                            const int k = 2 * lane + 128 * j;
+                            if (l == 0) {
+                                if (emitted) {
+                                    const uint32_t e = *(const uint32_t*)(p.emb + (size_t)last * H + k);
+                                    x[2 * j] = lo16(e);
+                                    x[2 * j + 1] = hi16(e);
+                                } else {
+                                    x[2 * j] = x[2 * j + 1] = 0.0f;
+                                }
+                            } else {
+                                const float2 v = ld2(hp(alt ^ 1, 0) + k);  // this update's layer-0 output
+                                x[2 * j] = v.x;
+                                x[2 * j + 1] = v.y;
+                            }
+                            const float2 hh = ld2(hp(alt, l) + k);
+                            hv[2 * j] = hh.x;
+                            hv[2 * j + 1] = hh.y;
+                        }
+                        float s[4];
+#pragma unroll
+                        for (int g = 0; g < 4; ++g) {
+                            float a = 0.0f;
+#pragma unroll
+                            for (int j = 0; j < KP; ++j) {
+                                a = __builtin_fmaf(lo16(wih[l][g][j]), x[2 * j], a);
+                                a = __builtin_fmaf(hi16(wih[l][g][j]), x[2 * j + 1], a);
+                                a = __builtin_fmaf(lo16(whh[l][g][j]), hv[2 * j], a);
+                                a = __builtin_fmaf(hi16(whh[l][g][j]), hv[2 * j + 1], a);
+                            }
+                            s[g] = wave_sum(a) + bias[l][g];
+                        }
+                        if (lane == 0) {
+                            const float ig = sigmoid(s[0]), fg = sigmoid(s[1]), cg = tanhf(s[2]), og = sigmoid(s[3]);
+                            const float cell = fg * ld1(cp(alt, l) + u) + ig * cg;
+                            st1(cp(alt ^ 1, l) + u, cell);
+                            st1(hp(alt ^ 1, l) + u, og * tanhf(cell));
+                        }
+                    }
+                    barrier(0);
+                    if (failed) break;
+                }
+                if (failed) break;
+                // ---- projection of the new layer-1 output
                 if (owns_unit) {
-                    float x[2 * KP], hv[2 * KP];
+                    float a = 0.0f;
 #pragma unroll
                     for (int j = 0; j < KP; ++j) {
-                        const int k = 2 * lane + 128 * j;
-                        if (l == 0) {
-                            if (emitted) {
-                                const uint32_t e = *(const uint32_t*)(p.emb + (size_t)last * H + k);
-                                x[2 * j] = lo16(e);
-                                x[2 * j + 1] = hi16(e);
-                            } else {
-                                x[2 * j] = x[2 * j + 1] = 0.0f;
-                            }
-                        } else {
-                            const float2 v = ld2(hp(alt ^ 1, 0) + k);  // this update's layer-0 output
-                            x[2 * j] = v.x;
-                            x[2 * j + 1] = v.y;
-                        }
-                        const float2 hh = ld2(hp(alt, l) + k);
-                        hv[2 * j] = hh.x;
-                        hv[2 * j + 1] = hh.y;
+                        const float2 v = ld2(hp(alt ^ 1, 1) + 2 * lane + 128 * j);
+                        a = __builtin_fmaf(lo16(wpj[j]), v.x, a);
+                        a = __builtin_fmaf(hi16(wpj[j]), v.y, a);
                     }
+                    a = wave_sum(a) + bpj;
+                    if (lane == 0) st1(pred + u, a);
+                }
+            } else {
+                // ---- layer 0: recurrent sums of the committed state (taken when it
+                // was the candidate) + bias + the token's table row (decoder.cu:619-648)
+                if (owns_unit && lane == 0) {
                     float s[4];
 #pragma unroll
                     for (int g = 0; g < 4; ++g) {
-                        float a = 0.0f;
-#pragma unroll
-                        for (int j = 0; j < KP; ++j) {
-                            a = __builtin_fmaf(lo16(wih[l][g][j]), x[2 * j], a);
-                            a = __builtin_fmaf(hi16(wih[l][g][j]), x[2 * j + 1], a);
-                            a = __builtin_fmaf(lo16(whh[l][g][j]), hv[2 * j], a);
-                            a = __builtin_fmaf(hi16(whh[l][g][j]), hv[2 * j + 1], a);
-                        }
-                        s[g] = wave_sum(a) + bias[l][g];
+                        const float tv = emitted ? h2f(p.table[(size_t)last * 4 * H + g * H + u]) : 0.0f;
+                        s[g] = __builtin_fmaf((float)rs[0][g], cq[0], bias[0][g]) + tv;
                     }
-                    if (lane == 0) {
-                        const float ig = sigmoid(s[0]), fg = sigmoid(s[1]), cg = tanhf(s[2]), og = sigmoid(s[3]);
-                        const float cell = fg * ld1(cp(alt, l) + u) + ig * cg;
-                        st1(cp(alt ^ 1, l) + u, cell);
-                        st1(hp(alt ^ 1, l) + u, og * tanhf(cell));
-                    }
+                    float h;
+                    lstm_cell(s, c_cur[0], c_new[0], h);
+                    qb_s[wave] = (uint32_t)(uint8_t)quant_i8(h * 127.0f);
                 }
+                __syncthreads();
+                if (tid == 0 && 4 * blk < H)
+                    st_word(qbank(alt ^ 1, 0) + blk, qb_s[0] | (qb_s[1] << 8) | (qb_s[2] << 16) | (qb_s[3] << 24));
                 barrier(0);
                 if (failed) break;
-            }
-            if (failed) break;
-            // ---- projection of the new layer-1 output
-            if (owns_unit) {
-                float a = 0.0f;
+                // ---- layer 1: its recurrent sums + W_ih1 x the new INT8 layer-0
+                // output (decoder.cu:650-670)
+                if (owns_unit) {
+                    uint32_t x[KD];
 #pragma unroll
-                for (int j = 0; j < KP; ++j) {
-                    const float2 v = ld2(hp(alt ^ 1, 1) + 2 * lane + 128 * j);
-                    a = __builtin_fmaf(lo16(wpj[j]), v.x, a);
-                    a = __builtin_fmaf(hi16(wpj[j]), v.y, a);
+                    for (int j = 0; j < KD; ++j) x[j] = 4 * lane + 256 * j < H ? ld_word(qbank(alt ^ 1, 0) + lane + 64 * j) : 0u;
+                    int in[4];
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        int a = 0;
+#pragma unroll
+                        for (int j = 0; j < KD; ++j) a = __builtin_amdgcn_sdot4((int)qw[2][g][j], (int)x[j], a, false);
+                        in[g] = wave_isum(a);
+                    }
+                    if (lane == 0) {
+                        float s[4];
+#pragma unroll
+                        for (int g = 0; g < 4; ++g)
+                            s[g] = __builtin_fmaf((float)in[g], cq[2], __builtin_fmaf((float)rs[1][g], cq[1], bias[1][g]));
+                        float h;
+                        lstm_cell(s, c_cur[1], c_new[1], h);
+                        st1(h1c + u, h);
+                        qb_s[wave] = (uint32_t)(uint8_t)quant_i8(h * 127.0f);
+                    }
                 }
-                a = wave_sum(a) + bpj;
-                if (lane == 0) st1(pred + u, a);
+                __syncthreads();
+                if (tid == 0 && 4 * blk < H)
+                    st_word(qbank(alt ^ 1, 1) + blk, qb_s[0] | (qb_s[1] << 8) | (qb_s[2] << 16) | (qb_s[3] << 24));
+                barrier(0);
+                if (failed) break;
+                // ---- projection of the new layer-1 output, and the recurrent sums of
+                // this candidate state for the update after it is committed
+                if (owns_unit) {
+                    uint32_t xq[2][KD];
+#pragma unroll
+                    for (int l = 0; l < 2; ++l)
+#pragma unroll
+                        for (int j = 0; j < KD; ++j) xq[l][j] = 4 * lane + 256 * j < H ? ld_word(qbank(alt ^ 1, l) + lane + 64 * j) : 0u;
+                    float a = 0.0f;
+#pragma unroll
+                    for (int j = 0; j < KP; ++j) {
+                        const float2 v = ld2(h1c + 2 * lane + 128 * j);
+                        a = __builtin_fmaf(lo16(wpj[j]), v.x, a);
+                        a = __builtin_fmaf(hi16(wpj[j]), v.y, a);
+                    }
+                    a = wave_sum(a) + bpj;
+                    if (lane == 0) st1(pred + u, a);
+#pragma unroll
+                    for (int l = 0; l < 2; ++l)
+#pragma unroll
+                        for (int g = 0; g < 4; ++g) {
+                            int d = 0;
+#pragma unroll
+                            for (int j = 0; j < KD; ++j) d = __builtin_amdgcn_sdot4((int)qw[l][g][j], (int)xq[l][j], d, false);
+                            rs_next[l][g] = wave_isum(d);
+                        }
+                }
             }
             barrier(0);
             if (failed) break;
@@ -358,6 +590,14 @@ __global__ __launch_bounds__(kDecThreads, 1) void tdt_decode_kernel(DecodeArgs p
                 emitted = true;
                 valid = false;
                 alt ^= 1;  // the candidate state becomes the committed one
+                if constexpr (kLong) {
+#pragma unroll
+                    for (int l = 0; l < 2; ++l) {
+                        c_cur[l] = c_new[l];
+#pragma unroll
+                        for (int g = 0; g < 4; ++g) rs[l][g] = rs_next[l][g];
+                    }
+                }
             }
             ++symbols;
             frame += dur;
@@ -381,9 +621,12 @@ __global__ void decode_clear_kernel(uint32_t* ws, int words) {
 
 }  // namespace
 
+// fp16 form: h, c (2 banks x 2 layers) and the prediction; long form: INT8
+// banks (H words), candidate layer-1 output (H), maxima (3 x blocks, <= 6H
+// for H >= 128) and the prediction at the same offset 8H.
 int decode_workspace_words(int hidden) { return kDecState + 9 * hidden; }
 
-int launch_tdt_decode(const uint16_t* enc, int frames, int enc_stride, const uint16_t* emb, const uint16_t* const* w_ih,
+int launch_tdt_decode(const uint16_t* enc, int frames, int enc_stride, const uint16_t* emb, const uint16_t* table, const uint16_t* const* w_ih,
                       const uint16_t* const* w_hh, const float* const* b_ih, const float* const* b_hh, const uint16_t* w_proj,
                       const float* b_proj, const void* w_joint, int joint_int8, const float* joint_scales, const float* b_joint,
                       int hidden, int token_outputs, int durations, int max_symbols, int32_t* tokens, int capacity, int32_t* result,
@@ -398,6 +641,7 @@ int launch_tdt_decode(const uint16_t* enc, int frames, int enc_stride, const uin
     DecodeArgs a{};
     a.enc = enc;
     a.emb = emb;
+    a.table = table;
     for (int l = 0; l < 2; ++l) {
         a.w_ih[l] = w_ih[l];
         a.w_hh[l] = w_hh[l];
@@ -421,10 +665,15 @@ int launch_tdt_decode(const uint16_t* enc, int frames, int enc_stride, const uin
     a.capacity = capacity;
     decode_clear_kernel<<<16, 256, 0, s>>>(workspace, decode_workspace_words(hidden));
     switch (hidden >> 7) {
-#define PK_DEC_CASE(KP)                                                                   \
-    case KP:                                                                              \
-        if (joint_int8) tdt_decode_kernel<true, KP><<<blocks, kDecThreads, 0, s>>>(a);   \
-        else tdt_decode_kernel<false, KP><<<blocks, kDecThreads, 0, s>>>(a);             \
+#define PK_DEC_CASE(KP)                                                                          \
+    case KP:                                                                                     \
+        if (table) {                                                                             \
+            if (joint_int8) tdt_decode_kernel<true, KP, true><<<blocks, kDecThreads, 0, s>>>(a);  \
+            else tdt_decode_kernel<false, KP, true><<<blocks, kDecThreads, 0, s>>>(a);            \
+        } else {                                                                                 \
+            if (joint_int8) tdt_decode_kernel<true, KP, false><<<blocks, kDecThreads, 0, s>>>(a); \
+            else tdt_decode_kernel<false, KP, false><<<blocks, kDecThreads, 0, s>>>(a);           \
+        }                                                                                        \
         break;
         PK_DEC_CASE(1) PK_DEC_CASE(2) PK_DEC_CASE(3) PK_DEC_CASE(4) PK_DEC_CASE(5) PK_DEC_CASE(6) PK_DEC_CASE(7) PK_DEC_CASE(8)
 #undef PK_DEC_CASE

@@ -28,7 +28,8 @@ int launch_joint_scan(const void* w, int w_int8, const float* w_scales, const fl
                       int* state, uint32_t* workspace, hipStream_t s);
 
 int decode_workspace_words(int hidden);
-int launch_tdt_decode(const uint16_t* enc, int frames, int enc_stride, const uint16_t* emb, const uint16_t* const* w_ih,
+// emb set: fp16 prediction network; table set (emb unused): the long form.
+int launch_tdt_decode(const uint16_t* enc, int frames, int enc_stride, const uint16_t* emb, const uint16_t* table, const uint16_t* const* w_ih,
                       const uint16_t* const* w_hh, const float* const* b_ih, const float* const* b_hh, const uint16_t* w_proj,
                       const float* b_proj, const void* w_joint, int joint_int8, const float* joint_scales, const float* b_joint,
                       int hidden, int token_outputs, int durations, int max_symbols, int32_t* tokens, int capacity, int32_t* result,

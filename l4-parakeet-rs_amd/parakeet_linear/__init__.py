@@ -94,6 +94,8 @@ SIGNATURES = {
     "pk_tdt_decode_workspace_bytes": (I, [I]),
     "pk_tdt_decode": (I, [P, I, I, P, P, P, P, P, P, P, P, P, P, P, P, I, P, P, I, I, I, I, P, I, P, P,
                           ctypes.c_uint64, P]),
+    "pk_tdt_decode_long": (I, [P, I, I, P, P, P, P, P, P, P, P, P, P, P, I, P, P, I, I, I, I, P, I, P, P,
+                               ctypes.c_uint64, P]),
     "pk_pack_score_vectors": (I, [P, P, P, I, P]),
     "pk_pack_key_int4": (I, [P, P, P, I, P]),
     "pk_quantize_value_int4": (I, [P, P, I, F, P]),
@@ -291,3 +293,35 @@ def launch_attention_arena(query, key, value_fp8, position, bias_u, bias_v, outp
     else:
         call("pk_local_relpos_attention_tc_scores", query, key, None, value_fp8, position, bias_u, bias_v, output,
              rows, padded_rows, valid_rows, ATTENTION_LEFT, ATTENTION_RIGHT, value_stride, stream=stream)
+
+
+# decoder.rs:15: utterances of at least this many frames take the long-request
+# decoder (INT8 recurrent weights, layer-0 input table).
+LONG_DECODE_MIN_FRAMES = 1024
+
+
+def launch_decode(encoder_projection, frames, lstm, projection, joint, tokens, result, workspace, *,
+                  input_table=None, joint_int8=False, joint_scales=None, hidden=640, token_outputs=1025,
+                  durations=5, max_symbols=10, stream=None):
+    """Mirror of decoder.rs:275-353 (launch_decode) after the encoder
+    projection: for frames >= LONG_DECODE_MIN_FRAMES the layer-0 input table
+    (embedding x W_ih0^T, fp16 [token_outputs - 1 x 4H], decoder.rs:355-377) is
+    derived with the fp16 linear into `input_table` and pk_tdt_decode_long
+    runs; otherwise pk_tdt_decode.  lstm = (embedding, w_ih0, w_hh0, b_ih0,
+    b_hh0, w_ih1, w_hh1, b_ih1, b_hh1); projection = (w, b); joint = (w, b).
+    Returns "long" or "fp16", the form that ran."""
+    emb, w_ih0, w_hh0, b_ih0, b_hh0, w_ih1, w_hh1, b_ih1, b_hh1 = lstm
+    capacity = tokens.numel()
+    wbytes = workspace.numel() * workspace.element_size()
+    if frames >= LONG_DECODE_MIN_FRAMES:
+        if input_table is None:
+            raise ValueError("the long decode needs an input_table buffer of (token_outputs - 1) x 4H halves")
+        launch_linear(emb, w_ih0, None, None, input_table, token_outputs - 1, 4 * hidden, hidden, stream=stream)
+        call("pk_tdt_decode_long", encoder_projection, frames, hidden, input_table, w_hh0, b_ih0, b_hh0, w_ih1, w_hh1,
+             b_ih1, b_hh1, projection[0], projection[1], joint[0], int(joint_int8), joint_scales, joint[1], hidden,
+             token_outputs, durations, max_symbols, tokens, capacity, result, workspace, wbytes, stream=stream)
+        return "long"
+    call("pk_tdt_decode", encoder_projection, frames, hidden, emb, w_ih0, w_hh0, b_ih0, b_hh0, w_ih1, w_hh1, b_ih1,
+         b_hh1, projection[0], projection[1], joint[0], int(joint_int8), joint_scales, joint[1], hidden, token_outputs,
+         durations, max_symbols, tokens, capacity, result, workspace, wbytes, stream=stream)
+    return "fp16"

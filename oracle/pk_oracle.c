@@ -1111,6 +1111,186 @@ int orc_tdt_decode(const uint16_t* enc, int frames, int enc_stride, const uint16
     return count;
 }
 
+/* ---- long-request TDT decode (decoder.cu:452-784, tdt_persistent_fp8) ----- */
+
+/* decoder.cu:95-97 quantize_i8: round to nearest even, clamp to +-127. */
+static int orc_quant_i8(float v) {
+    int q = (int)rintf(v);
+    return q < -127 ? -127 : (q > 127 ? 127 : q);
+}
+
+/* decoder.cu:520-575: per-tensor symmetric INT8 of an fp16 matrix of n
+ * elements: scale = max|w| / 127 (1 when every element is zero), q =
+ * quantize_i8(w / scale).  Returns the scale. */
+float orc_quantize_tensor_i8(const uint16_t* w, size_t n, int8_t* q) {
+    float m = 0.0f;
+    for (size_t i = 0; i < n; ++i) m = fmaxf(m, fabsf(orc_f16_to_f32(w[i])));
+    const float scale = m > 0.0f ? m / 127.0f : 1.0f;
+    for (size_t i = 0; i < n; ++i) q[i] = (int8_t)orc_quant_i8(orc_f16_to_f32(w[i]) / scale);
+    return scale;
+}
+
+/* Integer dot product of INT8 row r of a [4H x H] matrix with an INT8 vector. */
+static int orc_dot_i8(const int8_t* q, int row, const int8_t* x, int hidden) {
+    int acc = 0;
+    for (int k = 0; k < hidden; ++k) acc += (int)q[(size_t)row * hidden + k] * (int)x[k];
+    return acc;
+}
+
+/* exp(x) from IEEE basic operations (the long form's cell arithmetic, which
+ * the GPU evaluates operation for operation): Cody-Waite reduction x = n ln2
+ * + r with ln2 split into a 16-bit head and a tail, e^r by its degree-7
+ * Taylor polynomial, times 2^n.  Within 0.82 ulp of exp on [-87, 88]. */
+float orc_det_exp(float x) {
+    if (x != x) return x;
+    x = fminf(fmaxf(x, -104.0f), 89.0f);
+    const float n = rintf(x * 1.44269504f);
+    float r = fmaf(n, -0.693145751953125f, x);
+    r = fmaf(n, -1.428606765330187e-06f, r);
+    float q = 1.98412698e-04f;
+    q = fmaf(q, r, 1.38888889e-03f);
+    q = fmaf(q, r, 8.33333333e-03f);
+    q = fmaf(q, r, 4.16666667e-02f);
+    q = fmaf(q, r, 1.66666667e-01f);
+    q = fmaf(q, r, 0.5f);
+    q = fmaf(q, r, 1.0f);
+    q = fmaf(q, r, 1.0f);
+    return ldexpf(q, (int)n);
+}
+
+/* tanh(x) = sign(x) (1 - e^-2|x|) / (1 + e^-2|x|). */
+float orc_det_tanh(float v) {
+    const float t = orc_det_exp(-2.0f * fabsf(v));
+    return copysignf((1.0f - t) / (1.0f + t), v);
+}
+
+/* decoder.cu:116-129 lstm_cell with orc_det_exp / orc_det_tanh and the cell
+ * update as fma(f, c, i * g). */
+static void orc_cell(const float s[4], float c_prev, float* c_out, float* h_out) {
+    const float ig = 1.0f / (1.0f + orc_det_exp(-s[0]));
+    const float fg = 1.0f / (1.0f + orc_det_exp(-s[1]));
+    const float cg = orc_det_tanh(s[2]);
+    const float og = 1.0f / (1.0f + orc_det_exp(-s[3]));
+    *c_out = fmaf(fg, c_prev, ig * cg);
+    *h_out = og * orc_det_tanh(*c_out);
+}
+
+/* One prediction-network update of the long form (decoder.cu:613-672).
+ * q_hh0, q_hh1, q_ih1: INT8 [4H x H]; cq[3] = their scale / 127; bias[2][4H] =
+ * b_ih + b_hh per layer; qh (committed INT8 h of layers 0, 1, [2][H]) and c
+ * ([2][H]) are the committed state; table_row = the last token's
+ * [4H] fp16 input terms or NULL before the first token.  Writes the
+ * candidate INT8 h (qh_out [2][H]), cell states (c_out [2][H]) and layer-1
+ * output (h1_out [H]).  Gate sums: layer 0 fma(dot, cq0, bias) + table,
+ * layer 1 fma(dot_ih1, cq2, fma(dot_hh1, cq1, bias)); each integer dot is
+ * exact and converted once. */
+void orc_lstm_long_update(const int8_t* q_hh0, const int8_t* q_hh1, const int8_t* q_ih1, const float* cq,
+                          const float* bias, const uint16_t* table_row, const int8_t* qh, const float* c, int hidden,
+                          int8_t* qh_out, float* c_out, float* h1_out) {
+    for (int u = 0; u < hidden; ++u) {
+        float s[4], h;
+        for (int g = 0; g < 4; ++g) {
+            const int row = g * hidden + u;
+            const float tv = table_row ? orc_f16_to_f32(table_row[row]) : 0.0f;
+            s[g] = fmaf((float)orc_dot_i8(q_hh0, row, qh, hidden), cq[0], bias[row]) + tv;
+        }
+        orc_cell(s, c[u], &c_out[u], &h);
+        qh_out[u] = (int8_t)orc_quant_i8(h * 127.0f);
+    }
+    for (int u = 0; u < hidden; ++u) {
+        float s[4];
+        for (int g = 0; g < 4; ++g) {
+            const int row = g * hidden + u;
+            const float rec = fmaf((float)orc_dot_i8(q_hh1, row, qh + hidden, hidden), cq[1], bias[4 * hidden + row]);
+            s[g] = fmaf((float)orc_dot_i8(q_ih1, row, qh_out, hidden), cq[2], rec);
+        }
+        orc_cell(s, c[hidden + u], &c_out[hidden + u], &h1_out[u]);
+        qh_out[hidden + u] = (int8_t)orc_quant_i8(h1_out[u] * 127.0f);
+    }
+}
+
+/* decoder.cu:452-784 (tdt_persistent_fp8): the greedy decode of
+ * orc_tdt_decode with the long-request prediction network: per-tensor INT8
+ * W_hh0, W_hh1, W_ih1 (orc_quantize_tensor_i8), INT8 hidden states at 1/127,
+ * layer-0 input terms from input_table [(token_outputs - 1) x 4H] fp16, fp32
+ * cells, the projection of the fp32 layer-1 output.  The zero state and no
+ * input before the first token; the candidate state is committed when a token
+ * is emitted.  Returns the token count; pred_out, *frame_out as
+ * orc_tdt_decode. */
+int orc_tdt_decode_long(const uint16_t* enc, int frames, int enc_stride, const uint16_t* table, const uint16_t* w_hh0,
+                        const float* b_ih0, const float* b_hh0, const uint16_t* w_ih1, const uint16_t* w_hh1,
+                        const float* b_ih1, const float* b_hh1, const uint16_t* w_proj, const float* b_proj,
+                        const void* w_joint, int joint_int8, const float* joint_scales, const float* b_joint, int hidden,
+                        int token_outputs, int durations, int max_symbols, int32_t* tokens, int capacity,
+                        float* pred_out, int* frame_out) {
+    const int H = hidden, outputs = token_outputs + durations, blank = token_outputs - 1;
+    const size_t n = (size_t)4 * H * H;
+    int8_t* q = (int8_t*)malloc(3 * n);
+    float cq[3];
+    cq[0] = orc_quantize_tensor_i8(w_hh0, n, q) / 127.0f;
+    cq[1] = orc_quantize_tensor_i8(w_hh1, n, q + n) / 127.0f;
+    cq[2] = orc_quantize_tensor_i8(w_ih1, n, q + 2 * n) / 127.0f;
+    float* bias = (float*)malloc((size_t)8 * H * sizeof(float));
+    for (int i = 0; i < 4 * H; ++i) {
+        bias[i] = b_ih0[i] + b_hh0[i];
+        bias[4 * H + i] = b_ih1[i] + b_hh1[i];
+    }
+    int8_t* qh = (int8_t*)calloc((size_t)2 * H, 1);
+    int8_t* qh_cand = (int8_t*)calloc((size_t)2 * H, 1);
+    float* c = (float*)calloc((size_t)2 * H, sizeof(float));
+    float* c_cand = (float*)calloc((size_t)2 * H, sizeof(float));
+    float* h1 = (float*)calloc((size_t)H, sizeof(float));
+    float* pred = (float*)calloc((size_t)H, sizeof(float));
+    float* scores = (float*)malloc((size_t)outputs * sizeof(float));
+    int frame = 0, symbols = 0, last = blank, emitted = 0, valid = 0, count = 0;
+    while (frame < frames) {
+        if (!valid) {
+            orc_lstm_long_update(q, q + n, q + 2 * n, cq, bias, emitted ? table + (size_t)last * 4 * H : NULL, qh, c, H,
+                                 qh_cand, c_cand, h1);
+            for (int o = 0; o < H; ++o) {
+                double s = (double)b_proj[o];
+                for (int k = 0; k < H; ++k) s += (double)orc_f16_to_f32(w_proj[(size_t)o * H + k]) * (double)h1[k];
+                pred[o] = (float)s;
+            }
+            valid = 1;
+        }
+        const uint16_t* e = enc + (size_t)frame * enc_stride;
+        if (joint_int8)
+            orc_joint_scores_i8((const int8_t*)w_joint, joint_scales, b_joint, e, pred, outputs, H, scores);
+        else
+            orc_joint_scores_f16((const uint16_t*)w_joint, b_joint, e, pred, outputs, H, scores);
+        int tok, dur;
+        orc_joint_decide(scores, token_outputs, durations, &tok, &dur);
+        if (tok != blank) {
+            if (count < capacity) tokens[count] = tok;
+            ++count;
+            last = tok;
+            emitted = 1;
+            valid = 0;
+            memcpy(qh, qh_cand, (size_t)2 * H);
+            memcpy(c, c_cand, (size_t)2 * H * sizeof(float));
+        }
+        ++symbols;
+        frame += dur;
+        if (dur != 0 || symbols == max_symbols) {
+            if (dur == 0) ++frame;
+            symbols = 0;
+        }
+    }
+    memcpy(pred_out, pred, (size_t)H * sizeof(float));
+    *frame_out = frame;
+    free(q);
+    free(bias);
+    free(qh);
+    free(qh_cand);
+    free(c);
+    free(c_cand);
+    free(h1);
+    free(pred);
+    free(scores);
+    return count;
+}
+
 /* ======================================================================== */
 /* Local relative-position attention and its packers                        */
 /* (encoder.cu:1476-2097, launch_attention_arena encoder.rs:1839-1968).      */

@@ -107,6 +107,18 @@ int orc_tdt_decode(const uint16_t* enc, int frames, int enc_stride, const uint16
                    const float* b_proj, const void* w_joint, int joint_int8, const float* joint_scales,
                    const float* b_joint, int hidden, int token_outputs, int durations, int max_symbols,
                    int32_t* tokens, int capacity, float* pred_out, int* frame_out);
+float orc_det_exp(float x);
+float orc_det_tanh(float v);
+float orc_quantize_tensor_i8(const uint16_t* w, size_t n, int8_t* q);
+void orc_lstm_long_update(const int8_t* q_hh0, const int8_t* q_hh1, const int8_t* q_ih1, const float* cq,
+                          const float* bias, const uint16_t* table_row, const int8_t* qh, const float* c, int hidden,
+                          int8_t* qh_out, float* c_out, float* h1_out);
+int orc_tdt_decode_long(const uint16_t* enc, int frames, int enc_stride, const uint16_t* table, const uint16_t* w_hh0,
+                        const float* b_ih0, const float* b_hh0, const uint16_t* w_ih1, const uint16_t* w_hh1,
+                        const float* b_ih1, const float* b_hh1, const uint16_t* w_proj, const float* b_proj,
+                        const void* w_joint, int joint_int8, const float* joint_scales, const float* b_joint, int hidden,
+                        int token_outputs, int durations, int max_symbols, int32_t* tokens, int capacity,
+                        float* pred_out, int* frame_out);
 
 /* ---- local relative-position attention (encoder.cu:1476-2097) ----------- */
 int orc_score_vector_byte(int d);

@@ -83,6 +83,11 @@ def _declare(l):
         "orc_joint_decide": (None, [P, I, I, P, P]),
         "orc_lstm_step": (None, [P, P, P, P, P, P, P, I, P, P]),
         "orc_tdt_decode": (I, [P, I, I, P, P, P, P, P, P, P, P, P, P, P, P, I, P, P, I, I, I, I, P, I, P, P]),
+        "orc_det_exp": (F, [F]),
+        "orc_det_tanh": (F, [F]),
+        "orc_quantize_tensor_i8": (F, [P, S, P]),
+        "orc_lstm_long_update": (None, [P, P, P, P, P, P, P, P, I, P, P, P]),
+        "orc_tdt_decode_long": (I, [P, I, I, P, P, P, P, P, P, P, P, P, P, P, I, P, P, I, I, I, I, P, I, P, P]),
         "orc_score_vector_byte": (I, [I]),
         "orc_key_int4_nibble": (I, [I]),
         "orc_pack_score_vectors": (None, [P, I, P, P]),
@@ -539,6 +544,57 @@ def tdt_decode(enc, emb, lstm, proj, joint, token_outputs=1025, durations=5, max
                              _p(_h(proj[0])), _p(keep[4]), _p(wj), int(int8), _p(keep[6]) if int8 else None,
                              _p(keep[5]), hidden, token_outputs, durations, max_symbols, _p(toks), capacity,
                              _p(pred), ctypes.byref(frame))
+    return toks[:min(n, capacity)].copy(), frame.value, pred
+
+
+def quantize_tensor_i8(w):
+    """decoder.cu:520-575 per-tensor symmetric INT8 -> (int8 array, scale)."""
+    w = _h(w)
+    q = np.empty(w.shape, np.int8)
+    return q, float(lib().orc_quantize_tensor_i8(_p(w), w.size, _p(q)))
+
+
+def lstm_long_update(q_hh0, q_hh1, q_ih1, cq, bias, table_row, qh, c):
+    """decoder.cu:613-672: one long-form prediction-network update.  bias =
+    [2 x 4H] (b_ih + b_hh per layer), qh int8 [2 x H], c float32 [2 x H];
+    table_row fp16 [4H] or None.  Returns (qh', c', h1')."""
+    hidden = qh.shape[-1]
+    qh_out = np.empty((2, hidden), np.int8)
+    c_out = np.empty((2, hidden), np.float32)
+    h1 = np.empty(hidden, np.float32)
+    f32 = lambda a: np.ascontiguousarray(a, np.float32)
+    cq, bias, c = f32(cq), f32(bias), f32(c)
+    i8 = lambda a: np.ascontiguousarray(a, np.int8)
+    q_hh0, q_hh1, q_ih1, qh = i8(q_hh0), i8(q_hh1), i8(q_ih1), i8(qh)
+    lib().orc_lstm_long_update(_p(q_hh0), _p(q_hh1), _p(q_ih1), _p(cq), _p(bias),
+                               None if table_row is None else _p(_h(table_row)), _p(qh), _p(c), hidden, _p(qh_out),
+                               _p(c_out), _p(h1))
+    return qh_out, c_out, h1
+
+
+def tdt_decode_long(enc, table, lstm, proj, joint, token_outputs=1025, durations=5, max_symbols=10, capacity=None):
+    """decoder.cu:452-784 greedy TDT decode with the long-request prediction
+    network.  table = fp16 [(token_outputs - 1) x 4H] layer-0 input terms;
+    lstm = (w_hh0, b_ih0, b_hh0, w_ih1, w_hh1, b_ih1, b_hh1); proj and joint as
+    tdt_decode.  Returns (tokens, final frame, final prediction)."""
+    enc = _h(enc)
+    frames, hidden = enc.shape
+    f32 = lambda a: np.ascontiguousarray(a, np.float32)
+    w_hh0, b_ih0, b_hh0, w_ih1, w_hh1, b_ih1, b_hh1 = lstm
+    wj, sj, bj = joint
+    int8 = np.asarray(wj).dtype == np.int8
+    wj = np.ascontiguousarray(wj)
+    capacity = capacity or frames * max_symbols
+    toks = np.empty(capacity, np.int32)
+    pred = np.empty(hidden, np.float32)
+    frame = ctypes.c_int()
+    keep = [f32(b_ih0), f32(b_hh0), f32(b_ih1), f32(b_hh1), f32(proj[1]), f32(bj),
+            None if sj is None else f32(sj)]
+    n = lib().orc_tdt_decode_long(_p(enc), frames, hidden, _p(_h(table)), _p(_h(w_hh0)), _p(keep[0]), _p(keep[1]),
+                                  _p(_h(w_ih1)), _p(_h(w_hh1)), _p(keep[2]), _p(keep[3]), _p(_h(proj[0])),
+                                  _p(keep[4]), _p(wj), int(int8), _p(keep[6]) if int8 else None, _p(keep[5]), hidden,
+                                  token_outputs, durations, max_symbols, _p(toks), capacity, _p(pred),
+                                  ctypes.byref(frame))
     return toks[:min(n, capacity)].copy(), frame.value, pred
 
 

@@ -716,3 +716,65 @@ def test_tdt_decode(pk, orc, H, int8):
     assert np.array_equal(host(toks)[:count], ref_toks)
     pred = host(work).view(np.float32)[1032 + 8 * H:1032 + 9 * H]  # state after the 1032-word barrier area
     assert np.max(np.abs(pred - ref_pred)) <= 1e-4 * max(1.0, float(np.max(np.abs(ref_pred))))
+
+
+def run_long_decode(pk, orc, H, int8, frames, seed, T=1025, D=5):
+    """The long-request decode on the GPU against the oracle's long decode on
+    the same input table.  At frames >= 1024 it runs through the decoder.rs
+    launch mirror (which must pick the long form), below that the table and
+    pk_tdt_decode_long are called directly."""
+    lstm, proj, wj, bj, enc, emb = decode_case(H, T, D, frames, seed, int8)
+    if int8:
+        wq, ws = orc.quantize_int8_rows(wj)
+        joint = (wq, ws, bj)
+    else:
+        joint = (wj, None, bj)
+    d = [dev(a) for a in lstm]
+    cap = frames * 10
+    toks = torch.zeros(cap, dtype=torch.int32, device="cuda")
+    res = torch.zeros(4, dtype=torch.int32, device="cuda")
+    work = torch.zeros(pk.lib.pk_tdt_decode_workspace_bytes(H) // 4, dtype=torch.int32, device="cuda")
+    wbytes = work.numel() * 4
+    table_d = torch.zeros((T - 1, 4 * H), dtype=torch.float16, device="cuda")
+    js = None if joint[1] is None else dev(joint[1])
+    if frames >= pk.LONG_DECODE_MIN_FRAMES:
+        form = pk.launch_decode(dev(enc), frames, (dev(emb),) + tuple(d), (dev(proj[0]), dev(proj[1])),
+                                (dev(joint[0]), dev(bj)), toks, res, work, input_table=table_d, joint_int8=int8,
+                                joint_scales=js, hidden=H, token_outputs=T, durations=D)
+        assert form == "long"
+    else:
+        pk.launch_linear(dev(emb), d[0], None, None, table_d, T - 1, 4 * H, H)
+        pk.call("pk_tdt_decode_long", dev(enc), frames, H, table_d, d[1], d[2], d[3], d[4], d[5], d[6], d[7],
+                dev(proj[0]), dev(proj[1]), dev(joint[0]), int(int8), js, dev(bj), H, T, D, 10, toks, cap, res, work,
+                wbytes)
+    table = host(table_d)
+    # the table is the fp16 linear of the embedding with W_ih0: fp32 accumulation (error <= H * 2^-24 * sum|e w|)
+    # and one fp16 rounding (half an ulp: 2^-11 relative, 2^-25 absolute below the normal range)
+    e64, w64 = emb.astype(np.float64), lstm[0].astype(np.float64)
+    exact = e64 @ w64.T
+    bound = 2.0 ** -11 * np.abs(exact) + 2.0 ** -25 + H * 2.0 ** -24 * (np.abs(e64) @ np.abs(w64).T)
+    err = np.abs(table.astype(np.float64) - exact)
+    assert np.all(err <= bound * (1 + 1e-9)), float((err / bound).max())
+    ref = orc.tdt_decode_long(enc, table, lstm[1:], proj, joint, T, D)
+    return (toks, res, work), ref
+
+
+@pytest.mark.parametrize("H,int8,frames", [(640, False, 1100), (640, True, 96), (128, True, 96), (128, False, 96)])
+def test_tdt_decode_long(pk, orc, H, int8, frames):
+    """decoder.cu:452-784 long-request decode (INT8 recurrent weights derived
+    in the launch, INT8 hidden states, layer-0 input table): tokens and final
+    frame exact, final prediction within 1e-4 of the oracle's."""
+    note(f"tdt decode long H={H} int8={int8} frames={frames}")
+    (toks, res, work), (ref_toks, ref_frame, ref_pred) = run_long_decode(pk, orc, H, int8, frames, 380 + H + int8)
+    assert 3 <= len(ref_toks) <= 10 * frames, len(ref_toks)
+    count, frame, status, steps = (int(v) for v in host(res))
+    note(f"tdt decode long: {count} tokens, {steps} joint steps, status {status}")
+    got = host(toks)[:min(count, len(toks))]
+    n = min(len(got), len(ref_toks))
+    diff = np.nonzero(got[:n] != ref_toks[:n])[0]
+    note(f"  oracle {len(ref_toks)} tokens; first divergence at token {int(diff[0]) if len(diff) else n}")
+    assert status == 0
+    assert count == len(ref_toks) and frame == ref_frame
+    assert np.array_equal(host(toks)[:count], ref_toks)
+    pred = host(work).view(np.float32)[1032 + 8 * H:1032 + 9 * H]
+    assert np.max(np.abs(pred - ref_pred)) <= 1e-4 * max(1.0, float(np.max(np.abs(ref_pred))))
