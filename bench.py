@@ -333,7 +333,8 @@ def attention_bench(pk, torch, stream, frames=45000, tc_frames=1000, reps=20):
     the feature-major value quantizer (register variant) and the packed
     attention kernel, which the reference runs from padded_rows >= 1040.
     At T = `tc_frames`: the tc kernel (fp16 scores, e4m3 context), which the
-    reference runs for 512 <= padded_rows < 1040.  Each is timed over `reps`
+    reference runs for 512 <= padded_rows < 1040; at T = 496 the fp16
+    short-form kernel (padded_rows < 512).  Each is timed over `reps`
     launches with HIP events on the launch stream.  Algorithmic bytes per
     packed launch: q fp16 (2048 B/row), INT4 keys + scales (544 B/row), S4 V
     (512 B/row), e4m3 output (1024 B/row), plus the 8 x 272 packed position
@@ -353,6 +354,9 @@ def attention_bench(pk, torch, stream, frames=45000, tc_frames=1000, reps=20):
     t = attention_inputs(torch, tc_frames, seed=78)
     out16 = torch.empty((t["padded"], 1024), dtype=torch.float16, device="cuda")
     pk.call("pk_quantize_value_int4", t["vt"], t["vf"], t["padded"] * 1024, 56.0, stream=stream)
+    sh = attention_inputs(torch, 496, seed=79)
+    out_sh = torch.empty((sh["padded"], 1024), dtype=torch.float16, device="cuda")
+    v_sh = sh["vt"].t().contiguous()
     runs = {
         "pack_key_int4": lambda: pk.call("pk_pack_key_int4", d["k"], pk_key, k_sc, padded * 8, stream=stream),
         "pack_score_vectors": lambda: pk.call("pk_pack_score_vectors", d["pos"], pk_pos, p_sc, 8 * 272, stream=stream),
@@ -364,6 +368,8 @@ def attention_bench(pk, torch, stream, frames=45000, tc_frames=1000, reps=20):
         "attention_tc": lambda: pk.call("pk_local_relpos_attention_tc_scores", t["q"], t["k"], None, t["vf"], t["pos"],
                                         t["bu"], t["bv"], out16, tc_frames, t["padded"], tc_frames, 128, 128, t["padded"],
                                         stream=stream),
+        "attention_short": lambda: pk.call("pk_local_relpos_attention", sh["q"], sh["k"], v_sh, sh["pos"], sh["bu"],
+                                           sh["bv"], out_sh, 496, sh["padded"], 496, 128, 128, stream=stream),
     }
     nbytes = {
         "pack_key_int4": padded * (2048 + 512 + 32),
@@ -371,6 +377,7 @@ def attention_bench(pk, torch, stream, frames=45000, tc_frames=1000, reps=20):
         "quantize_value_int4": padded * (2048 + 512) + 4096 + 2 * 272 * 1024,
         "attention_packed": padded * (2048 + 544 + 512 + 1024) + 8 * 272 * 132 + 4096,
         "attention_tc": t["padded"] * (2048 + 2048 + 1024 + 2048) + 8 * 272 * 256,
+        "attention_short": sh["padded"] * 4 * 2048 + 8 * 272 * 256,
     }
     for f in runs.values():
         f()

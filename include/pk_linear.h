@@ -453,6 +453,25 @@ int32_t pk_local_relpos_attention_packed(const uint16_t* query, const uint16_t* 
                                          const uint8_t* packed_key, const float* key_scales,
                                          const uint8_t* packed_position, const float* position_scales,
                                          void* stream);
+/* encoder.cu:1338-1461 pk_sm89_local_relpos_attention (the reference's kernel
+ * for padded_rows < 512, encoder.rs:619,850-858): fp16 Q, K, V [padded_rows x
+ * 1024], packed position table [8 x 272 x 128] (pk_pack_position_heads), fp32
+ * scores (q + u).k + (q + v).p over 128 dimensions times 1/sqrt(128), softmax,
+ * fp16 output [padded_rows x 1024]; rows at or beyond min(rows, valid_rows)
+ * are zero.  attention_left, attention_right <= 128. */
+int32_t pk_local_relpos_attention(const uint16_t* query, const uint16_t* key, const uint16_t* value,
+                                  const uint16_t* position, const uint16_t* bias_u, const uint16_t* bias_v,
+                                  uint16_t* output, int32_t rows, int32_t padded_rows, int32_t valid_rows,
+                                  int32_t attention_left, int32_t attention_right, void* stream);
+/* encoder.cu:644-671 pk_sm89_quantize_fp8_fixed_transpose (encoder.rs:1293-1320):
+ * row-major fp16 V [rows x 1024] -> feature-major e4m3 [1024 x rows],
+ * out[f * rows + r] = e4m3(in[r * 1024 + f] * inverse_scale). */
+int32_t pk_quantize_fp8_fixed_transpose(const uint16_t* input, uint8_t* output, int32_t rows, float inverse_scale,
+                                        void* stream);
+/* encoder.cu:1321-1336 pk_sm89_pack_position_heads (encoder.rs:442-480): a
+ * position projection [272 x 1024] fp16 -> [8 heads x 272 x 128], the layout
+ * every attention kernel reads. */
+int32_t pk_pack_position_heads(const uint16_t* input, uint16_t* output, void* stream);
 
 #ifdef __cplusplus
 }

@@ -632,4 +632,47 @@ int32_t pk_local_relpos_attention_packed(const uint16_t* query, const uint16_t* 
                            position_scales, stream);
 }
 
+int32_t pk_local_relpos_attention(const uint16_t* query, const uint16_t* key, const uint16_t* value, const uint16_t* position,
+                                  const uint16_t* bias_u, const uint16_t* bias_v, uint16_t* output, int32_t rows,
+                                  int32_t padded_rows, int32_t valid_rows, int32_t attention_left, int32_t attention_right,
+                                  void* stream) {
+    if (padded_rows < 0 || rows < 0 || valid_rows < 0 || attention_left < 0 || attention_right < 0 ||
+        attention_left > 128 || attention_right > 128) {
+        set_error("invalid short attention shape rows=%d padded=%d valid=%d left=%d right=%d", rows, padded_rows, valid_rows,
+                  attention_left, attention_right);
+        return PK_E_SHAPE;
+    }
+    if (padded_rows == 0) return PK_OK;
+    if (!need(query, "query") || !need(key, "key") || !need(value, "value") || !need(position, "position") ||
+        !need(bias_u, "bias_u") || !need(bias_v, "bias_v") || !need(output, "output"))
+        return PK_E_ARG;
+    if (misaligned(query, 16) || misaligned(key, 16) || misaligned(position, 16) || misaligned(bias_u, 16) ||
+        misaligned(bias_v, 16) || misaligned(value, 4) || misaligned(output, 4)) {
+        set_error("query, key, position and biases must be 16-byte aligned, value and output 4-byte");
+        return PK_E_ALIGN;
+    }
+    launch_local_attention_short(query, key, value, position, bias_u, bias_v, output, rows, padded_rows, valid_rows,
+                                 attention_left, attention_right, STREAM);
+    return check_launch("local_relpos_attention");
+}
+
+int32_t pk_quantize_fp8_fixed_transpose(const uint16_t* input, uint8_t* output, int32_t rows, float inverse_scale, void* stream) {
+    if (rows < 0) { set_error("rows must be >= 0, got %d", rows); return PK_E_SHAPE; }
+    if (rows == 0) return PK_OK;
+    if (!need(input, "input") || !need(output, "output")) return PK_E_ARG;
+    if (misaligned(input, 16) || (rows % 16 == 0 && misaligned(output, 16))) {
+        set_error("input must be 16-byte aligned (and output too when rows %% 16 == 0)");
+        return PK_E_ALIGN;
+    }
+    launch_quantize_fp8_transpose(input, output, rows, inverse_scale, STREAM);
+    return check_launch("quantize_fp8_fixed_transpose");
+}
+
+int32_t pk_pack_position_heads(const uint16_t* input, uint16_t* output, void* stream) {
+    if (!need(input, "input") || !need(output, "output")) return PK_E_ARG;
+    if (misaligned(input, 16) || misaligned(output, 16)) { set_error("input and output must be 16-byte aligned"); return PK_E_ALIGN; }
+    launch_pack_position_heads(input, output, STREAM);
+    return check_launch("pack_position_heads");
+}
+
 }  // extern "C"

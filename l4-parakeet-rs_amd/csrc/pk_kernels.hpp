@@ -35,6 +35,12 @@ int launch_tdt_decode(const uint16_t* enc, int frames, int enc_stride, const uin
                       int hidden, int token_outputs, int durations, int max_symbols, int32_t* tokens, int capacity, int32_t* result,
                       uint32_t* workspace, hipStream_t s);
 
+void launch_quantize_fp8_transpose(const uint16_t* in, uint8_t* out, int rows, float inverse_scale, hipStream_t s);
+void launch_pack_position_heads(const uint16_t* in, uint16_t* out, hipStream_t s);
+void launch_local_attention_short(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* pos,
+                                  const uint16_t* bu, const uint16_t* bv, uint16_t* out, int rows, int padded_rows,
+                                  int valid_rows, int left, int right, hipStream_t s);
+
 int launch_pack_vectors(bool int4, const uint16_t* in, uint8_t* out, float* scales, int vectors, hipStream_t s);
 int launch_quantize_value_int4(const uint16_t* vt, uint8_t* out, int rows, float inverse_scale, bool edge_only, int valid_rows,
                                hipStream_t s);

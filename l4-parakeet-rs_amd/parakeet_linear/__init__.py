@@ -96,6 +96,9 @@ SIGNATURES = {
                           ctypes.c_uint64, P]),
     "pk_tdt_decode_long": (I, [P, I, I, P, P, P, P, P, P, P, P, P, P, P, I, P, P, I, I, I, I, P, I, P, P,
                                ctypes.c_uint64, P]),
+    "pk_local_relpos_attention": (I, [P, P, P, P, P, P, P, I, I, I, I, I, P]),
+    "pk_quantize_fp8_fixed_transpose": (I, [P, P, I, F, P]),
+    "pk_pack_position_heads": (I, [P, P, P]),
     "pk_pack_score_vectors": (I, [P, P, P, I, P]),
     "pk_pack_key_int4": (I, [P, P, P, I, P]),
     "pk_quantize_value_int4": (I, [P, P, I, F, P]),
@@ -275,14 +278,34 @@ ATTENTION_LEFT = ATTENTION_RIGHT = 128
 POSITION_ROWS_PADDED = 272
 
 
+# encoder.rs:619: the fp16 short-form attention below this many padded rows.
+SHORT_ATTENTION_ROWS = 512
+
+
+def cache_position_projection(position_input, position_weight, row_major, output, stream=None):
+    """Mirror of one layer of encoder.rs:442-480 (cache_position_projections):
+    the fp16 linear of the [272 x 1024] relative-position input with the
+    layer's position weight into `row_major`, then pk_pack_position_heads into
+    `output` [8 x 272 x 128]."""
+    launch_linear(position_input, position_weight, None, None, row_major, POSITION_ROWS_PADDED, 1024, 1024,
+                  stream=stream)
+    call("pk_pack_position_heads", row_major, output, stream=stream)
+
+
 def launch_attention_arena(query, key, value_fp8, position, bias_u, bias_v, output, rows, padded_rows,
-                           valid_rows, value_stride, packed=None, stream=None):
+                           valid_rows, value_stride, packed=None, value=None, stream=None):
     """Mirror of encoder.rs:1839-1968.  With `packed` (padded_rows >= 1040 in
     the reference) it is a dict of caller-owned buffers {key: u8 [padded_rows
     * 512], key_scales: f32 [padded_rows * 8], position: u8 [8 * 272 * 128],
     position_scales: f32 [8 * 272]} that receives the INT4 keys and INT8
     position vectors before pk_local_relpos_attention_packed runs (output e4m3
-    bytes); without it pk_local_relpos_attention_tc_scores runs (output fp16)."""
+    bytes); below SHORT_ATTENTION_ROWS padded rows (encoder.rs:619) the fp16
+    short-form kernel pk_local_relpos_attention runs on `value` (fp16 [padded_rows
+    x 1024]); otherwise pk_local_relpos_attention_tc_scores (output fp16)."""
+    if packed is None and padded_rows < SHORT_ATTENTION_ROWS:
+        call("pk_local_relpos_attention", query, key, value, position, bias_u, bias_v, output, rows, padded_rows,
+             valid_rows, ATTENTION_LEFT, ATTENTION_RIGHT, stream=stream)
+        return
     if packed is not None:
         call("pk_pack_key_int4", key, packed["key"], packed["key_scales"], padded_rows * 8, stream=stream)
         call("pk_pack_score_vectors", position, packed["position"], packed["position_scales"], 8 * POSITION_ROWS_PADDED,

@@ -1660,3 +1660,76 @@ void orc_local_attention(int packed, const uint16_t* query, const uint16_t* key,
             }
         }
 }
+
+/* ---- short-form attention and attention-side layouts ---------------------- */
+
+/* encoder.cu:644-671: out[f * rows + r] = e4m3(in[r * 1024 + f] * inverse_scale). */
+void orc_quantize_fp8_transpose(const uint16_t* in, int rows, float inverse_scale, uint8_t* out) {
+    for (int r = 0; r < rows; ++r)
+        for (int f = 0; f < ORC_MODEL; ++f)
+            out[(size_t)f * rows + r] = orc_f32_to_e4m3(orc_f16_to_f32(in[(size_t)r * ORC_MODEL + f]) * inverse_scale);
+}
+
+/* encoder.cu:1321-1336: [272 x 1024] -> [8 heads x 272 x 128]. */
+void orc_pack_position_heads(const uint16_t* in, uint16_t* out) {
+    for (int p = 0; p < ORC_POSROWS; ++p)
+        for (int h = 0; h < ORC_HEADS; ++h)
+            memcpy(out + ((size_t)h * ORC_POSROWS + p) * ORC_HEAD, in + (size_t)p * ORC_MODEL + h * ORC_HEAD,
+                   ORC_HEAD * sizeof(uint16_t));
+}
+
+/* encoder.cu:1338-1461 pk_sm89_local_relpos_attention: for query r < min(rows,
+ * valid_rows) and head h, keys first = max(0, r - left) .. min(valid - 1, r +
+ * right); score = ((q + u).k + (q + v).p[left - r + key]) / sqrt(128) with
+ * q + u, q + v formed in float and the dot products summed in double (the
+ * reference's lane order is not reproducible); probabilities expf(s - max) /
+ * their sum; context = fmaf over keys in order, rounded to fp16.  Other rows
+ * are zero.  position = packed [8 x 272 x 128]. */
+void orc_local_attention_short(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* pos,
+                               const uint16_t* bu, const uint16_t* bv, uint16_t* out, int rows, int padded_rows,
+                               int valid_rows, int left, int right) {
+#pragma omp parallel for schedule(dynamic, 4) num_threads(orc_threads())
+    for (int r = 0; r < padded_rows; ++r) {
+        float sc[ORC_MAXATT];
+        for (int h = 0; h < ORC_HEADS; ++h) {
+            uint16_t* o = out + (size_t)r * ORC_MODEL + h * ORC_HEAD;
+            if (r >= rows || r >= valid_rows) {
+                memset(o, 0, ORC_HEAD * sizeof(uint16_t));
+                continue;
+            }
+            const int first = r - left > 0 ? r - left : 0;
+            const int last = r + right < valid_rows - 1 ? r + right : valid_rows - 1;
+            const int count = last - first + 1;
+            float qu[ORC_HEAD], qv[ORC_HEAD];
+            for (int d = 0; d < ORC_HEAD; ++d) {
+                const float qf = orc_f16_to_f32(q[(size_t)r * ORC_MODEL + h * ORC_HEAD + d]);
+                qu[d] = qf + orc_f16_to_f32(bu[h * ORC_HEAD + d]);
+                qv[d] = qf + orc_f16_to_f32(bv[h * ORC_HEAD + d]);
+            }
+            float mx = -FLT_MAX;
+            for (int slot = 0; slot < count; ++slot) {
+                const int key = first + slot, prow = left - r + key;
+                double s = 0.0;
+                for (int d = 0; d < ORC_HEAD; ++d) {
+                    s += (double)qu[d] * orc_f16_to_f32(k[(size_t)key * ORC_MODEL + h * ORC_HEAD + d]);
+                    s += (double)qv[d] * orc_f16_to_f32(pos[((size_t)h * ORC_POSROWS + prow) * ORC_HEAD + d]);
+                }
+                sc[slot] = (float)s * 0.08838834764831845f;
+                mx = fmaxf(mx, sc[slot]);
+            }
+            double den = 0.0;
+            for (int slot = 0; slot < count; ++slot) {
+                sc[slot] = expf(sc[slot] - mx);
+                den += sc[slot];
+            }
+            const float denf = (float)den;
+            for (int d = 0; d < ORC_HEAD; ++d) {
+                float c = 0.0f;
+                for (int slot = 0; slot < count; ++slot)
+                    c = fmaf(sc[slot] / denf, orc_f16_to_f32(v[(size_t)(first + slot) * ORC_MODEL + h * ORC_HEAD + d]), c);
+                o[d] = orc_f32_to_f16(c);
+            }
+        }
+    }
+}
+

@@ -133,6 +133,12 @@ void orc_local_attention(int packed, const uint16_t* query, const uint16_t* key,
                          const uint8_t* packed_key, const float* key_scales, const uint8_t* packed_position,
                          const float* position_scales, int tile_begin, int tile_end);
 
+void orc_quantize_fp8_transpose(const uint16_t* in, int rows, float inverse_scale, uint8_t* out);
+void orc_pack_position_heads(const uint16_t* in, uint16_t* out);
+void orc_local_attention_short(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* pos,
+                               const uint16_t* bu, const uint16_t* bv, uint16_t* out, int rows, int padded_rows,
+                               int valid_rows, int left, int right);
+
 #ifdef __cplusplus
 }
 #endif

@@ -94,6 +94,9 @@ def _declare(l):
         "orc_pack_key_int4": (None, [P, I, P, P]),
         "orc_quantize_value_int4": (None, [P, I, F, I, I, P]),
         "orc_local_attention": (None, [I, P, P, P, P, P, P, P, I, I, I, I, I, I, P, P, P, P, I, I]),
+        "orc_quantize_fp8_transpose": (None, [P, I, F, P]),
+        "orc_pack_position_heads": (None, [P, P]),
+        "orc_local_attention_short": (None, [P, P, P, P, P, P, P, I, I, I, I, I]),
         "orc_threads": (I, []),
         "orc_set_threads": (None, [I]),
     }
@@ -655,3 +658,33 @@ def local_attention(packed, query, key, value_fp8, position, bias_u, bias_v, row
                               _p(position), _p(_h(bias_u)), _p(_h(bias_v)), _p(out), rows, padded_rows, valid_rows,
                               left, right, value_stride, _p(packed_key), _p(ks), _p(packed_position), _p(ps), t0, t1)
     return out
+
+
+def quantize_fp8_transpose(x16: np.ndarray, inverse_scale: float) -> np.ndarray:
+    """encoder.cu:644-671: row-major fp16 [rows x 1024] -> e4m3 [1024 x rows]."""
+    x16 = _h(x16)
+    rows = x16.shape[0]
+    out = np.empty((MODEL_WIDTH, rows), np.uint8)
+    lib().orc_quantize_fp8_transpose(_p(x16), rows, inverse_scale, _p(out))
+    return out
+
+
+def pack_position_heads(x16: np.ndarray) -> np.ndarray:
+    """encoder.cu:1321-1336: [272 x 1024] -> [8 x 272 x 128] fp16."""
+    x16 = _h(x16)
+    out = np.empty((HEADS, POSITION_ROWS, HEAD_WIDTH), np.float16)
+    lib().orc_pack_position_heads(_p(x16), _p(out))
+    return out
+
+
+def local_attention_short(query, key, value, position, bias_u, bias_v, rows, valid_rows=None, left=128, right=128):
+    """encoder.cu:1338-1461 short-form attention; position = packed [8 x 272 x
+    128].  Returns fp16 [padded_rows x 1024]."""
+    query, key, value, position = _h(query), _h(key), _h(value), _h(position)
+    padded_rows = query.shape[0]
+    valid_rows = rows if valid_rows is None else valid_rows
+    out = np.empty((padded_rows, MODEL_WIDTH), np.float16)
+    lib().orc_local_attention_short(_p(query), _p(key), _p(value), _p(position), _p(_h(bias_u)), _p(_h(bias_v)),
+                                    _p(out), rows, padded_rows, valid_rows, left, right)
+    return out
+

@@ -313,3 +313,53 @@ def test_value_quantizer_rejects_ragged_rows(lib):
     p = ctypes.c_void_p(0x10000)
     assert fn(p, p, 1024 * 8, 56.0, 8, None) == -1
     assert fn(p, p, 1024 * 16, 56.0, 17, None) == -1
+
+
+# ---- short-form attention and attention-side layouts (encoder.cu:644-671, 1321-1461) ----
+
+
+def test_quantize_fp8_transpose_against_torch(orc):
+    """e4m3 of x * s (torch float8_e4m3fn, RNE, in range), transposed."""
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(4)
+    rows = 77
+    x = (rng.standard_normal((rows, 1024)) * 3).astype(np.float16)
+    x[5, :8] = [0, -0.0, 1e-4, -1e-4, 7.9, -7.9, 0.015625, 2.0 ** -10]
+    assert np.abs(x.astype(np.float32) * 16).max() < 448
+    out = orc.quantize_fp8_transpose(x, 16.0)
+    ref = torch.from_numpy(x.astype(np.float32) * np.float32(16.0)).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    np.testing.assert_array_equal(out, ref.T)
+
+
+def test_pack_position_heads_is_the_head_major_reshape(orc):
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((272, 1024)).astype(np.float16)
+    out = orc.pack_position_heads(x)
+    np.testing.assert_array_equal(out, x.reshape(272, 8, 128).transpose(1, 0, 2))
+
+
+@pytest.mark.parametrize("rows,valid", [(300, 300), (300, 260), (64, 64)])
+def test_short_attention_matches_float64_attention(orc, rows, valid):
+    padded = (rows + 15) // 16 * 16
+    q, k, v, pos, bu, bv = make_inputs(23 + rows, padded)
+    out = orc.local_attention_short(q, k, v, pos, bu, bv, rows, valid_rows=valid)
+    live = min(rows, valid)
+    assert not out[live:].view(np.uint16).any()
+    sel = sorted({0, 1, live // 2, live - 1, min(live - 1, 130)})
+    ref = textbook(q, k, v, pos, bu, bv, sel, valid)
+    got = out[sel].astype(np.float64)
+    # fp16 output: error within half an fp16 ulp plus the float score / softmax rounding
+    assert np.abs(got - ref).max() <= 1e-3 * np.sqrt((ref ** 2).mean()) + np.abs(ref).max() * 2.0 ** -11
+    wrong = textbook(q, k, v, pos, bu, bv, sel, valid, position_term=False)
+    assert rel_rms(got, wrong) > 100 * rel_rms(got, ref)
+
+
+def test_short_attention_rejects_bad_shapes(lib):
+    P = ctypes.c_void_p
+    fn = lib.pk_local_relpos_attention
+    fn.argtypes = [P] * 7 + [ctypes.c_int] * 5 + [P]
+    fn.restype = ctypes.c_int
+    buf = ctypes.create_string_buffer(64)
+    a = ctypes.cast(buf, P)
+    assert fn(a, a, a, a, a, a, a, 16, 16, 16, 129, 128, None) == -1  # window beyond 128
+    assert fn(None, a, a, a, a, a, a, 16, 16, 16, 128, 128, None) != 0

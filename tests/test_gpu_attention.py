@@ -226,3 +226,46 @@ def test_attention_packed_full_size_tiles(pk, orc):
         ref = orc.local_attention(True, q, k, vfh, pos, bu, bv, rows, packed_key=pkk, key_scales=ks, packed_position=pp,
                                   position_scales=ps, tiles=(t0, t1))
         assert_e4m3_close(got[16 * t0:16 * t1], ref[16 * t0:16 * t1], f"full size tiles {t0}..{t1}")
+
+
+# ---- short-form attention and attention-side layouts ---------------------------------
+
+
+@pytest.mark.parametrize("rows", [1040, 77, 496])
+def test_quantize_fp8_transpose_bit_exact(pk, orc, rows):
+    note(f"quantize_fp8_fixed_transpose rows={rows}")
+    rng = np.random.default_rng(rows)
+    x = (rng.standard_normal((rows, 1024)) * 8).astype(np.float16)
+    out = torch.full((1024 * rows,), 0xAB, dtype=torch.uint8, device="cuda")
+    pk.call("pk_quantize_fp8_fixed_transpose", dev(x), out, rows, 56.0)
+    np.testing.assert_array_equal(host(out).reshape(1024, rows), orc.quantize_fp8_transpose(x, 56.0))
+
+
+def test_pack_position_heads_bit_exact(pk, orc):
+    rng = np.random.default_rng(6)
+    x = rng.standard_normal((272, 1024)).astype(np.float16)
+    out = torch.zeros((8, 272, 128), dtype=torch.float16, device="cuda")
+    pk.call("pk_pack_position_heads", dev(x), out)
+    np.testing.assert_array_equal(host(out).view(np.uint16), orc.pack_position_heads(x).view(np.uint16))
+
+
+@pytest.mark.parametrize("padded,rows,valid", [(496, 496, 496), (496, 490, 470), (64, 60, 64), (16, 3, 16)])
+def test_short_attention_parity(pk, orc, padded, rows, valid):
+    """encoder.cu:1338-1461 through the launch_attention_arena mirror (padded
+    rows < 512): fp16 output within max|err| <= 1e-2 * RMS of the oracle's;
+    rows beyond min(rows, valid_rows) zero."""
+    note(f"short attention padded={padded} rows={rows} valid={valid}")
+    q, k, v, pos, bu, bv = inputs(51 + padded + rows, padded)
+    out = torch.full((padded, 1024), 0x5A5A, dtype=torch.int16, device="cuda")
+    d = {n: dev(a) for n, a in dict(q=q, k=k, v=v, pos=pos, bu=bu, bv=bv).items()}
+    pk.launch_attention_arena(d["q"], d["k"], None, d["pos"], d["bu"], d["bv"], out, rows, padded, valid, padded,
+                              value=d["v"])
+    got = host(out).view(np.float16)
+    ref = orc.local_attention_short(q, k, v, pos, bu, bv, rows, valid_rows=valid)
+    live = min(rows, valid)
+    assert not got[live:].view(np.uint16).any()
+    g, r = got[:live].astype(np.float64), ref[:live].astype(np.float64)
+    err = np.abs(g - r).max()
+    rms = np.sqrt((r ** 2).mean())
+    note(f"short attention max|err| {err:.3e}, rms {rms:.3e}, {(g != r).mean():.2e} of outputs differ")
+    assert err <= TOL * rms
