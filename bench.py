@@ -622,6 +622,8 @@ def main():
     ap.add_argument("--only-attention", action="store_true",
                     help="run only the attention measurements and a 256 MiB device copy, for rocprofv3 passes")
     ap.add_argument("--only-decode", action="store_true", help="run only the TDT decode measurements")
+    ap.add_argument("--only-stack", action="store_true",
+                    help="run only the 24-layer stack (warmup + steps, no other measurement), for rocprofv3 passes")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -672,6 +674,11 @@ def main():
     for _ in range(args.warmup):
         stack.step()
     torch.cuda.synchronize()
+    if args.only_stack:
+        ms = time_events(torch, stack.step, args.steps, stream)
+        print(json.dumps({"stack_ms_per_step": ms, "steps": args.steps,
+                          "TOPS": FLOP_PER_FRAME * args.frames / (ms * 1e-3) / 1e12}), flush=True)
+        return
     print("[bench] timing", file=sys.stderr, flush=True)
     t0 = time.perf_counter()
     ms_total = time_events(torch, stack.step, args.steps, stream) * args.steps
