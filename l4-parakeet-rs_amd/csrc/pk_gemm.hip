@@ -1,4 +1,5 @@
 // Instantiations and the launcher of the byte-tile GEMM engine.
+#include <cstdlib>
 #include <mutex>
 
 #include "pk_gemm3.hpp"
@@ -40,29 +41,47 @@ static int launch_one(const GemmArgs& a, hipStream_t s) {
     return 0;
 }
 
-// The occupancy-2 engine: two 256x128-tile workgroups per CU.
-template <int F, int E>
+// The occupancy-2 engine: two workgroups per CU, 32*kAI x 128 tiles.
+template <int F, int E, int kAI>
 static int launch_two(const GemmArgs& a, hipStream_t s) {
+    using L = g3::L3<F, kAI>;
     static std::once_flag once;
     static hipError_t attr = hipSuccess;
     std::call_once(once, [] {
-        attr = hipFuncSetAttribute((const void*)g3::gemm3_kernel<F, E>, hipFuncAttributeMaxDynamicSharedMemorySize, g3::L3<F>::kBytes);
+        attr = hipFuncSetAttribute((const void*)g3::gemm3_kernel<F, E, kAI>, hipFuncAttributeMaxDynamicSharedMemorySize, L::kBytes);
     });
     if (attr != hipSuccess) {
-        set_error("hipFuncSetAttribute(LDS %d bytes) failed: %s", g3::L3<F>::kBytes, hipGetErrorString(attr));
+        set_error("hipFuncSetAttribute(LDS %d bytes) failed: %s", L::kBytes, hipGetErrorString(attr));
         return -3;
     }
-    const int tiles = ((a.m + g3::kBM - 1) / g3::kBM) * ((a.n + g3::kBN - 1) / g3::kBN);
+    const int tiles = ((a.m + L::kBM - 1) / L::kBM) * ((a.n + g3::kBN - 1) / g3::kBN);
     const int slots = 2 * cu_count();
     // two persistent workgroups per CU; a multiple of 8 keeps the XCD mapping
     const int grid = tiles < slots ? tiles : slots - slots % 8;
-    hipLaunchKernelGGL((g3::gemm3_kernel<F, E>), dim3(grid), dim3(g3::kThreads), g3::L3<F>::kBytes, s, a);
+    hipLaunchKernelGGL((g3::gemm3_kernel<F, E, kAI>), dim3(grid), dim3(g3::kThreads), L::kBytes, s, a);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
         set_error("gemm launch (fmt %d, epi %d) failed: %s", F, E, hipGetErrorString(e));
         return -3;
     }
     return 0;
+}
+
+// 128-row tiles (twice as many) when 256-row tiles would fill at most half of
+// the two-per-CU workgroup slots, by measurement: C1, attention-out / FF2 and
+// the sparse FF2 at T = 7500 and the INT4-g128 x INT8 linears at T = 750 run
+// 18-29 % faster; grids of 256-row tiles filling more than half the slots run
+// slower with 128 rows (pw1 at T = 7500: 480 tiles, -5 %).
+// PK_GEMM_TILE_ROWS = 128 or 256 forces one size (measurement only).
+template <int F, int E>
+static int launch_two(const GemmArgs& a, hipStream_t s) {
+    static const int force = [] {
+        const char* v = getenv("PK_GEMM_TILE_ROWS");
+        return v ? atoi(v) : 0;
+    }();
+    const int tiles256 = ((a.m + 255) / 256) * ((a.n + g3::kBN - 1) / g3::kBN);
+    const bool small = force ? force == 128 : 2 * tiles256 <= 2 * cu_count();
+    return small ? launch_two<F, E, 4>(a, s) : launch_two<F, E, 8>(a, s);
 }
 
 // Engine per format, by measurement on MI355X: the occupancy-2 engine for the

@@ -258,15 +258,15 @@ __device__ __forceinline__ uint32_t compress_quartet(uint32_t packed) {
 // lane finishes columns [gcol, gcol + 16) of one row (16 contiguous outputs,
 // one to four 16-byte stores).  Column scales / bias and the 8 row scales are
 // loaded once per tile; a residual row (kRes) is loaded one block ahead.
-template <int F, int E, bool kRes = true>
-__device__ __forceinline__ void epilogue(const GemmArgs& p, v4f (&accf)[8][4], v4i (&acci)[8][4], int m0, int n0, int wm,
+template <int F, int E, bool kRes = true, int kAI = 8>
+__device__ __forceinline__ void epilogue(const GemmArgs& p, v4f (&accf)[kAI][4], v4i (&acci)[kAI][4], int m0, int n0, int wm,
                                          int wn, int lane) {
     using T = FmtTraits<F>;
     const int g = lane >> 4, l16 = lane & 15;
     const int gcol = n0 + wn * 64 + g * 16;
     const int ccol = min(gcol, p.n - 16);
     const bool col_live = gcol < p.n;
-    float wsv[16], bsv[16], rsv[8];
+    float wsv[16], bsv[16], rsv[kAI];
     if constexpr (E != EPI_I32) {
 #pragma unroll
         for (int j = 0; j < 16; j += 4) {
@@ -276,15 +276,15 @@ __device__ __forceinline__ void epilogue(const GemmArgs& p, v4f (&accf)[8][4], v
             bsv[j] = b4.x; bsv[j + 1] = b4.y; bsv[j + 2] = b4.z; bsv[j + 3] = b4.w;
         }
 #pragma unroll
-        for (int ai = 0; ai < 8; ++ai) {
-            const int row = min(m0 + wm * 128 + ai * 16 + l16, p.m - 1);
+        for (int ai = 0; ai < kAI; ++ai) {
+            const int row = min(m0 + wm * 16 * kAI + ai * 16 + l16, p.m - 1);
             rsv[ai] = p.row_scales ? p.row_scales[row] : p.in_scale;
         }
     }
     // Retire the scale loads once here; a wait for them inside the block loop
     // would also wait for the previous block's stores.
     __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
-    auto row_of = [&](int ai) { return min(m0 + wm * 128 + ai * 16 + l16, p.m - 1); };
+    auto row_of = [&](int ai) { return min(m0 + wm * 16 * kAI + ai * 16 + l16, p.m - 1); };
     // Without a residual the loads read the (same-shaped) output instead and
     // a select discards them, keeping the block loop free of branches.
     const uint16_t* res_src = p.residual ? p.residual : (const uint16_t*)p.out;
@@ -296,8 +296,8 @@ __device__ __forceinline__ void epilogue(const GemmArgs& p, v4f (&accf)[8][4], v
         rn1 = rp[1];
     }
 #pragma unroll
-    for (int ai = 0; ai < 8; ++ai) {
-        const int grow = m0 + wm * 128 + ai * 16 + l16;
+    for (int ai = 0; ai < kAI; ++ai) {
+        const int grow = m0 + wm * 16 * kAI + ai * 16 + l16;
         const bool live = grow < p.m && col_live;
         float v[16];
         if constexpr (E == EPI_I32) {
@@ -329,7 +329,7 @@ __device__ __forceinline__ void epilogue(const GemmArgs& p, v4f (&accf)[8][4], v
             }
         } else if constexpr (E == EPI_F16) {
             const uint4 r0 = rn0, r1 = rn1;
-            if (kRes && ai + 1 < 8) {
+            if (kRes && ai + 1 < kAI) {
                 const uint4* rp = (const uint4*)(res_src + (size_t)row_of(ai + 1) * p.ldo + ccol);
                 rn0 = rp[0];
                 rn1 = rp[1];

@@ -24,14 +24,17 @@
 namespace pk {
 namespace g3 {
 
-constexpr int kBM = 256, kBN = 128, kThreads = 256;
-constexpr int kATile = kBM * kRowBytes;  // 32 KiB
-constexpr int kB = 2 * kATile;           // weight buffer offset
+constexpr int kBN = 128, kThreads = 256;
 
-// Weight tile bytes of one step, and the LDS of one workgroup: two activation
-// tiles, one weight tile and (G128 formats) a 2-entry ring of the step's
-// group scales (fp32) and zero-points (u8) for the tile's 128 columns.
-template <int F> struct L3 {
+// Tile rows: 32 * kAI (kAI = 16-row MFMA blocks per wave: 8 for 256-row tiles,
+// 4 for 128-row tiles, which double the tile count of small grids).  Weight
+// tile bytes of one step, and the LDS of one workgroup: two activation tiles,
+// one weight tile and (G128 formats) a 2-entry ring of the step's group scales
+// (fp32) and zero-points (u8) for the tile's 128 columns.
+template <int F, int kAI> struct L3 {
+    static constexpr int kBM = 32 * kAI;
+    static constexpr int kATile = kBM * kRowBytes;
+    static constexpr int kB = 2 * kATile;  // weight buffer offset
     static constexpr bool kG128 = (F == FMT_G128A8 || F == FMT_G128A16);
     static constexpr int kBTile = kBN * FmtTraits<F>::bRow;
     static constexpr int kTab = kB + kBTile;
@@ -40,10 +43,11 @@ template <int F> struct L3 {
     static constexpr int kBPerWave = (kBLoads + 3) / 4;
 };
 
-template <int F, int E>
+template <int F, int E, int kAI>
 __global__ __launch_bounds__(kThreads, 2) void gemm3_kernel(GemmArgs p) {
     using T = FmtTraits<F>;
-    using L = L3<F>;
+    using L = L3<F, kAI>;
+    constexpr int kBM = L::kBM, kATile = L::kATile, kB = L::kB;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
@@ -63,15 +67,16 @@ __global__ __launch_bounds__(kThreads, 2) void gemm3_kernel(GemmArgs p) {
     float* tab_s = (float*)(lds + L::kTab);                  // [2][128] group scales
     uint8_t* tab_z = lds + L::kTab + 2 * kBN * 4;            // [2][128] zero-points
 
-    // Activation load i of this wave covers tile rows wave*64 + 8i + q,
+    // Activation load i of this wave covers tile rows wave*8kAI + 8i + q,
     // q = lane / 8, 16-byte chunk position lane % 8.  swz_key of that row is
-    // kq(q) ^ ki(i), so a lane keeps only its first row and (lane % 8) ^ kq.
+    // kq(q) ^ ki((wave*kAI + i) & 7), so a lane keeps only its first row and
+    // (lane % 8) ^ kq.
     const int q = lane >> 3;
     const uint32_t a_cq = (uint32_t)((lane & 7) ^ ((q >> 1) & 1) ^ (((q >> 2) & 1) << 1) ^ ((q & 1) << 2));
     int a_row = 0;  // m0 + wave*64 + q of the issue tile
     // Formats whose decode leaves the registers keep the 8 offsets instead.
     constexpr bool kPreOff = F == FMT_FP8 || F == FMT_I8 || F == FMT_I8_SKIP || F == FMT_F16;
-    uint32_t a_off[kPreOff ? 8 : 1];
+    uint32_t a_off[kPreOff ? kAI : 1];
     uint32_t b_off[L::kBPerWave];
     uint32_t b_q4k = 0;  // Q4K: bit i set when weight load i carries quant bytes
     auto tile_origin = [&](int tt, int& m0, int& n0) {
@@ -83,11 +88,12 @@ __global__ __launch_bounds__(kThreads, 2) void gemm3_kernel(GemmArgs p) {
     };
     auto set_tile = [&](int tt, int& m0, int& n0) {
         tile_origin(tt, m0, n0);
-        a_row = m0 + wave * 64 + q;
+        a_row = m0 + wave * 8 * kAI + q;
         if constexpr (kPreOff) {
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const uint32_t ki = (uint32_t)((((i >> 1) & 1) << 1) | (((i ^ (i >> 2)) & 1) << 2));
+            for (int i = 0; i < kAI; ++i) {
+                const int x = (wave * kAI + i) & 7;
+                const uint32_t ki = (uint32_t)((((x >> 1) & 1) << 1) | (((x ^ (x >> 2)) & 1) << 2));
                 a_off[i] = (uint32_t)min(a_row + 8 * i, p.m - 1) * (uint32_t)lda + ((a_cq ^ ki) << 4);
             }
         }
@@ -109,15 +115,16 @@ __global__ __launch_bounds__(kThreads, 2) void gemm3_kernel(GemmArgs p) {
     auto issue_a = [&](int step, int buf) {
         const uint32_t base = lds_base + buf * kATile;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
+        for (int i = 0; i < kAI; ++i) {
             uint32_t off;
             if constexpr (kPreOff) {
                 off = a_off[i];
             } else {
-                const uint32_t ki = (uint32_t)((((i >> 1) & 1) << 1) | (((i ^ (i >> 2)) & 1) << 2));
+                const int x = (wave * kAI + i) & 7;
+                const uint32_t ki = (uint32_t)((((x >> 1) & 1) << 1) | (((x ^ (x >> 2)) & 1) << 2));
                 off = (uint32_t)min(a_row + 8 * i, p.m - 1) * (uint32_t)lda + ((a_cq ^ ki) << 4);
             }
-            dma16(pa + (size_t)step * kRowBytes, off, base + (wave * 8 + i) * 1024);
+            dma16(pa + (size_t)step * kRowBytes, off, base + (wave * kAI + i) * 1024);
         }
     };
     auto issue_b = [&](int step) {
@@ -181,15 +188,15 @@ __global__ __launch_bounds__(kThreads, 2) void gemm3_kernel(GemmArgs p) {
     }
     int buf = 0;
 
-    v4f accf[8][4];
-    v4i acci[8][4];
+    v4f accf[kAI][4];
+    v4i acci[kAI][4];
     uint32_t skipped = 0, blocks = 0;
 
     while (true) {
         const int t_next = t + G;
         const int cur_m0 = m0, cur_n0 = n0;
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
+        for (int i = 0; i < kAI; ++i)
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 accf[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
@@ -218,7 +225,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm3_kernel(GemmArgs p) {
                                w0[bj], w1[bj], gs[bj]);
             uint4 x0, x1, y0, y1;
             {
-                const int row = wm * 128 + l16;
+                const int row = wm * 16 * kAI + l16;
                 x0 = *(const uint4*)(As + swz(row, g));
                 x1 = *(const uint4*)(As + swz(row, 4 + g));
             }
@@ -231,9 +238,9 @@ __global__ __launch_bounds__(kThreads, 2) void gemm3_kernel(GemmArgs p) {
                 fetch_tab();       // for the step after nstep
             }
 #pragma unroll
-            for (int ai = 0; ai < 8; ++ai) {
-                if (ai + 1 < 8) {
-                    const int row = wm * 128 + (ai + 1) * 16 + l16;
+            for (int ai = 0; ai < kAI; ++ai) {
+                if (ai + 1 < kAI) {
+                    const int row = wm * 16 * kAI + (ai + 1) * 16 + l16;
                     y0 = *(const uint4*)(As + swz(row, g));
                     y1 = *(const uint4*)(As + swz(row, 4 + g));
                 }
@@ -256,17 +263,17 @@ __global__ __launch_bounds__(kThreads, 2) void gemm3_kernel(GemmArgs p) {
             if constexpr (F == FMT_FP8 || F == FMT_I8) {
                 constexpr int kMfma = F == FMT_FP8 ? 4 : 8;
 #pragma unroll
-                for (int ai = 0; ai < 8; ++ai) {
-                    if (ai + 1 < 8) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+                for (int ai = 0; ai < kAI; ++ai) {
+                    if (ai + 1 < kAI) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
                     __builtin_amdgcn_sched_group_barrier(0x008, kMfma, 0);
                 }
             }
             buf ^= 1;
         }
-        blocks += 8 * steps;
+        blocks += kAI * steps;
 
-        if constexpr (E == EPI_F16_RES) epilogue<F, EPI_F16, true>(p, accf, acci, cur_m0, cur_n0, wm, wn, lane);
-        else epilogue<F, E, false>(p, accf, acci, cur_m0, cur_n0, wm, wn, lane);
+        if constexpr (E == EPI_F16_RES) epilogue<F, EPI_F16, true, kAI>(p, accf, acci, cur_m0, cur_n0, wm, wn, lane);
+        else epilogue<F, E, false, kAI>(p, accf, acci, cur_m0, cur_n0, wm, wn, lane);
         if (t_next >= ntiles) break;
         t = t_next;
     }
