@@ -87,10 +87,19 @@ static int launch_two(const GemmArgs& a, hipStream_t s) {
 // Engine per format, by measurement on MI355X: the occupancy-2 engine for the
 // byte formats, the 256x256 engine for fp16 activations (FP16, G128A16, Q4K),
 // whose 64-K steps make its per-step barriers relatively more costly.
+// Grids too small to give each CU a 256 x 256 tile take the occupancy-2
+// engine's 128 x 128 tiles for the fp16-activation formats too.
 template <int F, int E>
 static int launch_fmt(const GemmArgs& a, hipStream_t s) {
-    if constexpr (F == FMT_F16 || F == FMT_G128A16 || F == FMT_Q4K) return launch_one<F, E>(a, s);
-    else return launch_two<F, E>(a, s);
+    if constexpr (F == FMT_F16 || F == FMT_G128A16) {
+        const int tiles256 = ((a.m + 255) / 256) * ((a.n + g3::kBN - 1) / g3::kBN);
+        if (tiles256 <= cu_count()) return launch_two<F, E, 4>(a, s);
+        return launch_one<F, E>(a, s);
+    } else if constexpr (F == FMT_Q4K) {
+        return launch_one<F, E>(a, s);
+    } else {
+        return launch_two<F, E>(a, s);
+    }
 }
 
 template <int F>
