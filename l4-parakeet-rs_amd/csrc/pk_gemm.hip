@@ -67,12 +67,14 @@ static int launch_two(const GemmArgs& a, hipStream_t s) {
     return 0;
 }
 
-// 128-row tiles (twice as many) when 256-row tiles would fill at most half of
-// the two-per-CU workgroup slots, by measurement: C1, attention-out / FF2 and
+// 64-row tiles when 128-row tiles would number at most a quarter of the CUs
+// (INT4-g128 x INT8 FF2 at T = 750: 59 -> 48 us); 128-row tiles (twice as
+// many) when 256-row tiles would fill at most half of the two-per-CU workgroup
+// slots, by measurement: C1, attention-out / FF2 and
 // the sparse FF2 at T = 7500 and the INT4-g128 x INT8 linears at T = 750 run
 // 18-29 % faster; grids of 256-row tiles filling more than half the slots run
 // slower with 128 rows (pw1 at T = 7500: 480 tiles, -5 %).
-// PK_GEMM_TILE_ROWS = 128 or 256 forces one size (measurement only).
+// PK_GEMM_TILE_ROWS = 64, 128 or 256 forces one size (measurement only).
 template <int F, int E>
 static int launch_two(const GemmArgs& a, hipStream_t s) {
     static const int force = [] {
@@ -80,6 +82,8 @@ static int launch_two(const GemmArgs& a, hipStream_t s) {
         return v ? atoi(v) : 0;
     }();
     const int tiles256 = ((a.m + 255) / 256) * ((a.n + g3::kBN - 1) / g3::kBN);
+    const int tiles128 = ((a.m + 127) / 128) * ((a.n + g3::kBN - 1) / g3::kBN);
+    if (force ? force == 64 : 4 * tiles128 <= cu_count()) return launch_two<F, E, 2>(a, s);
     const bool small = force ? force == 128 : 2 * tiles256 <= 2 * cu_count();
     return small ? launch_two<F, E, 4>(a, s) : launch_two<F, E, 8>(a, s);
 }
@@ -93,6 +97,8 @@ template <int F, int E>
 static int launch_fmt(const GemmArgs& a, hipStream_t s) {
     if constexpr (F == FMT_F16 || F == FMT_G128A16) {
         const int tiles256 = ((a.m + 255) / 256) * ((a.n + g3::kBN - 1) / g3::kBN);
+        const int tiles128 = ((a.m + 127) / 128) * ((a.n + g3::kBN - 1) / g3::kBN);
+        if (4 * tiles128 <= cu_count()) return launch_two<F, E, 2>(a, s);
         if (tiles256 <= cu_count()) return launch_two<F, E, 4>(a, s);
         return launch_one<F, E>(a, s);
     } else if constexpr (F == FMT_Q4K) {
