@@ -721,7 +721,7 @@ def main():
         "joint_gemv": joint,
         "tdt_decode": decode,
         "local_attention": attention,
-        "roofline": {"kernel": "g3::gemm3_kernel<FP8, EPI_F8> (FF1 expand 1024->4096, T=45000)",
+        "roofline": {"kernel": "g3::gemm3_kernel<FP8, EPI_F8, 256-row tiles> (FF1 expand 1024->4096, T=45000)",
                      "bound": "mfma", "achieved": round(k_tflops, 2), "peak": PEAK["fp8"],
                      "unit": "TFLOP/s", "frac": round(k_tflops / PEAK["fp8"], 4), "traffic": measured_traffic(),
                      "avg_ms": round(k_ms, 4), "algorithmic_bytes": k_bytes},
