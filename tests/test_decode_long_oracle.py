@@ -124,3 +124,33 @@ def test_deterministic_exp_and_tanh(oracle):
     for x in np.linspace(-12.0, 12.0, 24001).astype(np.float32):
         assert abs(lib.orc_det_tanh(float(x)) - math.tanh(float(x))) <= 2e-7, x
     assert lib.orc_det_tanh(30.0) == 1.0 and lib.orc_det_tanh(-30.0) == -1.0 and lib.orc_det_tanh(0.0) == 0.0
+
+
+def test_long_decode_abi_rejects_missing_table_and_bad_shapes():
+    """pk_tdt_decode_long validates before any GPU call: a missing input table
+    is an argument error (-4), a hidden size off the 128 grid a shape error
+    (-1), misaligned recurrent weights an alignment error (-2)."""
+    import ctypes
+    import os
+
+    lib_path = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "l4-parakeet-rs_amd", "build",
+                            "libpk_linear.so")
+    if not os.path.exists(lib_path):
+        pytest.fail("libpk_linear.so is not built")
+    lib = ctypes.CDLL(lib_path)
+    P, I = ctypes.c_void_p, ctypes.c_int32
+    fn = lib.pk_tdt_decode_long
+    fn.restype = I
+    fn.argtypes = [P, I, I, P, P, P, P, P, P, P, P, P, P, P, I, P, P, I, I, I, I, P, I, P, P, ctypes.c_uint64, P]
+    buf = ctypes.create_string_buffer(1 << 16)
+    base = (ctypes.addressof(buf) + 255) & ~255
+    a = P(base)
+    ws = lib.pk_tdt_decode_workspace_bytes(640)
+
+    def call(table=a, hidden=640, w=a):
+        return fn(a, 16, hidden, table, w, a, a, a, a, a, a, a, a, a, 0, None, a, hidden, 1025, 5, 10, a, 16, a, a, ws,
+                  None)
+
+    assert call(table=None) == -4
+    assert call(hidden=600) == -1
+    assert call(w=P(base + 8)) == -2
