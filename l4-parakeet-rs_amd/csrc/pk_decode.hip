@@ -638,6 +638,14 @@ int launch_tdt_decode(const uint16_t* enc, int frames, int enc_stride, const uin
         set_error("decode needs hidden <= %d and outputs <= %d on this GPU", 4 * blocks, 8 * blocks);
         return -1;
     }
+    // only as many workgroups as own a hidden unit (4 each) or joint rows (8
+    // each): every further one would only add a participant to each barrier
+    const int needed = max((hidden + 3) / 4, (outputs + 7) / 8);
+    if (needed < blocks) blocks = needed;
+    if (hidden > 4 * blocks || outputs > 8 * blocks) {
+        set_error("decode needs hidden <= %d and outputs <= %d on this GPU", 4 * blocks, 8 * blocks);
+        return -1;
+    }
     DecodeArgs a{};
     a.enc = enc;
     a.emb = emb;
