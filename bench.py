@@ -718,6 +718,17 @@ def main():
                    "format_plan_seed": "0x5EED0005", "parallelism": "none (1 GPU)"},
         "pct_mfma_peak": round(100.0 * tops / PEAK["fp8"], 2),
         "ms_per_audio_min": round(ms_step / audio_min, 4),
+        # BASELINE config 5 by part, each measured above in this run at T=45000 (60 min of audio):
+        # the linear stack, 24 layers of packed local attention with its packers, the greedy decode
+        "config5_ms_per_audio_min": {
+            "linear_stack": round(ms_step / audio_min, 4),
+            "attention_24_layers": attention.get("packed_24_layers_ms_per_audio_min"),
+            "tdt_decode": decode.get("ms_per_audio_min"),
+            "sum": round(ms_step / audio_min + (attention.get("packed_24_layers_ms_per_audio_min") or 0.0)
+                         + (decode.get("ms_per_audio_min") or 0.0), 4),
+            "note": "sum of the measured parts; the reference's other encoder kernels (LayerNorm, conv, "
+                    "subsampling convolutions) are outside this build",
+        },
         "joint_gemv": joint,
         "tdt_decode": decode,
         "local_attention": attention,
