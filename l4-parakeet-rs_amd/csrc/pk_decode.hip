@@ -46,6 +46,12 @@ constexpr uint32_t kDecSpinLimit = 1u << 22;
 constexpr int kDecWords = 8;                                // u32 offset of the barrier words
 constexpr int kDecState = kDecWords + 2 * kDecMaxBlocks * 2;  // u32 offset of the state vectors, after the words
 static_assert(kDecState == 1032, "workspace layout");
+// Frames a joint round scores against one prediction (its window), and the
+// words of the joint rounds' barrier: per workgroup one key per window frame,
+// each carrying the barrier tag (2 epoch slots x blocks x kWin u64), after
+// the state vectors.
+constexpr int kWin = 8;
+constexpr int kDecExtWords = 2 * kDecMaxBlocks * kWin * 2;
 
 struct DecodeArgs {
     const uint16_t* enc;    // [frames x enc_stride] fp16
@@ -149,12 +155,11 @@ template <bool kInt8, int KP, bool kLong>
 __global__ __launch_bounds__(kDecThreads, 1) void tdt_decode_kernel(DecodeArgs p) {
     constexpr int H = 128 * KP;
     constexpr int KD = (KP + 1) / 2;  // INT8 dwords per lane and row (long form)
-    __shared__ unsigned long long best_w[4];
     __shared__ float red_s[12];
     __shared__ uint32_t qb_s[4];
-    __shared__ unsigned long long payload_s;
-    __shared__ float dur_sc[8];
-    __shared__ int dur_s;
+    __shared__ float dur_sc[kWin][8];
+    __shared__ unsigned long long win_w[4][kWin];  // per wave, then the decided key per window frame
+    __shared__ int win_tok[kWin], win_dur[kWin];
     __shared__ int stop_s;
     const int blk = blockIdx.x, nblocks = gridDim.x;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -173,18 +178,18 @@ __global__ __launch_bounds__(kDecThreads, 1) void tdt_decode_kernel(DecodeArgs p
     float* h1c = st + H;
     float* maxima = st + 2 * H;
 
-    // Encoder rows of the frames the next joint step can land on (frame + d,
-    // d < durations, which also covers the max-symbols advance of one frame),
-    // loaded while the joint's barrier polls, so the step after a decision
-    // does not wait for its row.  pf_base = frame of candidate 0 (-1: none).
-    uint32_t cand[8][KP];
+    // Encoder rows of a joint round's window (frames pf_base .. pf_base +
+    // kWin - 1): loaded during the first barrier of a prediction update, when
+    // the next round's frame is known, or directly by a round whose window
+    // they are not.  pf_base = frame of candidate 0 (-1: none).
+    uint32_t cand[kWin][KP];
     int pf_base = -1;
     bool do_pf = false;
     auto prefetch = [&]() {
 #pragma unroll
-        for (int d = 0; d < 8; ++d) {
+        for (int d = 0; d < kWin; ++d) {
             const int f = pf_base + d;
-            const bool ok = d < D && f < p.frames;
+            const bool ok = f < p.frames;
             const uint16_t* e = p.enc + (size_t)(ok ? f : 0) * p.enc_stride + 2 * lane;
 #pragma unroll
             for (int j = 0; j < KP; ++j) cand[d][j] = ok ? *(const uint32_t*)(e + 128 * j) : 0u;
@@ -227,6 +232,45 @@ __global__ __launch_bounds__(kDecThreads, 1) void tdt_decode_kernel(DecodeArgs p
         }
         ++epoch;
         return mine;  // thread t holds workgroup t's word
+    };
+    // The joint rounds' barrier: thread c < kWin publishes this workgroup's key
+    // for window frame c, each key tagged, so all go out together and the poll
+    // itself gathers every workgroup's keys (thread t: workgroup t's, in got).
+    unsigned long long* wwords = (unsigned long long*)(p.ws + kDecState + 9 * H);  // [2][blocks][kWin]
+    auto barrier_win = [&](unsigned long long key, unsigned long long (&got)[kWin]) {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        const uint32_t tag = (epoch + 1) & 0x1fffu;
+        unsigned long long* slot = wwords + (size_t)(epoch & 1) * kDecMaxBlocks * kWin;
+        if (tid < kWin) __hip_atomic_store(slot + blk * kWin + tid, key | tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (do_pf) prefetch();
+        do_pf = false;
+        uint32_t spins = 0;
+#pragma unroll
+        for (int c = 0; c < kWin; ++c) got[c] = 0ull;
+        while (true) {
+            bool ready = true;
+            if (tid < nblocks) {
+#pragma unroll
+                for (int c = 0; c < kWin; ++c) {
+                    got[c] = __hip_atomic_load(slot + tid * kWin + c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    ready = ready && ((uint32_t)got[c] & 0x1fffu) == tag;
+                }
+            }
+            if (__syncthreads_and(ready)) break;
+            if ((++spins & 63) == 0) {
+                if (tid == 0)
+                    stop_s = spins > kDecSpinLimit || __hip_atomic_load(&p.ws[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u;
+                __syncthreads();
+                if (stop_s) {
+                    if (tid == 0) __hip_atomic_store(&p.ws[0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    failed = true;
+                    break;
+                }
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+        ++epoch;
     };
 
     // ---- weights into registers --------------------------------------------------
@@ -346,6 +390,8 @@ __global__ __launch_bounds__(kDecThreads, 1) void tdt_decode_kernel(DecodeArgs p
     float c_cur[2] = {0.0f, 0.0f}, c_new[2] = {0.0f, 0.0f};
     while (frame < p.frames && !failed) {
         if (!valid) {
+            pf_base = frame;  // the next round's window loads during this update's first barrier
+            do_pf = true;
             if constexpr (!kLong) {
                 // ---- two LSTM layers on the last token's embedding (zeros before any)
 #pragma unroll
@@ -495,116 +541,151 @@ __global__ __launch_bounds__(kDecThreads, 1) void tdt_decode_kernel(DecodeArgs p
             }
             valid = true;
         }
-        // ---- joint step at `frame`
+        // ---- joint round: frames frame .. frame + kWin - 1 against this prediction
+        if (pf_base != frame) {
+            pf_base = frame;
+            prefetch();
+        }
         {
-            float bs = -__builtin_huge_valf();
-            int bi = 0x7fffffff;
-            float x[2 * KP];
-            uint32_t evs[KP];
-            const int sel = frame - pf_base;
-            if (pf_base >= 0 && sel >= 0 && sel < D) {
+            // the 2 x kWin dot products first, then their wave sums level by
+            // level, so every butterfly step issues 2 kWin independent shuffles
+            float acc[kWin][2];
+#pragma unroll
+            for (int c = 0; c < kWin; ++c) {
+                float x[2 * KP];
 #pragma unroll
                 for (int j = 0; j < KP; ++j) {
-                    uint32_t v = cand[0][j];
-#pragma unroll
-                    for (int d = 1; d < 8; ++d) v = sel == d ? cand[d][j] : v;
-                    evs[j] = v;
+                    const uint32_t ev = cand[c][j];
+                    x[2 * j] = __builtin_fmaxf(lo16(ev) + pv[2 * j], 0.0f);
+                    x[2 * j + 1] = __builtin_fmaxf(hi16(ev) + pv[2 * j + 1], 0.0f);
                 }
-            } else {
-                const uint16_t* e = p.enc + (size_t)frame * p.enc_stride + 2 * lane;
 #pragma unroll
-                for (int j = 0; j < KP; ++j) evs[j] = *(const uint32_t*)(e + 128 * j);
-            }
+                for (int r = 0; r < 2; ++r) {
+                    float a = 0.0f;
 #pragma unroll
-            for (int j = 0; j < KP; ++j) {
-                const uint32_t ev = evs[j];
-                x[2 * j] = __builtin_fmaxf(lo16(ev) + pv[2 * j], 0.0f);
-                x[2 * j + 1] = __builtin_fmaxf(hi16(ev) + pv[2 * j + 1], 0.0f);
-            }
-#pragma unroll
-            for (int r = 0; r < 2; ++r) {
-                float a = 0.0f;
-#pragma unroll
-                for (int j = 0; j < KP; ++j) {
-                    float w0, w1;
-                    if constexpr (kInt8) {
-                        w0 = (float)(int8_t)(wj[r][j] & 0xffu);
-                        w1 = (float)(int8_t)((wj[r][j] >> 8) & 0xffu);
-                    } else {
-                        w0 = lo16(wj[r][j]);
-                        w1 = hi16(wj[r][j]);
+                    for (int j = 0; j < KP; ++j) {
+                        float w0, w1;
+                        if constexpr (kInt8) {
+                            w0 = (float)(int8_t)(wj[r][j] & 0xffu);
+                            w1 = (float)(int8_t)((wj[r][j] >> 8) & 0xffu);
+                        } else {
+                            w0 = lo16(wj[r][j]);
+                            w1 = hi16(wj[r][j]);
+                        }
+                        a = __builtin_fmaf(w0, x[2 * j], a);
+                        a = __builtin_fmaf(w1, x[2 * j + 1], a);
                     }
-                    a = __builtin_fmaf(w0, x[2 * j], a);
-                    a = __builtin_fmaf(w1, x[2 * j + 1], a);
-                }
-                const float score = __builtin_fmaf(wjs[r], wave_sum(a), wjb[r]);
-                const int id = jid[r];
-                if (id >= T) {
-                    if (lane == 0) dur_sc[id - T] = score;  // workgroup 0 only
-                } else if (id >= 0) {
-                    if (score > bs || (score == bs && id < bi)) { bs = score; bi = id; }
+                    acc[c][r] = a;
                 }
             }
-            if (lane == 0)
-                best_w[wave] = bi == 0x7fffffff ? 0ull
-                                                : (((unsigned long long)key_bits(bs) << 32) | ((unsigned long long)(0xffffu - (uint32_t)bi) << 16));
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1)
+#pragma unroll
+                for (int c = 0; c < kWin; ++c)
+#pragma unroll
+                    for (int r = 0; r < 2; ++r) acc[c][r] += __shfl_xor(acc[c][r], off, 64);
+#pragma unroll
+            for (int c = 0; c < kWin; ++c) {
+                float bs = -__builtin_huge_valf();
+                int bi = 0x7fffffff;
+#pragma unroll
+                for (int r = 0; r < 2; ++r) {
+                    const float score = __builtin_fmaf(wjs[r], acc[c][r], wjb[r]);
+                    const int id = jid[r];
+                    if (id >= T) {
+                        if (lane == 0) dur_sc[c][id - T] = score;  // workgroup 0 only
+                    } else if (id >= 0) {
+                        if (score > bs || (score == bs && id < bi)) {
+                            bs = score;
+                            bi = id;
+                        }
+                    }
+                }
+                if (lane == 0)
+                    win_w[wave][c] = bi == 0x7fffffff ? 0ull
+                                                      : (((unsigned long long)key_bits(bs) << 32) |
+                                                         ((unsigned long long)(0xffffu - (uint32_t)bi) << 16));
+            }
         }
         __syncthreads();
-        if (tid == 0) {
-            unsigned long long b = best_w[0];
-            for (int i = 1; i < 4; ++i) b = best_w[i] > b ? best_w[i] : b;
-            if (blk == 0) {  // first maximum of the duration scores
+        // thread c: this workgroup's key for window frame c (workgroup 0's with
+        // the first maximum of that frame's duration scores)
+        unsigned long long key = 0ull;
+        if (tid < kWin) {
+            key = win_w[0][tid];
+            for (int i = 1; i < 4; ++i) key = win_w[i][tid] > key ? win_w[i][tid] : key;
+            if (blk == 0) {
                 int d = 0;
                 for (int i = 1; i < D; ++i)
-                    if (dur_sc[i] > dur_sc[d]) d = i;
-                b |= (unsigned long long)d << 13;
+                    if (dur_sc[tid][i] > dur_sc[tid][d]) d = i;
+                key |= (unsigned long long)d << 13;
             }
-            payload_s = b;
         }
-        __syncthreads();
-        pf_base = frame;
+        // a blank run that leaves the window usually lands on its next frame:
+        // that window loads during the barrier (a token's update reloads)
+        pf_base = frame + kWin;
         do_pf = true;
-        const unsigned long long word = barrier(payload_s);
+        unsigned long long mine[kWin];
+        barrier_win(key, mine);
         if (failed) break;
-        // decision: the largest word is the best token; workgroup 0's carries the duration
+        // decisions of the window: per frame the largest key over the
+        // workgroups is the best token; workgroup 0's carries the duration
         {
-            unsigned long long b = tid < nblocks ? word : 0ull;
+            if (tid == 0)
 #pragma unroll
-            for (int off = 32; off > 0; off >>= 1) {
-                const unsigned long long o = __shfl_xor(b, off, 64);
-                b = o > b ? o : b;
-            }
-            if (lane == 0) best_w[wave] = b;
-            if (tid == 0) dur_s = (int)(((uint32_t)word >> 13) & 7u);
+                for (int c = 0; c < kWin; ++c) win_dur[c] = (int)(((uint32_t)mine[c] >> 13) & 7u);
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1)
+#pragma unroll
+                for (int c = 0; c < kWin; ++c) {
+                    const unsigned long long o = __shfl_xor(mine[c], off, 64);
+                    mine[c] = o > mine[c] ? o : mine[c];
+                }
+            if (lane == 0)
+#pragma unroll
+                for (int c = 0; c < kWin; ++c) win_w[wave][c] = mine[c];
             __syncthreads();
-            b = best_w[0];
-            for (int i = 1; i < 4; ++i) b = best_w[i] > b ? best_w[i] : b;
-            const int token = (int)(0xffffu - (((uint32_t)b) >> 16));
-            const int dur = dur_s;
-            __syncthreads();  // best_w / dur_s are reused next step
-            ++steps;
-            if (token != blank) {
-                if (blk == 0 && tid == 0 && count < p.capacity) p.tokens[count] = token;
-                ++count;
-                last = token;
-                emitted = true;
-                valid = false;
-                alt ^= 1;  // the candidate state becomes the committed one
-                if constexpr (kLong) {
+            if (tid < kWin) {
+                unsigned long long b = win_w[0][tid];
+                for (int i = 1; i < 4; ++i) b = win_w[i][tid] > b ? win_w[i][tid] : b;
+                win_tok[tid] = (int)(0xffffu - (((uint32_t)b) >> 16));
+            }
+            __syncthreads();
+            // the greedy rules (decoder.cu:773-783) over the window, identical in
+            // every thread: blank decisions keep the prediction, so later frames'
+            // decisions in the window stand until a token or the window's end
+            const int f0 = frame;
+            int c = 0;
+            while (true) {
+                const int token = win_tok[c], dur = win_dur[c];
+                ++steps;
+                if (token != blank) {
+                    if (blk == 0 && tid == 0 && count < p.capacity) p.tokens[count] = token;
+                    ++count;
+                    last = token;
+                    emitted = true;
+                    valid = false;
+                    alt ^= 1;  // the candidate state becomes the committed one
+                    if constexpr (kLong) {
 #pragma unroll
-                    for (int l = 0; l < 2; ++l) {
-                        c_cur[l] = c_new[l];
+                        for (int l = 0; l < 2; ++l) {
+                            c_cur[l] = c_new[l];
 #pragma unroll
-                        for (int g = 0; g < 4; ++g) rs[l][g] = rs_next[l][g];
+                            for (int g = 0; g < 4; ++g) rs[l][g] = rs_next[l][g];
+                        }
                     }
                 }
+                ++symbols;
+                frame += dur;
+                if (dur != 0 || symbols == p.max_symbols) {
+                    if (dur == 0) ++frame;
+                    symbols = 0;
+                }
+                if (token != blank || frame >= p.frames) break;
+                c = frame - f0;
+                if (c >= kWin) break;
             }
-            ++symbols;
-            frame += dur;
-            if (dur != 0 || symbols == p.max_symbols) {
-                if (dur == 0) ++frame;
-                symbols = 0;
-            }
+            __syncthreads();  // win_w / win_tok / win_dur are reused next round
         }
     }
     if (blk == 0 && tid == 0) {
@@ -624,7 +705,7 @@ __global__ void decode_clear_kernel(uint32_t* ws, int words) {
 // fp16 form: h, c (2 banks x 2 layers) and the prediction; long form: INT8
 // banks (H words), candidate layer-1 output (H), maxima (3 x blocks, <= 6H
 // for H >= 128) and the prediction at the same offset 8H.
-int decode_workspace_words(int hidden) { return kDecState + 9 * hidden; }
+int decode_workspace_words(int hidden) { return kDecState + 9 * hidden + kDecExtWords; }
 
 int launch_tdt_decode(const uint16_t* enc, int frames, int enc_stride, const uint16_t* emb, const uint16_t* table, const uint16_t* const* w_ih,
                       const uint16_t* const* w_hh, const float* const* b_ih, const float* const* b_hh, const uint16_t* w_proj,
