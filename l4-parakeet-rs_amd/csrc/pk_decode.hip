@@ -29,11 +29,16 @@
 // Long form: lane l holds bytes 4l + 256j (j < ceil(H/256)) of every INT8
 // row; a gate's INT8 dot product is summed exactly as an integer over the
 // wave (|sum| <= H * 127 * 127 < 2^24), converted once and scaled by
-// scale / 127.  The cell state stays in the owning wave's registers; the INT8
-// hidden vectors (candidate / committed banks), the candidate fp32 layer-1
-// output and the prediction go through the workspace.  The recurrent sums of
-// both layers are taken in the projection phase, from the candidate state
-// that the next update will consume once a token commits it.
+// scale / 127.  Layer 0 needs no weights of its own once its recurrent sums
+// are known (its input terms are table rows), so every workgroup evaluates all
+// of its units as soon as the token is decided and goes straight on to layer
+// 1: an update costs two grid barriers (after layer 1, after the projection),
+// not three.  The recurrent sums of a candidate state are taken as soon as
+// that state exists (layer 0's next to layer 1, layer 1's in the projection
+// phase) and used by the update after a token commits it.  Layer 1's cell
+// state stays in the owning wave's registers, layer 0's in every thread that
+// evaluates the unit; the INT8 layer-1 banks, the candidate fp32 layer-1
+// output, the layer-0 sums and the prediction go through the workspace.
 #include "pk_kernels.hpp"
 
 namespace pk {
@@ -161,6 +166,8 @@ __global__ __launch_bounds__(kDecThreads, 1) void tdt_decode_kernel(DecodeArgs p
     __shared__ unsigned long long win_w[4][kWin];  // per wave, then the decided key per window frame
     __shared__ int win_tok[kWin], win_dur[kWin];
     __shared__ int stop_s;
+    // long form: the new INT8 layer-0 output, computed whole by every workgroup
+    __shared__ uint32_t q0_s[kLong ? H / 4 : 1];
     const int blk = blockIdx.x, nblocks = gridDim.x;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int gw = blk * 4 + wave;
@@ -273,6 +280,10 @@ __global__ __launch_bounds__(kDecThreads, 1) void tdt_decode_kernel(DecodeArgs p
         ++epoch;
     };
 
+    // long form: layer-0 recurrent sums of the candidate state [bank][H][4 gates]
+    // (the committed bank is the other), published by the unit's owner
+    int32_t* rs0w = (int32_t*)(p.ws + kDecState + 9 * H + kDecExtWords);
+
     // ---- weights into registers --------------------------------------------------
     const bool owns_unit = gw < H;
     const int u = owns_unit ? gw : 0;
@@ -381,6 +392,24 @@ __global__ __launch_bounds__(kDecThreads, 1) void tdt_decode_kernel(DecodeArgs p
         wjb[r] = p.b_joint[row];
     }
 
+    // long form: layer 0 of every unit tid + 256 i is evaluated by this thread in
+    // every workgroup (identical operations, so identical values everywhere):
+    // its bias, committed / candidate cell state and the recurrent sums of the
+    // state the next update consumes
+    constexpr int NU = kLong ? (H + kDecThreads - 1) / kDecThreads : 1;
+    float b0[NU][4], c0c[NU], c0n[NU];
+    int r0[NU][4];
+#pragma unroll
+    for (int i = 0; i < NU; ++i) {
+        const int ui = min(tid + kDecThreads * i, H - 1);
+        c0c[i] = c0n[i] = 0.0f;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            b0[i][g] = p.b_ih[0][g * H + ui] + p.b_hh[0][g * H + ui];
+            r0[i][g] = 0;
+        }
+    }
+
     int frame = 0, symbols = 0, last = blank, count = 0, steps = 0, alt = 0;
     bool emitted = false, valid = false;
     float pv[2 * KP];
@@ -455,38 +484,51 @@ __global__ __launch_bounds__(kDecThreads, 1) void tdt_decode_kernel(DecodeArgs p
                     if (lane == 0) st1(pred + u, a);
                 }
             } else {
-                // ---- layer 0: recurrent sums of the committed state (taken when it
-                // was the candidate) + bias + the token's table row (decoder.cu:619-648)
-                if (owns_unit && lane == 0) {
-                    float s[4];
+                // ---- layer 0 of every unit, in every workgroup: recurrent sums of the
+                // committed state + bias + the token's table row (decoder.cu:619-648)
 #pragma unroll
-                    for (int g = 0; g < 4; ++g) {
-                        const float tv = emitted ? h2f(p.table[(size_t)last * 4 * H + g * H + u]) : 0.0f;
-                        s[g] = __builtin_fmaf((float)rs[0][g], cq[0], bias[0][g]) + tv;
+                for (int i = 0; i < NU; ++i) {
+                    const int ui = tid + kDecThreads * i;
+                    if (ui < H) {
+                        float s[4];
+#pragma unroll
+                        for (int g = 0; g < 4; ++g) {
+                            const float tv = emitted ? h2f(p.table[(size_t)last * 4 * H + g * H + ui]) : 0.0f;
+                            s[g] = __builtin_fmaf((float)r0[i][g], cq[0], b0[i][g]) + tv;
+                        }
+                        float h;
+                        lstm_cell(s, c0c[i], c0n[i], h);
+                        ((uint8_t*)q0_s)[ui] = (uint8_t)quant_i8(h * 127.0f);
                     }
-                    float h;
-                    lstm_cell(s, c_cur[0], c_new[0], h);
-                    qb_s[wave] = (uint32_t)(uint8_t)quant_i8(h * 127.0f);
                 }
                 __syncthreads();
-                if (tid == 0 && 4 * blk < H)
-                    st_word(qbank(alt ^ 1, 0) + blk, qb_s[0] | (qb_s[1] << 8) | (qb_s[2] << 16) | (qb_s[3] << 24));
-                barrier(0);
-                if (failed) break;
                 // ---- layer 1: its recurrent sums + W_ih1 x the new INT8 layer-0
-                // output (decoder.cu:650-670)
+                // output (decoder.cu:650-670); the layer-0 recurrent sums of the new
+                // candidate state go out for the update after it is committed
                 if (owns_unit) {
                     uint32_t x[KD];
 #pragma unroll
-                    for (int j = 0; j < KD; ++j) x[j] = 4 * lane + 256 * j < H ? ld_word(qbank(alt ^ 1, 0) + lane + 64 * j) : 0u;
-                    int in[4];
+                    for (int j = 0; j < KD; ++j) x[j] = 4 * lane + 256 * j < H ? q0_s[lane + 64 * j] : 0u;
+                    int in[4], r0n[4];
 #pragma unroll
                     for (int g = 0; g < 4; ++g) {
-                        int a = 0;
+                        int a = 0, d = 0;
 #pragma unroll
-                        for (int j = 0; j < KD; ++j) a = __builtin_amdgcn_sdot4((int)qw[2][g][j], (int)x[j], a, false);
-                        in[g] = wave_isum(a);
+                        for (int j = 0; j < KD; ++j) {
+                            a = __builtin_amdgcn_sdot4((int)qw[2][g][j], (int)x[j], a, false);
+                            d = __builtin_amdgcn_sdot4((int)qw[0][g][j], (int)x[j], d, false);
+                        }
+                        in[g] = a;
+                        r0n[g] = d;
                     }
+#pragma unroll
+                    for (int off = 32; off > 0; off >>= 1)
+#pragma unroll
+                        for (int g = 0; g < 4; ++g) {
+                            in[g] += __shfl_xor(in[g], off, 64);
+                            r0n[g] += __shfl_xor(r0n[g], off, 64);
+                        }
+                    if (lane < 4) st_word((uint32_t*)rs0w + ((alt ^ 1) * H + u) * 4 + lane, (uint32_t)r0n[lane]);
                     if (lane == 0) {
                         float s[4];
 #pragma unroll
@@ -503,14 +545,12 @@ __global__ __launch_bounds__(kDecThreads, 1) void tdt_decode_kernel(DecodeArgs p
                     st_word(qbank(alt ^ 1, 1) + blk, qb_s[0] | (qb_s[1] << 8) | (qb_s[2] << 16) | (qb_s[3] << 24));
                 barrier(0);
                 if (failed) break;
-                // ---- projection of the new layer-1 output, and the recurrent sums of
-                // this candidate state for the update after it is committed
+                // ---- projection of the new layer-1 output, and the layer-1 recurrent
+                // sums of this candidate state for the update after it is committed
                 if (owns_unit) {
-                    uint32_t xq[2][KD];
+                    uint32_t xq[KD];
 #pragma unroll
-                    for (int l = 0; l < 2; ++l)
-#pragma unroll
-                        for (int j = 0; j < KD; ++j) xq[l][j] = 4 * lane + 256 * j < H ? ld_word(qbank(alt ^ 1, l) + lane + 64 * j) : 0u;
+                    for (int j = 0; j < KD; ++j) xq[j] = 4 * lane + 256 * j < H ? ld_word(qbank(alt ^ 1, 1) + lane + 64 * j) : 0u;
                     float a = 0.0f;
 #pragma unroll
                     for (int j = 0; j < KP; ++j) {
@@ -521,14 +561,21 @@ __global__ __launch_bounds__(kDecThreads, 1) void tdt_decode_kernel(DecodeArgs p
                     a = wave_sum(a) + bpj;
                     if (lane == 0) st1(pred + u, a);
 #pragma unroll
-                    for (int l = 0; l < 2; ++l)
+                    for (int g = 0; g < 4; ++g) {
+                        int d = 0;
 #pragma unroll
-                        for (int g = 0; g < 4; ++g) {
-                            int d = 0;
+                        for (int j = 0; j < KD; ++j) d = __builtin_amdgcn_sdot4((int)qw[1][g][j], (int)xq[j], d, false);
+                        rs_next[1][g] = wave_isum(d);
+                    }
+                }
+                // the candidate's layer-0 sums (published before the last barrier),
+                // consumed by the next update once a token commits this state
 #pragma unroll
-                            for (int j = 0; j < KD; ++j) d = __builtin_amdgcn_sdot4((int)qw[l][g][j], (int)xq[l][j], d, false);
-                            rs_next[l][g] = wave_isum(d);
-                        }
+                for (int i = 0; i < NU; ++i) {
+                    const int ui = tid + kDecThreads * i;
+                    if (ui < H)
+#pragma unroll
+                        for (int g = 0; g < 4; ++g) r0[i][g] = (int)ld_word((const uint32_t*)rs0w + ((alt ^ 1) * H + ui) * 4 + g);
                 }
             }
             barrier(0);
@@ -667,12 +714,11 @@ __global__ __launch_bounds__(kDecThreads, 1) void tdt_decode_kernel(DecodeArgs p
                     valid = false;
                     alt ^= 1;  // the candidate state becomes the committed one
                     if constexpr (kLong) {
+                        c_cur[1] = c_new[1];
 #pragma unroll
-                        for (int l = 0; l < 2; ++l) {
-                            c_cur[l] = c_new[l];
+                        for (int g = 0; g < 4; ++g) rs[1][g] = rs_next[1][g];
 #pragma unroll
-                            for (int g = 0; g < 4; ++g) rs[l][g] = rs_next[l][g];
-                        }
+                        for (int i = 0; i < NU; ++i) c0c[i] = c0n[i];
                     }
                 }
                 ++symbols;
@@ -704,8 +750,9 @@ __global__ void decode_clear_kernel(uint32_t* ws, int words) {
 
 // fp16 form: h, c (2 banks x 2 layers) and the prediction; long form: INT8
 // banks (H words), candidate layer-1 output (H), maxima (3 x blocks, <= 6H
-// for H >= 128) and the prediction at the same offset 8H.
-int decode_workspace_words(int hidden) { return kDecState + 9 * hidden + kDecExtWords; }
+// for H >= 128) and the prediction at the same offset 8H; after the joint
+// rounds' words, the long form's layer-0 recurrent sums (2 banks x H x 4).
+int decode_workspace_words(int hidden) { return kDecState + 9 * hidden + kDecExtWords + 8 * hidden; }
 
 int launch_tdt_decode(const uint16_t* enc, int frames, int enc_stride, const uint16_t* emb, const uint16_t* table, const uint16_t* const* w_ih,
                       const uint16_t* const* w_hh, const float* const* b_ih, const float* const* b_hh, const uint16_t* w_proj,
