@@ -53,8 +53,8 @@ constexpr int kDecState = kDecWords + 2 * kDecMaxBlocks * 2;  // u32 offset of t
 static_assert(kDecState == 1032, "workspace layout");
 // Frames a joint round scores against one prediction (its window), and the
 // words of the joint rounds' barrier: per workgroup one key per window frame,
-// each carrying the barrier tag (2 epoch slots x blocks x kWin u64), after
-// the state vectors.
+// each carrying the barrier tag (2 epoch slots x kWin x 256 u64, word-major so
+// that the poll reads consecutive words), after the state vectors.
 constexpr int kWin = 8;
 constexpr int kDecExtWords = 2 * kDecMaxBlocks * kWin * 2;
 
@@ -243,13 +243,14 @@ __global__ __launch_bounds__(kDecThreads, 1) void tdt_decode_kernel(DecodeArgs p
     // The joint rounds' barrier: thread c < kWin publishes this workgroup's key
     // for window frame c, each key tagged, so all go out together and the poll
     // itself gathers every workgroup's keys (thread t: workgroup t's, in got).
-    unsigned long long* wwords = (unsigned long long*)(p.ws + kDecState + 9 * H);  // [2][blocks][kWin]
+    // word-major ([parity][frame][workgroup]): the poll's lanes read consecutive words
+    unsigned long long* wwords = (unsigned long long*)(p.ws + kDecState + 9 * H);  // [2][kWin][256]
     auto barrier_win = [&](unsigned long long key, unsigned long long (&got)[kWin]) {
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
         const uint32_t tag = (epoch + 1) & 0x1fffu;
         unsigned long long* slot = wwords + (size_t)(epoch & 1) * kDecMaxBlocks * kWin;
-        if (tid < kWin) __hip_atomic_store(slot + blk * kWin + tid, key | tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (tid < kWin) __hip_atomic_store(slot + tid * kDecMaxBlocks + blk, key | tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (do_pf) prefetch();
         do_pf = false;
         uint32_t spins = 0;
@@ -260,7 +261,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void tdt_decode_kernel(DecodeArgs p
             if (tid < nblocks) {
 #pragma unroll
                 for (int c = 0; c < kWin; ++c) {
-                    got[c] = __hip_atomic_load(slot + tid * kWin + c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    got[c] = __hip_atomic_load(slot + c * kDecMaxBlocks + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                     ready = ready && ((uint32_t)got[c] & 0x1fffu) == tag;
                 }
             }
