@@ -122,6 +122,12 @@ __device__ __forceinline__ int swz(int row, int chunk) { return row * kRowBytes 
 // Weight row (within the wave's 64 columns) held by MFMA row i of block bj.
 __device__ __forceinline__ int wrow(int i, int bj) { return ((i >> 2) << 4) + (bj << 2) + (i & 3); }
 
+// XOR key of a 64-byte G128A8 weight row's 16-byte chunks: the 16 rows one
+// fragment read covers, wrow(0..15, bj) = {0-3, 16-19, 32-35, 48-51} + 4 bj,
+// would put rows 16 apart on the same banks; keyed by (row >> 4) & 3 their
+// 8-byte reads fall on distinct banks (64 banks; at most 2 lanes a bank with 32).
+__device__ __forceinline__ int g128a8_key(int row) { return (row >> 4) & 3; }
+
 // Four unsigned nibbles (byte j of `w`, low nibble = k j, high = k 4+j) ->
 // eight int8 (q - z), natural k order, as two dwords.
 __device__ __forceinline__ void u4x8_minus_z(uint32_t w, uint32_t zz, uint32_t& first, uint32_t& second) {
@@ -400,8 +406,10 @@ __device__ __forceinline__ void weight_frag(const uint8_t* Bs, int row, int g, i
         if constexpr (F == FMT_G128A8) {
             gs = *(const v4f*)(sc + wn * 64 + g * 16 + bj * 4);
             const uint32_t zz = (uint32_t)z * 0x01010101u;
-            const uint2 q0 = *(const uint2*)(Bs + row * 64 + 8 * g);
-            const uint2 q1 = *(const uint2*)(Bs + row * 64 + 32 + 8 * g);
+            // logical bytes 8g and 32 + 8g of the row, its 16-byte chunks stored XOR-keyed
+            const int key = g128a8_key(row), half = (g & 1) << 3;
+            const uint2 q0 = *(const uint2*)(Bs + row * 64 + ((((g >> 1)) ^ key) << 4) + half);
+            const uint2 q1 = *(const uint2*)(Bs + row * 64 + (((2 + (g >> 1)) ^ key) << 4) + half);
             u4x8_minus_z(q0.x, zz, w0.x, w0.y);
             u4x8_minus_z(q0.y, zz, w0.z, w0.w);
             u4x8_minus_z(q1.x, zz, w1.x, w1.y);

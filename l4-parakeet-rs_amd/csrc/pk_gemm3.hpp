@@ -104,6 +104,9 @@ __global__ __launch_bounds__(kThreads, 2) void gemm3_kernel(GemmArgs p) {
             if constexpr (T::bRow == 128) {
                 row = o >> 7;
                 c = ((o >> 4) & 7) ^ swz_key(row);
+            } else if constexpr (F == FMT_G128A8) {
+                row = o >> 6;
+                c = ((o >> 4) & 3) ^ g128a8_key(row);
             } else {
                 row = o / T::bRow;
                 c = (o % T::bRow) / 16;
@@ -237,6 +240,37 @@ __global__ __launch_bounds__(kThreads, 2) void gemm3_kernel(GemmArgs p) {
                 store_tab(nstep);  // fetched a step ago
                 fetch_tab();       // for the step after nstep
             }
+            if constexpr (F == FMT_G128A8) {
+                // Software-pipelined over the wave's 4 kAI blocks (row block ai,
+                // column block bj): block b's exact int32 group sum goes to one
+                // of three rotating registers while block b - 2's is converted
+                // and scaled, so the MFMAs overlap the VALU work instead of
+                // waiting on it (and the next block's MFMAs on the register).
+                v4i gi[3];
+#pragma unroll
+                for (int b = 0; b < 4 * kAI + 2; ++b) {
+                    const int ai = b >> 2, bj = b & 3;
+                    if (b < 4 * kAI) {
+                        if (bj == 0 && ai + 1 < kAI) {
+                            const int row = wm * 16 * kAI + (ai + 1) * 16 + l16;
+                            y0 = *(const uint4*)(As + swz(row, g));
+                            y1 = *(const uint4*)(As + swz(row, 4 + g));
+                        }
+                        gi[b % 3] = __builtin_amdgcn_mfma_i32_16x16x64_i8(as_v4i(w0[bj]), as_v4i(x0), v4i{0, 0, 0, 0}, 0, 0, 0);
+                        gi[b % 3] = __builtin_amdgcn_mfma_i32_16x16x64_i8(as_v4i(w1[bj]), as_v4i(x1), gi[b % 3], 0, 0, 0);
+                        if (bj == 3) {
+                            x0 = y0;
+                            x1 = y1;
+                        }
+                    }
+                    if (b >= 2) {
+                        const int pa = (b - 2) >> 2, pj = (b - 2) & 3;
+#pragma unroll
+                        for (int r = 0; r < 4; ++r)
+                            accf[pa][pj][r] = __builtin_fmaf((float)gi[(b - 2) % 3][r], gs[pj][r], accf[pa][pj][r]);
+                    }
+                }
+            } else
 #pragma unroll
             for (int ai = 0; ai < kAI; ++ai) {
                 if (ai + 1 < kAI) {
