@@ -759,6 +759,53 @@ def run_long_decode(pk, orc, H, int8, frames, seed, T=1025, D=5):
     return (toks, res, work), ref
 
 
+@pytest.mark.parametrize("form", ["long", "fp16"])
+def test_tdt_decode_full_length(pk, orc, form):
+    """An hour of synthetic audio (45000 frames, H = 640, INT8 joint) in one
+    launch, twice: tens of thousands of barrier epochs (tag reuse, slot
+    parity, the joint rounds' windows) must end with status 0 and identical
+    tokens.  The greedy decode is causal (a decision at frame f reads encoder
+    rows <= f and the tokens before it), so the full decode's tokens begin
+    with exactly the oracle's decode of the first 1100 frames."""
+    H, T, D, frames, head = 640, 1025, 5, 45000, 1100
+    note(f"tdt decode full length form={form} frames={frames}")
+    lstm, proj, wj, bj, enc, emb = decode_case(H, T, D, frames, 977, True)
+    bj[T - 1] += 0.8  # about a token every 5 frames, as in speech; duration 0 rare, 1 preferred
+    bj[T] -= 3.0
+    bj[T + 1] += 0.5
+    wq, ws = orc.quantize_int8_rows(wj)
+    d = [dev(a) for a in lstm]
+    cap = frames * 10
+    work = torch.zeros(pk.lib.pk_tdt_decode_workspace_bytes(H) // 4, dtype=torch.int32, device="cuda")
+    table_d = torch.zeros((T - 1, 4 * H), dtype=torch.float16, device="cuda")
+    enc_d, emb_d, wq_d, ws_d, bj_d = dev(enc), dev(emb), dev(wq), dev(ws), dev(bj)
+    runs = []
+    for _ in range(2):
+        toks = torch.zeros(cap, dtype=torch.int32, device="cuda")
+        res = torch.zeros(4, dtype=torch.int32, device="cuda")
+        if form == "long":
+            got = pk.launch_decode(enc_d, frames, (emb_d,) + tuple(d), (dev(proj[0]), dev(proj[1])), (wq_d, bj_d), toks, res,
+                                   work, input_table=table_d, joint_int8=True, joint_scales=ws_d, hidden=H,
+                                   token_outputs=T, durations=D)
+            assert got == "long"
+        else:
+            pk.call("pk_tdt_decode", enc_d, frames, H, emb_d, *d, dev(proj[0]), dev(proj[1]), wq_d, 1, ws_d, bj_d, H, T,
+                    D, 10, toks, cap, res, work, work.numel() * 4)
+        count, frame, status, steps = (int(v) for v in host(res))
+        note(f"  {count} tokens, {steps} joint steps, final frame {frame}, status {status}")
+        assert status == 0 and frame >= frames and frames // 50 <= count <= cap and steps >= count
+        runs.append(host(toks)[:count])
+    assert np.array_equal(runs[0], runs[1])
+    assert np.all((runs[0] >= 0) & (runs[0] < T - 1))
+    joint = (wq, ws, bj)
+    if form == "long":
+        ref, _, _ = orc.tdt_decode_long(enc[:head], host(table_d), lstm[1:], proj, joint, T, D)
+    else:
+        ref, _, _ = orc.tdt_decode(enc[:head], emb, lstm, proj, joint, T, D)
+    assert len(ref) >= 20
+    assert np.array_equal(runs[0][:len(ref)], ref)
+
+
 @pytest.mark.parametrize("H,int8,frames", [(640, False, 1100), (640, True, 96), (128, True, 96), (128, False, 96)])
 def test_tdt_decode_long(pk, orc, H, int8, frames):
     """decoder.cu:452-784 long-request decode (INT8 recurrent weights derived
