@@ -912,7 +912,11 @@ int launch_local_attention(bool packed, const uint16_t* query, const uint16_t* k
         interior(s);
         boundary(side->stream);
         if (hipEventRecord(side->join, side->stream) == hipSuccess && hipStreamWaitEvent(s, side->join, 0) == hipSuccess) return 0;
-        hipStreamSynchronize(side->stream);  // could not order the join on the stream: complete it here
+        // could not order the join on the stream: complete the side stream's work here
+        if (hipStreamSynchronize(side->stream) != hipSuccess) {
+            set_error("attention: the boundary stream did not complete");
+            return -3;
+        }
         return 0;
     }
     interior(s);
