@@ -63,6 +63,68 @@ __device__ __forceinline__ void s4x8_to_s8(uint32_t w, uint32_t& lo, uint32_t& h
     hi = ((h ^ 0x08080808u) + 0x78787878u) ^ 0x80808080u;
 }
 
+// One butterfly level (off = 1, 2, 4, ..., 32, taken in ascending order),
+// without the LDS crossbar: xor 1 and xor 2 are quad permutes; once every lane
+// of a quad (of an 8-lane half row) holds the same partial, the row
+// half-mirror (mirror) delivers exactly the xor-4 (xor-8) partner's value; for
+// xor 16 / 32, v_permlane16_swap / v_permlane32_swap of a register with itself
+// hands every lane both values of its pair {v[l & ~off], v[l | off]}, which a
+// sum or maximum combines directly (the same operands as own + partner).
+template <int CTRL> __device__ __forceinline__ int dpp_mov(int v) { return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false); }
+__device__ __forceinline__ int partner(int v, int off) {  // off <= 8
+    switch (off) {
+    case 1: return dpp_mov<0xB1>(v);   // quad_perm [1, 0, 3, 2]
+    case 2: return dpp_mov<0x4E>(v);   // quad_perm [2, 3, 0, 1]
+    case 4: return dpp_mov<0x141>(v);  // row_half_mirror
+    default: return dpp_mov<0x140>(v); // row_mirror
+    }
+}
+// {v[l & ~off], v[l | off]} for off = 16 or 32
+__device__ __forceinline__ void pair_of(int v, int off, int& a, int& b) {
+    if (off == 16) {
+        const auto q = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+        a = (int)q[0];
+        b = (int)q[1];
+    } else {
+        const auto q = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+        a = (int)q[0];
+        b = (int)q[1];
+    }
+}
+__device__ __forceinline__ int add_level(int v, int off) {
+    if (off <= 8) return v + partner(v, off);
+    int a, b;
+    pair_of(v, off, a, b);
+    return a + b;
+}
+__device__ __forceinline__ float add_level(float v, int off) {
+    if (off <= 8) return v + __int_as_float(partner(__float_as_int(v), off));
+    int a, b;
+    pair_of(__float_as_int(v), off, a, b);
+    return __int_as_float(a) + __int_as_float(b);
+}
+__device__ __forceinline__ float max_level(float v, int off) {
+    if (off <= 8) return __builtin_fmaxf(v, __int_as_float(partner(__float_as_int(v), off)));
+    int a, b;
+    pair_of(__float_as_int(v), off, a, b);
+    return __builtin_fmaxf(__int_as_float(a), __int_as_float(b));
+}
+__device__ __forceinline__ unsigned long long max_level(unsigned long long v, int off) {
+    const int lo = (int)(uint32_t)v, hi = (int)(uint32_t)(v >> 32);
+    unsigned long long x, y;
+    if (off <= 8) {
+        x = v;
+        y = ((unsigned long long)(uint32_t)partner(hi, off) << 32) | (uint32_t)partner(lo, off);
+    } else {
+        int la, lb, ha, hb;
+        pair_of(lo, off, la, lb);
+        pair_of(hi, off, ha, hb);
+        x = ((unsigned long long)(uint32_t)ha << 32) | (uint32_t)la;
+        y = ((unsigned long long)(uint32_t)hb << 32) | (uint32_t)lb;
+    }
+    return x > y ? x : y;
+}
+
 // ---- reductions over a 256-thread block ------------------------------------
 __device__ __forceinline__ float wave_max(float v) {
     for (int off = 32; off > 0; off >>= 1) v = __builtin_fmaxf(v, __shfl_xor(v, off, 64));

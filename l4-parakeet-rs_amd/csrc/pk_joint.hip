@@ -284,7 +284,7 @@ __global__ __launch_bounds__(256) void joint_scan_kernel(ScanArgs p) {
                     sum = __builtin_fmaf(w1, x[2 * j + 1], sum);
                 }
 #pragma unroll
-                for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
+                for (int off = 1; off < 64; off <<= 1) sum = add_level(sum, off);
                 const float score = __builtin_fmaf(wsc[r], sum, wb[r]);
                 const int id = rid[r];
                 if (id >= T) {  // duration id - T, first maximum wins
@@ -334,10 +334,7 @@ __global__ __launch_bounds__(256) void joint_scan_kernel(ScanArgs p) {
         dur = (int)(((uint32_t)__shfl(mine, 0, 64) >> 13) & 7u);
         unsigned long long best = watcher ? mine : 0ull;
 #pragma unroll
-        for (int off = 32; off > 0; off >>= 1) {
-            const unsigned long long o = __shfl_xor(best, off, 64);
-            best = o > best ? o : best;
-        }
+        for (int off = 1; off < 64; off <<= 1) best = max_level(best, off);
         token = (int)(0xffffu - (((uint32_t)best) >> 16));
         // the LDS reduction slots are reused next step
         __syncthreads();
