@@ -166,7 +166,7 @@ __global__ __launch_bounds__(256) void pack_vectors_kernel(const uint16_t* __res
         m = __builtin_fmaxf(m, __builtin_fabsf(v[i]));
     }
 #pragma unroll
-    for (int off = 1; off < 16; off <<= 1) m = __builtin_fmaxf(m, __shfl_xor(m, off, 64));
+    for (int off = 1; off < 16; off <<= 1) m = max_level(m, off);  // DPP levels within the 16-lane vector
     const float scale = m > 0.0f ? m / (kInt4 ? 7.0f : 127.0f) : 1.0f;
     if (j == 0) scales[vec] = scale;
     float qv[8];
