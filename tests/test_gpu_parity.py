@@ -368,8 +368,11 @@ def test_int4g128_a16(pk, orc, m, n, k):
     assert_close(host(out), orc.gemm_g128_a16(x, q, s, z))
 
 
-@pytest.mark.parametrize("m,n,k", [(750, 4096, 1024), (97, 1024, 4096)])
+@pytest.mark.parametrize("m,n,k", [(750, 4096, 1024), (97, 1024, 4096), (300, 1040, 1024)])
 def test_int4g128_a8_exact(pk, orc, m, n, k):
+    """INT4-g128 weights x INT8 activations: fp32 outputs bit-exact against
+    the oracle (the last case's ragged column tile reads clamped weight rows
+    through the same XOR-keyed LDS layout)."""
     note(f"g128 a8 m={m} n={n} k={k}")
     x = acts(m, k, 111)
     w = weights(n, k, 112)
