@@ -326,6 +326,13 @@ int32_t pk_gemm(int32_t format, int32_t epilogue, const void* a, const void* b, 
                 const uint16_t* g_scales, const uint16_t* g_zeros, void* out, uint8_t* out_meta, int32_t ldo,
                 void* stream);
 
+/* Tile shape pk_gemm launches for an m x n output of `format` / `epilogue`
+ * (host only, no GPU work): returns the tile rows (64, 128 or 256) and sets
+ * *tile_cols (128, or 256 for the one-workgroup engine), or a negative PK_E_*
+ * status.  No counterpart in the reference (its kernels have one tile
+ * shape); it lets callers and tests see which kernel variant a shape runs. */
+int32_t pk_gemm_tile(int32_t format, int32_t epilogue, int32_t m, int32_t n, int32_t* tile_cols);
+
 /* ---- TDT joint (decoder.cu:690-759) ------------------------------------------ */
 
 /* Batch-1 joint GEMV for `steps` consecutive frames:

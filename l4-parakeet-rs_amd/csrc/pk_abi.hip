@@ -227,6 +227,17 @@ int32_t pk_gemm(int32_t format, int32_t epilogue, const void* a, const void* b, 
     return launch_gemm(format, epilogue, g, STREAM);
 }
 
+int32_t pk_gemm_tile(int32_t format, int32_t epilogue, int32_t m, int32_t n, int32_t* tile_cols) {
+    int cols = 0;
+    const int r = gemm_tile_plan(format, epilogue, m, n, &cols);
+    if (r < 0) {
+        set_error(r == PK_E_ARG ? "unknown format %d" : "PK_GEMM_TILE_ROWS must be 64, 128 or 256", format);
+        return r;
+    }
+    if (tile_cols) *tile_cols = cols;
+    return r;
+}
+
 int32_t pk_linear_fp16_epilogue(const uint16_t* in, const uint16_t* w, const float* bias, const uint16_t* residual, uint16_t* out,
                                 int32_t m, int32_t n, int32_t k, float out_scale, float res_scale, int32_t act, void* stream) {
     return pk_gemm(FMT_F16, EPI_F16, in, w, m, n, k, nullptr, nullptr, 1.0f, bias, residual, out_scale, res_scale, act, nullptr,
@@ -435,7 +446,8 @@ int32_t pk_joint_gemv(const void* w, int32_t w_int8, const float* w_scales, cons
     }
     if (!need(w, "weight") || !need(enc, "enc") || !need(pred, "pred") || !need(scores, "scores")) return PK_E_ARG;
     if (w_int8 && !need(w_scales, "w_scales")) return PK_E_ARG;
-    if (((uintptr_t)w & 15) || ((size_t)enc_stride % 2)) { set_error("joint weight must be 16-byte aligned"); return PK_E_ALIGN; }
+    if ((uintptr_t)w & 15) { set_error("joint weight must be 16-byte aligned"); return PK_E_ALIGN; }
+    if ((uintptr_t)enc & 1) { set_error("joint enc must be 2-byte aligned (fp16)"); return PK_E_ALIGN; }
     launch_joint(w, w_int8, w_scales, bias, enc, pred, scores, decision, outputs, hidden, token_outputs, durations, steps, enc_stride,
                  STREAM);
     return check_launch("joint_gemv");

@@ -67,44 +67,70 @@ static int launch_two(const GemmArgs& a, hipStream_t s) {
     return 0;
 }
 
-// 64-row tiles when 128-row tiles would number at most a quarter of the CUs
-// (INT4-g128 x INT8 FF2 at T = 750: 59 -> 48 us); 128-row tiles (twice as
-// many) when 256-row tiles would fill at most half of the two-per-CU workgroup
-// slots, by measurement: C1, attention-out / FF2 and
-// the sparse FF2 at T = 7500 and the INT4-g128 x INT8 linears at T = 750 run
-// 18-29 % faster; grids of 256-row tiles filling more than half the slots run
-// slower with 128 rows (pw1 at T = 7500: 480 tiles, -5 %).
-// PK_GEMM_TILE_ROWS = 64, 128 or 256 forces one size (measurement only).
-template <int F, int E>
-static int launch_two(const GemmArgs& a, hipStream_t s) {
+// Tile rows of the occupancy-2 engine for an m x n output: 64-row tiles when
+// 128-row tiles would number at most a quarter of the CUs (INT4-g128 x INT8
+// FF2 at T = 750: 59 -> 48 us); 128-row tiles (twice as many) when 256-row
+// tiles would fill at most half of the two-per-CU workgroup slots, by
+// measurement: C1, attention-out / FF2 and the sparse FF2 at T = 7500 and the
+// INT4-g128 x INT8 linears at T = 750 run 18-29 % faster; grids of 256-row
+// tiles filling more than half the slots run slower with 128 rows (pw1 at
+// T = 7500: 480 tiles, -5 %).  PK_GEMM_TILE_ROWS = 64, 128 or 256 forces one
+// size (measurement only); any other value is rejected at the first launch.
+static int forced_tile_rows() {
     static const int force = [] {
         const char* v = getenv("PK_GEMM_TILE_ROWS");
-        return v ? atoi(v) : 0;
+        if (!v || !*v) return 0;
+        const int r = atoi(v);
+        return (r == 64 || r == 128 || r == 256) ? r : -1;
     }();
-    const int tiles256 = ((a.m + 255) / 256) * ((a.n + g3::kBN - 1) / g3::kBN);
-    const int tiles128 = ((a.m + 127) / 128) * ((a.n + g3::kBN - 1) / g3::kBN);
-    if (force ? force == 64 : 4 * tiles128 <= cu_count()) return launch_two<F, E, 2>(a, s);
-    const bool small = force ? force == 128 : 2 * tiles256 <= 2 * cu_count();
-    return small ? launch_two<F, E, 4>(a, s) : launch_two<F, E, 8>(a, s);
+    return force;
+}
+
+static int byte_tile_rows(int m, int n) {
+    const int tiles256 = ((m + 255) / 256) * ((n + g3::kBN - 1) / g3::kBN);
+    const int tiles128 = ((m + 127) / 128) * ((n + g3::kBN - 1) / g3::kBN);
+    const int force = forced_tile_rows();
+    if (force > 0) return force;
+    if (4 * tiles128 <= cu_count()) return 64;
+    return 2 * tiles256 <= 2 * cu_count() ? 128 : 256;
 }
 
 // Engine per format, by measurement on MI355X: the occupancy-2 engine for the
 // byte formats, the 256x256 engine for fp16 activations (FP16, G128A16, Q4K),
 // whose 64-K steps make its per-step barriers relatively more costly.
 // Grids too small to give each CU a 256 x 256 tile take the occupancy-2
-// engine's 128 x 128 tiles for the fp16-activation formats too.
+// engine's 128 x 128 tiles for the fp16-activation formats too.  Returns the
+// tile rows and sets *cols (256 for the one-workgroup engine, 128 otherwise).
+static int tile_plan(int fmt, int epi, int m, int n, int* cols) {
+    *cols = g3::kBN;
+    if (fmt == FMT_Q4K || (fmt == FMT_FP8 && epi == EPI_GLU)) {
+        *cols = kBlockN;
+        return kBlockM;
+    }
+    if (fmt == FMT_F16 || fmt == FMT_G128A16) {
+        const int tiles256 = ((m + 255) / 256) * ((n + g3::kBN - 1) / g3::kBN);
+        const int tiles128 = ((m + 127) / 128) * ((n + g3::kBN - 1) / g3::kBN);
+        if (4 * tiles128 <= cu_count()) return 64;
+        if (tiles256 <= cu_count()) return 128;
+        *cols = kBlockN;
+        return kBlockM;
+    }
+    return byte_tile_rows(m, n);
+}
+
 template <int F, int E>
 static int launch_fmt(const GemmArgs& a, hipStream_t s) {
-    if constexpr (F == FMT_F16 || F == FMT_G128A16) {
-        const int tiles256 = ((a.m + 255) / 256) * ((a.n + g3::kBN - 1) / g3::kBN);
-        const int tiles128 = ((a.m + 127) / 128) * ((a.n + g3::kBN - 1) / g3::kBN);
-        if (4 * tiles128 <= cu_count()) return launch_two<F, E, 2>(a, s);
-        if (tiles256 <= cu_count()) return launch_two<F, E, 4>(a, s);
+    int cols = 0;
+    const int rows = tile_plan(F, E == EPI_F16_RES ? EPI_F16 : E, a.m, a.n, &cols);
+    if constexpr (F == FMT_Q4K) {
         return launch_one<F, E>(a, s);
-    } else if constexpr (F == FMT_Q4K) {
-        return launch_one<F, E>(a, s);
+    } else if constexpr (F == FMT_F16 || F == FMT_G128A16) {
+        if (cols == kBlockN) return launch_one<F, E>(a, s);
+        return rows == 64 ? launch_two<F, E, 2>(a, s) : launch_two<F, E, 4>(a, s);
     } else {
-        return launch_two<F, E>(a, s);
+        if (rows == 64) return launch_two<F, E, 2>(a, s);
+        if (rows == 128) return launch_two<F, E, 4>(a, s);
+        return launch_two<F, E, 8>(a, s);
     }
 }
 
@@ -178,6 +204,15 @@ int launch_gemm(int fmt, int epi, const GemmArgs& a, hipStream_t s) {
         set_error("operand pointers must be 16-byte aligned");
         return -2;
     }
+    // The epilogue reads residual rows, weight scales and biases as 16-byte vectors.
+    if (((uintptr_t)a.residual | (uintptr_t)a.w_scales | (uintptr_t)a.bias) & 15) {
+        set_error("residual, weight scale and bias pointers must be 16-byte aligned");
+        return -2;
+    }
+    if (forced_tile_rows() < 0) {
+        set_error("PK_GEMM_TILE_ROWS must be 64, 128 or 256");
+        return -1;
+    }
     if (a.m == 0) return 0;
     switch (fmt) {
     case FMT_FP8: return by_epi<FMT_FP8>(epi, a, s);
@@ -192,6 +227,12 @@ int launch_gemm(int fmt, int epi, const GemmArgs& a, hipStream_t s) {
     }
     set_error("unknown format %d", fmt);
     return -4;
+}
+
+int gemm_tile_plan(int fmt, int epi, int m, int n, int* cols) {
+    if (fmt < FMT_FP8 || fmt > FMT_Q4K) return -4;
+    if (forced_tile_rows() < 0) return -1;
+    return tile_plan(fmt, epi == EPI_F16_RES ? EPI_F16 : epi, m, n, cols);
 }
 
 }  // namespace pk

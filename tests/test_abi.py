@@ -89,3 +89,31 @@ def test_exl3_layout_matches_reference_tests(lib):
             assert int(out[5]) == case["trellis_bytes"] and int(out[6]) == case["scale_bytes"]
     out = np.zeros(7, np.uint64)
     assert fn(4, 4, 0, out.ctypes.data) < 0
+
+
+def _tile(lib, fmt, epi, m, n):
+    fn = lib.pk_gemm_tile
+    fn.argtypes = [ctypes.c_int32] * 4 + [ctypes.POINTER(ctypes.c_int32)]
+    fn.restype = ctypes.c_int32
+    cols = ctypes.c_int32(0)
+    rows = fn(fmt, epi, m, n, ctypes.byref(cols))
+    return rows, cols.value
+
+
+@pytest.mark.skipif(os.environ.get("PK_GEMM_TILE_ROWS") is not None, reason="tile size forced")
+def test_gemm_tile_plan(lib):
+    """The launcher's tile choice on a 256-CU part (the host-only fallback
+    when no GPU is visible, and MI355X's count): the BASELINE sizes the
+    full-size parity tests use reach the 256-row kernels."""
+    FP8, I8, G128A8, F16, I8SKIP, Q4K = 0, 1, 3, 4, 6, 7
+    EPI_F16, EPI_F8, EPI_F32 = 0, 1, 3
+    assert _tile(lib, FP8, EPI_F8, 7500, 4096) == (256, 128)
+    assert _tile(lib, FP8, EPI_F16, 45000, 1024) == (256, 128)
+    assert _tile(lib, G128A8, EPI_F16, 45000, 1024) == (256, 128)
+    assert _tile(lib, I8, EPI_F8, 7500, 4096) == (256, 128)
+    assert _tile(lib, FP8, EPI_F16, 7500, 1024) == (128, 128)
+    assert _tile(lib, I8SKIP, EPI_F32, 7500, 1024) == (128, 128)
+    assert _tile(lib, G128A8, EPI_F16, 750, 1024) == (64, 128)
+    assert _tile(lib, F16, EPI_F16, 45000, 1024) == (256, 256)
+    assert _tile(lib, Q4K, EPI_F16, 16, 256) == (256, 256)
+    assert _tile(lib, 99, EPI_F16, 16, 256)[0] == -4
