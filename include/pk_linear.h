@@ -366,6 +366,21 @@ int32_t pk_joint_scan(const void* weight, int32_t weight_int8, const float* w_sc
                       int32_t token_outputs, int32_t durations, int32_t frames, int32_t enc_stride,
                       int32_t max_symbols, int32_t* state, uint32_t* workspace, void* stream);
 
+/* pk_joint_scan without the workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.  The
+ * 512 words of scratch are a static device array of the library (one copy
+ * per GPU, held until the process ends; its address is looked up once per
+ * device), cleared by a fill kernel at the start of every call.  Same
+ * arguments, limits and results as pk_joint_scan; token_outputs + durations
+ * above 2048 return PK_E_SHAPE.  Calls on one GPU share the scratch: calls
+ * on one stream are ordered and independent, calls that overlap on one GPU
+ * (different streams) race.  Allocates nothing. */
+int32_t pk_joint_scan_noalloc(const void* weight, int32_t weight_int8, const float* w_scales, const float* bias,
+                              const uint16_t* enc, const float* pred, int32_t outputs, int32_t hidden,
+                              int32_t token_outputs, int32_t durations, int32_t frames, int32_t enc_stride,
+                              int32_t max_symbols, int32_t* state, void* stream);
+
 /* ---- TDT greedy decode (decoder.cu:146-445, fp16 prediction network) --------
  * The whole batch-1 greedy decode of one utterance in one persistent launch:
  * 2-layer LSTM prediction network (weights [4H x H] fp16 with gate rows

@@ -453,9 +453,9 @@ int32_t pk_joint_gemv(const void* w, int32_t w_int8, const float* w_scales, cons
     return check_launch("joint_gemv");
 }
 
-int32_t pk_joint_scan(const void* w, int32_t w_int8, const float* w_scales, const float* bias, const uint16_t* enc, const float* pred,
-                      int32_t outputs, int32_t hidden, int32_t token_outputs, int32_t durations, int32_t frames, int32_t enc_stride,
-                      int32_t max_symbols, int32_t* state, uint32_t* workspace, void* stream) {
+static int32_t joint_scan_checks(const void* w, int32_t w_int8, const float* w_scales, const uint16_t* enc, const float* pred,
+                                 int32_t outputs, int32_t hidden, int32_t token_outputs, int32_t durations, int32_t frames,
+                                 int32_t enc_stride, int32_t max_symbols, int32_t* state) {
     if (outputs <= 0 || hidden <= 0 || hidden > 1024 || hidden % 128 || token_outputs <= 0 || durations <= 0 || durations > 8 ||
         token_outputs + durations > outputs || token_outputs + durations > 2048 || token_outputs > 65535 || frames < 0 ||
         enc_stride < hidden || max_symbols <= 0) {
@@ -463,16 +463,50 @@ int32_t pk_joint_scan(const void* w, int32_t w_int8, const float* w_scales, cons
                   hidden, token_outputs, durations, frames, enc_stride, max_symbols);
         return PK_E_SHAPE;
     }
-    if (!need(w, "weight") || !need(enc, "enc") || !need(pred, "pred") || !need(state, "state") || !need(workspace, "workspace"))
-        return PK_E_ARG;
+    if (!need(w, "weight") || !need(enc, "enc") || !need(pred, "pred") || !need(state, "state")) return PK_E_ARG;
     if (w_int8 && !need(w_scales, "w_scales")) return PK_E_ARG;
-    if (((uintptr_t)w | (uintptr_t)enc | (uintptr_t)workspace) & 7 || enc_stride % 2) {
-        set_error("joint scan weight, enc and workspace must be 8-byte aligned, enc_stride even");
+    if (((uintptr_t)w | (uintptr_t)enc) & 7 || enc_stride % 2) {
+        set_error("joint scan weight and enc must be 8-byte aligned, enc_stride even");
+        return PK_E_ALIGN;
+    }
+    return PK_OK;
+}
+
+int32_t pk_joint_scan(const void* w, int32_t w_int8, const float* w_scales, const float* bias, const uint16_t* enc, const float* pred,
+                      int32_t outputs, int32_t hidden, int32_t token_outputs, int32_t durations, int32_t frames, int32_t enc_stride,
+                      int32_t max_symbols, int32_t* state, uint32_t* workspace, void* stream) {
+    const int32_t st = joint_scan_checks(w, w_int8, w_scales, enc, pred, outputs, hidden, token_outputs, durations, frames, enc_stride,
+                                         max_symbols, state);
+    if (st != PK_OK) return st;
+    if (!need(workspace, "workspace")) return PK_E_ARG;
+    if ((uintptr_t)workspace & 7) {
+        set_error("joint scan workspace must be 8-byte aligned");
         return PK_E_ALIGN;
     }
     launch_joint_scan(w, w_int8, w_scales, bias, enc, pred, outputs, hidden, token_outputs, durations, frames, enc_stride, max_symbols,
                       state, workspace, STREAM);
     return check_launch("joint_scan");
+}
+
+int32_t pk_joint_scan_noalloc(const void* w, int32_t w_int8, const float* w_scales, const float* bias, const uint16_t* enc,
+                              const float* pred, int32_t outputs, int32_t hidden, int32_t token_outputs, int32_t durations,
+                              int32_t frames, int32_t enc_stride, int32_t max_symbols, int32_t* state, void* stream) {
+    // The static scratch holds the published words of at most 64 workgroups
+    // of 32 joint rows: token_outputs + durations <= 2048.
+    if (token_outputs > 0 && durations > 0 && token_outputs + durations > 2048) {
+        set_error("joint scan without workspace: token_outputs + durations = %d exceeds the 2048 rows its %d-word static "
+                  "scratch serves", token_outputs + durations, kJointScanWorkspaceWords);
+        return PK_E_SHAPE;
+    }
+    const int32_t st = joint_scan_checks(w, w_int8, w_scales, enc, pred, outputs, hidden, token_outputs, durations, frames, enc_stride,
+                                         max_symbols, state);
+    if (st != PK_OK) return st;
+    uint32_t* scratch = nullptr;
+    const int r = joint_scan_scratch(&scratch);
+    if (r < 0) return r;
+    launch_joint_scan(w, w_int8, w_scales, bias, enc, pred, outputs, hidden, token_outputs, durations, frames, enc_stride, max_symbols,
+                      state, scratch, STREAM);
+    return check_launch("joint_scan_noalloc");
 }
 
 int32_t pk_tdt_decode_workspace_bytes(int32_t hidden) { return hidden > 0 ? 4 * decode_workspace_words(hidden) : PK_E_SHAPE; }

@@ -3,6 +3,8 @@
 // then the greedy token / duration decision.  The GEMV is HBM/L2-bound: one
 // wave64 per output row, each lane streaming 16 bytes (int8) or 16 bytes of
 // fp16 per pass, the activation vector staged once per block in LDS.
+#include <mutex>
+
 #include "pk_kernels.hpp"
 
 namespace pk {
@@ -384,6 +386,50 @@ int launch_joint_scan(const void* w, int w_int8, const float* w_scales, const fl
 #undef PK_SCAN_CASE
     default: break;
     }
+    return 0;
+}
+
+// ---- the same scan with library-owned scratch (no allocation) ---------------
+//
+// The scan's workspace (abort flag + 2 x 64 published words, 512 words) in a
+// file-scope device array: each GPU the library runs on holds its own copy
+// until the process ends.  Host code never passes the array's name to a
+// kernel (on the host it is only a stand-in for the symbol): the device
+// address of each GPU's copy is looked up once per device with
+// hipGetSymbolAddress, with that device current, and kept.  Every call on a
+// GPU shares that GPU's copy; launch_joint_scan clears it with a fill kernel
+// before the scan kernel, so calls on one stream are independent, and calls
+// that overlap on one GPU (different streams) race on it.
+static __device__ __align__(256) uint32_t scratch[kJointScanWorkspaceWords];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex scratch_mutex;
+uint32_t* scratch_ptr[kMaxDevices] = {};
+}  // namespace
+
+int joint_scan_scratch(uint32_t** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) {
+        set_error("hipGetDevice failed: %s", hipGetErrorString(e));
+        return -3;
+    }
+    if (dev < 0 || dev >= kMaxDevices) {
+        set_error("device %d beyond the %d devices the static scan scratch tracks", dev, kMaxDevices);
+        return -4;
+    }
+    std::lock_guard<std::mutex> lock(scratch_mutex);
+    if (!scratch_ptr[dev]) {
+        void* ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr) {
+            set_error("hipGetSymbolAddress(scan scratch) failed: %s", hipGetErrorString(e));
+            return -3;
+        }
+        scratch_ptr[dev] = (uint32_t*)ptr;
+    }
+    *out = scratch_ptr[dev];
     return 0;
 }
 

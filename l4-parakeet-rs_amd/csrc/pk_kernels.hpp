@@ -29,6 +29,10 @@ int launch_joint_scan(const void* w, int w_int8, const float* w_scales, const fl
                       int outputs, int hidden, int token_outputs, int durations, int frames, int enc_stride, int max_symbols,
                       int* state, uint32_t* workspace, hipStream_t s);
 
+// Device address of this device's static scan scratch (kJointScanWorkspaceWords
+// words), looked up on the first call per device.
+int joint_scan_scratch(uint32_t** out);
+
 int decode_workspace_words(int hidden);
 // emb set: fp16 prediction network; table set (emb unused): the long form.
 int launch_tdt_decode(const uint16_t* enc, int frames, int enc_stride, const uint16_t* emb, const uint16_t* table, const uint16_t* const* w_ih,

@@ -92,6 +92,7 @@ SIGNATURES = {
     "pk_gemm": (I, [I, I, P, P, I, I, I, P, P, F, P, P, F, F, I, P, P, P, P, I, P]),
     "pk_joint_gemv": (I, [P, I, P, P, P, P, P, P, I, I, I, I, I, I, P]),
     "pk_joint_scan": (I, [P, I, P, P, P, P, I, I, I, I, I, I, I, P, P, P]),
+    "pk_joint_scan_noalloc": (I, [P, I, P, P, P, P, I, I, I, I, I, I, I, P, P]),
     "pk_tdt_decode_workspace_bytes": (I, [I]),
     "pk_tdt_decode": (I, [P, I, I, P, P, P, P, P, P, P, P, P, P, P, P, I, P, P, I, I, I, I, P, I, P, P,
                           ctypes.c_uint64, P]),
