@@ -845,6 +845,7 @@ def main():
                     help="run only the HBM-streaming joint GEMV and a 256 MiB device copy, for rocprofv3 passes")
     ap.add_argument("--only-attention", action="store_true",
                     help="run only the attention measurements and a 256 MiB device copy, for rocprofv3 passes")
+    ap.add_argument("--classes", action="store_true", help="with --only-stack: also time every kernel class")
     ap.add_argument("--only-decode", action="store_true", help="run only the TDT decode measurements")
     ap.add_argument("--only-stack", action="store_true",
                     help="run only the 24-layer stack (warmup + steps, no other measurement), for rocprofv3 passes")
@@ -901,8 +902,11 @@ def main():
     torch.cuda.synchronize()
     if args.only_stack:
         ms = time_events(torch, stack.step, args.steps, stream)
-        print(json.dumps({"stack_ms_per_step": ms, "steps": args.steps,
-                          "TOPS": FLOP_PER_FRAME * args.frames / (ms * 1e-3) / 1e12}), flush=True)
+        out = {"stack_ms_per_step": ms, "steps": args.steps,
+               "TOPS": FLOP_PER_FRAME * args.frames / (ms * 1e-3) / 1e12}
+        if args.classes:
+            out["stack_classes"] = class_times(pk, torch, stack, stream)
+        print(json.dumps(out), flush=True)
         return
     print("[bench] timing", file=sys.stderr, flush=True)
     t0 = time.perf_counter()

@@ -26,6 +26,129 @@ namespace g3 {
 
 constexpr int kBN = 128, kThreads = 256;
 
+// Loads issued from inline asm are invisible to the compiler's wait
+// insertion: the code waits for them with an explicit s_waitcnt and then
+// passes the destinations through an empty asm (launder), so that no use is
+// scheduled before the wait.
+__device__ __forceinline__ uint4 asm_load4(const void* ptr) {
+    v4i r;
+    asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(r) : "v"(ptr) : "memory");
+    return __builtin_bit_cast(uint4, r);
+}
+__device__ __forceinline__ uint32_t asm_load1(const void* ptr) {
+    uint32_t r;
+    asm volatile("global_load_dword %0, %1, off" : "=v"(r) : "v"(ptr) : "memory");
+    return r;
+}
+__device__ __forceinline__ uint32_t launder(uint32_t x) {
+    asm volatile("" : "+v"(x));
+    return x;
+}
+__device__ __forceinline__ uint4 launder(uint4 x) {
+    v4i y = __builtin_bit_cast(v4i, x);
+    asm volatile("" : "+v"(y));
+    return __builtin_bit_cast(uint4, y);
+}
+
+// Epilogue whose scale loads are issued (as inline asm, invisible to the
+// compiler's wait insertion) before `issue` (the next tile's first direct-to-
+// LDS loads, kIssue per wave), then waited for with vmcnt(kIssue): the wait
+// never covers the next tile's loads.  Non-residual epilogues only.
+template <int F, int E, int kAI, int kIssue, typename Issue>
+__device__ __forceinline__ void epilogue_defer(const GemmArgs& p, v4f (&accf)[kAI][4], v4i (&acci)[kAI][4], int m0, int n0, int wm,
+                                               int wn, int lane, bool has_next, Issue&& issue) {
+    using T = FmtTraits<F>;
+    const int g = lane >> 4, l16 = lane & 15;
+    const int gcol = n0 + wn * 64 + g * 16;
+    const int ccol = min(gcol, p.n - 16);
+    const bool col_live = gcol < p.n;
+    const float* wsp = p.w_scales ? p.w_scales + ccol : (const float*)p.a;
+    const float* bp = p.bias ? p.bias + ccol : wsp;
+    uint4 wq[4], bq[4];
+    uint32_t rq[kAI];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) wq[j] = asm_load4(wsp + 4 * j);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) bq[j] = asm_load4(bp + 4 * j);
+#pragma unroll
+    for (int ai = 0; ai < kAI; ++ai) {
+        const int row = min(m0 + wm * 16 * kAI + ai * 16 + l16, p.m - 1);
+        const float* rp = p.row_scales ? p.row_scales + row : (const float*)p.a;
+        rq[ai] = asm_load1(rp);
+    }
+    if (has_next) {
+        issue();
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kIssue) : "memory");
+    } else {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+    // the loads above have landed: pass every destination through an empty
+    // asm so that no use can be scheduled before the wait
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        wq[j] = launder(wq[j]);
+        bq[j] = launder(bq[j]);
+    }
+#pragma unroll
+    for (int ai = 0; ai < kAI; ++ai) rq[ai] = launder(rq[ai]);
+    float wsv[16], bsv[16];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const float4 w4 = __builtin_bit_cast(float4, wq[j]);
+        const float4 b4 = __builtin_bit_cast(float4, bq[j]);
+        wsv[4 * j] = p.w_scales ? w4.x : 1.f; wsv[4 * j + 1] = p.w_scales ? w4.y : 1.f;
+        wsv[4 * j + 2] = p.w_scales ? w4.z : 1.f; wsv[4 * j + 3] = p.w_scales ? w4.w : 1.f;
+        bsv[4 * j] = p.bias ? b4.x : 0.f; bsv[4 * j + 1] = p.bias ? b4.y : 0.f;
+        bsv[4 * j + 2] = p.bias ? b4.z : 0.f; bsv[4 * j + 3] = p.bias ? b4.w : 0.f;
+    }
+#pragma unroll
+    for (int ai = 0; ai < kAI; ++ai) {
+        const int grow = m0 + wm * 16 * kAI + ai * 16 + l16;
+        const bool live = grow < p.m && col_live;
+        const float rs = p.row_scales ? __builtin_bit_cast(float, rq[ai]) : p.in_scale;
+        float v[16];
+#pragma unroll
+        for (int bj = 0; bj < 4; ++bj)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) v[bj * 4 + r] = T::kInt ? (float)acci[ai][bj][r] : accf[ai][bj][r];
+        if (p.fused_scale) {
+#pragma unroll
+            for (int j = 0; j < 16; ++j) v[j] = __builtin_fmaf(v[j], rs * wsv[j], bsv[j]);
+        } else {
+#pragma unroll
+            for (int j = 0; j < 16; ++j) v[j] = __builtin_fmaf(v[j] * rs, wsv[j], bsv[j]);
+        }
+        if constexpr (E == EPI_F32) {
+            if (live) {
+                float4* o = (float4*)((float*)p.out + (size_t)grow * p.ldo + gcol);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) o[j] = float4{v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]};
+            }
+        } else if constexpr (E == EPI_F16) {
+            uint32_t h[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                float x0 = v[2 * j] * p.out_scale, x1 = v[2 * j + 1] * p.out_scale;
+                x0 = p.act == 1 ? silu(x0) : (p.act == 2 ? __builtin_fmaxf(x0, 0.0f) : x0);
+                x1 = p.act == 1 ? silu(x1) : (p.act == 2 ? __builtin_fmaxf(x1, 0.0f) : x1);
+                h[j] = (uint32_t)f2h(x0) | ((uint32_t)f2h(x1) << 16);
+            }
+            if (live) {
+                uint4* o = (uint4*)((uint16_t*)p.out + (size_t)grow * p.ldo + gcol);
+                o[0] = uint4{h[0], h[1], h[2], h[3]};
+                o[1] = uint4{h[4], h[5], h[6], h[7]};
+            }
+        } else {
+            uint32_t w[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) w[j] = silu_fp8x4(v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]);
+            if (live) *(uint4*)((uint8_t*)p.out + (size_t)grow * p.ldo + gcol) = uint4{w[0], w[1], w[2], w[3]};
+        }
+    }
+}
+
+
+
 // Tile rows: 32 * kAI (kAI = 16-row MFMA blocks per wave: 8 for 256-row tiles,
 // 4 for 128-row tiles, which double the tile count of small grids).  Weight
 // tile bytes of one step, and the LDS of one workgroup: two activation tiles,
@@ -74,8 +197,11 @@ __global__ __launch_bounds__(kThreads, 2) void gemm3_kernel(GemmArgs p) {
     const int q = lane >> 3;
     const uint32_t a_cq = (uint32_t)((lane & 7) ^ ((q >> 1) & 1) ^ (((q >> 2) & 1) << 1) ^ ((q & 1) << 2));
     int a_row = 0;  // m0 + wave*64 + q of the issue tile
-    // Formats whose decode leaves the registers keep the 8 offsets instead.
-    constexpr bool kPreOff = F == FMT_FP8 || F == FMT_I8 || F == FMT_I8_SKIP || F == FMT_F16;
+    // FP8 / INT8 read activation fragments two row blocks ahead (three in
+    // registers), the others one ahead; the formats with registers to spare
+    // keep the 8 load offsets instead of deriving them at issue time.
+    constexpr bool kAhead2 = F == FMT_FP8 || F == FMT_I8;
+    constexpr bool kPreOff = F == FMT_I8_SKIP || F == FMT_F16;
     uint32_t a_off[kPreOff ? kAI : 1];
     uint32_t b_off[L::kBPerWave];
     uint32_t b_q4k = 0;  // Q4K: bit i set when weight load i carries quant bytes
@@ -190,6 +316,14 @@ __global__ __launch_bounds__(kThreads, 2) void gemm3_kernel(GemmArgs p) {
         fetch_tab();  // the second step
     }
     int buf = 0;
+    // fp16 / fp32 epilogues without a residual (FP8, INT8): the next tile's
+    // first loads are issued inside the epilogue, after its scale loads, so
+    // that its wait for the scales does not also wait for them; the first
+    // step of the next tile then waits for them with vmcnt(stores issued
+    // since), not for the epilogue's stores (QKV at T = 45000: 174 -> 162 us).
+    constexpr bool kDefer = kAhead2 && (E == EPI_F16 || E == EPI_F32);
+    constexpr int kStores = kAI * (E == EPI_F16 ? 2 : 4);
+    bool prev_full = false;  // the last epilogue issued all kStores stores
 
     v4f accf[kAI][4];
     v4i acci[kAI][4];
@@ -207,13 +341,14 @@ __global__ __launch_bounds__(kThreads, 2) void gemm3_kernel(GemmArgs p) {
             }
 
         for (int step = 0; step < steps; ++step) {
-            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            if (kDefer && step == 0 && prev_full) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kStores) : "memory");
+            else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
             __syncthreads();
             // The next step's (or next tile's first step's) activations load
             // into the other buffer, which every wave finished with last step.
             int nstep = -1;
             if (step + 1 < steps) nstep = step + 1;
-            else if (t_next < ntiles) {
+            else if (t_next < ntiles && !kDefer) {
                 set_tile(t_next, m0, n0);
                 nstep = 0;
             }
@@ -227,7 +362,15 @@ __global__ __launch_bounds__(kThreads, 2) void gemm3_kernel(GemmArgs p) {
                 weight_frag<F>(Bs, wn * 64 + wrow(l16, bj), g, bj, wn, step, tab_s + (step & 1) * kBN, tab_z + (step & 1) * kBN,
                                w0[bj], w1[bj], gs[bj]);
             uint4 x0, x1, y0, y1;
-            {
+            uint4 xr0[3], xr1[3];  // kAhead2: row blocks ai, ai + 1, ai + 2 in slots ai % 3 ...
+            if constexpr (kAhead2) {
+#pragma unroll
+                for (int i = 0; i < 2; ++i) {
+                    const int row = wm * 16 * kAI + i * 16 + l16;
+                    xr0[i] = *(const uint4*)(As + swz(row, g));
+                    xr1[i] = *(const uint4*)(As + swz(row, 4 + g));
+                }
+            } else {
                 const int row = wm * 16 * kAI + l16;
                 x0 = *(const uint4*)(As + swz(row, g));
                 x1 = *(const uint4*)(As + swz(row, 4 + g));
@@ -270,6 +413,37 @@ __global__ __launch_bounds__(kThreads, 2) void gemm3_kernel(GemmArgs p) {
                             accf[pa][pj][r] = __builtin_fmaf((float)gi[(b - 2) % 3][r], gs[pj][r], accf[pa][pj][r]);
                     }
                 }
+                // Issue order per block: its activation reads (every fourth
+                // block), its two MFMAs, then the eight conversions / FMAs of
+                // block b - 2, so the VALU work interleaves with the MFMAs
+                // (INT4-g128 x INT8 linears at T = 45000: 4-7 % faster; the
+                // residual variant, short of registers, ran 5 % slower with it).
+                if constexpr (E != EPI_F16_RES)
+#pragma unroll
+                for (int b = 0; b < 4 * kAI + 2; ++b) {
+                    if (b < 4 * kAI) {
+                        if ((b & 3) == 0 && (b >> 2) + 1 < kAI) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+                        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+                    }
+                    if (b >= 2) __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
+                }
+            } else if constexpr (kAhead2) {
+#pragma unroll
+                for (int ai = 0; ai < kAI; ++ai) {
+                    if (ai + 2 < kAI) {
+                        const int row = wm * 16 * kAI + (ai + 2) * 16 + l16;
+                        xr0[(ai + 2) % 3] = *(const uint4*)(As + swz(row, g));
+                        xr1[(ai + 2) % 3] = *(const uint4*)(As + swz(row, 4 + g));
+                    }
+#pragma unroll
+                    for (int bj = 0; bj < 4; ++bj) mfma_step<F>(accf[ai][bj], acci[ai][bj], w0[bj], w1[bj], xr0[ai % 3], xr1[ai % 3], gs[bj]);
+                }
+                constexpr int kMfma = F == FMT_FP8 ? 4 : 8;
+#pragma unroll
+                for (int ai = 0; ai < kAI; ++ai) {
+                    if (ai + 2 < kAI) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x008, kMfma, 0);
+                }
             } else
 #pragma unroll
             for (int ai = 0; ai < kAI; ++ai) {
@@ -294,20 +468,24 @@ __global__ __launch_bounds__(kThreads, 2) void gemm3_kernel(GemmArgs p) {
                 x0 = y0;
                 x1 = y1;
             }
-            if constexpr (F == FMT_FP8 || F == FMT_I8) {
-                constexpr int kMfma = F == FMT_FP8 ? 4 : 8;
-#pragma unroll
-                for (int ai = 0; ai < kAI; ++ai) {
-                    if (ai + 1 < kAI) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-                    __builtin_amdgcn_sched_group_barrier(0x008, kMfma, 0);
-                }
-            }
             buf ^= 1;
         }
         blocks += kAI * steps;
 
-        if constexpr (E == EPI_F16_RES) epilogue<F, EPI_F16, true, kAI>(p, accf, acci, cur_m0, cur_n0, wm, wn, lane);
-        else epilogue<F, E, false, kAI>(p, accf, acci, cur_m0, cur_n0, wm, wn, lane);
+        if constexpr (E == EPI_F16_RES) {
+            epilogue<F, EPI_F16, true, kAI>(p, accf, acci, cur_m0, cur_n0, wm, wn, lane);
+        } else if constexpr (kDefer) {
+            const bool has_next = t_next < ntiles;
+            if (has_next) set_tile(t_next, m0, n0);
+            static_assert(L::kBLoads % 4 == 0, "every wave issues the same number of weight loads");
+            epilogue_defer<F, E, kAI, kAI + L::kBPerWave>(p, accf, acci, cur_m0, cur_n0, wm, wn, lane, has_next, [&] {
+                issue_a(0, buf);
+                issue_b(0);
+            });
+            prev_full = cur_m0 + kBM <= p.m && cur_n0 + kBN <= p.n;
+        } else {
+            epilogue<F, E, false, kAI>(p, accf, acci, cur_m0, cur_n0, wm, wn, lane);
+        }
         if (t_next >= ntiles) break;
         t = t_next;
     }
