@@ -255,9 +255,9 @@ def time_events(torch, fn, reps, stream):
     return start.elapsed_time(end) / reps  # ms
 
 
-# The stack's largest time share (measured per class by class_times; see the
-# committed kernel trace): INT4-g128 x INT8 FF contract 4096 -> 1024 with the
-# fp16 + residual epilogue.
+# The stack's largest time share (measured per class by class_times in every
+# run; profiled by rocprofv3): INT4-g128 x INT8 FF contract 4096 -> 1024 with
+# the fp16 + residual epilogue.
 DOMINANT = ("int4g128", "res", D, FF)
 
 
