@@ -327,11 +327,14 @@ int32_t pk_gemm(int32_t format, int32_t epilogue, const void* a, const void* b, 
                 void* stream);
 
 /* Tile shape pk_gemm launches for an m x n output of `format` / `epilogue`
- * (host only, no GPU work): returns the tile rows (64, 128 or 256) and sets
- * *tile_cols (128, or 256 for the one-workgroup engine), or a negative PK_E_*
- * status.  No counterpart in the reference (its kernels have one tile
- * shape); it lets callers and tests see which kernel variant a shape runs. */
-int32_t pk_gemm_tile(int32_t format, int32_t epilogue, int32_t m, int32_t n, int32_t* tile_cols);
+ * (host only, no GPU work): returns the tile rows (32, 64, 128 or 256) and
+ * sets *tile_cols (128, or 256 for the one-workgroup 256 x 256 engine) and
+ * *stages (2 for the double-buffered engines; more for the one-tile-per-
+ * workgroup ring used when the tiles do not outnumber the CUs), or returns a
+ * negative PK_E_* status.  Either pointer may be NULL.  No counterpart in the
+ * reference (its kernels have one tile shape); it lets callers and tests see
+ * which kernel variant a shape runs. */
+int32_t pk_gemm_tile(int32_t format, int32_t epilogue, int32_t m, int32_t n, int32_t* tile_cols, int32_t* stages);
 
 /* ---- TDT joint (decoder.cu:690-759) ------------------------------------------ */
 

@@ -227,14 +227,15 @@ int32_t pk_gemm(int32_t format, int32_t epilogue, const void* a, const void* b, 
     return launch_gemm(format, epilogue, g, STREAM);
 }
 
-int32_t pk_gemm_tile(int32_t format, int32_t epilogue, int32_t m, int32_t n, int32_t* tile_cols) {
-    int cols = 0;
-    const int r = gemm_tile_plan(format, epilogue, m, n, &cols);
+int32_t pk_gemm_tile(int32_t format, int32_t epilogue, int32_t m, int32_t n, int32_t* tile_cols, int32_t* stages) {
+    int cols = 0, st = 0;
+    const int r = gemm_tile_plan(format, epilogue, m, n, &cols, &st);
     if (r < 0) {
         set_error(r == PK_E_ARG ? "unknown format %d" : "PK_GEMM_TILE_ROWS must be 64, 128 or 256", format);
         return r;
     }
     if (tile_cols) *tile_cols = cols;
+    if (stages) *stages = st;
     return r;
 }
 

@@ -67,6 +67,56 @@ static int launch_two(const GemmArgs& a, hipStream_t s) {
     return 0;
 }
 
+static int forced_tile_rows();
+
+// One tile per workgroup with an S-stage ring (grids of at most one tile per CU).
+template <int F, int E, int kAI>
+static int launch_ring(const GemmArgs& a, hipStream_t s) {
+    using L = g3::LS<F, kAI>;
+    static std::once_flag once;
+    static hipError_t attr = hipSuccess;
+    std::call_once(once, [] {
+        attr = hipFuncSetAttribute((const void*)g3::gemm3_ring_kernel<F, E, kAI>, hipFuncAttributeMaxDynamicSharedMemorySize, L::kBytes);
+    });
+    if (attr != hipSuccess) {
+        set_error("hipFuncSetAttribute(LDS %d bytes) failed: %s", L::kBytes, hipGetErrorString(attr));
+        return -3;
+    }
+    const int tiles = ((a.m + L::kBM - 1) / L::kBM) * ((a.n + g3::kBN - 1) / g3::kBN);
+    hipLaunchKernelGGL((g3::gemm3_ring_kernel<F, E, kAI>), dim3(tiles), dim3(g3::kThreads), L::kBytes, s, a);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        set_error("gemm launch (fmt %d, epi %d) failed: %s", F, E, hipGetErrorString(e));
+        return -3;
+    }
+    return 0;
+}
+
+// Formats with a ring variant and the tile rows it takes for an m x n
+// output: the smallest tile (32, 64 or 128 rows) whose tile count fits one
+// workgroup per CU, or 0 when even 128-row tiles outnumber the CUs.
+static bool has_ring(int fmt, int epi) {
+    return (fmt == FMT_FP8 || fmt == FMT_I8 || fmt == FMT_G128A8 || fmt == FMT_G128A16) && epi != EPI_GLU && epi != EPI_F8_24;
+}
+template <int F> static int ring_stages_of(int kAI) {
+    return kAI == 1 ? g3::LS<F, 1>::kS : (kAI == 2 ? g3::LS<F, 2>::kS : g3::LS<F, 4>::kS);
+}
+static int ring_stages(int fmt, int kAI) {
+    switch (fmt) {
+    case FMT_FP8: return ring_stages_of<FMT_FP8>(kAI);
+    case FMT_I8: return ring_stages_of<FMT_I8>(kAI);
+    case FMT_G128A8: return ring_stages_of<FMT_G128A8>(kAI);
+    default: return ring_stages_of<FMT_G128A16>(kAI);
+    }
+}
+static int ring_rows(int m, int n) {
+    if (forced_tile_rows() != 0) return 0;
+    const int cols = (n + g3::kBN - 1) / g3::kBN;
+    for (int rows = 32; rows <= 128; rows *= 2)
+        if (((m + rows - 1) / rows) * cols <= cu_count()) return rows;
+    return 0;
+}
+
 // Tile rows of the occupancy-2 engine for an m x n output: 64-row tiles when
 // 128-row tiles would number at most a quarter of the CUs (INT4-g128 x INT8
 // FF2 at T = 750: 59 -> 48 us); 128-row tiles (twice as many) when 256-row
@@ -101,8 +151,16 @@ static int byte_tile_rows(int m, int n) {
 // Grids too small to give each CU a 256 x 256 tile take the occupancy-2
 // engine's 128 x 128 tiles for the fp16-activation formats too.  Returns the
 // tile rows and sets *cols (256 for the one-workgroup engine, 128 otherwise).
-static int tile_plan(int fmt, int epi, int m, int n, int* cols) {
+static int tile_plan(int fmt, int epi, int m, int n, int* cols, int* stages) {
     *cols = g3::kBN;
+    *stages = 2;
+    if (has_ring(fmt, epi)) {
+        const int r = ring_rows(m, n);
+        if (r) {
+            *stages = ring_stages(fmt, r / 32);
+            return r;
+        }
+    }
     if (fmt == FMT_Q4K || (fmt == FMT_FP8 && epi == EPI_GLU)) {
         *cols = kBlockN;
         return kBlockM;
@@ -120,8 +178,13 @@ static int tile_plan(int fmt, int epi, int m, int n, int* cols) {
 
 template <int F, int E>
 static int launch_fmt(const GemmArgs& a, hipStream_t s) {
-    int cols = 0;
-    const int rows = tile_plan(F, E == EPI_F16_RES ? EPI_F16 : E, a.m, a.n, &cols);
+    int cols = 0, stages = 0;
+    const int rows = tile_plan(F, E == EPI_F16_RES ? EPI_F16 : E, a.m, a.n, &cols, &stages);
+    if constexpr (F == FMT_FP8 || F == FMT_I8 || F == FMT_G128A8 || F == FMT_G128A16) {
+        if constexpr (E != EPI_GLU && E != EPI_F8_24) {
+            if (stages > 2) return rows == 32 ? launch_ring<F, E, 1>(a, s) : (rows == 64 ? launch_ring<F, E, 2>(a, s) : launch_ring<F, E, 4>(a, s));
+        }
+    }
     if constexpr (F == FMT_Q4K) {
         return launch_one<F, E>(a, s);
     } else if constexpr (F == FMT_F16 || F == FMT_G128A16) {
@@ -229,10 +292,10 @@ int launch_gemm(int fmt, int epi, const GemmArgs& a, hipStream_t s) {
     return -4;
 }
 
-int gemm_tile_plan(int fmt, int epi, int m, int n, int* cols) {
+int gemm_tile_plan(int fmt, int epi, int m, int n, int* cols, int* stages) {
     if (fmt < FMT_FP8 || fmt > FMT_Q4K) return -4;
     if (forced_tile_rows() < 0) return -1;
-    return tile_plan(fmt, epi == EPI_F16_RES ? EPI_F16 : epi, m, n, cols);
+    return tile_plan(fmt, epi == EPI_F16_RES ? EPI_F16 : epi, m, n, cols, stages);
 }
 
 }  // namespace pk

@@ -497,5 +497,170 @@ __global__ __launch_bounds__(kThreads, 2) void gemm3_kernel(GemmArgs p) {
     }
 }
 
+
+// ---- small grids: one tile per workgroup, an S-stage ring -----------------
+//
+// When a launch has no more tiles than CUs (INT4-g128 at
+// T = 750), every workgroup computes exactly one tile and the K-loop is the
+// whole latency chain: with the engine's one-step prefetch each K-step waits
+// for a memory round trip.  This variant gives the one workgroup of a CU an
+// S-stage LDS ring of (activation + weight) stages, so that a stage's loads
+// have S - 1 steps to land, and one barrier per step: at step s the wave
+// waits for stage s (vmcnt counts only the younger stages), the barrier
+// makes it visible and frees the slot of step s - 1, stage s + S - 1 starts
+// loading into that slot, and the fragments of stage s are read and
+// multiplied.  The INT4-g128 group tables of the tile's columns (all K groups)
+// are loaded once into [group][column] fp32 scales and u8 zero points and
+// indexed by the step's group.  Arithmetic, fragment layouts and
+// epilogues are those of gemm3_kernel, so results are identical.
+template <int F, int kAI> struct LS {
+    static constexpr int kBM = 32 * kAI;
+    static constexpr int kATile = kBM * kRowBytes;
+    static constexpr int kBTile = kBN * FmtTraits<F>::bRow;
+    static constexpr int kStageBytes = kATile + kBTile;
+    static constexpr bool kG128 = (F == FMT_G128A8 || F == FMT_G128A16);
+    static constexpr int kTabBytes = kG128 ? kMaxG128Groups * kBN * 5 : 0;   // fp32 scales + u8 zeros [group][column]
+    static constexpr int kFit = (150 * 1024 - kTabBytes) / kStageBytes;
+    static constexpr int kS = kFit > 8 ? 8 : kFit;
+    static constexpr int kTab = kS * kStageBytes;
+    static constexpr int kBytes = kTab + kTabBytes;
+    static constexpr int kBLoads = kBTile / 1024;
+    static constexpr int kBPerWave = kBLoads / 4;
+    static constexpr int kOps = kAI + kBPerWave;  // direct-to-LDS loads per wave and stage
+    static_assert(kBLoads % 4 == 0 && kS >= 3 && kBytes <= 160 * 1024, "ring layout");
+};
+
+template <int N> __device__ __forceinline__ void wait_vm() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory"); }
+
+// vmcnt(kOps * younger) for a runtime count of younger stages (0 .. 7).
+template <int kOps> __device__ __forceinline__ void wait_stages(int younger) {
+    switch (younger) {
+    case 0: wait_vm<0>(); break;
+    case 1: wait_vm<kOps>(); break;
+    case 2: wait_vm<2 * kOps>(); break;
+    case 3: wait_vm<3 * kOps>(); break;
+    case 4: wait_vm<4 * kOps>(); break;
+    case 5: wait_vm<5 * kOps>(); break;
+    case 6: wait_vm<6 * kOps>(); break;
+    default: wait_vm<7 * kOps>(); break;
+    }
+}
+
+template <int F, int E, int kAI>
+__global__ __launch_bounds__(kThreads, 1) void gemm3_ring_kernel(GemmArgs p) {
+    using T = FmtTraits<F>;
+    using L = LS<F, kAI>;
+    constexpr int kS = L::kS, kBM = L::kBM;
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int g = lane >> 4, l16 = lane & 15;
+    const int tiles_n = (p.n + kBN - 1) / kBN;
+    const int tiles_m = (p.m + kBM - 1) / kBM;
+    const int tile = blockIdx.x;
+    if (tile >= tiles_m * tiles_n) return;
+    // tiles of one column strip are consecutive blocks (the strip's weights stay in L2)
+    const int m0 = (tile % tiles_m) * kBM, n0 = (tile / tiles_m) * kBN;
+    const size_t lda = (size_t)p.k * T::aElemNum / T::aElemDen;
+    const size_t ldb = (size_t)p.k * T::bNum / T::bDen;
+    const int steps = p.k / T::kStep;
+    const int groups = p.k >> 7;
+    const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)lds;
+    float* tab_s = (float*)(lds + L::kTab);
+    uint8_t* tab_z = lds + L::kTab + kMaxG128Groups * kBN * 4;
+
+    const int q = lane >> 3;
+    const uint32_t a_cq = (uint32_t)((lane & 7) ^ ((q >> 1) & 1) ^ (((q >> 2) & 1) << 1) ^ ((q & 1) << 2));
+    const int a_row = m0 + wave * 8 * kAI + q;
+    uint32_t a_off[kAI], b_off[L::kBPerWave];
+#pragma unroll
+    for (int i = 0; i < kAI; ++i) {
+        const int x = (wave * kAI + i) & 7;
+        const uint32_t ki = (uint32_t)((((x >> 1) & 1) << 1) | (((x ^ (x >> 2)) & 1) << 2));
+        a_off[i] = (uint32_t)min(a_row + 8 * i, p.m - 1) * (uint32_t)lda + ((a_cq ^ ki) << 4);
+    }
+#pragma unroll
+    for (int i = 0; i < L::kBPerWave; ++i) {
+        const int o = (i * 4 + wave) * 1024 + lane * 16;
+        int row, c;
+        if constexpr (T::bRow == 128) {
+            row = o >> 7;
+            c = ((o >> 4) & 7) ^ swz_key(row);
+        } else if constexpr (F == FMT_G128A8) {
+            row = o >> 6;
+            c = ((o >> 4) & 3) ^ g128a8_key(row);
+        } else {
+            row = o / T::bRow;
+            c = (o % T::bRow) / 16;
+        }
+        b_off[i] = (uint32_t)min(n0 + row, p.n - 1) * (uint32_t)ldb + (uint32_t)(c * 16);
+    }
+    auto issue = [&](int step) {
+        const uint32_t sbase = lds_base + (uint32_t)((step % kS) * L::kStageBytes);
+#pragma unroll
+        for (int i = 0; i < kAI; ++i) dma16(p.a + (size_t)step * kRowBytes, a_off[i], sbase + (wave * kAI + i) * 1024);
+#pragma unroll
+        for (int i = 0; i < L::kBPerWave; ++i)
+            dma16(p.b + (size_t)step * T::bRow, b_off[i], sbase + L::kATile + (i * 4 + wave) * 1024);
+    };
+
+    const int pre = min(kS - 1, steps);
+    for (int s = 0; s < pre; ++s) issue(s);
+    // Group tables of the tile's columns, all K groups, loaded after the
+    // first stages (whose latency they share): [group][column] fp32 scales
+    // and u8 zero points.
+    if constexpr (L::kG128) {
+        for (int e = tid; e < kBN * groups; e += kThreads) {
+            const int col = e % kBN, grp = e / kBN;
+            const size_t gi = (size_t)min(n0 + col, p.n - 1) * groups + grp;
+            tab_s[grp * kBN + col] = h2f(p.g_scales[gi]);
+            tab_z[grp * kBN + col] = (uint8_t)(int)h2f(p.g_zeros[gi]);
+        }
+    }
+
+    v4f accf[kAI][4];
+    v4i acci[kAI][4];
+#pragma unroll
+    for (int i = 0; i < kAI; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            accf[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+            acci[i][j] = v4i{0, 0, 0, 0};
+        }
+
+    for (int step = 0; step < steps; ++step) {
+        wait_stages<L::kOps>(min(step + kS - 2, steps - 1) - step);
+        __syncthreads();
+        if (step + kS - 1 < steps) issue(step + kS - 1);
+        const uint8_t* As = lds + (step % kS) * L::kStageBytes;
+        const uint8_t* Bs = As + L::kATile;
+        const int grp = (step * T::kStep) >> 7;
+        uint4 w0[4], w1[4];
+        v4f gs[4];
+#pragma unroll
+        for (int bj = 0; bj < 4; ++bj)
+            weight_frag<F>(Bs, wn * 64 + wrow(l16, bj), g, bj, wn, step, tab_s + grp * kBN, tab_z + grp * kBN, w0[bj], w1[bj], gs[bj]);
+        uint4 xr0[3], xr1[3];
+#pragma unroll
+        for (int i = 0; i < 2 && i < kAI; ++i) {
+            const int row = wm * 16 * kAI + i * 16 + l16;
+            xr0[i] = *(const uint4*)(As + swz(row, g));
+            xr1[i] = *(const uint4*)(As + swz(row, 4 + g));
+        }
+#pragma unroll
+        for (int ai = 0; ai < kAI; ++ai) {
+            if (ai + 2 < kAI) {
+                const int row = wm * 16 * kAI + (ai + 2) * 16 + l16;
+                xr0[(ai + 2) % 3] = *(const uint4*)(As + swz(row, g));
+                xr1[(ai + 2) % 3] = *(const uint4*)(As + swz(row, 4 + g));
+            }
+#pragma unroll
+            for (int bj = 0; bj < 4; ++bj) mfma_step<F>(accf[ai][bj], acci[ai][bj], w0[bj], w1[bj], xr0[ai % 3], xr1[ai % 3], gs[bj]);
+        }
+    }
+    if constexpr (E == EPI_F16_RES) epilogue<F, EPI_F16, true, kAI>(p, accf, acci, m0, n0, wm, wn, lane);
+    else epilogue<F, E, false, kAI>(p, accf, acci, m0, n0, wm, wn, lane);
+}
+
 }  // namespace g3
 }  // namespace pk

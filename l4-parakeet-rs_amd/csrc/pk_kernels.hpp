@@ -11,8 +11,9 @@
 namespace pk {
 
 int launch_gemm(int fmt, int epi, const GemmArgs& args, hipStream_t stream);
-// Tile rows the launcher picks for an m x n output (sets *cols), or a negative status.
-int gemm_tile_plan(int fmt, int epi, int m, int n, int* cols);
+// Tile rows the launcher picks for an m x n output (sets *cols and the
+// number of LDS stages), or a negative status.
+int gemm_tile_plan(int fmt, int epi, int m, int n, int* cols, int* stages);
 int launch_quantize_static(const void* in, void* out, float inverse_scale, size_t elements, bool int8, hipStream_t s);
 int launch_quantize_rows(int kind, const void* in, void* out, float* scales, int rows, int valid_rows, int k, hipStream_t s);
 int launch_pack_rows(int kind, const void* w, void* out, float* scales, int n, int k, hipStream_t s);

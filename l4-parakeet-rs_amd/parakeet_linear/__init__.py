@@ -88,7 +88,7 @@ SIGNATURES = {
     "pk_subsample_projection_fp8": (I, [P, P, P, P, P, P, I, P]),
     "pk_subsample_pointwise_fp8": (I, [P, P, P, P, P, P, I, P]),
     "pk_ffn_contract_int8_rowskip": (I, [P, P, P, P, P, I, P, P]),
-    "pk_gemm_tile": (I, [I, I, I, I, ctypes.POINTER(I)]),
+    "pk_gemm_tile": (I, [I, I, I, I, ctypes.POINTER(I), ctypes.POINTER(I)]),
     "pk_gemm": (I, [I, I, P, P, I, I, I, P, P, F, P, P, F, F, I, P, P, P, P, I, P]),
     "pk_joint_gemv": (I, [P, I, P, P, P, P, P, P, I, I, I, I, I, I, P]),
     "pk_joint_scan": (I, [P, I, P, P, P, P, I, I, I, I, I, I, I, P, P, P]),
@@ -202,13 +202,13 @@ def gemm(fmt, epi, a, b, m, n, k, out, *, w_scales=None, row_scales=None, in_sca
          stream=stream)
 
 
-def gemm_tile(fmt, epi, m, n):
-    """(tile rows, tile cols) pk_gemm launches for an m x n output."""
-    cols = I(0)
-    rows = lib.pk_gemm_tile(fmt, epi, m, n, ctypes.byref(cols))
+def gemm_tile(fmt, epi, m, n, stages=False):
+    """(tile rows, tile cols[, LDS stages]) pk_gemm launches for an m x n output."""
+    cols, st = I(0), I(0)
+    rows = lib.pk_gemm_tile(fmt, epi, m, n, ctypes.byref(cols), ctypes.byref(st))
     if rows < 0:
         raise PkError(f"pk_gemm_tile: status {rows}: {last_error()}")
-    return rows, cols.value
+    return (rows, cols.value, st.value) if stages else (rows, cols.value)
 
 
 FMT_FP8, FMT_I8, FMT_S4, FMT_G128A8, FMT_F16, FMT_G128A16, FMT_I8_SKIP, FMT_Q4K = range(8)

@@ -93,27 +93,33 @@ def test_exl3_layout_matches_reference_tests(lib):
 
 def _tile(lib, fmt, epi, m, n):
     fn = lib.pk_gemm_tile
-    fn.argtypes = [ctypes.c_int32] * 4 + [ctypes.POINTER(ctypes.c_int32)]
+    fn.argtypes = [ctypes.c_int32] * 4 + [ctypes.POINTER(ctypes.c_int32)] * 2
     fn.restype = ctypes.c_int32
-    cols = ctypes.c_int32(0)
-    rows = fn(fmt, epi, m, n, ctypes.byref(cols))
-    return rows, cols.value
+    cols, stages = ctypes.c_int32(0), ctypes.c_int32(0)
+    rows = fn(fmt, epi, m, n, ctypes.byref(cols), ctypes.byref(stages))
+    return rows, cols.value, stages.value
 
 
 @pytest.mark.skipif(os.environ.get("PK_GEMM_TILE_ROWS") is not None, reason="tile size forced")
 def test_gemm_tile_plan(lib):
     """The launcher's tile choice on a 256-CU part (the host-only fallback
     when no GPU is visible, and MI355X's count): the BASELINE sizes the
-    full-size parity tests use reach the 256-row kernels."""
+    full-size parity tests use reach the 256-row kernels; grids of at most
+    one tile per CU take the one-tile-per-workgroup ring (more stages)."""
     FP8, I8, G128A8, F16, I8SKIP, Q4K = 0, 1, 3, 4, 6, 7
     EPI_F16, EPI_F8, EPI_F32 = 0, 1, 3
-    assert _tile(lib, FP8, EPI_F8, 7500, 4096) == (256, 128)
-    assert _tile(lib, FP8, EPI_F16, 45000, 1024) == (256, 128)
-    assert _tile(lib, G128A8, EPI_F16, 45000, 1024) == (256, 128)
-    assert _tile(lib, I8, EPI_F8, 7500, 4096) == (256, 128)
-    assert _tile(lib, FP8, EPI_F16, 7500, 1024) == (128, 128)
-    assert _tile(lib, I8SKIP, EPI_F32, 7500, 1024) == (128, 128)
-    assert _tile(lib, G128A8, EPI_F16, 750, 1024) == (64, 128)
-    assert _tile(lib, F16, EPI_F16, 45000, 1024) == (256, 256)
-    assert _tile(lib, Q4K, EPI_F16, 16, 256) == (256, 256)
+    assert _tile(lib, FP8, EPI_F8, 7500, 4096) == (256, 128, 2)
+    assert _tile(lib, FP8, EPI_F16, 45000, 1024) == (256, 128, 2)
+    assert _tile(lib, G128A8, EPI_F16, 45000, 1024) == (256, 128, 2)
+    assert _tile(lib, I8, EPI_F8, 7500, 4096) == (256, 128, 2)
+    assert _tile(lib, FP8, EPI_F16, 7500, 1024) == (128, 128, 2)
+    assert _tile(lib, I8SKIP, EPI_F32, 7500, 1024) == (128, 128, 2)
+    assert _tile(lib, F16, EPI_F16, 45000, 1024) == (256, 256, 2)
+    assert _tile(lib, Q4K, EPI_F16, 16, 256) == (256, 256, 2)
+    # small grids: BASELINE config 1 (750 x 4096) in 128-row ring tiles,
+    # the T = 750 INT4-g128 FF2 (750 x 1024) in 32-row ring tiles
+    rows, cols, stages = _tile(lib, I8, EPI_F32, 750, 4096)
+    assert (rows, cols) == (128, 128) and stages >= 3
+    rows, cols, stages = _tile(lib, G128A8, EPI_F16, 750, 1024)
+    assert (rows, cols) == (32, 128) and stages >= 3
     assert _tile(lib, 99, EPI_F16, 16, 256)[0] == -4
