@@ -859,6 +859,7 @@ def main():
                     help="run only the attention measurements and a 256 MiB device copy, for rocprofv3 passes")
     ap.add_argument("--classes", action="store_true", help="with --only-stack: also time every kernel class")
     ap.add_argument("--only-decode", action="store_true", help="run only the TDT decode measurements")
+    ap.add_argument("--only-producers", action="store_true", help="run only the activation producers' timing")
     ap.add_argument("--only-stack", action="store_true",
                     help="run only the 24-layer stack (warmup + steps, no other measurement), for rocprofv3 passes")
     args = ap.parse_args()
@@ -912,6 +913,9 @@ def main():
     for _ in range(args.warmup):
         stack.step()
     torch.cuda.synchronize()
+    if args.only_producers:
+        print(json.dumps(producers_bench(pk, torch, stack, stream, reps=20)), flush=True)
+        return
     if args.only_stack:
         ms = time_events(torch, stack.step, args.steps, stream)
         out = {"stack_ms_per_step": ms, "steps": args.steps,

@@ -47,6 +47,20 @@ __device__ __forceinline__ float e4m3_to_f32(uint32_t byte) {
     return (byte & 0x80) ? -mag : mag;
 }
 
+// x / s correctly rounded (the IEEE quotient) from inv = 1 / s correctly
+// rounded, in three operations: q0 = x * inv is within one ulp of x / s, the
+// residual r = q0 * s - x is exact in one fma, and q0 - r * inv rounds to the
+// correctly rounded quotient (Markstein's theorem, P. Markstein, "Computation
+// of elementary functions on the IBM RISC System/6000 processor", IBM J. Res.
+// Dev. 34(1), 1990).  Zeros keep their sign (r is +0 and q0 - (+0) * inv is
+// q0).  Requires a finite, nonzero s and x finite or NaN (NaN gives NaN);
+// x / s and r must stay clear of the fp32 overflow and underflow ranges.
+__device__ __forceinline__ float div_rn(float x, float s, float inv) {
+    const float q0 = x * inv;
+    const float r = __builtin_fmaf(q0, s, -x);
+    return __builtin_fmaf(-r, inv, q0);
+}
+
 // ---- integer helpers -------------------------------------------------------
 __device__ __forceinline__ int rne_clamp(float v, int lo, int hi) {
     float r = __builtin_rintf(v);

@@ -1,6 +1,7 @@
 // Activation quantizers, load-time weight packers and LayerNorm producers.
-// All are HBM-bound byte work: one 256-thread block per row for the per-row
-// kinds, 8 elements (16 bytes of fp16) per thread for the elementwise kinds.
+// All are HBM-bound byte work: one wave per row for the per-row activation
+// kinds, one 256-thread block per row for the load-time weight packers, 8
+// elements (16 bytes of fp16) per thread for the elementwise kinds.
 #include "pk_kernels.hpp"
 
 namespace pk {
@@ -42,61 +43,165 @@ __device__ __forceinline__ float block_max_256(float v, float* red) {
     return r;
 }
 
+// Byte packing and the per-element fast paths of the row quantizers.  They
+// assume a finite scale (rows with an inf or NaN take the exact path).
+//  * INT8: |x / scale| <= 127 (1 + 2^-23) when scale = RN(max|x| / 127), so
+//    rne needs no clamp; adding 1.5 * 2^23 leaves rne(q) in the low mantissa
+//    bits, whose low byte is the two's-complement int8.
+//  * FP8: |x / scale| can exceed 448 by an ulp; the clamp keeps the
+//    conversion saturating.
+__device__ __forceinline__ uint32_t rne_bits(float q) { return __builtin_bit_cast(uint32_t, q + 12582912.0f); }
+__device__ __forceinline__ uint32_t low_bytes4(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+    const uint32_t ab = __builtin_amdgcn_perm(b, a, 0x0c0c0400u);
+    const uint32_t cd = __builtin_amdgcn_perm(d, c, 0x0c0c0400u);
+    return __builtin_amdgcn_perm(cd, ab, 0x05040100u);
+}
+__device__ __forceinline__ uint32_t e4m3x4_sat(float a, float b, float c, float d) {
+    const float lo = -448.0f, hi = 448.0f;
+    uint32_t w = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(__builtin_amdgcn_fmed3f(a, lo, hi), __builtin_amdgcn_fmed3f(b, lo, hi), 0, false);
+    return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(__builtin_amdgcn_fmed3f(c, lo, hi), __builtin_amdgcn_fmed3f(d, lo, hi), (int)w, true);
+}
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+// max over two fp16 magnitudes per word, as integers: for non-NaN halves the
+// order of (bits & 0x7fff) is the order of |x|; any value above 0x7c00 is NaN.
+__device__ __forceinline__ uint32_t abs_max16(uint32_t acc, uint32_t w) {
+    return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(u16x2, acc), __builtin_bit_cast(u16x2, w & 0x7fff7fffu)));
+}
+
 // Dynamic per-row quantization of fp16 rows [rows x k] (k % 8 == 0).
 //   kind 0: FP8,  scale = max|x| / 448 (encoder.cu:1129-1180, :264-292)
 //   kind 1: INT8, scale = max|x| / 127 (per-token dynamic INT8)
 //   kind 2: INT4, scale = max(max(x/7, -x/8)), nibble pairs (encoder.cu:264-290)
 // Scale is 1 for a row without a positive maximum; rows >= valid_rows are
 // written as zeros with scale 1 (padding rows, encoder.cu:226-237).
-template <int kind>
+// One wave per row (four rows per 256-thread block, rows strided over the
+// grid): a lane holds up to kCh 16-byte chunks of its row in registers as
+// fp16 (with kPrefetch it issues the loads of its next row before it works
+// on the current one); the maximum is a wave reduction (order-free); rows
+// longer than 64 * kCh * 8 are read a second time for the quantization pass.
+// Kinds 0 and 1 fold |x| as packed integers and quantize with the fast paths
+// above unless the row holds an inf or NaN; kind 2 and those rows divide.
+template <int kind, int kCh, bool kPrefetch>
 __global__ __launch_bounds__(256) void quantize_rows_kernel(const uint16_t* __restrict__ in, uint8_t* __restrict__ out,
-                                                            float* __restrict__ scales, int k, int valid_rows) {
-    __shared__ float red[4];
-    const int row = blockIdx.x;
-    const uint16_t* x = in + (size_t)row * k;
+                                                            float* __restrict__ scales, int rows, int k, int valid_rows) {
+    const int lane = threadIdx.x & 63;
+    const int nw = gridDim.x * 4;
+    const int chunks = k >> 3;
     const int out_row = kind == 2 ? k / 2 : k;
-    uint8_t* o = out + (size_t)row * out_row;
-    if (row >= valid_rows) {
-        for (int i = threadIdx.x * 8; i < out_row; i += 256 * 8) {
-            if (i + 8 <= out_row) *(uint2*)(o + i) = uint2{0, 0};
-            else for (int j = i; j < out_row; ++j) o[j] = 0;
+    uint4 cur[kCh], nxt[kPrefetch ? kCh : 1];
+    auto load = [&](int row, uint4* r) {
+        const uint16_t* x = in + (size_t)row * k;
+#pragma unroll
+        for (int i = 0; i < kCh; ++i) {
+            const int c = lane + 64 * i;
+            r[i] = (row < valid_rows && c < chunks) ? *(const uint4*)(x + c * 8) : uint4{0, 0, 0, 0};
         }
-        if (threadIdx.x == 0) scales[row] = 1.0f;
-        return;
-    }
-    float m = 0.0f;
-    for (int i = threadIdx.x * 8; i < k; i += 256 * 8) {
-        const uint4 raw = *(const uint4*)(x + i);
-        const uint16_t* h = (const uint16_t*)&raw;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const float v = h2f(h[j]);
-            m = kind == 2 ? __builtin_fmaxf(m, __builtin_fmaxf(v / 7.0f, -v / 8.0f)) : __builtin_fmaxf(m, __builtin_fabsf(v));
-        }
-    }
-    m = block_max_256(m, red);
-    const float scale = m > 0.0f ? (kind == 0 ? m / 448.0f : (kind == 1 ? m / 127.0f : m)) : 1.0f;
-    if (threadIdx.x == 0) scales[row] = scale;
-    for (int i = threadIdx.x * 8; i < k; i += 256 * 8) {
-        const uint4 raw = *(const uint4*)(x + i);
-        const uint16_t* h = (const uint16_t*)&raw;
-        float v[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = h2f(h[j]) / scale;
-        if constexpr (kind == 0) {
-            const uint32_t w0 = e4m3x2(v[0], v[1]) | (e4m3x2(v[2], v[3]) << 16);
-            const uint32_t w1 = e4m3x2(v[4], v[5]) | (e4m3x2(v[6], v[7]) << 16);
-            *(uint2*)(o + i) = uint2{w0, w1};
-        } else if constexpr (kind == 1) {
-            uint32_t w[2] = {0, 0};
-#pragma unroll
-            for (int j = 0; j < 8; ++j) w[j >> 2] |= ((uint32_t)rne_clamp(v[j], -127, 127) & 255u) << (8 * (j & 3));
-            *(uint2*)(o + i) = uint2{w[0], w[1]};
+    };
+    int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (kPrefetch && row < rows) load(row, cur);
+    for (; row < rows; row += nw) {
+        if constexpr (kPrefetch) {
+            if (row + nw < rows) load(row + nw, nxt);
         } else {
-            uint32_t w = 0;
+            load(row, cur);
+        }
+        const uint16_t* x = in + (size_t)row * k;
+        uint8_t* o = out + (size_t)row * out_row;
+        if (row >= valid_rows) {
+            for (int c = lane; c < chunks; c += 64) {
+                if constexpr (kind == 2) *(uint32_t*)(o + c * 4) = 0u;
+                else *(uint2*)(o + c * 8) = uint2{0, 0};
+            }
+            if (lane == 0) scales[row] = 1.0f;
+        } else {
+            float m = 0.0f;
+            bool exact = true;
+            if constexpr (kind == 2) {
+                auto fold = [&](const uint4& r) {
+                    const uint16_t* h = (const uint16_t*)&r;
 #pragma unroll
-            for (int j = 0; j < 8; ++j) w |= ((uint32_t)rne_clamp(v[j], -8, 7) & 15u) << (4 * j);
-            *(uint32_t*)(o + i / 2) = w;
+                    for (int j = 0; j < 8; ++j) {
+                        const float v = h2f(h[j]);
+                        m = __builtin_fmaxf(m, __builtin_fmaxf(v / 7.0f, -v / 8.0f));
+                    }
+                };
+#pragma unroll
+                for (int i = 0; i < kCh; ++i) fold(cur[i]);
+                for (int c = lane + 64 * kCh; c < chunks; c += 64) fold(*(const uint4*)(x + c * 8));
+                m = wave_max(m);
+            } else {
+                uint32_t acc = 0;
+                auto fold = [&](const uint4& r) { acc = abs_max16(abs_max16(abs_max16(abs_max16(acc, r.x), r.y), r.z), r.w); };
+#pragma unroll
+                for (int i = 0; i < kCh; ++i) fold(cur[i]);
+                for (int c = lane + 64 * kCh; c < chunks; c += 64) fold(*(const uint4*)(x + c * 8));
+                const uint32_t lane_max = (acc & 0xffffu) > (acc >> 16) ? (acc & 0xffffu) : (acc >> 16);
+                const uint32_t bits = __builtin_amdgcn_readfirstlane((uint32_t)wave_max((float)lane_max));
+                exact = bits >= 0x7c00u;  // inf or NaN in the row
+                // NaN is ignored by the maximum (fmaxf), as in the oracle
+                if (exact) {
+                    m = 0.0f;
+#pragma unroll
+                    for (int i = 0; i < kCh; ++i) {
+                        const uint16_t* h = (const uint16_t*)&cur[i];
+#pragma unroll
+                        for (int j = 0; j < 8; ++j) m = __builtin_fmaxf(m, __builtin_fabsf(h2f(h[j])));
+                    }
+                    for (int c = lane + 64 * kCh; c < chunks; c += 64) {
+                        const uint4 r = *(const uint4*)(x + c * 8);
+                        const uint16_t* h = (const uint16_t*)&r;
+                        for (int j = 0; j < 8; ++j) m = __builtin_fmaxf(m, __builtin_fabsf(h2f(h[j])));
+                    }
+                    m = wave_max(m);
+                } else {
+                    m = h2f((uint16_t)bits);
+                }
+            }
+            const float scale = m > 0.0f ? (kind == 0 ? m / 448.0f : (kind == 1 ? m / 127.0f : m)) : 1.0f;
+            const float inv = 1.0f / scale;
+            if (lane == 0) scales[row] = scale;
+            auto emit = [&](int c, const uint4& r) {
+                const uint16_t* h = (const uint16_t*)&r;
+                if constexpr (kind == 2) {
+                    uint32_t w = 0;
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) w |= ((uint32_t)rne_clamp(h2f(h[j]) / scale, -8, 7) & 15u) << (4 * j);
+                    *(uint32_t*)(o + c * 4) = w;
+                } else if (exact) {
+                    uint32_t w[2] = {0, 0};
+#pragma unroll
+                    for (int j = 0; j < 8; j += 2) {
+                        const float a = h2f(h[j]) / scale, b = h2f(h[j + 1]) / scale;
+                        const uint32_t pair = kind == 0 ? e4m3x2(a, b)
+                                                        : (((uint32_t)rne_clamp(a, -127, 127) & 255u) | (((uint32_t)rne_clamp(b, -127, 127) & 255u) << 8));
+                        w[j >> 2] |= pair << (8 * (j & 3));
+                    }
+                    *(uint2*)(o + c * 8) = uint2{w[0], w[1]};
+                } else {
+                    float v[8];
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) v[j] = div_rn(h2f(h[j]), scale, inv);
+                    uint2 w;
+                    if constexpr (kind == 0) {
+                        w.x = e4m3x4_sat(v[0], v[1], v[2], v[3]);
+                        w.y = e4m3x4_sat(v[4], v[5], v[6], v[7]);
+                    } else {
+                        w.x = low_bytes4(rne_bits(v[0]), rne_bits(v[1]), rne_bits(v[2]), rne_bits(v[3]));
+                        w.y = low_bytes4(rne_bits(v[4]), rne_bits(v[5]), rne_bits(v[6]), rne_bits(v[7]));
+                    }
+                    *(uint2*)(o + c * 8) = w;
+                }
+            };
+#pragma unroll
+            for (int i = 0; i < kCh; ++i) {
+                const int c = lane + 64 * i;
+                if (c < chunks) emit(c, cur[i]);
+            }
+            for (int c = lane + 64 * kCh; c < chunks; c += 64) emit(c, *(const uint4*)(x + c * 8));
+        }
+        if constexpr (kPrefetch) {
+#pragma unroll
+            for (int i = 0; i < kCh; ++i) cur[i] = nxt[i];
         }
     }
 }
@@ -171,89 +276,122 @@ __global__ void pack_g128_kernel(const uint16_t* __restrict__ w, uint32_t* __res
 }
 
 // LayerNorm over 1024 features + dynamic per-row FP8 / INT4 quantization
-// (encoder.cu:211-306).  The sums keep the reference's reduction shape:
-// thread t folds x[t], x[t+256], x[t+512], x[t+768]; lanes 0..31 combine
-// (t, t+128), (t+64, t+192), (t+32, t+160), (t+96, t+224) as
-// ((s0 + s1) + (s2 + s3)) and a shuffle-down tree over 32 lanes finishes
-// (encoder.cu:36-54).  inverse_std = 1 / sqrtf(.) correctly rounded.
-__device__ __forceinline__ float tree_sum_256(float v, float* part) {
-    const int t = threadIdx.x;
-    part[t] = v;
-    __syncthreads();
-    float r = 0.0f;
-    if (t < 64) {
-        const int l = t & 31;
-        const float s0 = part[l] + part[l + 128];
-        const float s1 = part[l + 64] + part[l + 192];
-        const float s2 = part[l + 32] + part[l + 160];
-        const float s3 = part[l + 96] + part[l + 224];
-        r = (s0 + s1) + (s2 + s3);
-        for (int off = 16; off > 0; off >>= 1) {
-            const float o = __shfl_down(r, off, 32);
-            r = (l + off < 32) ? r + o : r;
-        }
-        if (t == 0) part[256] = r;
+// (encoder.cu:211-306), one wave per row (four rows per 256-thread block,
+// rows strided over the grid; gamma and beta stay in registers).  The sums
+// keep the reference's reduction shape, whose 256 partials are
+// partial(t) = ((x[t] + x[t+256]) + x[t+512]) + x[t+768]: lane l holds
+// partials t = l, l+64, l+128, l+192; lanes 0..31 form
+// (p[l] + p[l+128]) + (p[l+64] + p[l+192]) and add lane l+32's value of the
+// same expression (= (p[l+32] + p[l+160]) + (p[l+96] + p[l+224])), then a
+// shuffle-down tree over 32 lanes finishes (encoder.cu:36-54).  inverse_std =
+// 1 / sqrtf(.) correctly rounded.
+__device__ __forceinline__ float ln_tree_sum(const float (&p)[4]) {
+    const int lane = threadIdx.x & 63;
+    float r = (p[0] + p[2]) + (p[1] + p[3]);
+    r = r + __shfl(r, (lane + 32) & 63, 64);
+#pragma unroll
+    for (int off = 16; off > 0; off >>= 1) {
+        const float o = __shfl(r, (lane + off) & 63, 64);
+        r = ((lane & 31) + off < 32) ? r + o : r;
     }
-    __syncthreads();
-    r = part[256];
-    __syncthreads();
-    return r;
+    return __shfl(r, 0, 64);
 }
 
+//
+// Quantization: y is finite unless mean, inverse_std, gamma or beta is not
+// (normalized values are bounded by sqrt(1024)) or its fp16 rounding
+// overflows; rows where either may have happened take the exact per-element
+// divisions, the others the fast paths: the maximum comes from the row's
+// extremes (x / 7 rounded is monotone in x), the quotients from div_rn and
+// the INT4 codes need no clamp (|y / scale| <= 8 (1 + 2^-23)).
 template <bool kInt4>
 __global__ __launch_bounds__(256) void layer_norm_quantize_kernel(const uint16_t* __restrict__ in, const uint16_t* __restrict__ gamma,
                                                                   const uint16_t* __restrict__ beta, uint8_t* __restrict__ out,
                                                                   float* __restrict__ scales, uint16_t* __restrict__ normalized,
-                                                                  int rows, float epsilon) {
-    __shared__ float part[257];
-    __shared__ float red[4];
-    const int row = blockIdx.x, t = threadIdx.x;
-    if (row >= rows) {
-        for (int f = t; f < 1024; f += 256) {
-            if (kInt4) { if ((f & 1) == 0) out[((size_t)row * 1024 + f) / 2] = 0; }
-            else out[(size_t)row * 1024 + f] = 0;
-            if (normalized) normalized[(size_t)row * 1024 + f] = 0;
+                                                                  int rows, int padded_rows, float epsilon) {
+    const int lane = threadIdx.x & 63;
+    const int nw = gridDim.x * 4;
+    // element e = 4 i + j of a lane is feature f = lane + 64 j + 256 i
+    float g[16], b[16];
+    bool gb_finite = true;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+        const int f = lane + 64 * (e & 3) + 256 * (e >> 2);
+        g[e] = h2f(gamma[f]);
+        b[e] = h2f(beta[f]);
+        gb_finite = gb_finite && __builtin_isfinite(g[e]) && __builtin_isfinite(b[e]);
+    }
+    gb_finite = __all(gb_finite);
+    for (int row = blockIdx.x * 4 + (threadIdx.x >> 6); row < padded_rows; row += nw) {
+        if (row >= rows) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int f = lane + 64 * (e & 3) + 256 * (e >> 2);
+                if (kInt4) { if ((f & 1) == 0) out[((size_t)row * 1024 + f) / 2] = 0; }
+                else out[(size_t)row * 1024 + f] = 0;
+                if (normalized) normalized[(size_t)row * 1024 + f] = 0;
+            }
+            if (lane == 0) scales[row] = 1.0f;
+            continue;
         }
-        if (t == 0) scales[row] = 1.0f;
-        return;
-    }
-    float v[4];
-    float sum = 0.0f;
+        float v[16];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        v[i] = h2f(in[(size_t)row * 1024 + t + 256 * i]);
-        sum += v[i];
-    }
-    const float mean = tree_sum_256(sum, part) / 1024.0f;
-    float sq = 0.0f;
+        for (int e = 0; e < 16; ++e) v[e] = h2f(in[(size_t)row * 1024 + lane + 64 * (e & 3) + 256 * (e >> 2)]);
+        float p[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const float d = v[i] - mean;
-        sq += d * d;
-    }
-    const float inverse_std = 1.0f / sqrtf(tree_sum_256(sq, part) / 1024.0f + epsilon);
-    float m = 0.0f;
+        for (int j = 0; j < 4; ++j) p[j] = ((v[j] + v[4 + j]) + v[8 + j]) + v[12 + j];
+        const float mean = ln_tree_sum(p) / 1024.0f;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int f = t + 256 * i;
-        const float y = (v[i] - mean) * inverse_std * h2f(gamma[f]) + h2f(beta[f]);
-        const uint16_t h = f2h(y);
-        if (normalized) normalized[(size_t)row * 1024 + f] = h;
-        v[i] = h2f(h);
-        m = kInt4 ? __builtin_fmaxf(m, __builtin_fmaxf(v[i] / 7.0f, -v[i] / 8.0f)) : __builtin_fmaxf(m, __builtin_fabsf(v[i]));
-    }
-    m = block_max_256(m, red);
-    const float scale = m > 0.0f ? (kInt4 ? m : m / 448.0f) : 1.0f;
-    if (t == 0) scales[row] = scale;
+        for (int j = 0; j < 4; ++j) {
+            float sq = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int f = t + 256 * i;
-        if constexpr (kInt4) {
-            const int q = rne_clamp(v[i] / scale, -8, 7);
-            const int other = __shfl_xor(q, 1, 64);
-            if ((t & 1) == 0) out[((size_t)row * 1024 + f) / 2] = (uint8_t)((q & 15) | ((other & 15) << 4));
+            for (int i = 0; i < 4; ++i) {
+                const float d = v[4 * i + j] - mean;
+                sq += d * d;
+            }
+            p[j] = sq;
+        }
+        const float inverse_std = 1.0f / sqrtf(ln_tree_sum(p) / 1024.0f + epsilon);
+        float hi = 0.0f, lo = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const int f = lane + 64 * (e & 3) + 256 * (e >> 2);
+            const float y = (v[e] - mean) * inverse_std * g[e] + b[e];
+            const uint16_t h = f2h(y);
+            if (normalized) normalized[(size_t)row * 1024 + f] = h;
+            v[e] = h2f(h);
+            hi = __builtin_fmaxf(hi, v[e]);
+            lo = __builtin_fminf(lo, v[e]);
+        }
+        hi = wave_max(hi);
+        lo = -wave_max(-lo);
+        // wave-uniform: every lane holds the same reductions
+        const bool fast = __builtin_amdgcn_readfirstlane(gb_finite && __builtin_isfinite(mean) && __builtin_isfinite(inverse_std) &&
+                                                         __builtin_isfinite(hi) && __builtin_isfinite(lo));
+        float m;
+        if (fast) {
+            m = kInt4 ? __builtin_fmaxf(div_rn(hi, 7.0f, 1.0f / 7.0f), -lo / 8.0f) : __builtin_fmaxf(hi, -lo);
         } else {
-            out[(size_t)row * 1024 + f] = e4m3(v[i] / scale);
+            m = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 16; ++e)
+                m = kInt4 ? __builtin_fmaxf(m, __builtin_fmaxf(v[e] / 7.0f, -v[e] / 8.0f)) : __builtin_fmaxf(m, __builtin_fabsf(v[e]));
+            m = wave_max(m);
+        }
+        const float scale = m > 0.0f ? (kInt4 ? m : m / 448.0f) : 1.0f;
+        const float inv = 1.0f / scale;
+        if (lane == 0) scales[row] = scale;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const int f = lane + 64 * (e & 3) + 256 * (e >> 2);
+            if constexpr (kInt4) {
+                const int q = fast ? (int)rne_bits(div_rn(v[e], scale, inv)) : rne_clamp(v[e] / scale, -8, 7);
+                const int other = __shfl_xor(q, 1, 64);
+                if ((lane & 1) == 0) out[((size_t)row * 1024 + f) / 2] = (uint8_t)((q & 15) | ((other & 15) << 4));
+            } else {
+                out[(size_t)row * 1024 + f] =
+                    fast ? (uint8_t)e4m3x4_sat(div_rn(v[e], scale, inv), 0.0f, 0.0f, 0.0f) : e4m3(v[e] / scale);
+            }
         }
     }
 }
@@ -288,11 +426,27 @@ int launch_quantize_static(const void* in, void* out, float inverse_scale, size_
     return 0;
 }
 
+static unsigned row_grid(int rows) {
+    // four rows per block, at most eight blocks per CU (rows are strided)
+    const int blocks = (rows + 3) / 4, cap = 8 * cu_count();
+    return (unsigned)(blocks < cap ? blocks : cap);
+}
+
 int launch_quantize_rows(int kind, const void* in, void* out, float* scales, int rows, int valid_rows, int k, hipStream_t s) {
     if (rows == 0) return 0;
-    if (kind == 0) quantize_rows_kernel<0><<<rows, 256, 0, s>>>((const uint16_t*)in, (uint8_t*)out, scales, k, valid_rows);
-    else if (kind == 1) quantize_rows_kernel<1><<<rows, 256, 0, s>>>((const uint16_t*)in, (uint8_t*)out, scales, k, valid_rows);
-    else quantize_rows_kernel<2><<<rows, 256, 0, s>>>((const uint16_t*)in, (uint8_t*)out, scales, k, valid_rows);
+    const unsigned grid = row_grid(rows);
+    const uint16_t* x = (const uint16_t*)in;
+    uint8_t* o = (uint8_t*)out;
+    // rows of up to 1024 (kCh 2) or 4096 (kCh 8) elements stay in registers
+    if (k <= 1024) {
+        if (kind == 0) quantize_rows_kernel<0, 2, true><<<grid, 256, 0, s>>>(x, o, scales, rows, k, valid_rows);
+        else if (kind == 1) quantize_rows_kernel<1, 2, true><<<grid, 256, 0, s>>>(x, o, scales, rows, k, valid_rows);
+        else quantize_rows_kernel<2, 2, true><<<grid, 256, 0, s>>>(x, o, scales, rows, k, valid_rows);
+    } else {
+        if (kind == 0) quantize_rows_kernel<0, 8, false><<<grid, 256, 0, s>>>(x, o, scales, rows, k, valid_rows);
+        else if (kind == 1) quantize_rows_kernel<1, 8, false><<<grid, 256, 0, s>>>(x, o, scales, rows, k, valid_rows);
+        else quantize_rows_kernel<2, 8, false><<<grid, 256, 0, s>>>(x, o, scales, rows, k, valid_rows);
+    }
     return 0;
 }
 
@@ -314,12 +468,13 @@ int launch_pack_g128(const void* w, uint32_t* q, uint16_t* scales, uint16_t* zer
 int launch_layer_norm_quantize(bool int4, const void* in, const void* gamma, const void* beta, void* out, float* scales,
                                void* normalized, int rows, int padded_rows, float epsilon, hipStream_t s) {
     if (padded_rows == 0) return 0;
+    const unsigned grid = row_grid(padded_rows);
     if (int4)
-        layer_norm_quantize_kernel<true><<<padded_rows, 256, 0, s>>>((const uint16_t*)in, (const uint16_t*)gamma, (const uint16_t*)beta,
-                                                                      (uint8_t*)out, scales, (uint16_t*)normalized, rows, epsilon);
+        layer_norm_quantize_kernel<true><<<grid, 256, 0, s>>>((const uint16_t*)in, (const uint16_t*)gamma, (const uint16_t*)beta,
+                                                               (uint8_t*)out, scales, (uint16_t*)normalized, rows, padded_rows, epsilon);
     else
-        layer_norm_quantize_kernel<false><<<padded_rows, 256, 0, s>>>((const uint16_t*)in, (const uint16_t*)gamma, (const uint16_t*)beta,
-                                                                       (uint8_t*)out, scales, (uint16_t*)normalized, rows, epsilon);
+        layer_norm_quantize_kernel<false><<<grid, 256, 0, s>>>((const uint16_t*)in, (const uint16_t*)gamma, (const uint16_t*)beta,
+                                                                (uint8_t*)out, scales, (uint16_t*)normalized, rows, padded_rows, epsilon);
     return 0;
 }
 

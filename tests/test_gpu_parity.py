@@ -128,6 +128,80 @@ def test_quantize_rows(pk, orc, kind, m, k, valid):
     assert np.array_equal(host(scales), ref[1])
 
 
+@pytest.mark.parametrize("kind", [0, 1, 2])
+@pytest.mark.parametrize("k", [1024, 4096])
+def test_quantize_rows_all_fp16_inputs(pk, orc, kind, k):
+    """Every finite fp16 x with |x| <= M goes through x / scale for twelve row
+    maxima M (each row holds M, -M and a run of the enumeration): the kernel's
+    quotient must round exactly as the oracle's IEEE division does, ties and
+    near-ties at the rounding boundaries included."""
+    note(f"quantize_rows exhaustive kind={kind} k={k}")
+    allh = np.arange(65536, dtype=np.uint16).view(np.float16)
+    allh = allh[np.isfinite(allh.astype(np.float32))]
+    rows = []
+    for mx in (65504.0, 448.0, 127.0, 100.0, 37.3, 7.0, 1.0, 0.3, 1.0 / 3.0, 6.1e-5, 1e-6, 6e-8):
+        m = np.float16(mx)
+        vals = allh[np.abs(allh.astype(np.float32)) <= np.float32(m)]
+        per = k - 2
+        for i in range(0, vals.size, per):
+            r = np.zeros(k, np.float16)
+            r[0], r[1] = m, -m
+            chunk = vals[i:i + per]
+            r[2:2 + chunk.size] = chunk
+            rows.append(r)
+    x = np.stack(rows)
+    m = x.shape[0]
+    out = empty((m, k // 2 if kind == 2 else k), torch.uint8)
+    scales = empty(m, torch.float32)
+    pk.call("pk_quantize_rows", kind, dev(x), out, scales, m, m, k)
+    ref = {0: orc.quantize_fp8_rows, 1: orc.quantize_int8_rows, 2: orc.quantize_int4_rows}[kind](x, m)
+    assert np.array_equal(host(scales), ref[1])
+    assert np.array_equal(host(out).view(np.uint8), ref[0].view(np.uint8))
+
+
+@pytest.mark.parametrize("kind", [0, 1, 2])
+@pytest.mark.parametrize("k", [1024, 4096])
+def test_quantize_rows_non_finite(pk, orc, kind, k):
+    """Rows holding inf, -inf or NaN next to ordinary values, and rows of
+    ordinary values only, in one launch (the kernel picks a path per row)."""
+    note(f"quantize_rows non-finite kind={kind} k={k}")
+    x = acts(12, k, 77 + k)
+    x[1, 5] = np.inf
+    x[3, 0] = -np.inf
+    x[5, 9] = np.nan
+    x[7, 1:4] = [np.nan, np.inf, -np.inf]
+    x[9] = np.nan
+    out = empty((12, k // 2 if kind == 2 else k), torch.uint8)
+    scales = empty(12, torch.float32)
+    pk.call("pk_quantize_rows", kind, dev(x), out, scales, 12, 12, k)
+    ref = {0: orc.quantize_fp8_rows, 1: orc.quantize_int8_rows, 2: orc.quantize_int4_rows}[kind](x, 12)
+    assert np.array_equal(host(scales), ref[1], equal_nan=True)
+    assert np.array_equal(host(out).view(np.uint8), ref[0].view(np.uint8))
+
+
+@pytest.mark.parametrize("int4", [False, True])
+def test_layer_norm_quantize_non_finite(pk, orc, int4):
+    """Rows with inf / NaN inputs, a row whose fp16 output overflows (gamma
+    large), and ordinary rows: each row's path must match the oracle."""
+    note(f"layer_norm_quantize non-finite int4={int4}")
+    m = 8
+    x = (acts(m, 1024, 17).astype(np.float32) * 2).astype(np.float16)
+    x[1, 3] = np.inf
+    x[2, 7] = np.nan
+    x[4] = 0  # constant row: variance 0
+    x[5, 0] = 3000.0  # one large outlier: normalized value near sqrt(1023)
+    g = np.random.default_rng(18).uniform(0.5, 1.5, 1024).astype(np.float16)
+    g[0] = 30000.0  # feature 0 overflows fp16 in row 5
+    b = (np.random.default_rng(19).standard_normal(1024) * 0.1).astype(np.float16)
+    out = empty((m, 512 if int4 else 1024), torch.uint8)
+    scales = empty(m, torch.float32)
+    name = "pk_layer_norm_quantize_int4_dynamic" if int4 else "pk_layer_norm_quantize_fp8_dynamic"
+    pk.call(name, dev(x), dev(g), dev(b), out, scales, m, m, 1e-5)
+    q, s, _ = orc.layer_norm_quantize(x, g, b, 1e-5, int4, valid_rows=m)
+    assert np.array_equal(host(scales), s, equal_nan=True)
+    assert np.array_equal(host(out), q)
+
+
 @pytest.mark.parametrize("int4", [False, True])
 def test_layer_norm_quantize(pk, orc, int4):
     note(f"layer_norm_quantize int4={int4}")
