@@ -172,7 +172,8 @@ int32_t pk_quantize_rows(int32_t kind, const uint16_t* input, void* output, floa
                          int32_t valid_rows, int32_t k, void* stream);
 /* encoder.cu:211-306 pk_sm89_layer_norm_quantize_{fp8,int4}_dynamic: LayerNorm
  * over 1024 features, fp16 rounding, per-row dynamic FP8 / INT4 (+ scales);
- * rows in [rows, padded_rows) are zero with scale 1. */
+ * rows in [rows, padded_rows) are zero with scale 1.  input, weight and bias
+ * 8-byte aligned, output 4-byte (FP8) / 2-byte (INT4) aligned (PK_E_ALIGN). */
 int32_t pk_layer_norm_quantize_fp8_dynamic(const uint16_t* input, const uint16_t* weight, const uint16_t* bias,
                                            uint8_t* output, float* scales, int32_t rows, int32_t padded_rows,
                                            float epsilon, void* stream);

@@ -189,6 +189,10 @@ static int32_t ln_quantize(bool int4, const uint16_t* in, const uint16_t* w, con
     if (rows < 0 || padded_rows < rows) { set_error("need 0 <= rows <= padded_rows"); return PK_E_SHAPE; }
     if (padded_rows && (!need(in, "input") || !need(w, "weight") || !need(b, "bias") || !need(out, "output") || !need(scales, "scales")))
         return PK_E_ARG;
+    if (((uintptr_t)in | (uintptr_t)w | (uintptr_t)b) & 7 || (uintptr_t)out & (int4 ? 1 : 3)) {
+        set_error("layer_norm_quantize needs 8-byte aligned input, weight and bias and a %d-byte aligned output", int4 ? 2 : 4);
+        return PK_E_ALIGN;
+    }
     launch_layer_norm_quantize(int4, in, w, b, out, scales, nullptr, rows, padded_rows, eps, STREAM);
     return check_launch("layer_norm_quantize");
 }

@@ -277,12 +277,15 @@ __global__ void pack_g128_kernel(const uint16_t* __restrict__ w, uint32_t* __res
 
 // LayerNorm over 1024 features + dynamic per-row FP8 / INT4 quantization
 // (encoder.cu:211-306), one wave per row (four rows per 256-thread block,
-// rows strided over the grid; gamma and beta stay in registers).  The sums
-// keep the reference's reduction shape, whose 256 partials are
-// partial(t) = ((x[t] + x[t+256]) + x[t+512]) + x[t+768]: lane l holds
-// partials t = l, l+64, l+128, l+192; lanes 0..31 form
+// rows strided over the grid).  Lane l holds features 4l..4l+3 of each
+// 256-feature quarter i (8-byte loads, 4-byte FP8 / 2-byte INT4 stores) and
+// its gamma and beta in registers.  The sums keep the reference's reduction
+// shape, whose 256 partials are
+// partial(t) = ((x[t] + x[t+256]) + x[t+512]) + x[t+768]: lane l forms
+// partials 4l..4l+3 and writes them to its wave's slice of LDS; lane l then
+// reads partials t = l, l+64, l+128, l+192, lanes 0..31 form
 // (p[l] + p[l+128]) + (p[l+64] + p[l+192]) and add lane l+32's value of the
-// same expression (= (p[l+32] + p[l+160]) + (p[l+96] + p[l+224])), then a
+// same expression (= (p[l+32] + p[l+160]) + (p[l+96] + p[l+224])), and a
 // shuffle-down tree over 32 lanes finishes (encoder.cu:36-54).  inverse_std =
 // 1 / sqrtf(.) correctly rounded.
 __device__ __forceinline__ float ln_tree_sum(const float (&p)[4]) {
@@ -297,6 +300,25 @@ __device__ __forceinline__ float ln_tree_sum(const float (&p)[4]) {
     return __shfl(r, 0, 64);
 }
 
+// LDS ordering inside one wave: the wave's LDS operations execute in order;
+// the fences keep the compiler from moving them across this point.
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Sum of the 256 partials part[t] (lane l holds t = 4l..4l+3) in the tree
+// above, through the wave's 256-float LDS slice.
+__device__ __forceinline__ float ln_partials_sum(const float (&part)[4], float* slice) {
+    const int lane = threadIdx.x & 63;
+    *(float4*)(slice + 4 * lane) = float4{part[0], part[1], part[2], part[3]};
+    wave_lds_sync();
+    const float p[4] = {slice[lane], slice[lane + 64], slice[lane + 128], slice[lane + 192]};
+    wave_lds_sync();
+    return ln_tree_sum(p);
+}
+
 //
 // Quantization: y is finite unless mean, inverse_std, gamma or beta is not
 // (normalized values are bounded by sqrt(1024)) or its fp16 rounding
@@ -309,59 +331,77 @@ __global__ __launch_bounds__(256) void layer_norm_quantize_kernel(const uint16_t
                                                                   const uint16_t* __restrict__ beta, uint8_t* __restrict__ out,
                                                                   float* __restrict__ scales, uint16_t* __restrict__ normalized,
                                                                   int rows, int padded_rows, float epsilon) {
+    __shared__ __attribute__((aligned(16))) float red[4][2][256];
     const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
     const int nw = gridDim.x * 4;
-    // element e = 4 i + j of a lane is feature f = lane + 64 j + 256 i
+    // element e = 4 i + u of a lane is feature f = 256 i + 4 lane + u
     float g[16], b[16];
     bool gb_finite = true;
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-        const int f = lane + 64 * (e & 3) + 256 * (e >> 2);
-        g[e] = h2f(gamma[f]);
-        b[e] = h2f(beta[f]);
-        gb_finite = gb_finite && __builtin_isfinite(g[e]) && __builtin_isfinite(b[e]);
+    for (int i = 0; i < 4; ++i) {
+        const uint2 gw = *(const uint2*)(gamma + 256 * i + 4 * lane);
+        const uint2 bw = *(const uint2*)(beta + 256 * i + 4 * lane);
+        const uint16_t* gh = (const uint16_t*)&gw;
+        const uint16_t* bh = (const uint16_t*)&bw;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            g[4 * i + u] = h2f(gh[u]);
+            b[4 * i + u] = h2f(bh[u]);
+            gb_finite = gb_finite && __builtin_isfinite(g[4 * i + u]) && __builtin_isfinite(b[4 * i + u]);
+        }
     }
     gb_finite = __all(gb_finite);
-    for (int row = blockIdx.x * 4 + (threadIdx.x >> 6); row < padded_rows; row += nw) {
+    const size_t out_row = kInt4 ? 512 : 1024;
+    for (int row = blockIdx.x * 4 + wave; row < padded_rows; row += nw) {
+        uint8_t* o = out + (size_t)row * out_row;
+        uint16_t* nrm = normalized ? normalized + (size_t)row * 1024 : nullptr;
         if (row >= rows) {
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const int f = lane + 64 * (e & 3) + 256 * (e >> 2);
-                if (kInt4) { if ((f & 1) == 0) out[((size_t)row * 1024 + f) / 2] = 0; }
-                else out[(size_t)row * 1024 + f] = 0;
-                if (normalized) normalized[(size_t)row * 1024 + f] = 0;
+            for (int i = 0; i < 4; ++i) {
+                if (kInt4) *(uint16_t*)(o + 128 * i + 2 * lane) = 0;
+                else *(uint32_t*)(o + 256 * i + 4 * lane) = 0u;
+                if (nrm) *(uint2*)(nrm + 256 * i + 4 * lane) = uint2{0, 0};
             }
             if (lane == 0) scales[row] = 1.0f;
             continue;
         }
         float v[16];
 #pragma unroll
-        for (int e = 0; e < 16; ++e) v[e] = h2f(in[(size_t)row * 1024 + lane + 64 * (e & 3) + 256 * (e >> 2)]);
-        float p[4];
+        for (int i = 0; i < 4; ++i) {
+            const uint2 w = *(const uint2*)(in + (size_t)row * 1024 + 256 * i + 4 * lane);
+            const uint16_t* h = (const uint16_t*)&w;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) p[j] = ((v[j] + v[4 + j]) + v[8 + j]) + v[12 + j];
-        const float mean = ln_tree_sum(p) / 1024.0f;
+            for (int u = 0; u < 4; ++u) v[4 * i + u] = h2f(h[u]);
+        }
+        float part[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int u = 0; u < 4; ++u) part[u] = ((v[u] + v[4 + u]) + v[8 + u]) + v[12 + u];
+        const float mean = ln_partials_sum(part, red[wave][0]) / 1024.0f;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
             float sq = 0.0f;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const float d = v[4 * i + j] - mean;
+                const float d = v[4 * i + u] - mean;
                 sq += d * d;
             }
-            p[j] = sq;
+            part[u] = sq;
         }
-        const float inverse_std = 1.0f / sqrtf(ln_tree_sum(p) / 1024.0f + epsilon);
+        const float inverse_std = 1.0f / sqrtf(ln_partials_sum(part, red[wave][1]) / 1024.0f + epsilon);
         float hi = 0.0f, lo = 0.0f;
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            const int f = lane + 64 * (e & 3) + 256 * (e >> 2);
-            const float y = (v[e] - mean) * inverse_std * g[e] + b[e];
-            const uint16_t h = f2h(y);
-            if (normalized) normalized[(size_t)row * 1024 + f] = h;
-            v[e] = h2f(h);
-            hi = __builtin_fmaxf(hi, v[e]);
-            lo = __builtin_fminf(lo, v[e]);
+        for (int i = 0; i < 4; ++i) {
+            uint16_t h[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int e = 4 * i + u;
+                h[u] = f2h((v[e] - mean) * inverse_std * g[e] + b[e]);
+                v[e] = h2f(h[u]);
+                hi = __builtin_fmaxf(hi, v[e]);
+                lo = __builtin_fminf(lo, v[e]);
+            }
+            if (nrm) *(uint2*)(nrm + 256 * i + 4 * lane) = uint2{h[0] | ((uint32_t)h[1] << 16), h[2] | ((uint32_t)h[3] << 16)};
         }
         hi = wave_max(hi);
         lo = -wave_max(-lo);
@@ -382,15 +422,19 @@ __global__ __launch_bounds__(256) void layer_norm_quantize_kernel(const uint16_t
         const float inv = 1.0f / scale;
         if (lane == 0) scales[row] = scale;
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            const int f = lane + 64 * (e & 3) + 256 * (e >> 2);
+        for (int i = 0; i < 4; ++i) {
+            const float* y = v + 4 * i;
             if constexpr (kInt4) {
-                const int q = fast ? (int)rne_bits(div_rn(v[e], scale, inv)) : rne_clamp(v[e] / scale, -8, 7);
-                const int other = __shfl_xor(q, 1, 64);
-                if ((lane & 1) == 0) out[((size_t)row * 1024 + f) / 2] = (uint8_t)((q & 15) | ((other & 15) << 4));
+                uint32_t q[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) q[u] = fast ? rne_bits(div_rn(y[u], scale, inv)) : (uint32_t)rne_clamp(y[u] / scale, -8, 7);
+                *(uint16_t*)(o + 128 * i + 2 * lane) =
+                    (uint16_t)((q[0] & 15u) | ((q[1] & 15u) << 4) | ((q[2] & 15u) << 8) | ((q[3] & 15u) << 12));
             } else {
-                out[(size_t)row * 1024 + f] =
-                    fast ? (uint8_t)e4m3x4_sat(div_rn(v[e], scale, inv), 0.0f, 0.0f, 0.0f) : e4m3(v[e] / scale);
+                const uint32_t w = fast ? e4m3x4_sat(div_rn(y[0], scale, inv), div_rn(y[1], scale, inv), div_rn(y[2], scale, inv),
+                                                     div_rn(y[3], scale, inv))
+                                        : (e4m3x2(y[0] / scale, y[1] / scale) | (e4m3x2(y[2] / scale, y[3] / scale) << 16));
+                *(uint32_t*)(o + 256 * i + 4 * lane) = w;
             }
         }
     }
