@@ -114,7 +114,8 @@ def test_quantize_int8_all_fp16_inputs(pk, orc):
 
 
 @pytest.mark.parametrize("kind", [0, 1, 2])
-@pytest.mark.parametrize("m,k,valid", [(1, 1024, 1), (37, 1024, 30), (16, 4096, 16), (5, 256, 5)])
+@pytest.mark.parametrize("m,k,valid", [(1, 1024, 1), (37, 1024, 30), (16, 4096, 16), (5, 256, 5), (3, 8, 3),
+                                        (9, 1032, 7), (6, 8192, 5), (4, 6152, 4)])
 def test_quantize_rows(pk, orc, kind, m, k, valid):
     note(f"quantize_rows kind={kind} m={m} k={k}")
     x = acts(m, k, 100 + m + k)
