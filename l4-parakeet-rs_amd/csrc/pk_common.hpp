@@ -141,7 +141,8 @@ __device__ __forceinline__ unsigned long long max_level(unsigned long long v, in
 
 // ---- reductions over a 256-thread block ------------------------------------
 __device__ __forceinline__ float wave_max(float v) {
-    for (int off = 32; off > 0; off >>= 1) v = __builtin_fmaxf(v, __shfl_xor(v, off, 64));
+#pragma unroll
+    for (int off = 1; off <= 32; off <<= 1) v = max_level(v, off);
     return v;
 }
 

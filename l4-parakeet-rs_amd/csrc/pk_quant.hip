@@ -289,15 +289,22 @@ __global__ void pack_g128_kernel(const uint16_t* __restrict__ w, uint32_t* __res
 // shuffle-down tree over 32 lanes finishes (encoder.cu:36-54).  inverse_std =
 // 1 / sqrtf(.) correctly rounded.
 __device__ __forceinline__ float ln_tree_sum(const float (&p)[4]) {
-    const int lane = threadIdx.x & 63;
+    // (p[l] + p[l+128]) + (p[l+64] + p[l+192]) in lane l, then the tree over
+    // pairs (l, l + off) for off = 32, 16, ..., 1.  Lane 0 holds the total:
+    // at every level the lanes it depends on (l < 2 off) read exactly their
+    // partner l + off -- permlane32 / permlane16 swaps for off = 32 / 16, DPP
+    // row shifts (lane l reads lane l + off of its 16-lane row) below.
     float r = (p[0] + p[2]) + (p[1] + p[3]);
-    r = r + __shfl(r, (lane + 32) & 63, 64);
-#pragma unroll
-    for (int off = 16; off > 0; off >>= 1) {
-        const float o = __shfl(r, (lane + off) & 63, 64);
-        r = ((lane & 31) + off < 32) ? r + o : r;
-    }
-    return __shfl(r, 0, 64);
+    int a, b;
+    pair_of(__float_as_int(r), 32, a, b);
+    r = __int_as_float(a) + __int_as_float(b);
+    pair_of(__float_as_int(r), 16, a, b);
+    r = __int_as_float(a) + __int_as_float(b);
+    r = r + __int_as_float(dpp_mov<0x108>(__float_as_int(r)));  // row_shl:8
+    r = r + __int_as_float(dpp_mov<0x104>(__float_as_int(r)));  // row_shl:4
+    r = r + __int_as_float(dpp_mov<0x102>(__float_as_int(r)));  // row_shl:2
+    r = r + __int_as_float(dpp_mov<0x101>(__float_as_int(r)));  // row_shl:1
+    return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(r)));
 }
 
 // LDS ordering inside one wave: the wave's LDS operations execute in order;
