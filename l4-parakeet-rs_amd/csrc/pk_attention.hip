@@ -363,24 +363,21 @@ __device__ void attention_query(float* scores, const uint16_t* __restrict__ quer
                 s = __builtin_fmaf(su[quarter].y, h2f((uint16_t)(k >> 16)), s);
                 s = __builtin_fmaf(sv[quarter].y, h2f((uint16_t)(p >> 16)), s);
             }
-#pragma unroll
-            for (int off = 8; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+            s = sum_desc<16>(s);  // xor 8, 4, 2, 1
             if (hl == 0 && slot < count) scores[slot] = s * kScoreScale;
         }
     }
     wave_sync();
     float mx = -FLT_MAX;
     for (int slot = lane; slot < count; slot += 64) mx = __builtin_fmaxf(mx, scores[slot]);
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) mx = __builtin_fmaxf(mx, __shfl_xor(mx, off, 64));
+    mx = wave_max(mx);
     for (int slot = lane; slot < count; slot += 64) scores[slot] = expf(scores[slot] - mx);
     wave_sync();
     float den = 0.0f;
     if (lane < 32)
         for (int slot = lane; slot < count; slot += 32) den += scores[slot];
-#pragma unroll
-    for (int off = 16; off > 0; off >>= 1) den += __shfl_xor(den, off, 64);
-    den = __shfl(den, 0, 64);
+    den = sum_desc<32>(den);  // xor 16, ..., 1 over lanes 0..31
+    den = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(den)));
     wave_sync();
     for (int slot = lane; slot < count; slot += 64) scores[slot] = scores[slot] / den;
     wave_sync();
@@ -419,7 +416,7 @@ __device__ __forceinline__ float softmax_half(float (&l)[9], int ln) {
     for (int part = 0; part < 9; ++part)
         if (ln + 32 * part < kMaxAtt) mx = __builtin_fmaxf(mx, l[part]);
 #pragma unroll
-    for (int off = 16; off > 0; off >>= 1) mx = __builtin_fmaxf(mx, __shfl_xor(mx, off, 64));
+    for (int off = 1; off <= 16; off <<= 1) mx = max_level(mx, off);
     float den = 0.0f;
 #pragma unroll
     for (int part = 0; part < 9; ++part)
@@ -427,9 +424,7 @@ __device__ __forceinline__ float softmax_half(float (&l)[9], int ln) {
             l[part] = expf(l[part] - mx);
             den += l[part];
         }
-#pragma unroll
-    for (int off = 16; off > 0; off >>= 1) den += __shfl_xor(den, off, 64);
-    return __shfl(den, 0, 32);
+    return sum_desc<32>(den);  // xor 16, ..., 1 within the half wave
 }
 
 // encoder.cu:1687-1966 for the interior tiles [t0, t1) of one head: INT4

@@ -151,16 +151,14 @@ __global__ __launch_bounds__(256) void attention_short_kernel(ShortArgs a) {
     wave_fence();
     float mx = -3.402823466e38f;
     for (int slot = lane; slot < count; slot += 64) mx = __builtin_fmaxf(mx, sc[slot]);
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) mx = __builtin_fmaxf(mx, __shfl_xor(mx, off, 64));
+    mx = wave_max(mx);
     float den = 0.0f;
     for (int slot = lane; slot < count; slot += 64) {
         const float e = expf(sc[slot] - mx);
         sc[slot] = e;
         den += e;
     }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) den += __shfl_xor(den, off, 64);
+    den = sum_desc<64>(den);  // xor 32, ..., 1
     // probabilities, each divided once (the reference divides per lane and key: same value)
     for (int slot = lane; slot < count; slot += 64) sc[slot] = sc[slot] / den;
     wave_fence();

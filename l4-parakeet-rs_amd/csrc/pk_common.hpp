@@ -139,6 +139,31 @@ __device__ __forceinline__ unsigned long long max_level(unsigned long long v, in
     return x > y ? x : y;
 }
 
+// Sum over an aligned group of kWidth lanes (16, 32 or 64) in the association
+// of the descending xor butterfly (off = kWidth / 2, ..., 2, 1, own +
+// partner), the total in every lane of the group.  The xor-32 / xor-16
+// levels are permlane swaps; below them DPP row rotations by 8, 4, 2, 1
+// stand in for xor 8, 4, 2, 1: after the levels above, the lane a rotation
+// reads holds the same value as the xor partner (they differ only in bits
+// already reduced), so every lane adds exactly the butterfly's operands.
+template <int CTRL> __device__ __forceinline__ float dpp_f(float v) { return __int_as_float(dpp_mov<CTRL>(__float_as_int(v))); }
+template <int kWidth> __device__ __forceinline__ float sum_desc(float v) {
+    int a, b;
+    if constexpr (kWidth >= 64) {
+        pair_of(__float_as_int(v), 32, a, b);
+        v = __int_as_float(a) + __int_as_float(b);
+    }
+    if constexpr (kWidth >= 32) {
+        pair_of(__float_as_int(v), 16, a, b);
+        v = __int_as_float(a) + __int_as_float(b);
+    }
+    v = v + dpp_f<0x128>(v);  // row_ror:8
+    v = v + dpp_f<0x124>(v);  // row_ror:4
+    v = v + dpp_f<0x122>(v);  // row_ror:2
+    v = v + dpp_f<0x121>(v);  // row_ror:1
+    return v;
+}
+
 // ---- reductions over a 256-thread block ------------------------------------
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
