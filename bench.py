@@ -344,6 +344,31 @@ def measured_traffic(spec):
         return None
 
 
+def hipblaslt_yardstick(pk, torch, stream, t=T, reps=20):
+    """A yardstick, not part of this library's path: torch._scaled_mm (hipBLASLt)
+    on the stack's three FP8 GEMM shapes (per-tensor scales, bf16 output, no
+    epilogue) beside this library's FP8 kernels on the same shapes with their
+    stack epilogues (FF1 expand: SiLU e4m3; FF contract: fp16 + residual; QKV:
+    fp16), each warmed up for a quarter second and averaged over `reps`."""
+    out = {}
+    sa = torch.tensor(1.0, device="cuda")
+    sb = torch.tensor(1.0, device="cuda")
+    for name, n, k, kind in (("ff1_expand", FF, D, "f8"), ("ff_contract", D, FF, "res"), ("qkv", 3 * D, D, "f16")):
+        a = torch.randn(t, k, device="cuda").to(torch.float8_e4m3fn)
+        b = torch.randn(n, k, device="cuda").to(torch.float8_e4m3fn)
+        f = lambda: torch._scaled_mm(a, b.t(), scale_a=sa, scale_b=sb, out_dtype=torch.bfloat16)
+        warm_up(torch, f, 0.25)
+        lib_ms = time_events(torch, f, reps, stream)
+        del a, b
+        ours_ms, flops, _ = kernel_time(pk, torch, t, ("fp8", kind, n, k), stream, reps)
+        out[name] = {"m": t, "n": n, "k": k, "hipblaslt_us": round(lib_ms * 1e3, 1),
+                     "hipblaslt_TFLOPs": round(flops / (lib_ms * 1e-3) / 1e12, 1),
+                     "ours_us": round(ours_ms * 1e3, 1), "ours_TFLOPs": round(flops / (ours_ms * 1e-3) / 1e12, 1),
+                     "ours_epilogue": EPI_NAME[kind]}
+        torch.cuda.empty_cache()
+    return out
+
+
 def producers_bench(pk, torch, stack, stream, reps=3):
     """The activation producers a stack step needs ahead of its linears
     (encoder.rs:1020-1080 runs them between the GEMMs), timed on their own at
@@ -879,6 +904,8 @@ def main():
     ap.add_argument("--classes", action="store_true", help="with --only-stack: also time every kernel class")
     ap.add_argument("--only-decode", action="store_true", help="run only the TDT decode measurements")
     ap.add_argument("--only-producers", action="store_true", help="run only the activation producers' timing")
+    ap.add_argument("--hipblaslt", action="store_true",
+                    help="yardstick: hipBLASLt (torch._scaled_mm) against this library's FP8 kernels on the stack's shapes")
     ap.add_argument("--only-stack", action="store_true",
                     help="run only the 24-layer stack (warmup + steps, no other measurement), for rocprofv3 passes")
     args = ap.parse_args()
@@ -894,6 +921,9 @@ def main():
 
     torch.cuda.set_device(0)
     stream = torch.cuda.current_stream()
+    if args.hipblaslt:
+        print(json.dumps(hipblaslt_yardstick(pk, torch, stream, args.frames)), flush=True)
+        return
     if args.only_joint:
         res = joint_streaming(pk, torch, stream, reps=20)
         src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
