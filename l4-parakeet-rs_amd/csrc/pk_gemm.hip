@@ -136,13 +136,25 @@ static int forced_tile_rows() {
     return force;
 }
 
-static int byte_tile_rows(int m, int n) {
+// Tile rows of the occupancy-2 engine.  Grids whose 256-row tiles would not
+// give every CU one take 128 (or, for a quarter of the CUs, 64) rows.  When
+// both heights fill the chip, the one with fewer whole rounds of the 2 x CUs
+// persistent workgroups wins by a margin, a 128-row tile costing half a
+// 256-row one times its measured overhead (the smaller tile moves more operand bytes per MFMA:
+// 9 % for FP8 / INT8, 22 % for INT4-g128 x INT8 at T = 45000).  E.g. QKV at
+// T = 7500: 720 tiles of 256 rows take 2 rounds of 512 (the second 40 % full),
+// 1416 of 128 rows 3 rounds of half the cost.
+static int byte_tile_rows(int fmt, int m, int n) {
     const int tiles256 = ((m + 255) / 256) * ((n + g3::kBN - 1) / g3::kBN);
     const int tiles128 = ((m + 127) / 128) * ((n + g3::kBN - 1) / g3::kBN);
     const int force = forced_tile_rows();
     if (force > 0) return force;
-    if (4 * tiles128 <= cu_count()) return 64;
-    return 2 * tiles256 <= 2 * cu_count() ? 128 : 256;
+    const int cus = cu_count(), slots = 2 * cus;
+    if (4 * tiles128 <= cus) return 64;
+    if (tiles256 <= cus) return 128;
+    const int r256 = (tiles256 + slots - 1) / slots, r128 = (tiles128 + slots - 1) / slots;
+    const float overhead = fmt == FMT_G128A8 ? 1.22f : 1.09f;
+    return 0.5f * overhead * (float)r128 < 0.95f * (float)r256 ? 128 : 256;  // a clear win only
 }
 
 // Engine per format, by measurement on MI355X: the occupancy-2 engine for the
@@ -173,7 +185,7 @@ static int tile_plan(int fmt, int epi, int m, int n, int* cols, int* stages) {
         *cols = kBlockN;
         return kBlockM;
     }
-    return byte_tile_rows(m, n);
+    return byte_tile_rows(fmt, m, n);
 }
 
 template <int F, int E>

@@ -109,6 +109,11 @@ def test_gemm_tile_plan(lib):
     FP8, I8, G128A8, F16, I8SKIP, Q4K = 0, 1, 3, 4, 6, 7
     EPI_F16, EPI_F8, EPI_F32 = 0, 1, 3
     assert _tile(lib, FP8, EPI_F8, 7500, 4096) == (256, 128, 2)
+    # 720 tiles of 256 rows would leave the second round of 512 slots 40 % full
+    assert _tile(lib, FP8, EPI_F16, 7500, 3072) == (128, 128, 2)
+    assert _tile(lib, FP8, EPI_F16, 45000, 3072) == (256, 128, 2)
+    assert _tile(lib, FP8, EPI_F16, 45000, 2048) == (256, 128, 2)
+    assert _tile(lib, G128A8, EPI_F8, 45000, 4096) == (256, 128, 2)
     assert _tile(lib, FP8, EPI_F16, 45000, 1024) == (256, 128, 2)
     assert _tile(lib, G128A8, EPI_F16, 45000, 1024) == (256, 128, 2)
     assert _tile(lib, I8, EPI_F8, 7500, 4096) == (256, 128, 2)
