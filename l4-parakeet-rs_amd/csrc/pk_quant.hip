@@ -339,26 +339,26 @@ __global__ __launch_bounds__(256) void layer_norm_quantize_kernel(const uint16_t
                                                                   float* __restrict__ scales, uint16_t* __restrict__ normalized,
                                                                   int rows, int padded_rows, float epsilon) {
     __shared__ __attribute__((aligned(16))) float red[4][2][256];
+    // gamma and beta as fp32 in LDS, read per row (registers stay free for
+    // occupancy): gb[i][lane] holds features 256 i + 4 lane .. + 3
+    __shared__ __attribute__((aligned(16))) float4 gb_s[2][4][64];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int nw = gridDim.x * 4;
     // element e = 4 i + u of a lane is feature f = 256 i + 4 lane + u
-    float g[16], b[16];
     bool gb_finite = true;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    {
+        const int i = wave;  // wave i stages quarter i
         const uint2 gw = *(const uint2*)(gamma + 256 * i + 4 * lane);
         const uint2 bw = *(const uint2*)(beta + 256 * i + 4 * lane);
         const uint16_t* gh = (const uint16_t*)&gw;
         const uint16_t* bh = (const uint16_t*)&bw;
+        gb_s[0][i][lane] = float4{h2f(gh[0]), h2f(gh[1]), h2f(gh[2]), h2f(gh[3])};
+        gb_s[1][i][lane] = float4{h2f(bh[0]), h2f(bh[1]), h2f(bh[2]), h2f(bh[3])};
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            g[4 * i + u] = h2f(gh[u]);
-            b[4 * i + u] = h2f(bh[u]);
-            gb_finite = gb_finite && __builtin_isfinite(g[4 * i + u]) && __builtin_isfinite(b[4 * i + u]);
-        }
+        for (int u = 0; u < 4; ++u) gb_finite = gb_finite && __builtin_isfinite(h2f(gh[u])) && __builtin_isfinite(h2f(bh[u]));
     }
-    gb_finite = __all(gb_finite);
+    gb_finite = __syncthreads_and(gb_finite);
     const size_t out_row = kInt4 ? 512 : 1024;
     for (int row = blockIdx.x * 4 + wave; row < padded_rows; row += nw) {
         uint8_t* o = out + (size_t)row * out_row;
@@ -400,10 +400,12 @@ __global__ __launch_bounds__(256) void layer_norm_quantize_kernel(const uint16_t
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             uint16_t h[4];
+            const float4 g4 = gb_s[0][i][lane], b4 = gb_s[1][i][lane];
+            const float g[4] = {g4.x, g4.y, g4.z, g4.w}, b[4] = {b4.x, b4.y, b4.z, b4.w};
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
                 const int e = 4 * i + u;
-                h[u] = f2h((v[e] - mean) * inverse_std * g[e] + b[e]);
+                h[u] = f2h((v[e] - mean) * inverse_std * g[u] + b[u]);
                 v[e] = h2f(h[u]);
                 hi = __builtin_fmaxf(hi, v[e]);
                 lo = __builtin_fminf(lo, v[e]);
