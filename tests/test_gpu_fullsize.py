@@ -313,3 +313,45 @@ def test_c4_rowskip_T7500(pk, orc, sparsity):
     assert total == 2 * row_blocks * col_tiles * steps, total
     zero_blocks = row_blocks - (t - pad + 15) // 16
     assert skipped >= 2 * zero_blocks * col_tiles * steps, (skipped, total)
+
+
+# ---- activation producers at the stack's size --------------------------------------
+# One wave per row with rows strided over a grid of at most 8 blocks per CU, so
+# at T = 45000 every wave works through several rows (the small parity tests
+# give each wave at most one).  Sampled rows, padding rows included, against
+# the oracle bit for bit.
+
+@pytest.mark.parametrize("int4", [False, True])
+def test_layer_norm_quantize_T45000(pk, orc, int4):
+    t, pad = 45000, 45056
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(4500 + int(int4))
+    x = (torch.randn((pad, D), generator=gen, device="cuda") * 2 + 0.3).half()
+    g = (torch.rand(D, generator=gen, device="cuda") + 0.5).half()
+    b = (torch.randn(D, generator=gen, device="cuda") * 0.1).half()
+    out = torch.empty((pad, D // 2 if int4 else D), dtype=torch.uint8, device="cuda")
+    scales = torch.empty(pad, dtype=torch.float32, device="cuda")
+    name = "pk_layer_norm_quantize_int4_dynamic" if int4 else "pk_layer_norm_quantize_fp8_dynamic"
+    note(f"layer_norm_quantize T={t} padded={pad} int4={int4}")
+    pk.call(name, x, g, b, out, scales, t, pad, 1e-5)
+    idx = np.union1d(sample_rows(pad, 31 + int(int4), per_strip=2), np.arange(t - 3, pad))
+    q, s, _ = orc.layer_norm_quantize(rows_of(x, idx), host(g), host(b), 1e-5, int4, valid_rows=int((idx < t).sum()))
+    assert np.array_equal(host(scales)[idx], s)
+    assert np.array_equal(rows_of(out, idx), q)
+
+
+@pytest.mark.parametrize("kind,k", [(0, D), (1, FF), (2, D)])
+def test_quantize_rows_T45000(pk, orc, kind, k):
+    t, valid = 45000, 44990
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(450 + kind)
+    x = torch.randn((t, k), generator=gen, device="cuda").half()
+    out = torch.empty((t, k // 2 if kind == 2 else k), dtype=torch.uint8, device="cuda")
+    scales = torch.empty(t, dtype=torch.float32, device="cuda")
+    note(f"quantize_rows T={t} k={k} kind={kind}")
+    pk.call("pk_quantize_rows", kind, x, out, scales, t, valid, k)
+    idx = np.union1d(sample_rows(t, 41 + kind, per_strip=2), np.arange(valid - 3, t))
+    ref = {0: orc.quantize_fp8_rows, 1: orc.quantize_int8_rows, 2: orc.quantize_int4_rows}[kind](
+        rows_of(x, idx), int((idx < valid).sum()))
+    assert np.array_equal(host(scales)[idx], ref[1])
+    assert np.array_equal(rows_of(out, idx).view(np.uint8), ref[0].view(np.uint8))
