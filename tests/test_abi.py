@@ -128,3 +128,34 @@ def test_gemm_tile_plan(lib):
     rows, cols, stages = _tile(lib, G128A8, EPI_F16, 750, 1024)
     assert (rows, cols) == (32, 128) and stages >= 3
     assert _tile(lib, 99, EPI_F16, 16, 256)[0] == -4
+
+
+def test_argument_checks_reject_before_any_launch(lib):
+    """Entry points reject bad shapes, null and misaligned pointers with their
+    PK_E_* code and a message, before touching a device (fake addresses are
+    never dereferenced on these paths)."""
+    E_SHAPE, E_ALIGN, E_ARG = -1, -2, -4
+    vp = ctypes.c_void_p
+    err = lib.pk_last_error
+    err.restype = ctypes.c_char_p
+    ln = lib.pk_layer_norm_quantize_fp8_dynamic
+    ln.argtypes = [vp, vp, vp, vp, vp, ctypes.c_int32, ctypes.c_int32, ctypes.c_float, vp]
+    ln.restype = ctypes.c_int32
+    ok = dict(i=0x10000, w=0x20000, b=0x30000, o=0x40000, s=0x50000)
+    assert ln(0x10004, ok["w"], ok["b"], ok["o"], ok["s"], 4, 4, 1e-5, None) == E_ALIGN
+    assert b"aligned" in err()
+    assert ln(ok["i"], ok["w"], 0x30002, ok["o"], ok["s"], 4, 4, 1e-5, None) == E_ALIGN
+    assert ln(ok["i"], ok["w"], ok["b"], 0x40002, ok["s"], 4, 4, 1e-5, None) == E_ALIGN
+    assert ln(ok["i"], ok["w"], ok["b"], ok["o"], ok["s"], 5, 4, 1e-5, None) == E_SHAPE
+    assert ln(None, ok["w"], ok["b"], ok["o"], ok["s"], 4, 4, 1e-5, None) == E_ARG
+    ln4 = lib.pk_layer_norm_quantize_int4_dynamic
+    ln4.argtypes = ln.argtypes
+    ln4.restype = ctypes.c_int32
+    assert ln4(ok["i"], ok["w"], ok["b"], 0x40001, ok["s"], 4, 4, 1e-5, None) == E_ALIGN
+    qr = lib.pk_quantize_rows
+    qr.argtypes = [ctypes.c_int32, vp, vp, vp, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, vp]
+    qr.restype = ctypes.c_int32
+    assert qr(1, 0x10008, ok["o"], ok["s"], 4, 4, 1024, None) == E_ALIGN
+    assert qr(1, ok["i"], ok["o"], ok["s"], 4, 4, 1020, None) == E_SHAPE
+    assert qr(3, ok["i"], ok["o"], ok["s"], 4, 4, 1024, None) == E_ARG
+    assert qr(1, None, ok["o"], ok["s"], 4, 4, 1024, None) == E_ARG
