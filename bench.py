@@ -794,6 +794,13 @@ def config_results(pk, torch, stream, reps=10):
     counts = torch.zeros(2, dtype=torch.int32, device=dev)
     qbuf = torch.empty((t, k), dtype=torch.int8, device=dev)
     qsc = torch.empty(t, device=dev)
+    sp_data = torch.empty((t, k // 2), dtype=torch.uint8, device=dev)
+    sp_meta = torch.empty((t, k // 8), dtype=torch.uint8, device=dev)
+    sp_cnt = torch.empty(t, dtype=torch.int32, device=dev)
+    sp_ovf = torch.empty((t, k // 2), dtype=torch.int32, device=dev)
+    wt = torch.empty((k, n), dtype=torch.int8, device=dev)
+    pk.call("pk_transpose_int8", wq, wt, n, k, stream=stream)
+    y2 = torch.empty((t, n), device=dev)
     c4 = {}
     for sp in (0.5, 0.8, 0.9, 0.95):
         a = torch.nn.functional.silu(torch.randn((t, k), generator=g, device=dev)).half()
@@ -816,6 +823,31 @@ def config_results(pk, torch, stream, reps=10):
 
         with_quantize()
         e["with_quantize_us"] = round(time_events(torch, with_quantize, reps, stream) * 1e3, 1)
+        # exact 2:4 form: 2:4 INT8 data + metadata + per-row overflow lists
+        pk.call("pk_quantize_rows_int8_sparse24", a, sp_data, sp_meta, qsc, sp_cnt, sp_ovf, t, t, k, stream=stream)
+
+        def sparse24():
+            pk.call("pk_ffn_contract_int8_sparse24", sp_data, sp_meta, qsc, sp_cnt, sp_ovf, wq, wt, ws, y2, t,
+                    stream=stream)
+
+        def sparse24_with_quantize():
+            pk.call("pk_quantize_rows_int8_sparse24", a, sp_data, sp_meta, qsc, sp_cnt, sp_ovf, t, t, k, stream=stream)
+            sparse24()
+
+        sparse24_with_quantize()
+        pk.call("pk_quantize_rows", 1, a, qbuf, qsc, t, t, k, stream=stream)
+        with_quantize()
+        torch.cuda.synchronize()
+        same = bool(torch.equal(y, y2))
+        ms24 = timed(sparse24)
+        e24 = entry(ms24, f, t * k // 2 + t * k // 8 + 4 * t + 4 * int(sp_cnt.sum()) + n * k + 4 * n + 4 * t * n,
+                    useful=(1.0 - sp) * f)
+        e24["overflow_entries_per_row"] = round(float(sp_cnt.double().mean()), 2)
+        e24["with_quantize_us"] = round(time_events(torch, sparse24_with_quantize, reps, stream) * 1e3, 1)
+        e24["equal_to_dense"] = same
+        if not same:
+            raise SystemExit("config 4: the exact 2:4 contract differs from the dense INT8 contract")
+        e["exact_2to4"] = e24
         c4[f"sparsity_{int(sp * 100)}"] = e
         del a, xq
     out["c4_sparse_ff2_int8_T7500"] = c4
@@ -914,6 +946,7 @@ def main():
     ap.add_argument("--only-producers", action="store_true", help="run only the activation producers' timing")
     ap.add_argument("--hipblaslt", action="store_true",
                     help="yardstick: hipBLASLt (torch._scaled_mm) against this library's FP8 kernels on the stack's shapes")
+    ap.add_argument("--only-configs", action="store_true", help="run only the BASELINE config 1-4 measurements")
     ap.add_argument("--only-stack", action="store_true",
                     help="run only the 24-layer stack (warmup + steps, no other measurement), for rocprofv3 passes")
     args = ap.parse_args()
@@ -963,6 +996,9 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"kernel": list(spec), "avg_ms": k_ms, "algorithmic_bytes": k_bytes,
                           "copy_bytes": 256 << 20}), flush=True)
+        return
+    if args.only_configs:
+        print(json.dumps(config_results(pk, torch, stream)), flush=True)
         return
     plan = format_plan()
     print(f"[bench] building stack T={args.frames}", file=sys.stderr, flush=True)

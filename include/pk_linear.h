@@ -314,6 +314,35 @@ int32_t pk_ffn_contract_int8_rowskip(const int8_t* input, const float* input_sca
                                      const float* weight_scales, float* output, int32_t rows, uint32_t* skip_counts,
                                      void* stream);
 
+/* Exact 2:4 form of the activation-sparse FF2.  The
+ * reference's sparse FF2 (encoder.cu:685-704 selection, :1037-1095 contract)
+ * keeps the two largest magnitudes of every quartet and drops the rest; here
+ * the dropped nonzeros are kept in a per-row overflow list, so the contract
+ * is exact.
+ *
+ * pk_quantize_rows_int8_sparse24: the INT8 per-row dynamic quantization of
+ * pk_quantize_rows kind 1 (same scales and bytes), written as 2:4 data
+ * [rows x k/2] and metadata [rows x k/8] (quartet p: idx0 | idx1 << 2 at bits
+ * 4 (p % 2) of byte p / 2, the reference's layout) plus, per row,
+ * overflow_counts[row] entries at overflow[row * k/2 ...], each
+ * (element << 8) | int8 byte, in ascending element order (at most k/2).
+ * k % 128 == 0, k <= 4096; input 16-byte aligned, data / overflow /
+ * overflow_counts 4-byte aligned.  Rows >= valid_rows are zero, scale 1. */
+int32_t pk_quantize_rows_int8_sparse24(const uint16_t* input, uint8_t* data, uint8_t* meta, float* scales,
+                                       uint32_t* overflow_counts, uint32_t* overflow, int32_t rows, int32_t valid_rows,
+                                       int32_t k, void* stream);
+/* Load-time derivation: weight_t [k x n] = transpose of the INT8 weight [n x k]
+ * (the overflow pass of the contract below reads weight columns). */
+int32_t pk_transpose_int8(const int8_t* weight, int8_t* weight_t, int32_t n, int32_t k, void* stream);
+/* The FF2 contract 4096 -> 1024 on that form: fp32 output [rows x 1024] equal
+ * bit for bit to pk_ffn_contract_int8_rowskip's on the dense INT8 rows,
+ * out = (acc * input_scale[r]) * weight_scale[n].  data, meta, weight,
+ * weight_t, weight_scales and output 16-byte aligned. */
+int32_t pk_ffn_contract_int8_sparse24(const uint8_t* data, const uint8_t* meta, const float* input_scales,
+                                      const uint32_t* overflow_counts, const uint32_t* overflow, const int8_t* weight,
+                                      const int8_t* weight_t, const float* weight_scales, float* output, int32_t rows,
+                                      void* stream);
+
 /* ---- generic fused GEMM ------------------------------------------------------
  * format: 0 FP8, 1 INT8, 2 INT4 (s4 x s4), 3 INT4-g128 x INT8, 4 FP16,
  * 5 INT4-g128 x FP16, 6 INT8 with zero-block skip, 7 Q4_K x FP16 (epilogues

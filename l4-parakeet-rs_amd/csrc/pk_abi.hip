@@ -438,6 +438,40 @@ int32_t pk_ffn_contract_int8_rowskip(const int8_t* in, const float* in_scales, c
     return launch_gemm(FMT_I8_SKIP, EPI_F32, g, STREAM);
 }
 
+int32_t pk_quantize_rows_int8_sparse24(const uint16_t* in, uint8_t* data, uint8_t* meta, float* scales, uint32_t* overflow_counts,
+                                       uint32_t* overflow, int32_t rows, int32_t valid_rows, int32_t k, void* stream) {
+    if (rows < 0 || k <= 0 || k % 128 || k > 4096) {
+        set_error("sparse24 quantizer needs rows >= 0 and k %% 128 == 0, k <= 4096 (k=%d)", k);
+        return PK_E_SHAPE;
+    }
+    if (rows && (!need(in, "input") || !need(data, "data") || !need(meta, "meta") || !need(scales, "scales") ||
+                 !need(overflow_counts, "overflow_counts") || !need(overflow, "overflow")))
+        return PK_E_ARG;
+    if (((uintptr_t)in & 15) || ((uintptr_t)data & 3) || ((uintptr_t)overflow & 3) || ((uintptr_t)overflow_counts & 3)) {
+        set_error("sparse24 quantizer: input must be 16-byte aligned, data / overflow / overflow_counts 4-byte aligned");
+        return PK_E_ALIGN;
+    }
+    launch_quantize_rows_sp24(in, data, meta, scales, overflow_counts, overflow, rows, valid_rows < 0 ? 0 : valid_rows, k, STREAM);
+    return check_launch("quantize_rows_int8_sparse24");
+}
+
+int32_t pk_transpose_int8(const int8_t* w, int8_t* wt, int32_t n, int32_t k, void* stream) {
+    if (n < 0 || k < 0) { set_error("negative transpose shape"); return PK_E_SHAPE; }
+    if (n && k && (!need(w, "weight") || !need(wt, "weight_t"))) return PK_E_ARG;
+    return launch_transpose_i8(w, wt, n, k, STREAM);
+}
+
+int32_t pk_ffn_contract_int8_sparse24(const uint8_t* data, const uint8_t* meta, const float* in_scales, const uint32_t* overflow_counts,
+                                      const uint32_t* overflow, const int8_t* w, const int8_t* wt, const float* ws, float* out,
+                                      int32_t rows, void* stream) {
+    if (rows < 0) { set_error("negative rows"); return PK_E_SHAPE; }
+    if (rows == 0) return PK_OK;
+    if (!need(data, "data") || !need(meta, "meta") || !need(in_scales, "input_scales") || !need(overflow_counts, "overflow_counts") ||
+        !need(overflow, "overflow") || !need(w, "weight") || !need(wt, "weight_t") || !need(ws, "weight_scales") || !need(out, "output"))
+        return PK_E_ARG;
+    return launch_sparse24_i8_contract(data, meta, in_scales, overflow_counts, overflow, w, wt, ws, out, rows, 1024, 4096, STREAM);
+}
+
 // ---- joint ------------------------------------------------------------------------
 
 int32_t pk_joint_gemv(const void* w, int32_t w_int8, const float* w_scales, const float* bias, const uint16_t* enc, const float* pred,

@@ -16,6 +16,9 @@ int launch_gemm(int fmt, int epi, const GemmArgs& args, hipStream_t stream);
 int gemm_tile_plan(int fmt, int epi, int m, int n, int* cols, int* stages);
 int launch_quantize_static(const void* in, void* out, float inverse_scale, size_t elements, bool int8, hipStream_t s);
 int launch_quantize_rows(int kind, const void* in, void* out, float* scales, int rows, int valid_rows, int k, hipStream_t s);
+// INT8 rows as 2:4 data / metadata plus per-row overflow lists (k % 128 == 0, k <= 4096).
+int launch_quantize_rows_sp24(const void* in, uint8_t* data, uint8_t* meta, float* scales, uint32_t* ovf_count, uint32_t* ovf,
+                              int rows, int valid_rows, int k, hipStream_t s);
 int launch_pack_rows(int kind, const void* w, void* out, float* scales, int n, int k, hipStream_t s);
 int launch_q4k_dequant(const uint8_t* blocks, uint16_t* out, int n, int k, hipStream_t s);
 int launch_pack_g128(const void* w, uint32_t* q, uint16_t* scales, uint16_t* zeros, int n, int k, hipStream_t s);
@@ -56,6 +59,10 @@ int launch_local_attention(bool packed, const uint16_t* query, const uint16_t* k
                            int padded_rows, int valid_rows, int left, int right, int value_stride, const uint8_t* packed_key,
                            const float* key_scales, const uint8_t* packed_position, const float* position_scales, hipStream_t s);
 
+int launch_sparse24_i8_contract(const uint8_t* data, const uint8_t* meta, const float* in_scales, const uint32_t* ovf_count,
+                                const uint32_t* ovf, const int8_t* w, const int8_t* wt, const float* w_scales, float* out, int m,
+                                int n, int k, hipStream_t s);
+int launch_transpose_i8(const int8_t* w, int8_t* wt, int n, int k, hipStream_t s);
 void set_error(const char* fmt, ...);
 int cu_count();
 int launch_sparse24_contract(const uint8_t* data, const uint8_t* meta, const uint8_t* w, const float* w_scales, float in_scale,

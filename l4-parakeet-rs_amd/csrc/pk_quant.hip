@@ -206,6 +206,137 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(const uint16_t* __re
     }
 }
 
+// ---- INT8 rows in 2:4 form plus an overflow list (activation-sparse FF2) ----
+//
+// Quartet (4 consecutive int8 of a row) -> the reference's 2:4 selection
+// (encoder.cu:685-704, there on e4m3 bytes): keep the two largest |v|, ties to
+// the lower index, in index order; returns the two kept bytes in bits 0-15,
+// idx0 | idx1 << 2 in bits 16-19, and in `drop` bit i set for each nonzero
+// byte i that was not kept (at most two).  The kept pair plus the dropped
+// nonzeros are the quartet, exactly.
+__device__ __forceinline__ uint32_t compress_i8_quartet(uint32_t packed, uint32_t& drop) {
+    int mag[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int v = (int)(int8_t)(packed >> (8 * i));
+        mag[i] = v < 0 ? -v : v;
+    }
+    uint32_t d = 0, md = 0;
+    int count = 0;
+    drop = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        int rank = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            if (j != i) rank += (mag[j] > mag[i]) || (mag[j] == mag[i] && j < i);
+        if (rank < 2) {
+            d |= ((packed >> (8 * i)) & 255u) << (8 * count);
+            md |= (uint32_t)i << (2 * count);
+            ++count;
+        } else if (mag[i] != 0) {
+            drop |= 1u << i;
+        }
+    }
+    return d | (md << 16);
+}
+
+// Dynamic per-row INT8 quantization (the arithmetic of quantize_rows_kernel
+// kind 1: scale = max|x| / 127, 1 for rows without a positive maximum, rows
+// >= valid_rows zero with scale 1), written as 2:4 data [rows x k/2] and
+// metadata [rows x k/8] (quartet p's idx0 | idx1 << 2 at bits 4 (p % 2) of
+// byte p / 2) plus, per row, the nonzeros the 2:4 selection dropped:
+// ovf_count[row] entries at ovf[row * k/2 ...], each (kk << 8) | byte for
+// element kk, in ascending kk.  At most two per quartet, so k/2 entries per
+// row always suffice.  One wave per row, the row held in registers (k <= 64 *
+// kCh * 8); a lane handles chunk c = lane + 64 i (8 elements = 2 quartets) and
+// the overflow slots are a wave prefix sum over the lanes' counts.
+template <int kCh>
+__global__ __launch_bounds__(256) void quantize_rows_sp24_kernel(const uint16_t* __restrict__ in, uint8_t* __restrict__ data,
+                                                                 uint8_t* __restrict__ meta, float* __restrict__ scales,
+                                                                 uint32_t* __restrict__ ovf_count, uint32_t* __restrict__ ovf,
+                                                                 int rows, int k, int valid_rows) {
+    const int lane = threadIdx.x & 63;
+    const int nw = gridDim.x * 4;
+    const int chunks = k >> 3;
+    const uint64_t below = (1ull << lane) - 1ull;
+    for (int row = blockIdx.x * 4 + (threadIdx.x >> 6); row < rows; row += nw) {
+        const bool live = row < valid_rows;
+        const uint16_t* x = in + (size_t)row * k;
+        uint4 cur[kCh];
+#pragma unroll
+        for (int i = 0; i < kCh; ++i) {
+            const int c = lane + 64 * i;
+            cur[i] = (live && c < chunks) ? *(const uint4*)(x + c * 8) : uint4{0, 0, 0, 0};
+        }
+        uint32_t acc = 0;
+#pragma unroll
+        for (int i = 0; i < kCh; ++i) acc = abs_max16(abs_max16(abs_max16(abs_max16(acc, cur[i].x), cur[i].y), cur[i].z), cur[i].w);
+        const uint32_t lane_max = (acc & 0xffffu) > (acc >> 16) ? (acc & 0xffffu) : (acc >> 16);
+        const uint32_t bits = __builtin_amdgcn_readfirstlane((uint32_t)wave_max((float)lane_max));
+        const bool exact = bits >= 0x7c00u;  // inf or NaN in the row: plain division
+        float m;
+        if (exact) {
+            m = 0.0f;
+#pragma unroll
+            for (int i = 0; i < kCh; ++i) {
+                const uint16_t* h = (const uint16_t*)&cur[i];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) m = __builtin_fmaxf(m, __builtin_fabsf(h2f(h[j])));
+            }
+            m = wave_max(m);
+        } else {
+            m = h2f((uint16_t)bits);
+        }
+        const float scale = m > 0.0f ? m / 127.0f : 1.0f;
+        const float inv = 1.0f / scale;
+        if (lane == 0) scales[row] = scale;
+        uint8_t* drow = data + (size_t)row * (k >> 1);
+        uint8_t* mrow = meta + (size_t)row * (k >> 3);
+        uint32_t* orow = ovf + (size_t)row * (k >> 1);
+        uint32_t base = 0;
+#pragma unroll
+        for (int i = 0; i < kCh; ++i) {
+            const int c = lane + 64 * i;
+            const uint16_t* h = (const uint16_t*)&cur[i];
+            uint32_t w[2];
+            if (exact) {
+                w[0] = w[1] = 0;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) w[j >> 2] |= ((uint32_t)rne_clamp(h2f(h[j]) / scale, -127, 127) & 255u) << (8 * (j & 3));
+            } else {
+                float v[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) v[j] = div_rn(h2f(h[j]), scale, inv);
+                w[0] = low_bytes4(rne_bits(v[0]), rne_bits(v[1]), rne_bits(v[2]), rne_bits(v[3]));
+                w[1] = low_bytes4(rne_bits(v[4]), rne_bits(v[5]), rne_bits(v[6]), rne_bits(v[7]));
+            }
+            uint32_t drop0, drop1;
+            const uint32_t q0 = compress_i8_quartet(w[0], drop0);
+            const uint32_t q1 = compress_i8_quartet(w[1], drop1);
+            const uint32_t drops = drop0 | (drop1 << 4);  // element j of the chunk
+            const uint32_t n = (uint32_t)__builtin_popcount(drops);
+            // exclusive prefix of n over the lanes below (n <= 4: three bit planes)
+            const uint64_t b0 = __builtin_amdgcn_ballot_w64((n & 1u) != 0);
+            const uint64_t b1 = __builtin_amdgcn_ballot_w64((n & 2u) != 0);
+            const uint64_t b2 = __builtin_amdgcn_ballot_w64((n & 4u) != 0);
+            const uint32_t pre = (uint32_t)__builtin_popcountll(b0 & below) + 2u * (uint32_t)__builtin_popcountll(b1 & below) +
+                                 4u * (uint32_t)__builtin_popcountll(b2 & below);
+            if (c < chunks) {
+                *(uint32_t*)(drow + 4 * c) = (q0 & 0xffffu) | (q1 << 16);
+                mrow[c] = (uint8_t)(((q0 >> 16) & 15u) | (((q1 >> 16) & 15u) << 4));
+                uint32_t slot = base + pre;
+                for (uint32_t d = drops; d != 0; d &= d - 1) {
+                    const int j = __builtin_ctz(d);
+                    orow[slot++] = ((uint32_t)(8 * c + j) << 8) | ((w[j >> 2] >> (8 * (j & 3))) & 255u);
+                }
+            }
+            base += (uint32_t)__builtin_popcountll(b0) + 2u * (uint32_t)__builtin_popcountll(b1) + 4u * (uint32_t)__builtin_popcountll(b2);
+        }
+        if (lane == 0) ovf_count[row] = base;
+    }
+}
+
 // Per-row weight packers (load-time derivation, encoder.rs:361-422 and
 // quant_benchmark.rs:779-829), rows of fp16 [n x k]:
 //   kind 0: FP8  scale = max|w| / 448 (1 for zero rows)
@@ -500,6 +631,16 @@ int launch_quantize_rows(int kind, const void* in, void* out, float* scales, int
         else if (kind == 1) quantize_rows_kernel<1, 8, false><<<grid, 256, 0, s>>>(x, o, scales, rows, k, valid_rows);
         else quantize_rows_kernel<2, 8, false><<<grid, 256, 0, s>>>(x, o, scales, rows, k, valid_rows);
     }
+    return 0;
+}
+
+int launch_quantize_rows_sp24(const void* in, uint8_t* data, uint8_t* meta, float* scales, uint32_t* ovf_count, uint32_t* ovf,
+                              int rows, int valid_rows, int k, hipStream_t s) {
+    if (rows == 0) return 0;
+    const unsigned grid = row_grid(rows);
+    const uint16_t* x = (const uint16_t*)in;
+    if (k <= 1024) quantize_rows_sp24_kernel<2><<<grid, 256, 0, s>>>(x, data, meta, scales, ovf_count, ovf, rows, k, valid_rows);
+    else quantize_rows_sp24_kernel<8><<<grid, 256, 0, s>>>(x, data, meta, scales, ovf_count, ovf, rows, k, valid_rows);
     return 0;
 }
 

@@ -698,6 +698,40 @@ void orc_compress_24(const uint8_t* x, int rows, int k, uint8_t* data, uint8_t* 
     }
 }
 
+/* Exact 2:4 form of INT8 rows (the activation-sparse FF2 of BASELINE config
+ * 4): per quartet the selection of orc_compress_24 on int8 magnitudes |v|
+ * (encoder.cu:685-704 keeps the two largest, ties to the lower index, in index
+ * order), and every nonzero it drops goes to the row's overflow list as
+ * (element << 8) | byte in ascending element order.  counts[r] entries at
+ * ovf[r * k/2 ...]. */
+void orc_compress_24_i8_exact(const int8_t* x, int rows, int k, uint8_t* data, uint8_t* meta, uint32_t* counts, uint32_t* ovf) {
+    memset(meta, 0, (size_t)rows * k / 8);
+    for (int r = 0; r < rows; ++r) {
+        uint32_t n = 0;
+        for (int p = 0; p < k / 4; ++p) {
+            const int8_t* v = x + (size_t)r * k + 4 * p;
+            int count = 0, nibble = 0;
+            for (int i = 0; i < 4; ++i) {
+                int rank = 0;
+                const int mi = abs((int)v[i]);
+                for (int j = 0; j < 4; ++j) {
+                    const int mj = abs((int)v[j]);
+                    rank += j != i && (mj > mi || (mj == mi && j < i));
+                }
+                if (rank < 2) {
+                    data[(size_t)r * k / 2 + 2 * p + count] = (uint8_t)v[i];
+                    nibble |= i << (2 * count);
+                    ++count;
+                } else if (v[i] != 0) {
+                    ovf[(size_t)r * (k / 2) + n++] = ((uint32_t)(4 * p + i) << 8) | (uint8_t)v[i];
+                }
+            }
+            meta[(size_t)r * k / 8 + p / 2] |= (uint8_t)(nibble << (4 * (p % 2)));
+        }
+        counts[r] = n;
+    }
+}
+
 void orc_decompress_24(const uint8_t* data, const uint8_t* meta, int rows, int k, uint8_t* x) {
     memset(x, 0, (size_t)rows * k);
     for (int r = 0; r < rows; ++r) {

@@ -66,6 +66,7 @@ def _declare(l):
         "orc_quantize_int8_rows": (None, [P, I, I, I, P, P]),
         "orc_quantize_int4_rows": (None, [P, I, I, I, P, P]),
         "orc_layer_norm_quantize": (None, [P, P, P, I, I, I, F, I, P, P, P]),
+        "orc_compress_24_i8_exact": (None, [P, I, I, P, P, P, P]),
         "orc_compress_24": (None, [P, I, I, P, P]),
         "orc_decompress_24": (None, [P, P, I, I, P]),
         "orc_gemm_i8_i32": (None, [P, P, I, I, I, P]),
@@ -329,6 +330,19 @@ def compress_24(x8: np.ndarray):
     meta = np.empty((m, k // 8), np.uint8)
     lib().orc_compress_24(_p(x8), m, k, _p(data), _p(meta))
     return data, meta
+
+
+def compress_24_i8_exact(x8: np.ndarray):
+    """INT8 rows -> (2:4 data, metadata, overflow counts, overflow lists);
+    entry j of row r is (element << 8) | byte, lists padded with zeros to k/2."""
+    x8 = np.ascontiguousarray(x8, dtype=np.int8)
+    m, k = x8.shape
+    data = np.empty((m, k // 2), np.uint8)
+    meta = np.empty((m, k // 8), np.uint8)
+    counts = np.empty(m, np.uint32)
+    ovf = np.zeros((m, k // 2), np.uint32)
+    lib().orc_compress_24_i8_exact(_p(x8), m, k, _p(data), _p(meta), _p(counts), _p(ovf))
+    return data, meta, counts, ovf
 
 
 def decompress_24(data: np.ndarray, meta: np.ndarray) -> np.ndarray:

@@ -234,6 +234,47 @@ def test_decompress_inverts_compress_on_sparse_rows(oracle):
     assert np.array_equal(oracle.decompress_24(data, meta), x)
 
 
+def test_compress_24_i8_exact_brute_force(oracle):
+    """Every quartet over an int8 alphabet with ties, signs, zeros and -128:
+    the kept pair is the two largest |v| (ties to the lower index) in index
+    order, the overflow holds exactly the other nonzeros in element order,
+    and kept pair + overflow rebuild the quartet."""
+    alphabet = [0, 1, -1, 2, -2, 127, -127, -128]
+    quartets = np.array(list(itertools.product(alphabet, repeat=4)), np.int8)
+    row = quartets.reshape(1, -1)
+    data, meta, counts, ovf = oracle.compress_24_i8_exact(row)
+    data = data.reshape(-1, 2).view(np.int8)
+    meta = meta.reshape(-1)
+    expect_ovf = []
+    for p, quartet in enumerate(quartets):
+        order = sorted(range(4), key=lambda i: (-abs(int(quartet[i])), i))[:2]
+        order.sort()
+        nib = (meta[p // 2] >> (4 * (p % 2))) & 15
+        assert [nib & 3, (nib >> 2) & 3] == order
+        assert data[p].tolist() == [int(quartet[order[0]]), int(quartet[order[1]])]
+        expect_ovf += [((4 * p + i) << 8) | (int(quartet[i]) & 255) for i in range(4) if i not in order and quartet[i] != 0]
+    assert counts[0] == len(expect_ovf) <= row.shape[1] // 2
+    assert ovf[0, :counts[0]].tolist() == expect_ovf
+
+
+def test_compress_24_i8_exact_rebuilds_rows(oracle):
+    """decompress(2:4 part) + scattered overflow == the row, on dense rows (two
+    overflow entries per full quartet: the k/2 bound), sparse and zero rows."""
+    rng = np.random.default_rng(10)
+    x = rng.integers(-128, 128, (6, 512), dtype=np.int8)
+    x[1, rng.random(512) < 0.9] = 0
+    x[2] = 0
+    x[3] = rng.integers(1, 128, 512)
+    data, meta, counts, ovf = oracle.compress_24_i8_exact(x)
+    rebuilt = oracle.decompress_24(data, meta).view(np.int8).copy()
+    for r in range(6):
+        for e in ovf[r, :counts[r]]:
+            assert rebuilt[r, e >> 8] == 0
+            rebuilt[r, e >> 8] = np.uint8(e & 255).view(np.int8)
+    assert np.array_equal(rebuilt, x)
+    assert counts[3] == 256 and counts[2] == 0
+
+
 # ---- GEMMs against numpy --------------------------------------------------------------
 
 def test_gemm_i8_exact(oracle):
