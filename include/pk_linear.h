@@ -365,6 +365,13 @@ int32_t pk_gemm(int32_t format, int32_t epilogue, const void* a, const void* b, 
  * reference (its kernels have one tile shape); it lets callers and tests see
  * which kernel variant a shape runs. */
 int32_t pk_gemm_tile(int32_t format, int32_t epilogue, int32_t m, int32_t n, int32_t* tile_cols, int32_t* stages);
+/* K split of pk_gemm's launch for an m x n x k output (host only): 4 when each
+ * 32-row tile's K-steps are divided over the four waves of its workgroup and
+ * the partial tiles summed in K order (INT4-g128 formats on grids that take
+ * 32-row tiles, k >= 1024; each wave then has its own LDS ring, and *stages
+ * of pk_gemm_tile is the plain ring's), else 1; or a negative PK_E_* status.
+ * No counterpart in the reference. */
+int32_t pk_gemm_k_split(int32_t format, int32_t epilogue, int32_t m, int32_t n, int32_t k);
 
 /* ---- TDT joint (decoder.cu:690-759) ------------------------------------------ */
 

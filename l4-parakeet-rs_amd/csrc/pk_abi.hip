@@ -243,6 +243,13 @@ int32_t pk_gemm_tile(int32_t format, int32_t epilogue, int32_t m, int32_t n, int
     return r;
 }
 
+int32_t pk_gemm_k_split(int32_t format, int32_t epilogue, int32_t m, int32_t n, int32_t k) {
+    if (m < 0 || n <= 0 || k <= 0) { set_error("invalid GEMM shape m=%d n=%d k=%d", m, n, k); return PK_E_SHAPE; }
+    const int r = gemm_k_split(format, epilogue, m, n, k);
+    if (r < 0) set_error(r == PK_E_ARG ? "unknown format %d" : "PK_GEMM_TILE_ROWS must be 64, 128 or 256", format);
+    return r;
+}
+
 int32_t pk_linear_fp16_epilogue(const uint16_t* in, const uint16_t* w, const float* bias, const uint16_t* residual, uint16_t* out,
                                 int32_t m, int32_t n, int32_t k, float out_scale, float res_scale, int32_t act, void* stream) {
     return pk_gemm(FMT_F16, EPI_F16, in, w, m, n, k, nullptr, nullptr, 1.0f, bias, residual, out_scale, res_scale, act, nullptr,

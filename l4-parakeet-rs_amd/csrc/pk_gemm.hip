@@ -92,6 +92,30 @@ static int launch_ring(const GemmArgs& a, hipStream_t s) {
     return 0;
 }
 
+// One 32-row tile per workgroup with K split over its 4 waves (INT4-g128
+// formats, grids that take 32-row ring tiles, K >= 1024).
+template <int F, int E>
+static int launch_splitk(const GemmArgs& a, hipStream_t s) {
+    using L = g3::LK<F>;
+    static std::once_flag once;
+    static hipError_t attr = hipSuccess;
+    std::call_once(once, [] {
+        attr = hipFuncSetAttribute((const void*)g3::gemm3_splitk_kernel<F, E>, hipFuncAttributeMaxDynamicSharedMemorySize, L::kBytes);
+    });
+    if (attr != hipSuccess) {
+        set_error("hipFuncSetAttribute(LDS %d bytes) failed: %s", L::kBytes, hipGetErrorString(attr));
+        return -3;
+    }
+    const int tiles = ((a.m + L::kBM - 1) / L::kBM) * ((a.n + g3::kBN - 1) / g3::kBN);
+    hipLaunchKernelGGL((g3::gemm3_splitk_kernel<F, E>), dim3(tiles), dim3(g3::kThreads), L::kBytes, s, a);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        set_error("gemm launch (fmt %d, epi %d) failed: %s", F, E, hipGetErrorString(e));
+        return -3;
+    }
+    return 0;
+}
+
 // Formats with a ring variant and the tile rows it takes for an m x n
 // output: the smallest tile (32, 64 or 128 rows) whose tile count fits one
 // workgroup per CU, or 0 when even 128-row tiles outnumber the CUs.
@@ -108,6 +132,14 @@ static int ring_stages(int fmt, int kAI) {
     case FMT_G128A8: return ring_stages_of<FMT_G128A8>(kAI);
     default: return ring_stages_of<FMT_G128A16>(kAI);
     }
+}
+// The K split of a launch: 4 (gemm3_splitk_kernel) for the INT4-g128 formats
+// when the ring takes 32-row tiles and K >= 1024 (C3 FF2 at T = 750: the ring
+// kernel's 64 / 32 K-steps per tile become 16 / 8 per wave), else 1.
+static int ring_rows(int m, int n);
+static int k_split(int fmt, int epi, int m, int n, int k) {
+    if ((fmt != FMT_G128A8 && fmt != FMT_G128A16) || !has_ring(fmt, epi) || k < 1024) return 1;
+    return ring_rows(m, n) == 32 ? 4 : 1;
 }
 static int ring_rows(int m, int n) {
     if (forced_tile_rows() != 0) return 0;
@@ -192,6 +224,11 @@ template <int F, int E>
 static int launch_fmt(const GemmArgs& a, hipStream_t s) {
     int cols = 0, stages = 0;
     const int rows = tile_plan(F, E == EPI_F16_RES ? EPI_F16 : E, a.m, a.n, &cols, &stages);
+    if constexpr (F == FMT_G128A8 || F == FMT_G128A16) {
+        if constexpr (E != EPI_GLU && E != EPI_F8_24) {
+            if (k_split(F, E == EPI_F16_RES ? EPI_F16 : E, a.m, a.n, a.k) == 4) return launch_splitk<F, E>(a, s);
+        }
+    }
     if constexpr (F == FMT_FP8 || F == FMT_I8 || F == FMT_G128A8 || F == FMT_G128A16) {
         if constexpr (E != EPI_GLU && E != EPI_F8_24) {
             if (stages > 2) return rows == 32 ? launch_ring<F, E, 1>(a, s) : (rows == 64 ? launch_ring<F, E, 2>(a, s) : launch_ring<F, E, 4>(a, s));
@@ -302,6 +339,12 @@ int launch_gemm(int fmt, int epi, const GemmArgs& a, hipStream_t s) {
     }
     set_error("unknown format %d", fmt);
     return -4;
+}
+
+int gemm_k_split(int fmt, int epi, int m, int n, int k) {
+    if (fmt < FMT_FP8 || fmt > FMT_Q4K) return -4;
+    if (forced_tile_rows() < 0) return -1;
+    return k_split(fmt, epi == EPI_F16_RES ? EPI_F16 : epi, m, n, k);
 }
 
 int gemm_tile_plan(int fmt, int epi, int m, int n, int* cols, int* stages) {

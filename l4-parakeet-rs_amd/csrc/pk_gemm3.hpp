@@ -672,5 +672,192 @@ __global__ __launch_bounds__(kThreads, 1) void gemm3_ring_kernel(GemmArgs p) {
     else epilogue<F, E, false, kAI>(p, accf, acci, m0, n0, wm, wn, lane);
 }
 
+
+// ---- small grids, long K: one 32 x 128 tile per workgroup, K split over its 4 waves ----
+//
+// For the group-wise INT4 formats at small T (BASELINE config 3 at T = 750:
+// 192 tiles of 32 rows for FF2, K = 4096) the ring kernel above is a chain of
+// K-steps whose every link is an LDS read, the INT4 decode and the MFMAs; the
+// tile count cannot grow.  Here each wave takes a quarter of the K-steps and
+// computes the whole 32 x 128 tile (2 x 8 blocks of 16 x 16) over it, with a
+// private LDS ring (its own direct-to-LDS loads, waited for by vmcnt; no
+// barrier inside the K-loop), so the chain is a quarter as long.  The group
+// tables of the tile's columns (fp16 scales, u8 zero points, all groups) are
+// loaded once.  Then the four partial tiles meet in LDS and wave q adds the
+// partials of quarter q in K order, ((p0 + p1) + p2) + p3, and runs the
+// epilogue of the ring kernel's wave q on them.  Within a part the arithmetic
+// is the ring kernel's (INT4-g128 x INT8: exact int32 group sums, each scaled
+// and added in group order), so the result is the ring kernel's with the fp32
+// sum over groups associated by parts.
+template <int F> struct LK {
+    static constexpr int kBM = 32;
+    static constexpr int kATile = kBM * kRowBytes;
+    static constexpr int kBTile = kBN * FmtTraits<F>::bRow;
+    static constexpr int kStage = kATile + kBTile;
+    static constexpr int kTabBytes = kMaxG128Groups * kBN * 3;  // fp16 scales + u8 zero points [group][column]
+    static constexpr int kFit = (160 * 1024 - kTabBytes) / (4 * kStage);
+    static constexpr int kS = kFit > 4 ? 4 : kFit;
+    static constexpr int kWave = kS * kStage;  // one wave's ring
+    static constexpr int kTab = 4 * kWave;
+    static constexpr int kBytes = kTab + kTabBytes;
+    static constexpr int kBLoads = kBTile / 1024;
+    static constexpr int kOps = 4 + kBLoads;  // direct-to-LDS loads per wave and stage
+    static constexpr int kRed = 16 * 64 * 64;  // partials [quarter][wave][lane] x 16 floats
+    static_assert(kS >= 2 && kS <= 4 && kBytes <= 160 * 1024 && kRed <= kTab, "split-K layout");
+};
+
+template <int F, int E>
+__global__ __launch_bounds__(kThreads, 1) void gemm3_splitk_kernel(GemmArgs p) {
+    static_assert(F == FMT_G128A8 || F == FMT_G128A16, "group-wise INT4 formats");
+    using T = FmtTraits<F>;
+    using L = LK<F>;
+    constexpr int kS = L::kS;
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int g = lane >> 4, l16 = lane & 15;
+    const int tiles_n = (p.n + kBN - 1) / kBN;
+    const int tiles_m = (p.m + L::kBM - 1) / L::kBM;
+    const int tile = blockIdx.x;
+    if (tile >= tiles_m * tiles_n) return;
+    const int m0 = (tile % tiles_m) * L::kBM, n0 = (tile / tiles_m) * kBN;
+    const size_t lda = (size_t)p.k * T::aElemNum / T::aElemDen;
+    const size_t ldb = (size_t)p.k * T::bNum / T::bDen;
+    const int steps = p.k / T::kStep;
+    const int groups = p.k >> 7;
+    // this wave's K-steps (wave-uniform: the loads' global base is a scalar operand)
+    const int s0 = __builtin_amdgcn_readfirstlane(steps * wave / 4);
+    const int ns = __builtin_amdgcn_readfirstlane(steps * (wave + 1) / 4) - s0;
+    const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)lds;
+    const uint32_t ring = lds_base + (uint32_t)(wave * L::kWave);
+    uint16_t* tab_s = (uint16_t*)(lds + L::kTab);
+    uint8_t* tab_z = lds + L::kTab + kMaxG128Groups * kBN * 2;
+
+    // activation load i: tile rows 8i + lane / 8, 16-byte chunk position lane % 8
+    // (holding source chunk position ^ swz_key(row)); weight loads as the ring kernel's
+    uint32_t a_off[4], b_off[L::kBLoads];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int r = 8 * i + (lane >> 3);
+        a_off[i] = (uint32_t)min(m0 + r, p.m - 1) * (uint32_t)lda + (uint32_t)((((lane & 7) ^ swz_key(r))) << 4);
+    }
+#pragma unroll
+    for (int i = 0; i < L::kBLoads; ++i) {
+        const int o = i * 1024 + lane * 16;
+        int row, c;
+        if constexpr (F == FMT_G128A8) {
+            row = o >> 6;
+            c = ((o >> 4) & 3) ^ g128a8_key(row);
+        } else {
+            row = o / T::bRow;
+            c = (o % T::bRow) / 16;
+        }
+        b_off[i] = (uint32_t)min(n0 + row, p.n - 1) * (uint32_t)ldb + (uint32_t)(c * 16);
+    }
+    auto issue = [&](int j) {
+        const int step = s0 + j;
+        const uint32_t base = ring + (uint32_t)((j % kS) * L::kStage);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dma16(p.a + (size_t)step * kRowBytes, a_off[i], base + i * 1024);
+#pragma unroll
+        for (int i = 0; i < L::kBLoads; ++i) dma16(p.b + (size_t)step * T::bRow, b_off[i], base + L::kATile + i * 1024);
+    };
+    const int pre = min(kS - 1, ns);
+    for (int j = 0; j < pre; ++j) issue(j);
+    for (int e = tid; e < kBN * groups; e += kThreads) {
+        const int col = e % kBN, grp = e / kBN;
+        const size_t gi = (size_t)min(n0 + col, p.n - 1) * groups + grp;
+        tab_s[grp * kBN + col] = p.g_scales[gi];
+        tab_z[grp * kBN + col] = (uint8_t)(int)h2f(p.g_zeros[gi]);
+    }
+    __syncthreads();
+
+    v4f accf[2][8];
+    v4i acci[2][8];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            accf[i][c] = v4f{0.f, 0.f, 0.f, 0.f};
+            acci[i][c] = v4i{0, 0, 0, 0};
+        }
+    for (int j = 0; j < ns; ++j) {
+        switch (min(j + kS - 2, ns - 1) - j) {  // younger stages still loading: 0 .. kS - 2 <= 2
+        case 0: wait_vm<0>(); break;
+        case 1: wait_vm<L::kOps>(); break;
+        default: wait_vm<2 * L::kOps>(); break;
+        }
+        if (j + kS - 1 < ns) issue(j + kS - 1);
+        const uint8_t* As = lds + wave * L::kWave + (j % kS) * L::kStage;
+        const uint8_t* Bs = As + L::kATile;
+        const int grp = ((s0 + j) * T::kStep) >> 7;
+        const uint16_t* ts = tab_s + grp * kBN;
+        const uint8_t* tz = tab_z + grp * kBN;
+        uint4 x0[2], x1[2];
+#pragma unroll
+        for (int rw = 0; rw < 2; ++rw) {
+            x0[rw] = *(const uint4*)(As + swz(rw * 16 + l16, g));
+            x1[rw] = *(const uint4*)(As + swz(rw * 16 + l16, 4 + g));
+        }
+#pragma unroll
+        for (int cb = 0; cb < 8; ++cb) {
+            const int cw = cb >> 2, bj = cb & 3;
+            const int row = cw * 64 + wrow(l16, bj);
+            const uint32_t z = tz[row];
+            uint4 w0, w1;
+            v4f gs = v4f{1.f, 1.f, 1.f, 1.f};
+            if constexpr (F == FMT_G128A8) {
+                const uint16_t* sc = ts + cw * 64 + g * 16 + bj * 4;
+                gs = v4f{h2f(sc[0]), h2f(sc[1]), h2f(sc[2]), h2f(sc[3])};
+                const uint32_t zz = z * 0x01010101u;
+                const int key = g128a8_key(row), half = (g & 1) << 3;
+                const uint2 q0 = *(const uint2*)(Bs + row * 64 + ((((g >> 1)) ^ key) << 4) + half);
+                const uint2 q1 = *(const uint2*)(Bs + row * 64 + (((2 + (g >> 1)) ^ key) << 4) + half);
+                u4x8_minus_z(q0.x, zz, w0.x, w0.y);
+                u4x8_minus_z(q0.y, zz, w0.z, w0.w);
+                u4x8_minus_z(q1.x, zz, w1.x, w1.y);
+                u4x8_minus_z(q1.y, zz, w1.z, w1.w);
+            } else {
+                const _Float16 sh = __builtin_bit_cast(_Float16, ts[row]);
+                const _Float16 zh = (_Float16)(1024 + (int)z);
+                const v2h ss = {sh, sh}, zzh = {zh, zh};
+                const uint32_t q0 = *(const uint32_t*)(Bs + row * 32 + 4 * g);
+                const uint32_t q1 = *(const uint32_t*)(Bs + row * 32 + 16 + 4 * g);
+                w0 = __builtin_bit_cast(uint4, u4x8_to_h(q0, zzh, ss));
+                w1 = __builtin_bit_cast(uint4, u4x8_to_h(q1, zzh, ss));
+            }
+#pragma unroll
+            for (int rw = 0; rw < 2; ++rw) mfma_step<F>(accf[rw][cb], acci[rw][cb], w0, w1, x0[rw], x1[rw], gs);
+        }
+    }
+
+    // partials of quarter q = (rows 16 (q / 2), columns 64 (q % 2)) to LDS
+    __syncthreads();  // every wave is done with its ring
+    float* red = (float*)lds;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        float4* dst = (float4*)(red + ((q * 4 + wave) * 64 + lane) * 16);
+#pragma unroll
+        for (int bj = 0; bj < 4; ++bj) {
+            const v4f v = accf[q >> 1][(q & 1) * 4 + bj];
+            dst[bj] = float4{v[0], v[1], v[2], v[3]};
+        }
+    }
+    __syncthreads();
+    v4f sum[1][4];
+    v4i isum[1][4];
+#pragma unroll
+    for (int bj = 0; bj < 4; ++bj) {
+        const float4 a0 = ((const float4*)(red + ((wave * 4 + 0) * 64 + lane) * 16))[bj];
+        const float4 a1 = ((const float4*)(red + ((wave * 4 + 1) * 64 + lane) * 16))[bj];
+        const float4 a2 = ((const float4*)(red + ((wave * 4 + 2) * 64 + lane) * 16))[bj];
+        const float4 a3 = ((const float4*)(red + ((wave * 4 + 3) * 64 + lane) * 16))[bj];
+        sum[0][bj] = v4f{((a0.x + a1.x) + a2.x) + a3.x, ((a0.y + a1.y) + a2.y) + a3.y, ((a0.z + a1.z) + a2.z) + a3.z,
+                         ((a0.w + a1.w) + a2.w) + a3.w};
+        isum[0][bj] = v4i{0, 0, 0, 0};
+    }
+    if constexpr (E == EPI_F16_RES) epilogue<F, EPI_F16, true, 1>(p, sum, isum, m0, n0, wave >> 1, wave & 1, lane);
+    else epilogue<F, E, false, 1>(p, sum, isum, m0, n0, wave >> 1, wave & 1, lane);
+}
+
 }  // namespace g3
 }  // namespace pk

@@ -14,6 +14,8 @@ int launch_gemm(int fmt, int epi, const GemmArgs& args, hipStream_t stream);
 // Tile rows the launcher picks for an m x n output (sets *cols and the
 // number of LDS stages), or a negative status.
 int gemm_tile_plan(int fmt, int epi, int m, int n, int* cols, int* stages);
+// K split of an m x n x k launch (4: one tile per workgroup, K over its waves; else 1).
+int gemm_k_split(int fmt, int epi, int m, int n, int k);
 int launch_quantize_static(const void* in, void* out, float inverse_scale, size_t elements, bool int8, hipStream_t s);
 int launch_quantize_rows(int kind, const void* in, void* out, float* scales, int rows, int valid_rows, int k, hipStream_t s);
 // INT8 rows as 2:4 data / metadata plus per-row overflow lists (k % 128 == 0, k <= 4096).

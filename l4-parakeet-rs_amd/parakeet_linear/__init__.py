@@ -91,6 +91,7 @@ SIGNATURES = {
     "pk_quantize_rows_int8_sparse24": (I, [P, P, P, P, P, P, I, I, I, P]),
     "pk_transpose_int8": (I, [P, P, I, I, P]),
     "pk_ffn_contract_int8_sparse24": (I, [P, P, P, P, P, P, P, P, P, I, P]),
+    "pk_gemm_k_split": (I, [I, I, I, I, I]),
     "pk_gemm_tile": (I, [I, I, I, I, ctypes.POINTER(I), ctypes.POINTER(I)]),
     "pk_gemm": (I, [I, I, P, P, I, I, I, P, P, F, P, P, F, F, I, P, P, P, P, I, P]),
     "pk_joint_gemv": (I, [P, I, P, P, P, P, P, P, I, I, I, I, I, I, P]),
@@ -212,6 +213,14 @@ def gemm_tile(fmt, epi, m, n, stages=False):
     if rows < 0:
         raise PkError(f"pk_gemm_tile: status {rows}: {last_error()}")
     return (rows, cols.value, st.value) if stages else (rows, cols.value)
+
+
+def gemm_k_split(fmt, epi, m, n, k):
+    """K split (1 or 4) of pk_gemm's launch for an m x n x k output."""
+    r = lib.pk_gemm_k_split(fmt, epi, m, n, k)
+    if r < 0:
+        raise PkError(f"pk_gemm_k_split: status {r}: {last_error()}")
+    return r
 
 
 FMT_FP8, FMT_I8, FMT_S4, FMT_G128A8, FMT_F16, FMT_G128A16, FMT_I8_SKIP, FMT_Q4K = range(8)

@@ -855,23 +855,32 @@ void orc_gemm_g128_a16(const uint16_t* x, const uint32_t* q, const uint16_t* sca
 }
 
 /* W4A8: exact i32 per-group accumulators acc_g = sum x_i8 * (q - z) (z is an
- * integer), then out = x_scale * (sum over g in order of fmaf(acc_g, s_g, .)). */
+ * integer), then out = x_scale * (sum over g in order of fmaf(acc_g, s_g, .)).
+ * parts > 1: the groups are split into `parts` contiguous runs (run p: groups
+ * [groups p / parts, groups (p + 1) / parts)), each summed in order from 0,
+ * and the run sums added in order -- the association of the kernel that
+ * splits a tile's K-steps over its waves. */
 void orc_gemm_g128_a8(const int8_t* x, const float* x_scales, const uint32_t* q,
-                      const uint16_t* scales, const uint16_t* zeros, int m, int n, int k,
+                      const uint16_t* scales, const uint16_t* zeros, int m, int n, int k, int parts,
                       int32_t* group_acc, float* out) {
     int groups = k / 128;
+    if (parts < 1) parts = 1;
 #pragma omp parallel for schedule(static) num_threads(g_threads)
     for (int i = 0; i < m; ++i) {
         for (int j = 0; j < n; ++j) {
             float total = 0.0f;
-            for (int g = 0; g < groups; ++g) {
-                int z = (int)orc_f16_to_f32(zeros[(size_t)j * groups + g]);
-                int32_t a = 0;
-                for (int t = g * 128; t < g * 128 + 128; ++t) {
-                    a += (int32_t)x[(size_t)i * k + t] * (g128_level(q, k, j, t) - z);
+            for (int p = 0; p < parts; ++p) {
+                float part = 0.0f;
+                for (int g = groups * p / parts; g < groups * (p + 1) / parts; ++g) {
+                    int z = (int)orc_f16_to_f32(zeros[(size_t)j * groups + g]);
+                    int32_t a = 0;
+                    for (int t = g * 128; t < g * 128 + 128; ++t) {
+                        a += (int32_t)x[(size_t)i * k + t] * (g128_level(q, k, j, t) - z);
+                    }
+                    if (group_acc) group_acc[((size_t)i * n + j) * groups + g] = a;
+                    part = fmaf((float)a, orc_f16_to_f32(scales[(size_t)j * groups + g]), part);
                 }
-                if (group_acc) group_acc[((size_t)i * n + j) * groups + g] = a;
-                total = fmaf((float)a, orc_f16_to_f32(scales[(size_t)j * groups + g]), total);
+                total = p == 0 ? part : total + part;
             }
             out[(size_t)i * n + j] = total * x_scales[i];
         }

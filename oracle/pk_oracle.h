@@ -72,7 +72,7 @@ void orc_gemm_f16_f32(const uint16_t* x, const uint16_t* w, int m, int n, int k,
 void orc_gemm_g128_a16(const uint16_t* x, const uint32_t* q, const uint16_t* scales,
                        const uint16_t* zeros, int m, int n, int k, float* out);
 void orc_gemm_g128_a8(const int8_t* x, const float* x_scales, const uint32_t* q,
-                      const uint16_t* scales, const uint16_t* zeros, int m, int n, int k,
+                      const uint16_t* scales, const uint16_t* zeros, int m, int n, int k, int parts,
                       int32_t* group_acc, float* out);
 void orc_gemm_q4k_f32(const uint16_t* x, const uint8_t* blocks, int m, int n, int k, float* acc);
 

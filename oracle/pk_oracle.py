@@ -74,7 +74,7 @@ def _declare(l):
         "orc_gemm_e4m3_f32": (None, [P, P, I, I, I, P]),
         "orc_gemm_f16_f32": (None, [P, P, I, I, I, P]),
         "orc_gemm_g128_a16": (None, [P, P, P, P, I, I, I, P]),
-        "orc_gemm_g128_a8": (None, [P, P, P, P, P, I, I, I, P, P]),
+        "orc_gemm_g128_a8": (None, [P, P, P, P, P, I, I, I, I, P, P]),
         "orc_gemm_q4k_f32": (None, [P, P, I, I, I, P]),
         "orc_epilogue": (None, [P, P, F, P, P, I, I, I, I, P, P]),
         "orc_epilogue_linear": (None, [P, P, P, I, I, F, F, I, P]),
@@ -406,14 +406,14 @@ def gemm_g128_a16(x16, q, s, z) -> np.ndarray:
     return out
 
 
-def gemm_g128_a8(x8, x_scales, q, s, z, want_group_acc=False):
+def gemm_g128_a8(x8, x_scales, q, s, z, want_group_acc=False, parts=1):
     x8 = np.ascontiguousarray(x8, np.int8)
     m, k = x8.shape
     n = q.shape[0]
     out = np.empty((m, n), np.float32)
     gacc = np.empty((m, n, k // 128), np.int32) if want_group_acc else None
     lib().orc_gemm_g128_a8(_p(x8), _p(np.ascontiguousarray(x_scales, np.float32)),
-                           _p(np.ascontiguousarray(q)), _p(_h(s)), _p(_h(z)), m, n, k,
+                           _p(np.ascontiguousarray(q)), _p(_h(s)), _p(_h(z)), m, n, k, parts,
                            _p(gacc), _p(out))
     return (out, gacc) if want_group_acc else out
 

@@ -455,8 +455,9 @@ def test_int4g128_a8_exact(pk, orc, m, n, k):
     xq, xs = orc.quantize_int8_rows(x)
     out = empty((m, n), torch.float32)
     pk.call("pk_linear_int4g128_a8", dev(xq), dev(xs), dev(q), dev(s), dev(z), None, out, 1, m, n, k)
-    ref = orc.gemm_g128_a8(xq, xs, q, s, z)
-    assert np.array_equal(host(out), ref)
+    parts = pk.gemm_k_split(pk.FMT_G128A8, pk.EPI_F32, m, n, k)
+    ref = orc.gemm_g128_a8(xq, xs, q, s, z, parts=parts)
+    assert np.array_equal(host(out), ref), f"K split {parts}"
 
 
 # ---- Q4_K ----------------------------------------------------------------------------------

@@ -120,10 +120,17 @@ def test_ring_fp8_epilogues(pk, orc, m, n, k):
                  tol=2e-2)
 
 
-@pytest.mark.parametrize("m,n,k", [(750, 1024, 4096), (97, 1024, 4096), (750, 4096, 1024), (5, 256, 256)])
+# shapes whose 32-row ring tiles split K over the workgroup's four waves
+SPLIT_SHAPES = {(750, 1024, 4096), (97, 1024, 4096), (45, 1024, 1280), (33, 256, 1024)}
+
+
+@pytest.mark.parametrize("m,n,k", [(750, 1024, 4096), (97, 1024, 4096), (750, 4096, 1024), (5, 256, 256),
+                                   (45, 1024, 1280), (33, 256, 1024)])
 def test_ring_int4g128_a8_exact(pk, orc, m, n, k):
     """INT4-g128 x INT8: fp32 (and fp16 + residual) outputs bit for bit; the
-    ring loads each tile's group tables once and indexes them by K-step."""
+    ring loads each tile's group tables once and indexes them by K-step.  The
+    split-K shapes (10 groups over 4 waves: runs of 2, 3, 2, 3; 8 over 4)
+    compare with the oracle's matching association of the group sum."""
     rows = ring(pk, pk.FMT_G128A8, pk.EPI_F32, m, n)
     note(f"g128 a8 m={m} n={n} k={k} ring rows={rows}")
     rng = np.random.default_rng(11 * m + k)
@@ -133,7 +140,9 @@ def test_ring_int4g128_a8_exact(pk, orc, m, n, k):
     xq, xs = orc.quantize_int8_rows(x)
     out = torch.empty((m, n), dtype=torch.float32, device="cuda")
     pk.call("pk_linear_int4g128_a8", dev(xq), dev(xs), dev(q), dev(s), dev(z), None, out, 1, m, n, k)
-    ref = orc.gemm_g128_a8(xq, xs, q, s, z)
+    parts = pk.gemm_k_split(pk.FMT_G128A8, pk.EPI_F32, m, n, k)
+    assert parts == (4 if (m, n, k) in SPLIT_SHAPES else 1), parts
+    ref = orc.gemm_g128_a8(xq, xs, q, s, z, parts=parts)
     assert np.array_equal(host(out), ref)
     res = rng.standard_normal((m, n)).astype(np.float16)
     st = dev(res.copy())
@@ -141,11 +150,22 @@ def test_ring_int4g128_a8_exact(pk, orc, m, n, k):
             res_scale=1.0, g_scales=dev(s), g_zeros=dev(z))
     want = orc.epilogue(ref, 2, np.ones(n, np.float32), residual=res)
     assert np.array_equal(host(st).view(np.uint16), want.view(np.uint16))
+    if (m, n, k) in SPLIT_SHAPES:
+        # the SiLU -> e4m3 epilogue on the split path (one e4m3 step on < 1 % of codes)
+        o8 = torch.empty((m, n), dtype=torch.uint8, device="cuda")
+        pk.gemm(pk.FMT_G128A8, pk.EPI_F8, dev(xq), dev(q), m, n, k, o8, row_scales=dev(xs), g_scales=dev(s),
+                g_zeros=dev(z))
+        ref8 = orc.epilogue(ref, 1, np.ones(n, np.float32))
+        got8 = host(o8)
+        t = orc.e4m3_table().astype(np.float64)
+        assert np.mean(got8 == ref8) >= 0.99
+        assert np.all(np.abs(t[got8] - t[ref8]) <= np.abs(t[ref8]) / 8 + 2.0 ** -9 + 1e-12)
 
 
-@pytest.mark.parametrize("m,n,k", [(750, 1024, 4096), (750, 4096, 1024), (97, 1024, 4096)])
+@pytest.mark.parametrize("m,n,k", [(750, 1024, 4096), (750, 4096, 1024), (97, 1024, 4096), (45, 1024, 1280)])
 def test_ring_int4g128_a16(pk, orc, m, n, k):
     ring(pk, pk.FMT_G128A16, pk.EPI_F32, m, n)
+    note(f"g128 a16 m={m} n={n} k={k} split={pk.gemm_k_split(pk.FMT_G128A16, pk.EPI_F32, m, n, k)}")
     rng = np.random.default_rng(13 * m + k)
     w = (rng.standard_normal((n, k)) * 0.02).astype(np.float16)
     q, s, z = orc.pack_int4_g128(w)

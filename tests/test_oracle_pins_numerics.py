@@ -256,6 +256,28 @@ def test_gemm_g128_a8_fold_order(oracle):
     assert np.array_equal(out, total * xs[:, None])
 
 
+def test_gemm_g128_a8_parts_association(oracle):
+    """parts > 1: each contiguous run of groups folded from 0 in order, the run
+    sums added in order (the association of the split-K kernel), emulated
+    exactly for 2 and 4 runs of 4 groups; 3 runs of 4 groups: runs [0,1),
+    [1,2), [2,4)."""
+    rng = np.random.default_rng(21)
+    w = (rng.standard_normal((24, 512)) * 0.02).astype(np.float16)
+    q, s, z = oracle.pack_int4_g128(w)
+    x = (rng.standard_normal((9, 512)) * 2).astype(np.float16)
+    x8, xs = oracle.quantize_int8_rows(x)
+    _, gacc = oracle.gemm_g128_a8(x8, xs, q, s, z, want_group_acc=True)
+    for parts, runs in ((2, [(0, 2), (2, 4)]), (4, [(0, 1), (1, 2), (2, 3), (3, 4)]), (3, [(0, 1), (1, 2), (2, 4)])):
+        total = None
+        for lo, hi in runs:
+            part = np.zeros((9, 24), F32)
+            for g in range(lo, hi):
+                part = f32_fma(gacc[:, :, g].astype(F32), s[:, g].astype(F32)[None, :], part)
+            total = part if total is None else (total + part).astype(F32)
+        out = oracle.gemm_g128_a8(x8, xs, q, s, z, parts=parts)
+        assert np.array_equal(out, total * xs[:, None]), parts
+
+
 def test_joint_scores_i8_matches_float64(oracle):
     """score[o] = w_scale[o] * sum_k W[o,k] relu(f32(enc_k) + pred_k) + b[o]."""
     rng = np.random.default_rng(19)
