@@ -702,7 +702,7 @@ template <int F> struct LK {
     static constexpr int kBytes = kTab + kTabBytes;
     static constexpr int kBLoads = kBTile / 1024;
     static constexpr int kOps = 4 + kBLoads;  // direct-to-LDS loads per wave and stage
-    static constexpr int kRed = 16 * 64 * 64;  // partials [quarter][wave][lane] x 16 floats
+    static constexpr int kRed = 16 * 64 * 64;  // partials [quarter][wave][block][lane] x 4 floats
     static_assert(kS >= 2 && kS <= 4 && kBytes <= 160 * 1024 && kRed <= kTab, "split-K layout");
 };
 
@@ -806,8 +806,9 @@ __global__ __launch_bounds__(kThreads, 1) void gemm3_splitk_kernel(GemmArgs p) {
             uint4 w0, w1;
             v4f gs = v4f{1.f, 1.f, 1.f, 1.f};
             if constexpr (F == FMT_G128A8) {
-                const uint16_t* sc = ts + cw * 64 + g * 16 + bj * 4;
-                gs = v4f{h2f(sc[0]), h2f(sc[1]), h2f(sc[2]), h2f(sc[3])};
+                const uint2 sc = *(const uint2*)(ts + cw * 64 + g * 16 + bj * 4);  // 4 fp16 scales, one read
+                gs = v4f{h2f((uint16_t)(sc.x & 0xffffu)), h2f((uint16_t)(sc.x >> 16)), h2f((uint16_t)(sc.y & 0xffffu)),
+                         h2f((uint16_t)(sc.y >> 16))};
                 const uint32_t zz = z * 0x01010101u;
                 const int key = g128a8_key(row), half = (g & 1) << 3;
                 const uint2 q0 = *(const uint2*)(Bs + row * 64 + ((((g >> 1)) ^ key) << 4) + half);
@@ -832,25 +833,24 @@ __global__ __launch_bounds__(kThreads, 1) void gemm3_splitk_kernel(GemmArgs p) {
 
     // partials of quarter q = (rows 16 (q / 2), columns 64 (q % 2)) to LDS
     __syncthreads();  // every wave is done with its ring
-    float* red = (float*)lds;
+    // [quarter][wave][block][lane] float4: consecutive lanes write consecutive 16 bytes
+    float4* red = (float4*)lds;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        float4* dst = (float4*)(red + ((q * 4 + wave) * 64 + lane) * 16);
+    for (int q = 0; q < 4; ++q)
 #pragma unroll
         for (int bj = 0; bj < 4; ++bj) {
             const v4f v = accf[q >> 1][(q & 1) * 4 + bj];
-            dst[bj] = float4{v[0], v[1], v[2], v[3]};
+            red[((q * 4 + wave) * 4 + bj) * 64 + lane] = float4{v[0], v[1], v[2], v[3]};
         }
-    }
     __syncthreads();
     v4f sum[1][4];
     v4i isum[1][4];
 #pragma unroll
     for (int bj = 0; bj < 4; ++bj) {
-        const float4 a0 = ((const float4*)(red + ((wave * 4 + 0) * 64 + lane) * 16))[bj];
-        const float4 a1 = ((const float4*)(red + ((wave * 4 + 1) * 64 + lane) * 16))[bj];
-        const float4 a2 = ((const float4*)(red + ((wave * 4 + 2) * 64 + lane) * 16))[bj];
-        const float4 a3 = ((const float4*)(red + ((wave * 4 + 3) * 64 + lane) * 16))[bj];
+        const float4 a0 = red[((wave * 4 + 0) * 4 + bj) * 64 + lane];
+        const float4 a1 = red[((wave * 4 + 1) * 4 + bj) * 64 + lane];
+        const float4 a2 = red[((wave * 4 + 2) * 4 + bj) * 64 + lane];
+        const float4 a3 = red[((wave * 4 + 3) * 4 + bj) * 64 + lane];
         sum[0][bj] = v4f{((a0.x + a1.x) + a2.x) + a3.x, ((a0.y + a1.y) + a2.y) + a3.y, ((a0.z + a1.z) + a2.z) + a3.z,
                          ((a0.w + a1.w) + a2.w) + a3.w};
         isum[0][bj] = v4i{0, 0, 0, 0};
