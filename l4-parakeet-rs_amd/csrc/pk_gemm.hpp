@@ -260,6 +260,27 @@ __device__ __forceinline__ uint32_t compress_quartet(uint32_t packed) {
     return d | (md << 16);
 }
 
+// fp16 row-block stores that write whole cache lines.  A lane holds 16
+// consecutive fp16 outputs (two 16-byte halves) of row r = 16-row block + l16,
+// so the four lanes of a row cover the wave's 128-byte row segment and each
+// plain 16-byte store instruction writes half of every line it touches.  The
+// lanes holding rows r (l16 even) and r + 1 trade halves (one DPP quad_perm
+// [1, 0, 3, 2] per dword): the first store then writes row r from both lanes,
+// the second row r + 1, each instruction 8 rows x whole 128-byte segments.
+__device__ __forceinline__ void store_f16_rowpair(uint16_t* out, size_t ldo, int grow, int gcol, int m, bool col_live, int l16,
+                                                  const uint32_t (&h)[8]) {
+    const bool odd = (l16 & 1) != 0;
+    uint32_t y[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) y[i] = (uint32_t)dpp_mov<0xB1>((int)(odd ? h[i] : h[4 + i]));
+    const int r0 = grow - (odd ? 1 : 0);
+    const int col = gcol + (odd ? 8 : 0);
+    const uint4 s1 = odd ? uint4{y[0], y[1], y[2], y[3]} : uint4{h[0], h[1], h[2], h[3]};
+    const uint4 s2 = odd ? uint4{h[4], h[5], h[6], h[7]} : uint4{y[0], y[1], y[2], y[3]};
+    if (col_live && r0 < m) *(uint4*)(out + (size_t)r0 * ldo + col) = s1;
+    if (col_live && r0 + 1 < m) *(uint4*)(out + (size_t)(r0 + 1) * ldo + col) = s2;
+}
+
 // Epilogue straight from the accumulators: for each of its 8 row blocks a
 // lane finishes columns [gcol, gcol + 16) of one row (16 contiguous outputs,
 // one to four 16-byte stores).  Column scales / bias and the 8 row scales are
@@ -351,7 +372,12 @@ __device__ __forceinline__ void epilogue(const GemmArgs& p, v4f (&accf)[kAI][4],
                 x1 = p.act == 1 ? silu(x1) : (p.act == 2 ? __builtin_fmaxf(x1, 0.0f) : x1);
                 h[j] = (uint32_t)f2h(x0) | ((uint32_t)f2h(x1) << 16);
             }
-            if (live) {
+            if constexpr (kRes) {
+                // residual epilogues (read-modify-write of the output rows): whole-line stores
+                // measured 2-11 % faster; plain fp16 outputs keep the direct stores
+                (void)live;
+                store_f16_rowpair((uint16_t*)p.out, (size_t)p.ldo, grow, gcol, p.m, col_live, l16, h);
+            } else if (live) {
                 uint4* o = (uint4*)((uint16_t*)p.out + (size_t)grow * p.ldo + gcol);
                 o[0] = uint4{h[0], h[1], h[2], h[3]};
                 o[1] = uint4{h[4], h[5], h[6], h[7]};
