@@ -130,6 +130,25 @@ def test_gemm_tile_plan(lib):
     assert _tile(lib, 99, EPI_F16, 16, 256)[0] == -4
 
 
+def test_gemm_k_split(lib):
+    """The K split over a ring workgroup's waves: INT4-g128 formats on 32-row
+    ring tiles with k >= 1024 only (the T = 750 FF2 of BASELINE config 3)."""
+    I8, G128A8, G128A16 = 1, 3, 5
+    EPI_F16, EPI_F8, EPI_F32 = 0, 1, 3
+    ks = lib.pk_gemm_k_split
+    ks.argtypes = [ctypes.c_int32] * 5
+    ks.restype = ctypes.c_int32
+    assert ks(G128A8, EPI_F32, 750, 1024, 4096) == 4
+    assert ks(G128A16, EPI_F16, 750, 1024, 4096) == 4
+    assert ks(G128A8, EPI_F8, 97, 1024, 1024) == 4
+    assert ks(G128A8, EPI_F32, 750, 1024, 512) == 1    # K too short
+    assert ks(G128A8, EPI_F32, 750, 4096, 1024) == 1   # 128-row ring tiles
+    assert ks(G128A8, EPI_F16, 45000, 1024, 4096) == 1  # persistent engine
+    assert ks(I8, EPI_F32, 750, 1024, 4096) == 1       # not an INT4-g128 format
+    assert ks(G128A8, EPI_F32, 750, 0, 4096) == -1
+    assert ks(99, EPI_F32, 750, 1024, 4096) == -4
+
+
 def test_argument_checks_reject_before_any_launch(lib):
     """Entry points reject bad shapes, null and misaligned pointers with their
     PK_E_* code and a message, before touching a device (fake addresses are
