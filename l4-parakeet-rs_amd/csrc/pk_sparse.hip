@@ -32,6 +32,17 @@ __device__ __forceinline__ int sp_key(int row) { return ((row >> 1) & 2) | (((ro
 __device__ __forceinline__ int spw_key(int row) { return (row >> 2) & 7; }
 __device__ __forceinline__ int spw(int row, int chunk) { return row * 128 + ((chunk ^ spw_key(row)) << 4); }
 
+// INT8 2:4 contract's weight tile: weight row r of the tile lives in LDS slot
+// (r & 3) * 32 + r / 4 with its 16-byte chunks XOR-keyed by (slot >> 1) & 7, so
+// the 16 lanes of a fragment read (rows 4 l16 + bj) hit 16 distinct 16-byte
+// bank groups (alternating slot parity x 8 keys).
+__device__ __forceinline__ int sp8w_slot(int row) { return ((row & 3) << 5) | (row >> 2); }
+__device__ __forceinline__ int sp8w_row(int slot) { return ((slot & 31) << 2) | (slot >> 5); }
+__device__ __forceinline__ int sp8w(int row, int chunk) {
+    const int slot = sp8w_slot(row);
+    return slot * 128 + ((chunk ^ ((slot >> 1) & 7)) << 4);
+}
+
 struct SparseArgs {
     const uint8_t* data;    // [M x K/2]
     const uint8_t* meta;    // [M x K/8]
@@ -297,8 +308,8 @@ __global__ __launch_bounds__(256, kAI == 8 ? 1 : 2) void sparse24_i8_kernel(Spar
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int o = (wave * 4 + i) * 1024 + lane * 16;
-        const int row = o >> 7, c = ((o >> 4) & 7) ^ spw_key(row);
-        w_off[i] = (uint32_t)((size_t)(n0 + row) * p.k + c * 16);
+        const int slot = o >> 7, c = ((o >> 4) & 7) ^ ((slot >> 1) & 7);
+        w_off[i] = (uint32_t)((size_t)(n0 + sp8w_row(slot)) * p.k + c * 16);
     }
     auto issue = [&](int step) {
         const uint32_t base = lds_base + (uint32_t)((step % kS) * L::kStage);
@@ -329,8 +340,8 @@ __global__ __launch_bounds__(256, kAI == 8 ? 1 : 2) void sparse24_i8_kernel(Spar
 #pragma unroll
         for (int bj = 0; bj < 4; ++bj) {
             const int row = wn * 64 + 4 * l16 + bj;
-            const uint4 w0 = *(const uint4*)(Ws + spw(row, g));
-            const uint4 w1 = *(const uint4*)(Ws + spw(row, 4 + g));
+            const uint4 w0 = *(const uint4*)(Ws + sp8w(row, g));
+            const uint4 w1 = *(const uint4*)(Ws + sp8w(row, 4 + g));
             wf[bj] = v8i{(int)w0.x, (int)w0.y, (int)w0.z, (int)w0.w, (int)w1.x, (int)w1.y, (int)w1.z, (int)w1.w};
         }
 #pragma unroll
