@@ -70,20 +70,20 @@ static int launch_two(const GemmArgs& a, hipStream_t s) {
 static int forced_tile_rows();
 
 // One tile per workgroup with an S-stage ring (grids of at most one tile per CU).
-template <int F, int E, int kAI>
+template <int F, int E, int kAI, int kOcc = 1>
 static int launch_ring(const GemmArgs& a, hipStream_t s) {
-    using L = g3::LS<F, kAI>;
+    using L = g3::LS<F, kAI, kOcc>;
     static std::once_flag once;
     static hipError_t attr = hipSuccess;
     std::call_once(once, [] {
-        attr = hipFuncSetAttribute((const void*)g3::gemm3_ring_kernel<F, E, kAI>, hipFuncAttributeMaxDynamicSharedMemorySize, L::kBytes);
+        attr = hipFuncSetAttribute((const void*)g3::gemm3_ring_kernel<F, E, kAI, kOcc>, hipFuncAttributeMaxDynamicSharedMemorySize, L::kBytes);
     });
     if (attr != hipSuccess) {
         set_error("hipFuncSetAttribute(LDS %d bytes) failed: %s", L::kBytes, hipGetErrorString(attr));
         return -3;
     }
     const int tiles = ((a.m + L::kBM - 1) / L::kBM) * ((a.n + g3::kBN - 1) / g3::kBN);
-    hipLaunchKernelGGL((g3::gemm3_ring_kernel<F, E, kAI>), dim3(tiles), dim3(g3::kThreads), L::kBytes, s, a);
+    hipLaunchKernelGGL((g3::gemm3_ring_kernel<F, E, kAI, kOcc>), dim3(tiles), dim3(g3::kThreads), L::kBytes, s, a);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
         set_error("gemm launch (fmt %d, epi %d) failed: %s", F, E, hipGetErrorString(e));
@@ -133,10 +133,20 @@ static int ring_stages(int fmt, int kAI) {
     default: return ring_stages_of<FMT_G128A16>(kAI);
     }
 }
+// INT4-g128 x INT8 grids whose ring tiles would be 128 rows but whose 64-row
+// tiles fit two workgroups per CU run 64-row ring tiles two per CU (3-stage
+// rings of 16 KiB stages, 68 KiB each): twice the workgroups for the chain of
+// K-steps (C3 FF1 at T = 750, 384 tiles: 16.6 -> 14.2 us).  Measured and not
+// taken for INT8 (C1: 13.4 vs 13.5 us) and INT4-g128 x fp16 (23.2 -> 24.9 us).
+static int ring_rows(int m, int n);
+static bool ring_occ2(int fmt, int m, int n) {
+    if (fmt != FMT_G128A8 || ring_rows(m, n) != 128) return false;
+    return ((m + 63) / 64) * ((n + g3::kBN - 1) / g3::kBN) <= 2 * cu_count();
+}
+
 // The K split of a launch: 4 (gemm3_splitk_kernel) for the INT4-g128 formats
 // when the ring takes 32-row tiles and K >= 1024 (C3 FF2 at T = 750: the ring
 // kernel's 64 / 32 K-steps per tile become 16 / 8 per wave), else 1.
-static int ring_rows(int m, int n);
 static int k_split(int fmt, int epi, int m, int n, int k) {
     if ((fmt != FMT_G128A8 && fmt != FMT_G128A16) || !has_ring(fmt, epi) || k < 1024) return 1;
     return ring_rows(m, n) == 32 ? 4 : 1;
@@ -199,6 +209,10 @@ static int tile_plan(int fmt, int epi, int m, int n, int* cols, int* stages) {
     *cols = g3::kBN;
     *stages = 2;
     if (has_ring(fmt, epi)) {
+        if (ring_occ2(fmt, m, n)) {
+            *stages = g3::LS<FMT_G128A8, 2, 2>::kS;
+            return 64;
+        }
         const int r = ring_rows(m, n);
         if (r) {
             *stages = ring_stages(fmt, r / 32);
@@ -231,7 +245,12 @@ static int launch_fmt(const GemmArgs& a, hipStream_t s) {
     }
     if constexpr (F == FMT_FP8 || F == FMT_I8 || F == FMT_G128A8 || F == FMT_G128A16) {
         if constexpr (E != EPI_GLU && E != EPI_F8_24) {
-            if (stages > 2) return rows == 32 ? launch_ring<F, E, 1>(a, s) : (rows == 64 ? launch_ring<F, E, 2>(a, s) : launch_ring<F, E, 4>(a, s));
+            if (stages > 2) {
+                if constexpr (F == FMT_G128A8) {
+                    if (ring_occ2(F, a.m, a.n)) return launch_ring<F, E, 2, 2>(a, s);
+                }
+                return rows == 32 ? launch_ring<F, E, 1>(a, s) : (rows == 64 ? launch_ring<F, E, 2>(a, s) : launch_ring<F, E, 4>(a, s));
+            }
         }
     }
     if constexpr (F == FMT_Q4K) {

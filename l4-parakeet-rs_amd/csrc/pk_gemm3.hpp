@@ -522,15 +522,16 @@ __global__ __launch_bounds__(kThreads, 2) void gemm3_kernel(GemmArgs p) {
 // multiplied.  The INT4-g128 group tables of the tile's columns (all K groups)
 // are loaded once into [group][column] fp32 scales and u8 zero points and
 // indexed by the step's group.  Arithmetic, fragment layouts and
-// epilogues are those of gemm3_kernel, so results are identical.
-template <int F, int kAI> struct LS {
+// epilogues are those of gemm3_kernel, so results are identical.  kOcc = 2
+// sizes the ring for two workgroups per CU (80 KiB each) instead of one.
+template <int F, int kAI, int kOcc = 1> struct LS {
     static constexpr int kBM = 32 * kAI;
     static constexpr int kATile = kBM * kRowBytes;
     static constexpr int kBTile = kBN * FmtTraits<F>::bRow;
     static constexpr int kStageBytes = kATile + kBTile;
     static constexpr bool kG128 = (F == FMT_G128A8 || F == FMT_G128A16);
     static constexpr int kTabBytes = kG128 ? kMaxG128Groups * kBN * 5 : 0;   // fp32 scales + u8 zeros [group][column]
-    static constexpr int kFit = (150 * 1024 - kTabBytes) / kStageBytes;
+    static constexpr int kFit = ((kOcc == 1 ? 150 : 80) * 1024 - kTabBytes) / kStageBytes;
     static constexpr int kS = kFit > 8 ? 8 : kFit;
     static constexpr int kTab = kS * kStageBytes;
     static constexpr int kBytes = kTab + kTabBytes;
@@ -556,10 +557,10 @@ template <int kOps> __device__ __forceinline__ void wait_stages(int younger) {
     }
 }
 
-template <int F, int E, int kAI>
-__global__ __launch_bounds__(kThreads, 1) void gemm3_ring_kernel(GemmArgs p) {
+template <int F, int E, int kAI, int kOcc = 1>
+__global__ __launch_bounds__(kThreads, kOcc) void gemm3_ring_kernel(GemmArgs p) {
     using T = FmtTraits<F>;
-    using L = LS<F, kAI>;
+    using L = LS<F, kAI, kOcc>;
     constexpr int kS = L::kS, kBM = L::kBM;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;

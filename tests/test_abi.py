@@ -127,6 +127,10 @@ def test_gemm_tile_plan(lib):
     assert (rows, cols) == (128, 128) and stages >= 3
     rows, cols, stages = _tile(lib, G128A8, EPI_F16, 750, 1024)
     assert (rows, cols) == (32, 128) and stages >= 3
+    # the T = 750 INT4-g128 x INT8 FF1 (750 x 4096): 64-row ring tiles, two per CU
+    assert _tile(lib, G128A8, EPI_F16, 750, 4096) == (64, 128, 3)
+    rows, cols, stages = _tile(lib, I8, EPI_F32, 750, 4096)
+    assert (rows, cols) == (128, 128) and stages > 3
     assert _tile(lib, 99, EPI_F16, 16, 256)[0] == -4
 
 
