@@ -215,30 +215,24 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(const uint16_t* __re
 // byte i that was not kept (at most two).  The kept pair plus the dropped
 // nonzeros are the quartet, exactly.
 __device__ __forceinline__ uint32_t compress_i8_quartet(uint32_t packed, uint32_t& drop) {
-    int mag[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int v = (int)(int8_t)(packed >> (8 * i));
-        mag[i] = v < 0 ? -v : v;
-    }
-    uint32_t d = 0, md = 0;
-    int count = 0;
-    drop = 0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        int rank = 0;
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-            if (j != i) rank += (mag[j] > mag[i]) || (mag[j] == mag[i] && j < i);
-        if (rank < 2) {
-            d |= ((packed >> (8 * i)) & 255u) << (8 * count);
-            md |= (uint32_t)i << (2 * count);
-            ++count;
-        } else if (mag[i] != 0) {
-            drop |= 1u << i;
-        }
-    }
-    return d | (md << 16);
+    // |v| per byte (0 .. 128) without carries between bytes: (x ^ 0xff) + 1 for negatives
+    const uint32_t sgn = (packed >> 7) & 0x01010101u;
+    const uint32_t mag = (packed ^ (sgn * 255u)) + sgn;
+    // keys 4 |v_i| + (3 - i) are distinct and order the bytes by magnitude, ties
+    // to the lower index; the two largest keys are the kept pair
+    const uint32_t k0 = ((mag & 0xffu) << 2) | 3u, k1 = (((mag >> 8) & 0xffu) << 2) | 2u;
+    const uint32_t k2 = (((mag >> 16) & 0xffu) << 2) | 1u, k3 = (mag >> 24) << 2;
+    const uint32_t h01 = max(k0, k1), l01 = min(k0, k1), h23 = max(k2, k3), l23 = min(k2, k3);
+    const uint32_t top = max(h01, h23), next = max(min(h01, h23), max(l01, l23));
+    const uint32_t ia = 3u - (top & 3u), ib = 3u - (next & 3u);
+    const uint32_t i0 = min(ia, ib), i1 = max(ia, ib);
+    // bytes i0, i1 of the quartet to bytes 0, 1 (selector 0x0c gives zero)
+    const uint32_t d = __builtin_amdgcn_perm(0u, packed, i0 | (i1 << 8) | 0x0c0c0000u);
+    // nonzero bytes: |v| + 0x7f sets the byte's top bit iff |v| > 0 (no carry out at 128)
+    const uint32_t t = (mag + 0x7f7f7f7fu) & 0x80808080u;
+    const uint32_t nz = ((t >> 7) & 1u) | ((t >> 14) & 2u) | ((t >> 21) & 4u) | ((t >> 28) & 8u);
+    drop = nz & ~((1u << i0) | (1u << i1));
+    return (d & 0xffffu) | ((i0 | (i1 << 2)) << 16);
 }
 
 // Dynamic per-row INT8 quantization (the arithmetic of quantize_rows_kernel
@@ -259,7 +253,6 @@ __global__ __launch_bounds__(256) void quantize_rows_sp24_kernel(const uint16_t*
     const int lane = threadIdx.x & 63;
     const int nw = gridDim.x * 4;
     const int chunks = k >> 3;
-    const uint64_t below = (1ull << lane) - 1ull;
     for (int row = blockIdx.x * 4 + (threadIdx.x >> 6); row < rows; row += nw) {
         const bool live = row < valid_rows;
         const uint16_t* x = in + (size_t)row * k;
@@ -320,8 +313,10 @@ __global__ __launch_bounds__(256) void quantize_rows_sp24_kernel(const uint16_t*
             const uint64_t b0 = __builtin_amdgcn_ballot_w64((n & 1u) != 0);
             const uint64_t b1 = __builtin_amdgcn_ballot_w64((n & 2u) != 0);
             const uint64_t b2 = __builtin_amdgcn_ballot_w64((n & 4u) != 0);
-            const uint32_t pre = (uint32_t)__builtin_popcountll(b0 & below) + 2u * (uint32_t)__builtin_popcountll(b1 & below) +
-                                 4u * (uint32_t)__builtin_popcountll(b2 & below);
+            auto below_count = [](uint64_t b) {  // set bits of b in the lanes below this one
+                return __builtin_amdgcn_mbcnt_hi((uint32_t)(b >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
+            };
+            const uint32_t pre = below_count(b0) + 2u * below_count(b1) + 4u * below_count(b2);
             if (c < chunks) {
                 *(uint32_t*)(drow + 4 * c) = (q0 & 0xffffu) | (q1 << 16);
                 mrow[c] = (uint8_t)(((q0 >> 16) & 15u) | (((q1 >> 16) & 15u) << 4));

@@ -216,11 +216,12 @@ int launch_sparse24_contract(const uint8_t* data, const uint8_t* meta, const uin
 // INT8 dot products and the fp32 output, (acc * input_scale[r]) *
 // weight_scale[n], equals the dense INT8 contract's bit for bit.
 //
-// Workgroup: 4 waves (2 x 2), tile (32 kAI) x 128, wave (16 kAI) x 64 = kAI x
-// 4 blocks of 16 x 16.  The launcher runs kAI = 4: 128-row tiles, two
-// workgroups per CU, a 3-stage LDS ring of 26 KiB stages (kAI = 8, 256-row
-// tiles with one workgroup per CU and 4 stages of 36 KiB, measured 15-20 %
-// slower at T = 7500).  A stage holds one 128-K step: compressed data (64
+// Workgroup: 2 kWM waves (kWM along M x 2 along N), tile (16 kAI kWM) x 128,
+// wave (16 kAI) x 64 = kAI x 4 blocks of 16 x 16.  The launcher runs kAI = 4:
+// 256-row tiles of 8 waves (kWM = 4), one workgroup per CU, a 4-stage LDS ring
+// of 36 KiB stages, where those tiles give at least half the CUs one, else
+// 128-row tiles of 4 waves, two workgroups per CU, a 3-stage ring of 26 KiB
+// stages (256-row tiles of 4 waves, 128 x 64 each, measured 15-20 % slower).  A stage holds one 128-K step: compressed data (64
 // bytes a row), metadata (16 bytes a row) and the weight tile (128 rows x 128
 // bytes); its direct-to-LDS loads have kS - 1 steps to land, and there is one
 // barrier per step.  Blocks are laid out so that the column tiles of one row
@@ -233,20 +234,24 @@ int launch_sparse24_contract(const uint8_t* data, const uint8_t* meta, const uin
 // the transposed weights W^T [K x N], direct-to-LDS) are staged in LDS; each
 // lane then walks the entries of its rows and adds v * W[n, k] to the
 // accumulators of its 4 columns.
-template <int kAI> struct Sp8 {
-    static constexpr int kRows = 32 * kAI;
+template <int kAI, int kWM = 2> struct Sp8 {
+    static constexpr int kRows = 16 * kAI * kWM;   // tile rows: kWM waves along M, each kAI blocks of 16
+    static constexpr int kWaves = 2 * kWM, kThreads = 64 * kWaves;
+    static constexpr int kOcc = kRows <= 128 ? 2 : 1;  // workgroups per CU
     static constexpr int kData = kRows * 64, kMeta = kRows * 16, kW = 128 * 128;
     static constexpr int kStage = kData + kMeta + kW;
-    static constexpr int kS = kAI == 8 ? 4 : 3;
+    static constexpr int kFit = (kOcc == 2 ? 80 : 150) * 1024 / kStage;
+    static constexpr int kS = kFit > 4 ? 4 : kFit;
     static constexpr int kLds = kS * kStage;
-    static constexpr int kOps = kAI / 2 + 1 + 4;  // direct-to-LDS loads per wave and stage
+    static constexpr int kWLoads = 16 / kWaves;     // 1 KiB weight loads per wave and stage
+    static constexpr int kOps = kAI / 2 + 1 + kWLoads;  // direct-to-LDS loads per wave and stage
     static constexpr int kMetaLanes = 8 * kAI;     // metadata rows per wave
     // overflow staging inside the ring: counts, offsets (+ wave totals), entries
     // (tile row and byte; then k), weight rows
-    static constexpr int kChunk = kAI == 8 ? 1024 : 512;
+    static constexpr int kChunk = kOcc == 1 ? 1024 : 512;
     static constexpr int kCnt = 0, kOff = kRows * 4, kEnt = kOff + (kRows + 8) * 4, kWt = kEnt + 8 * kChunk;
-    static_assert(kWt + kChunk * 128 <= kLds, "overflow staging fits the ring");
-    static_assert(kLds <= 160 * 1024 && (kAI == 8 || 2 * kLds <= 160 * 1024), "LDS");
+    static_assert(kS >= 3 && kWt + kChunk * 128 <= kLds, "overflow staging fits the ring");
+    static_assert(kLds * kOcc <= 160 * 1024 && kMetaLanes <= 64 && 16 % kWaves == 0, "layout");
 };
 
 struct Sparse8Args {
@@ -273,9 +278,9 @@ template <int kOps> __device__ __forceinline__ void sp8_wait_stages(int younger)
     }
 }
 
-template <int kAI>
-__global__ __launch_bounds__(256, kAI == 8 ? 1 : 2) void sparse24_i8_kernel(Sparse8Args p) {
-    using L = Sp8<kAI>;
+template <int kAI, int kWM>
+__global__ __launch_bounds__((Sp8<kAI, kWM>::kThreads), (Sp8<kAI, kWM>::kOcc)) void sparse24_i8_kernel(Sparse8Args p) {
+    using L = Sp8<kAI, kWM>;
     constexpr int kS = L::kS;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -296,8 +301,8 @@ __global__ __launch_bounds__(256, kAI == 8 ? 1 : 2) void sparse24_i8_kernel(Spar
     const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)lds;
 
     // direct-to-LDS sources: kAI / 2 data loads (16 rows x 64 bytes each), one
-    // metadata load (8 kAI rows x 16 bytes), 4 weight loads (8 rows x 128 bytes)
-    uint32_t d_off[kAI / 2], w_off[4];
+    // metadata load (8 kAI rows x 16 bytes), kWLoads weight loads (8 rows x 128 bytes)
+    uint32_t d_off[kAI / 2], w_off[L::kWLoads];
 #pragma unroll
     for (int i = 0; i < kAI / 2; ++i) {
         const int o = (wave * (kAI / 2) + i) * 1024 + lane * 16;
@@ -306,8 +311,8 @@ __global__ __launch_bounds__(256, kAI == 8 ? 1 : 2) void sparse24_i8_kernel(Spar
     }
     const uint32_t m_off = (uint32_t)((size_t)min(m0 + wave * L::kMetaLanes + (lane % L::kMetaLanes), p.m - 1) * ld_meta);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int o = (wave * 4 + i) * 1024 + lane * 16;
+    for (int i = 0; i < L::kWLoads; ++i) {
+        const int o = (wave * L::kWLoads + i) * 1024 + lane * 16;
         const int slot = o >> 7, c = ((o >> 4) & 7) ^ ((slot >> 1) & 7);
         w_off[i] = (uint32_t)((size_t)(n0 + sp8w_row(slot)) * p.k + c * 16);
     }
@@ -317,7 +322,8 @@ __global__ __launch_bounds__(256, kAI == 8 ? 1 : 2) void sparse24_i8_kernel(Spar
         for (int i = 0; i < kAI / 2; ++i) dma16(p.data + d_off[i] + (size_t)step * 64, base + (wave * (kAI / 2) + i) * 1024);
         if (lane < L::kMetaLanes) dma16(p.meta + m_off + (size_t)step * 16, base + L::kData + wave * L::kMetaLanes * 16);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) dma16(p.w + w_off[i] + (size_t)step * 128, base + L::kData + L::kMeta + (wave * 4 + i) * 1024);
+        for (int i = 0; i < L::kWLoads; ++i)
+            dma16(p.w + w_off[i] + (size_t)step * 128, base + L::kData + L::kMeta + (wave * L::kWLoads + i) * 1024);
     };
 
     v4i acc[kAI][4];
@@ -386,7 +392,7 @@ __global__ __launch_bounds__(256, kAI == 8 ? 1 : 2) void sparse24_i8_kernel(Spar
         const int len = (int)min((uint32_t)L::kChunk, total - c0);
         // stage entries as (tile row << 8) | byte; issue the weight-row loads
         // straight from the global entries (k = entry >> 8)
-        for (int e = tid; e < len; e += 256) {
+        for (int e = tid; e < len; e += L::kThreads) {
             const uint32_t gi = c0 + (uint32_t)e;
             int lo = 0, hi = L::kRows - 1;  // last row r with off[r] <= gi
             while (lo < hi) {
@@ -399,7 +405,7 @@ __global__ __launch_bounds__(256, kAI == 8 ? 1 : 2) void sparse24_i8_kernel(Spar
             ent_s[L::kChunk + e] = en >> 8;  // k, read back by the weight-row loads below
         }
         __syncthreads();
-        for (int blk = wave; blk * 8 < len; blk += 4) {
+        for (int blk = wave; blk * 8 < len; blk += L::kWaves) {
             const int e = min(blk * 8 + (lane >> 3), len - 1);
             const uint32_t kk = ent_s[L::kChunk + e];
             dma16(p.wt + (size_t)kk * p.n + n0 + (lane & 7) * 16, lds_base + L::kWt + blk * 1024);
@@ -439,19 +445,19 @@ __global__ __launch_bounds__(256, kAI == 8 ? 1 : 2) void sparse24_i8_kernel(Spar
         }
 }
 
-template <int kAI>
+template <int kAI, int kWM>
 static int launch_sp8(const Sparse8Args& a, hipStream_t s) {
-    using L = Sp8<kAI>;
+    using L = Sp8<kAI, kWM>;
     static std::once_flag once;
     static hipError_t attr = hipSuccess;
-    std::call_once(once, [] { attr = hipFuncSetAttribute((const void*)sparse24_i8_kernel<kAI>, hipFuncAttributeMaxDynamicSharedMemorySize, L::kLds); });
+    std::call_once(once, [] { attr = hipFuncSetAttribute((const void*)sparse24_i8_kernel<kAI, kWM>, hipFuncAttributeMaxDynamicSharedMemorySize, L::kLds); });
     if (attr != hipSuccess) {
         set_error("hipFuncSetAttribute failed: %s", hipGetErrorString(attr));
         return -3;
     }
     const int tiles_m = (a.m + L::kRows - 1) / L::kRows, tiles_n = a.n / 128;
     const int grid = 8 * ((tiles_m + 7) / 8) * tiles_n;
-    hipLaunchKernelGGL(sparse24_i8_kernel<kAI>, dim3(grid), dim3(256), L::kLds, s, a);
+    hipLaunchKernelGGL((sparse24_i8_kernel<kAI, kWM>), dim3(grid), dim3(L::kThreads), L::kLds, s, a);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
         set_error("sparse INT8 contract launch failed: %s", hipGetErrorString(e));
@@ -477,7 +483,11 @@ int launch_sparse24_i8_contract(const uint8_t* data, const uint8_t* meta, const 
         return -1;
     }
     const Sparse8Args a{data, meta, in_scales, ovf_count, ovf, w, wt, w_scales, out, m, n, k};
-    return launch_sp8<4>(a, s);
+    // 256-row tiles of 8 waves, one workgroup per CU and a 4-stage ring, where
+    // they give at least half the CUs a tile (T = 7500: 41.5 -> 39.4 us at 95 %
+    // sparsity); smaller grids keep 128-row tiles two per CU
+    const long tiles256 = (long)((m + 255) / 256) * (n / 128);
+    return 2 * tiles256 >= cu_count() ? launch_sp8<4, 4>(a, s) : launch_sp8<4, 2>(a, s);
 }
 
 // W [n x k] int8 -> W^T [k x n] (load-time derivation for the overflow pass).
