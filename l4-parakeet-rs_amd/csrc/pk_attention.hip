@@ -43,6 +43,12 @@ __device__ __forceinline__ void wave_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// The reference builds encoder.cu with --use_fast_math (build.rs:67-72), so
+// the softmax exponentials of its tensor-core paths are the hardware's
+// approximate exponential, not the correctly rounded expf; HIP's __expf is
+// the same kind of function here (v_exp_f32 of x * log2(e)).
+__device__ __forceinline__ float softmax_exp(float x) { return __expf(x); }
+
 __device__ __forceinline__ uint16_t bf16_rn(float v) {  // finite inputs only
     const uint32_t b = __builtin_bit_cast(uint32_t, v);
     return (uint16_t)((b + 0x7fffu + ((b >> 16) & 1u)) >> 16);
@@ -88,6 +94,24 @@ __device__ __forceinline__ uint32_t pack_i8x4(float a, float b, float c, float d
            ((uint32_t)(int)d << 24);
 }
 typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+// Integers n with |n| < 2^22 and the float 1.5 * 2^23 + n share bits: the
+// float's bits are 0x4B400000 + n.  An integer MFMA whose accumulator starts
+// at kIntBias therefore ends with the bits of the float kFloatBias + sum, and
+// one exact subtraction gives (float)sum (full-rate VALU instead of
+// v_cvt_f32_i32); adding kFloatBias to an integer-valued float leaves n in
+// the low byte of its bits (two's complement), so the byte is a plain store.
+constexpr int kIntBias = 0x4B400000;
+constexpr float kFloatBias = 12582912.0f;
+__device__ __forceinline__ float unbias(int biased) { return __builtin_bit_cast(float, biased) - kFloatBias; }
+__device__ __forceinline__ uint32_t biased_bits(float integral) { return __builtin_bit_cast(uint32_t, integral + kFloatBias); }
+// Four integer-valued floats in [-128, 127] -> four int8 bytes (low bytes of
+// their biased bits, gathered by v_perm_b32).
+__device__ __forceinline__ uint32_t pack_i8x4_biased(float a, float b, float c, float d) {
+    const uint32_t ab = __builtin_amdgcn_perm(biased_bits(b), biased_bits(a), 0x0c0c0400u);
+    const uint32_t cd = __builtin_amdgcn_perm(biased_bits(d), biased_bits(c), 0x04000c0cu);
+    return ab | cd;
+}
+
 
 // Byte `b` of w as OCP e4m3 -> float (v_cvt_f32_fp8, exact); b folds to a
 // constant in unrolled loops.
@@ -421,7 +445,7 @@ __device__ __forceinline__ float softmax_half(float (&l)[9], int ln) {
 #pragma unroll
     for (int part = 0; part < 9; ++part)
         if (ln + 32 * part < kMaxAtt) {
-            l[part] = expf(l[part] - mx);
+            l[part] = softmax_exp(l[part] - mx);
             den += l[part];
         }
     return sum_desc<32>(den);  // xor 16, ..., 1 within the half wave
@@ -519,8 +543,8 @@ __device__ void attention_packed_stream(StreamShared& sh, const uint16_t* __rest
                     fv[i] = __builtin_rintf((float)av[i / 2][i & 1] / sv);
                 }
             }
-            const uint32_t ue = pack_i8x4(fu[0], fu[2], fu[4], fu[6]), uo = pack_i8x4(fu[1], fu[3], fu[5], fu[7]);
-            const uint32_t v8[2] = {pack_i8x4(fv[0], fv[1], fv[2], fv[3]), pack_i8x4(fv[4], fv[5], fv[6], fv[7])};
+            const uint32_t ue = pack_i8x4_biased(fu[0], fu[2], fu[4], fu[6]), uo = pack_i8x4_biased(fu[1], fu[3], fu[5], fu[7]);
+            const uint32_t v8[2] = {pack_i8x4_biased(fv[0], fv[1], fv[2], fv[3]), pack_i8x4_biased(fv[4], fv[5], fv[6], fv[7])};
             // INT4 plane: dimension 8j+i sits at storage nibble 2*off_j + i of
             // the key vectors; widen_s4x16 of the key's bytes [32m + 8g, +8)
             // yields even nibbles then odd nibbles per word, hence this order.
@@ -566,15 +590,17 @@ __device__ void attention_packed_stream(StreamShared& sh, const uint16_t* __rest
                 slot = slot >= kRing ? slot - kRing : slot;
                 const uint2 k0 = *(const uint2*)&sh.ring_k[slot][8 * g], k1 = *(const uint2*)&sh.ring_k[slot][32 + 8 * g];
                 const float ks = sh.ring_ks[slot], pscl = psc[i];
-                v4i acu = __builtin_amdgcn_mfma_i32_16x16x64_i8(au0, widen_s4x16(k0), v4i{0, 0, 0, 0}, 0, 0, 0);
+                // |sums| <= 7 * 128 * 128 (INT4 x widened INT4) and 127 * 127 * 128 (INT8), below 2^22
+                const v4i bias = v4i{kIntBias, kIntBias, kIntBias, kIntBias};
+                v4i acu = __builtin_amdgcn_mfma_i32_16x16x64_i8(au0, widen_s4x16(k0), bias, 0, 0, 0);
                 acu = __builtin_amdgcn_mfma_i32_16x16x64_i8(au1, widen_s4x16(k1), acu, 0, 0, 0);
-                v4i acv = __builtin_amdgcn_mfma_i32_16x16x64_i8(av0, __builtin_bit_cast(v4i, pq[i][0]), v4i{0, 0, 0, 0}, 0, 0, 0);
+                v4i acv = __builtin_amdgcn_mfma_i32_16x16x64_i8(av0, __builtin_bit_cast(v4i, pq[i][0]), bias, 0, 0, 0);
                 acv = __builtin_amdgcn_mfma_i32_16x16x64_i8(av1, __builtin_bit_cast(v4i, pq[i][1]), acv, 0, 0, 0);
                 if (wave + 4 * i < kPosRows / 16) {
 #pragma unroll
                     for (int r = 0; r < 4; r += 2) {
-                        const uint32_t c2 = bf16x2_rn((float)acu[r] * (qsu[r] * ks), (float)acu[r + 1] * (qsu[r + 1] * ks));
-                        const uint32_t p2 = bf16x2_rn((float)acv[r] * (qsv[r] * pscl), (float)acv[r + 1] * (qsv[r + 1] * pscl));
+                        const uint32_t c2 = bf16x2_rn(unbias(acu[r]) * (qsu[r] * ks), unbias(acu[r + 1]) * (qsu[r + 1] * ks));
+                        const uint32_t p2 = bf16x2_rn(unbias(acv[r]) * (qsv[r] * pscl), unbias(acv[r + 1]) * (qsv[r + 1] * pscl));
                         sh.cs[4 * g + r][col] = (uint16_t)c2;
                         sh.cs[4 * g + r + 1][col] = (uint16_t)(c2 >> 16);
                         sh.ps[4 * g + r][col] = (uint16_t)p2;
@@ -604,7 +630,7 @@ __device__ void attention_packed_stream(StreamShared& sh, const uint16_t* __rest
 #pragma unroll
             for (int k = 0; k < 17; ++k) {
                 if (j + 16 * k < kMaxAtt) {
-                    l[k] = expf(l[k] - mx);
+                    l[k] = softmax_exp(l[k] - mx);
                     if (k & 1) odd += l[k];
                     else even += l[k];
                 }
@@ -614,14 +640,15 @@ __device__ void attention_packed_stream(StreamShared& sh, const uint16_t* __rest
             uint8_t* prow = &sh.prob[lq][prob_pos(lq + j)];  // slot j + 16k sits 16k further
 #pragma unroll
             for (int k = 0; k < 17; ++k)
-                if (j + 16 * k < kMaxAtt) prow[16 * k] = (uint8_t)(int)__builtin_rintf(l[k] * 15.0f);
+                if (j + 16 * k < kMaxAtt) prow[16 * k] = (uint8_t)biased_bits(l[k] * 15.0f);  // rint: the add rounds to nearest even
         }
         __syncthreads();
 
         // Phase 4: context = U4 probabilities x S4 V over keys 0..271 (five
         // K=64 steps; keys >= 272 contribute zero operands).
         {
-            v4i acc[2] = {v4i{0, 0, 0, 0}, v4i{0, 0, 0, 0}};
+            // |sums| <= 15 * 128 * 320, below 2^22
+            v4i acc[2] = {v4i{kIntBias, kIntBias, kIntBias, kIntBias}, v4i{kIntBias, kIntBias, kIntBias, kIntBias}};
             const int ring0 = first_key % kRing;
 #pragma unroll
             for (int st = 0; st < 5; ++st) {
@@ -637,14 +664,15 @@ __device__ void attention_packed_stream(StreamShared& sh, const uint16_t* __rest
             }
             float ps4[4];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) ps4[r] = sh.pscale[4 * g + r];
+            for (int r = 0; r < 4; ++r) ps4[r] = sh.pscale[4 * g + r] * 0.0625f;  // the sums carry V x 16
 #pragma unroll
             for (int c = 0; c < 2; ++c) {
                 const int fl = 16 * (2 * wave + c) + l16;
 #pragma unroll
                 for (int r = 0; r < 4; r += 2) {
-                    const float x0 = (float)(acc[c][r] >> 4) * (ps4[r] * vs[c]);
-                    const float x1 = (float)(acc[c][r + 1] >> 4) * (ps4[r + 1] * vs[c]);
+                    // (sum / 16) * (p * v) == sum * ((p / 16) * v): scaling by 2^-4 is exact
+                    const float x0 = unbias(acc[c][r]) * (ps4[r] * vs[c]);
+                    const float x1 = unbias(acc[c][r + 1]) * (ps4[r + 1] * vs[c]);
                     const uint32_t b2 = e4m3x2_finite(round_f16(x0) * 28.0f, round_f16(x1) * 28.0f);
                     sh.out[4 * g + r][fl] = (uint8_t)b2;
                     sh.out[4 * g + r + 1][fl] = (uint8_t)(b2 >> 8);

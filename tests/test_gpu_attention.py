@@ -3,9 +3,11 @@
 
 Packers and the value quantizer are integer/byte work: bit-exact.  The
 attention outputs follow the reference operation by operation; the only
-arithmetic the GPU and the oracle do not share is expf (device library vs
-host libm, both within an ulp), which can move a U4 probability or an output
-rounding by one step.  The packed kernel's e4m3 bytes must therefore be equal
+arithmetic the GPU and the oracle do not share is the softmax exponential
+(host libm expf in the oracle; in the packed and tc kernels the hardware's
+approximate exponential, as the reference's --use_fast_math build has it,
+within a few ulp; in the boundary path the device expf), which can move a U4
+probability or an output rounding by one step.  The packed kernel's e4m3 bytes must therefore be equal
 except for at most 0.1 % of them, which may differ by one code.  The tc
 kernel's fp16 outputs: its fp32 score sums run in the MFMA's order (as on
 the reference's tensor cores, unspecified), so an e4m3 probability that lies
