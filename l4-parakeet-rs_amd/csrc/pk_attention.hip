@@ -43,7 +43,7 @@ __device__ __forceinline__ void wave_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// The reference builds encoder.cu with --use_fast_math (build.rs:67-72), so
+// The reference builds encoder.cu with --use_fast_math (build.rs:68-73, :101-103), so
 // the softmax exponentials of its tensor-core paths are the hardware's
 // approximate exponential, not the correctly rounded expf; HIP's __expf is
 // the same kind of function here (v_exp_f32 of x * log2(e)).
