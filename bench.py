@@ -796,6 +796,8 @@ def config_results(pk, torch, stream, reps=10):
     qsc = torch.empty(t, device=dev)
     sp_data = torch.empty((t, k // 2), dtype=torch.uint8, device=dev)
     sp_meta = torch.empty((t, k // 8), dtype=torch.uint8, device=dev)
+    sp_data2 = torch.empty((t, k // 2), dtype=torch.uint8, device=dev)
+    sp_meta2 = torch.empty((t, k // 8), dtype=torch.uint8, device=dev)
     sp_cnt = torch.empty(t, dtype=torch.int32, device=dev)
     sp_ovf = torch.empty((t, k // 2), dtype=torch.int32, device=dev)
     wt = torch.empty((k, n), dtype=torch.int8, device=dev)
@@ -823,15 +825,18 @@ def config_results(pk, torch, stream, reps=10):
 
         with_quantize()
         e["with_quantize_us"] = round(time_events(torch, with_quantize, reps, stream) * 1e3, 1)
-        # exact 2:4 form: 2:4 INT8 data + metadata + per-row overflow lists
-        pk.call("pk_quantize_rows_int8_sparse24", a, sp_data, sp_meta, qsc, sp_cnt, sp_ovf, t, t, k, stream=stream)
+        # exact 2:4 form: 2:4 INT8 data + metadata + per-row overflow lists, and
+        # the residual 2:4 form that tiles with many overflow entries take instead
+        pk.call("pk_quantize_rows_int8_sparse24", a, sp_data, sp_meta, qsc, sp_cnt, sp_ovf, sp_data2, sp_meta2, t, t, k,
+                stream=stream)
 
-        def sparse24():
-            pk.call("pk_ffn_contract_int8_sparse24", sp_data, sp_meta, qsc, sp_cnt, sp_ovf, wq, wt, ws, y2, t,
-                    stream=stream)
+        def sparse24(residual=True):
+            pk.call("pk_ffn_contract_int8_sparse24", sp_data, sp_meta, qsc, sp_cnt, sp_ovf,
+                    sp_data2 if residual else None, sp_meta2 if residual else None, wq, wt, ws, y2, t, stream=stream)
 
         def sparse24_with_quantize():
-            pk.call("pk_quantize_rows_int8_sparse24", a, sp_data, sp_meta, qsc, sp_cnt, sp_ovf, t, t, k, stream=stream)
+            pk.call("pk_quantize_rows_int8_sparse24", a, sp_data, sp_meta, qsc, sp_cnt, sp_ovf, sp_data2, sp_meta2, t, t, k,
+                    stream=stream)
             sparse24()
 
         sparse24_with_quantize()
@@ -842,8 +847,14 @@ def config_results(pk, torch, stream, reps=10):
         ms24 = timed(sparse24)
         e24 = entry(ms24, f, t * k // 2 + t * k // 8 + 4 * t + 4 * int(sp_cnt.sum()) + n * k + 4 * n + 4 * t * n,
                     useful=(1.0 - sp) * f)
-        e24["overflow_entries_per_row"] = round(float(sp_cnt.double().mean()), 2)
+        per_row = float(sp_cnt.double().mean())
+        e24["overflow_entries_per_row"] = round(per_row, 2)
+        e24["second_part"] = "residual 2:4 pass" if per_row > 8 else "overflow lists"  # chosen per 256-row tile
         e24["with_quantize_us"] = round(time_events(torch, sparse24_with_quantize, reps, stream) * 1e3, 1)
+        sparse24(residual=False)
+        torch.cuda.synchronize()
+        same = same and bool(torch.equal(y, y2))
+        e24["lists_only_us"] = round(time_events(torch, lambda: sparse24(residual=False), reps, stream) * 1e3, 1)
         e24["equal_to_dense"] = same
         if not same:
             raise SystemExit("config 4: the exact 2:4 contract differs from the dense INT8 contract")

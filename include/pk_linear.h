@@ -326,22 +326,30 @@ int32_t pk_ffn_contract_int8_rowskip(const int8_t* input, const float* input_sca
  * 4 (p % 2) of byte p / 2, the reference's layout) plus, per row,
  * overflow_counts[row] entries at overflow[row * k/2 ...], each
  * (element << 8) | int8 byte, in ascending element order (at most k/2).
- * k % 128 == 0, k <= 4096; input 16-byte aligned, data / overflow /
- * overflow_counts 4-byte aligned.  Rows >= valid_rows are zero, scale 1. */
+ * residual_data [rows x k/2] / residual_meta [rows x k/8] (both or neither,
+ * no counterpart in the reference): the residual 2:4 form, per quartet the
+ * two positions the selection did not keep, ascending, with their bytes, in
+ * the layout of data / meta.  k % 128 == 0, k <= 4096; input 16-byte
+ * aligned, data / residual_data / overflow / overflow_counts 4-byte aligned.
+ * Rows >= valid_rows are zero, scale 1. */
 int32_t pk_quantize_rows_int8_sparse24(const uint16_t* input, uint8_t* data, uint8_t* meta, float* scales,
-                                       uint32_t* overflow_counts, uint32_t* overflow, int32_t rows, int32_t valid_rows,
-                                       int32_t k, void* stream);
+                                       uint32_t* overflow_counts, uint32_t* overflow, uint8_t* residual_data,
+                                       uint8_t* residual_meta, int32_t rows, int32_t valid_rows, int32_t k, void* stream);
 /* Load-time derivation: weight_t [k x n] = transpose of the INT8 weight [n x k]
  * (the overflow pass of the contract below reads weight columns). */
 int32_t pk_transpose_int8(const int8_t* weight, int8_t* weight_t, int32_t n, int32_t k, void* stream);
 /* The FF2 contract 4096 -> 1024 on that form: fp32 output [rows x 1024] equal
  * bit for bit to pk_ffn_contract_int8_rowskip's on the dense INT8 rows,
- * out = (acc * input_scale[r]) * weight_scale[n].  data, meta, weight,
- * weight_t, weight_scales and output 16-byte aligned. */
+ * out = (acc * input_scale[r]) * weight_scale[n].  With residual_data /
+ * residual_meta (both or neither, from the quantizer above), row tiles
+ * whose rows hold more than 8 overflow entries each on average add the
+ * residual 2:4 form in a second sparse pass instead of walking the lists.
+ * data, meta, residual data / meta, weight, weight_t, weight_scales and
+ * output 16-byte aligned. */
 int32_t pk_ffn_contract_int8_sparse24(const uint8_t* data, const uint8_t* meta, const float* input_scales,
-                                      const uint32_t* overflow_counts, const uint32_t* overflow, const int8_t* weight,
-                                      const int8_t* weight_t, const float* weight_scales, float* output, int32_t rows,
-                                      void* stream);
+                                      const uint32_t* overflow_counts, const uint32_t* overflow, const uint8_t* residual_data,
+                                      const uint8_t* residual_meta, const int8_t* weight, const int8_t* weight_t,
+                                      const float* weight_scales, float* output, int32_t rows, void* stream);
 
 /* ---- generic fused GEMM ------------------------------------------------------
  * format: 0 FP8, 1 INT8, 2 INT4 (s4 x s4), 3 INT4-g128 x INT8, 4 FP16,

@@ -446,7 +446,8 @@ int32_t pk_ffn_contract_int8_rowskip(const int8_t* in, const float* in_scales, c
 }
 
 int32_t pk_quantize_rows_int8_sparse24(const uint16_t* in, uint8_t* data, uint8_t* meta, float* scales, uint32_t* overflow_counts,
-                                       uint32_t* overflow, int32_t rows, int32_t valid_rows, int32_t k, void* stream) {
+                                       uint32_t* overflow, uint8_t* residual_data, uint8_t* residual_meta, int32_t rows,
+                                       int32_t valid_rows, int32_t k, void* stream) {
     if (rows < 0 || k <= 0 || k % 128 || k > 4096) {
         set_error("sparse24 quantizer needs rows >= 0 and k %% 128 == 0, k <= 4096 (k=%d)", k);
         return PK_E_SHAPE;
@@ -454,11 +455,17 @@ int32_t pk_quantize_rows_int8_sparse24(const uint16_t* in, uint8_t* data, uint8_
     if (rows && (!need(in, "input") || !need(data, "data") || !need(meta, "meta") || !need(scales, "scales") ||
                  !need(overflow_counts, "overflow_counts") || !need(overflow, "overflow")))
         return PK_E_ARG;
-    if (((uintptr_t)in & 15) || ((uintptr_t)data & 3) || ((uintptr_t)overflow & 3) || ((uintptr_t)overflow_counts & 3)) {
-        set_error("sparse24 quantizer: input must be 16-byte aligned, data / overflow / overflow_counts 4-byte aligned");
+    if ((residual_data == nullptr) != (residual_meta == nullptr)) {
+        set_error("sparse24 quantizer: residual_data and residual_meta go together");
+        return PK_E_ARG;
+    }
+    if (((uintptr_t)in & 15) || ((uintptr_t)data & 3) || ((uintptr_t)residual_data & 3) || ((uintptr_t)overflow & 3) ||
+        ((uintptr_t)overflow_counts & 3)) {
+        set_error("sparse24 quantizer: input must be 16-byte aligned, data / residual_data / overflow / overflow_counts 4-byte aligned");
         return PK_E_ALIGN;
     }
-    launch_quantize_rows_sp24(in, data, meta, scales, overflow_counts, overflow, rows, valid_rows < 0 ? 0 : valid_rows, k, STREAM);
+    launch_quantize_rows_sp24(in, data, meta, scales, overflow_counts, overflow, residual_data, residual_meta, rows,
+                              valid_rows < 0 ? 0 : valid_rows, k, STREAM);
     return check_launch("quantize_rows_int8_sparse24");
 }
 
@@ -469,14 +476,19 @@ int32_t pk_transpose_int8(const int8_t* w, int8_t* wt, int32_t n, int32_t k, voi
 }
 
 int32_t pk_ffn_contract_int8_sparse24(const uint8_t* data, const uint8_t* meta, const float* in_scales, const uint32_t* overflow_counts,
-                                      const uint32_t* overflow, const int8_t* w, const int8_t* wt, const float* ws, float* out,
-                                      int32_t rows, void* stream) {
+                                      const uint32_t* overflow, const uint8_t* residual_data, const uint8_t* residual_meta,
+                                      const int8_t* w, const int8_t* wt, const float* ws, float* out, int32_t rows, void* stream) {
     if (rows < 0) { set_error("negative rows"); return PK_E_SHAPE; }
     if (rows == 0) return PK_OK;
     if (!need(data, "data") || !need(meta, "meta") || !need(in_scales, "input_scales") || !need(overflow_counts, "overflow_counts") ||
         !need(overflow, "overflow") || !need(w, "weight") || !need(wt, "weight_t") || !need(ws, "weight_scales") || !need(out, "output"))
         return PK_E_ARG;
-    return launch_sparse24_i8_contract(data, meta, in_scales, overflow_counts, overflow, w, wt, ws, out, rows, 1024, 4096, STREAM);
+    if ((residual_data == nullptr) != (residual_meta == nullptr)) {
+        set_error("sparse INT8 contract: residual_data and residual_meta go together");
+        return PK_E_ARG;
+    }
+    return launch_sparse24_i8_contract(data, meta, in_scales, overflow_counts, overflow, residual_data, residual_meta, w, wt, ws, out,
+                                       rows, 1024, 4096, STREAM);
 }
 
 // ---- joint ------------------------------------------------------------------------

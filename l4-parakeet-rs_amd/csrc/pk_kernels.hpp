@@ -18,9 +18,10 @@ int gemm_tile_plan(int fmt, int epi, int m, int n, int* cols, int* stages);
 int gemm_k_split(int fmt, int epi, int m, int n, int k);
 int launch_quantize_static(const void* in, void* out, float inverse_scale, size_t elements, bool int8, hipStream_t s);
 int launch_quantize_rows(int kind, const void* in, void* out, float* scales, int rows, int valid_rows, int k, hipStream_t s);
-// INT8 rows as 2:4 data / metadata plus per-row overflow lists (k % 128 == 0, k <= 4096).
+// INT8 rows as 2:4 data / metadata plus per-row overflow lists (k % 128 == 0, k <= 4096),
+// and, when data2 / meta2 are given, the residual 2:4 form of the positions not kept.
 int launch_quantize_rows_sp24(const void* in, uint8_t* data, uint8_t* meta, float* scales, uint32_t* ovf_count, uint32_t* ovf,
-                              int rows, int valid_rows, int k, hipStream_t s);
+                              uint8_t* data2, uint8_t* meta2, int rows, int valid_rows, int k, hipStream_t s);
 int launch_pack_rows(int kind, const void* w, void* out, float* scales, int n, int k, hipStream_t s);
 int launch_q4k_dequant(const uint8_t* blocks, uint16_t* out, int n, int k, hipStream_t s);
 int launch_pack_g128(const void* w, uint32_t* q, uint16_t* scales, uint16_t* zeros, int n, int k, hipStream_t s);
@@ -62,8 +63,8 @@ int launch_local_attention(bool packed, const uint16_t* query, const uint16_t* k
                            const float* key_scales, const uint8_t* packed_position, const float* position_scales, hipStream_t s);
 
 int launch_sparse24_i8_contract(const uint8_t* data, const uint8_t* meta, const float* in_scales, const uint32_t* ovf_count,
-                                const uint32_t* ovf, const int8_t* w, const int8_t* wt, const float* w_scales, float* out, int m,
-                                int n, int k, hipStream_t s);
+                                const uint32_t* ovf, const uint8_t* data2, const uint8_t* meta2, const int8_t* w, const int8_t* wt,
+                                const float* w_scales, float* out, int m, int n, int k, hipStream_t s);
 int launch_transpose_i8(const int8_t* w, int8_t* wt, int n, int k, hipStream_t s);
 void set_error(const char* fmt, ...);
 int cu_count();

@@ -214,7 +214,7 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(const uint16_t* __re
 // idx0 | idx1 << 2 in bits 16-19, and in `drop` bit i set for each nonzero
 // byte i that was not kept (at most two).  The kept pair plus the dropped
 // nonzeros are the quartet, exactly.
-__device__ __forceinline__ uint32_t compress_i8_quartet(uint32_t packed, uint32_t& drop) {
+__device__ __forceinline__ uint32_t compress_i8_quartet(uint32_t packed, uint32_t& drop, uint32_t& rest) {
     // |v| per byte (0 .. 128) without carries between bytes: (x ^ 0xff) + 1 for negatives
     const uint32_t sgn = (packed >> 7) & 0x01010101u;
     const uint32_t mag = (packed ^ (sgn * 255u)) + sgn;
@@ -231,7 +231,11 @@ __device__ __forceinline__ uint32_t compress_i8_quartet(uint32_t packed, uint32_
     // nonzero bytes: |v| + 0x7f sets the byte's top bit iff |v| > 0 (no carry out at 128)
     const uint32_t t = (mag + 0x7f7f7f7fu) & 0x80808080u;
     const uint32_t nz = ((t >> 7) & 1u) | ((t >> 14) & 2u) | ((t >> 21) & 4u) | ((t >> 28) & 8u);
-    drop = nz & ~((1u << i0) | (1u << i1));
+    const uint32_t others = 15u & ~((1u << i0) | (1u << i1));
+    drop = nz & others;
+    // the residual pair: the two positions not kept, ascending, with their bytes
+    const uint32_t j0 = (uint32_t)__builtin_ctz(others), j1 = 31u - (uint32_t)__builtin_clz(others);
+    rest = (__builtin_amdgcn_perm(0u, packed, j0 | (j1 << 8) | 0x0c0c0000u) & 0xffffu) | ((j0 | (j1 << 2)) << 16);
     return (d & 0xffffu) | ((i0 | (i1 << 2)) << 16);
 }
 
@@ -242,13 +246,16 @@ __device__ __forceinline__ uint32_t compress_i8_quartet(uint32_t packed, uint32_
 // byte p / 2) plus, per row, the nonzeros the 2:4 selection dropped:
 // ovf_count[row] entries at ovf[row * k/2 ...], each (kk << 8) | byte for
 // element kk, in ascending kk.  At most two per quartet, so k/2 entries per
-// row always suffice.  One wave per row, the row held in registers (k <= 64 *
+// row always suffice.  With data2 / meta2 (both or neither) the residual 2:4
+// form as well: per quartet the two positions not kept, ascending, with their
+// bytes, in the layout of data / meta.  One wave per row, the row held in registers (k <= 64 *
 // kCh * 8); a lane handles chunk c = lane + 64 i (8 elements = 2 quartets) and
 // the overflow slots are a wave prefix sum over the lanes' counts.
 template <int kCh>
 __global__ __launch_bounds__(256) void quantize_rows_sp24_kernel(const uint16_t* __restrict__ in, uint8_t* __restrict__ data,
                                                                  uint8_t* __restrict__ meta, float* __restrict__ scales,
                                                                  uint32_t* __restrict__ ovf_count, uint32_t* __restrict__ ovf,
+                                                                 uint8_t* __restrict__ data2, uint8_t* __restrict__ meta2,
                                                                  int rows, int k, int valid_rows) {
     const int lane = threadIdx.x & 63;
     const int nw = gridDim.x * 4;
@@ -304,9 +311,9 @@ __global__ __launch_bounds__(256) void quantize_rows_sp24_kernel(const uint16_t*
                 w[0] = low_bytes4(rne_bits(v[0]), rne_bits(v[1]), rne_bits(v[2]), rne_bits(v[3]));
                 w[1] = low_bytes4(rne_bits(v[4]), rne_bits(v[5]), rne_bits(v[6]), rne_bits(v[7]));
             }
-            uint32_t drop0, drop1;
-            const uint32_t q0 = compress_i8_quartet(w[0], drop0);
-            const uint32_t q1 = compress_i8_quartet(w[1], drop1);
+            uint32_t drop0, drop1, r0, r1;
+            const uint32_t q0 = compress_i8_quartet(w[0], drop0, r0);
+            const uint32_t q1 = compress_i8_quartet(w[1], drop1, r1);
             const uint32_t drops = drop0 | (drop1 << 4);  // element j of the chunk
             const uint32_t n = (uint32_t)__builtin_popcount(drops);
             // exclusive prefix of n over the lanes below (n <= 4: three bit planes)
@@ -320,6 +327,10 @@ __global__ __launch_bounds__(256) void quantize_rows_sp24_kernel(const uint16_t*
             if (c < chunks) {
                 *(uint32_t*)(drow + 4 * c) = (q0 & 0xffffu) | (q1 << 16);
                 mrow[c] = (uint8_t)(((q0 >> 16) & 15u) | (((q1 >> 16) & 15u) << 4));
+                if (data2) {
+                    *(uint32_t*)(data2 + (size_t)row * (k >> 1) + 4 * c) = (r0 & 0xffffu) | (r1 << 16);
+                    meta2[(size_t)row * (k >> 3) + c] = (uint8_t)(((r0 >> 16) & 15u) | (((r1 >> 16) & 15u) << 4));
+                }
                 uint32_t slot = base + pre;
                 for (uint32_t d = drops; d != 0; d &= d - 1) {
                     const int j = __builtin_ctz(d);
@@ -640,12 +651,12 @@ int launch_quantize_rows(int kind, const void* in, void* out, float* scales, int
 }
 
 int launch_quantize_rows_sp24(const void* in, uint8_t* data, uint8_t* meta, float* scales, uint32_t* ovf_count, uint32_t* ovf,
-                              int rows, int valid_rows, int k, hipStream_t s) {
+                              uint8_t* data2, uint8_t* meta2, int rows, int valid_rows, int k, hipStream_t s) {
     if (rows == 0) return 0;
     const unsigned grid = row_grid(rows);
     const uint16_t* x = (const uint16_t*)in;
-    if (k <= 1024) quantize_rows_sp24_kernel<2><<<grid, 256, 0, s>>>(x, data, meta, scales, ovf_count, ovf, rows, k, valid_rows);
-    else quantize_rows_sp24_kernel<8><<<grid, 256, 0, s>>>(x, data, meta, scales, ovf_count, ovf, rows, k, valid_rows);
+    if (k <= 1024) quantize_rows_sp24_kernel<2><<<grid, 256, 0, s>>>(x, data, meta, scales, ovf_count, ovf, data2, meta2, rows, k, valid_rows);
+    else quantize_rows_sp24_kernel<8><<<grid, 256, 0, s>>>(x, data, meta, scales, ovf_count, ovf, data2, meta2, rows, k, valid_rows);
     return 0;
 }
 

@@ -233,7 +233,9 @@ int launch_sparse24_contract(const uint8_t* data, const uint8_t* meta, const uin
 // each, the 128 bytes of its weight column for the tile's columns (a row of
 // the transposed weights W^T [K x N], direct-to-LDS) are staged in LDS; each
 // lane then walks the entries of its rows and adds v * W[n, k] to the
-// accumulators of its 4 columns.
+// accumulators of its 4 columns.  When the producer also wrote the residual
+// 2:4 form (the two positions of each quartet the selection did not keep),
+// tiles with many entries run the K-loop a second time on it instead.
 template <int kAI, int kWM = 2> struct Sp8 {
     static constexpr int kRows = 16 * kAI * kWM;   // tile rows: kWM waves along M, each kAI blocks of 16
     static constexpr int kWaves = 2 * kWM, kThreads = 64 * kWaves;
@@ -260,6 +262,8 @@ struct Sparse8Args {
     const float* in_scales;     // [M]
     const uint32_t* ovf_count;  // [M]
     const uint32_t* ovf;        // [M x K/2]
+    const uint8_t* data2;       // [M x K/2] residual 2:4 form, or null
+    const uint8_t* meta2;       // [M x K/8]
     const int8_t* w;            // [N x K]
     const int8_t* wt;           // [K x N]
     const float* w_scales;      // [N]
@@ -277,6 +281,8 @@ template <int kOps> __device__ __forceinline__ void sp8_wait_stages(int younger)
     default: sp8_wait<3 * kOps>(); break;
     }
 }
+
+constexpr int kResidualPerRow = 8;
 
 template <int kAI, int kWM>
 __global__ __launch_bounds__((Sp8<kAI, kWM>::kThreads), (Sp8<kAI, kWM>::kOcc)) void sparse24_i8_kernel(Sparse8Args p) {
@@ -316,11 +322,13 @@ __global__ __launch_bounds__((Sp8<kAI, kWM>::kThreads), (Sp8<kAI, kWM>::kOcc)) v
         const int slot = o >> 7, c = ((o >> 4) & 7) ^ ((slot >> 1) & 7);
         w_off[i] = (uint32_t)((size_t)(n0 + sp8w_row(slot)) * p.k + c * 16);
     }
+    const uint8_t* src_d = p.data;  // the 2:4 form the K-loop reads: the kept pairs, then (residual pass) the rest
+    const uint8_t* src_m = p.meta;
     auto issue = [&](int step) {
         const uint32_t base = lds_base + (uint32_t)((step % kS) * L::kStage);
 #pragma unroll
-        for (int i = 0; i < kAI / 2; ++i) dma16(p.data + d_off[i] + (size_t)step * 64, base + (wave * (kAI / 2) + i) * 1024);
-        if (lane < L::kMetaLanes) dma16(p.meta + m_off + (size_t)step * 16, base + L::kData + wave * L::kMetaLanes * 16);
+        for (int i = 0; i < kAI / 2; ++i) dma16(src_d + d_off[i] + (size_t)step * 64, base + (wave * (kAI / 2) + i) * 1024);
+        if (lane < L::kMetaLanes) dma16(src_m + m_off + (size_t)step * 16, base + L::kData + wave * L::kMetaLanes * 16);
 #pragma unroll
         for (int i = 0; i < L::kWLoads; ++i)
             dma16(p.w + w_off[i] + (size_t)step * 128, base + L::kData + L::kMeta + (wave * L::kWLoads + i) * 1024);
@@ -332,6 +340,7 @@ __global__ __launch_bounds__((Sp8<kAI, kWM>::kThreads), (Sp8<kAI, kWM>::kOcc)) v
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) acc[i][jj] = v4i{0, 0, 0, 0};
 
+    auto kloop = [&]() {
     const int pre = min(kS - 1, steps);
     for (int st = 0; st < pre; ++st) issue(st);
     for (int step = 0; step < steps; ++step) {
@@ -361,6 +370,8 @@ __global__ __launch_bounds__((Sp8<kAI, kWM>::kThreads), (Sp8<kAI, kWM>::kOcc)) v
         }
     }
     __syncthreads();  // every wave is done with the ring
+    };
+    kloop();
 
     // ---- overflow entries of the tile's rows ----
     uint32_t* cnt_s = (uint32_t*)(lds + L::kCnt);
@@ -388,7 +399,19 @@ __global__ __launch_bounds__((Sp8<kAI, kWM>::kThreads), (Sp8<kAI, kWM>::kOcc)) v
     }
     __syncthreads();
     const uint32_t total = off_s[L::kRows];
-    for (uint32_t c0 = 0; c0 < total; c0 += L::kChunk) {
+    // Tiles with more than kResidualPerRow overflow entries per row take the
+    // residual 2:4 form through a second K-loop instead of the entry lists:
+    // its cost is one more pass over K, the lists' grows with every entry
+    // (T = 7500: the lists add about 2.6 us per entry per row, the second pass
+    // about 21 us, so they meet near 8 entries per row).
+    const bool residual = p.data2 != nullptr && total > (uint32_t)(kResidualPerRow * L::kRows);
+    if (residual) {
+        src_d = p.data2;
+        src_m = p.meta2;
+        __syncthreads();  // every thread has read the offsets before the ring is reused
+        kloop();
+    }
+    for (uint32_t c0 = 0; !residual && c0 < total; c0 += L::kChunk) {
         const int len = (int)min((uint32_t)L::kChunk, total - c0);
         // stage entries as (tile row << 8) | byte; issue the weight-row loads
         // straight from the global entries (k = entry >> 8)
@@ -467,22 +490,27 @@ static int launch_sp8(const Sparse8Args& a, hipStream_t s) {
 }
 
 int launch_sparse24_i8_contract(const uint8_t* data, const uint8_t* meta, const float* in_scales, const uint32_t* ovf_count,
-                                const uint32_t* ovf, const int8_t* w, const int8_t* wt, const float* w_scales, float* out, int m,
-                                int n, int k, hipStream_t s) {
+                                const uint32_t* ovf, const uint8_t* data2, const uint8_t* meta2, const int8_t* w, const int8_t* wt,
+                                const float* w_scales, float* out, int m, int n, int k, hipStream_t s) {
     if (m == 0) return 0;
     if (n <= 0 || k <= 0 || n % 128 != 0 || k % 128 != 0 || k > (1 << 24)) {
         set_error("sparse INT8 contract: n and k must be positive multiples of 128 (k <= 2^24), got n=%d k=%d", n, k);
         return -1;
     }
-    if (((uintptr_t)data | (uintptr_t)meta | (uintptr_t)w | (uintptr_t)wt | (uintptr_t)w_scales | (uintptr_t)out) & 15) {
-        set_error("sparse INT8 contract: data, meta, weight, weight_t, weight_scales and output must be 16-byte aligned");
+    if (((uintptr_t)data | (uintptr_t)meta | (uintptr_t)data2 | (uintptr_t)meta2 | (uintptr_t)w | (uintptr_t)wt | (uintptr_t)w_scales |
+         (uintptr_t)out) & 15) {
+        set_error("sparse INT8 contract: data, meta, residual data / meta, weight, weight_t, weight_scales and output must be 16-byte aligned");
         return -2;
+    }
+    if ((data2 == nullptr) != (meta2 == nullptr)) {
+        set_error("sparse INT8 contract: residual data and metadata go together");
+        return -1;
     }
     if (((size_t)m * (size_t)(k / 2)) >> 32 || ((size_t)n * (size_t)k) >> 32) {
         set_error("sparse INT8 contract: operands past 4 GiB are not supported");
         return -1;
     }
-    const Sparse8Args a{data, meta, in_scales, ovf_count, ovf, w, wt, w_scales, out, m, n, k};
+    const Sparse8Args a{data, meta, in_scales, ovf_count, ovf, data2, meta2, w, wt, w_scales, out, m, n, k};
     // 256-row tiles of 8 waves, one workgroup per CU and a 4-stage ring, where
     // they give at least half the CUs a tile (T = 7500: 41.5 -> 39.4 us at 95 %
     // sparsity); smaller grids keep 128-row tiles two per CU

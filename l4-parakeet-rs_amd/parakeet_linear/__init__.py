@@ -88,9 +88,9 @@ SIGNATURES = {
     "pk_subsample_projection_fp8": (I, [P, P, P, P, P, P, I, P]),
     "pk_subsample_pointwise_fp8": (I, [P, P, P, P, P, P, I, P]),
     "pk_ffn_contract_int8_rowskip": (I, [P, P, P, P, P, I, P, P]),
-    "pk_quantize_rows_int8_sparse24": (I, [P, P, P, P, P, P, I, I, I, P]),
+    "pk_quantize_rows_int8_sparse24": (I, [P, P, P, P, P, P, P, P, I, I, I, P]),
     "pk_transpose_int8": (I, [P, P, I, I, P]),
-    "pk_ffn_contract_int8_sparse24": (I, [P, P, P, P, P, P, P, P, P, I, P]),
+    "pk_ffn_contract_int8_sparse24": (I, [P, P, P, P, P, P, P, P, P, P, P, I, P]),
     "pk_gemm_k_split": (I, [I, I, I, I, I]),
     "pk_gemm_tile": (I, [I, I, I, I, ctypes.POINTER(I), ctypes.POINTER(I)]),
     "pk_gemm": (I, [I, I, P, P, I, I, I, P, P, F, P, P, F, F, I, P, P, P, P, I, P]),

@@ -732,6 +732,32 @@ void orc_compress_24_i8_exact(const int8_t* x, int rows, int k, uint8_t* data, u
     }
 }
 
+/* Residual 2:4 form of the same INT8 rows (no counterpart in the reference;
+ * this build's alternative to the overflow lists for rows with many dropped
+ * nonzeros): per quartet the two positions the selection in `meta` (above)
+ * did not keep, in ascending order, with their bytes (zero or not), so that
+ * decompressing (data, meta) and (data2, meta2) gives disjoint parts whose
+ * union is the row. */
+void orc_residual_24_i8(const int8_t* x, const uint8_t* meta, int rows, int k, uint8_t* data2, uint8_t* meta2) {
+    memset(meta2, 0, (size_t)rows * k / 8);
+    for (int r = 0; r < rows; ++r) {
+        for (int p = 0; p < k / 4; ++p) {
+            const int nibble = (meta[(size_t)r * k / 8 + p / 2] >> (4 * (p % 2))) & 15;
+            const int kept = (1 << (nibble & 3)) | (1 << ((nibble >> 2) & 3));
+            int count = 0, out = 0;
+            for (int i = 0; i < 4; ++i) {
+                if (kept & (1 << i)) continue;
+                if (count < 2) {
+                    data2[(size_t)r * k / 2 + 2 * p + count] = (uint8_t)x[(size_t)r * k + 4 * p + i];
+                    out |= i << (2 * count);
+                }
+                ++count;
+            }
+            meta2[(size_t)r * k / 8 + p / 2] |= (uint8_t)(out << (4 * (p % 2)));
+        }
+    }
+}
+
 void orc_decompress_24(const uint8_t* data, const uint8_t* meta, int rows, int k, uint8_t* x) {
     memset(x, 0, (size_t)rows * k);
     for (int r = 0; r < rows; ++r) {

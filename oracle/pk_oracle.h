@@ -62,6 +62,7 @@ void orc_layer_norm_quantize(const uint16_t* x, const uint16_t* gamma, const uin
                              uint8_t* q, float* scales, uint16_t* normalized);
 void orc_compress_24(const uint8_t* x, int rows, int k, uint8_t* data, uint8_t* meta);
 void orc_compress_24_i8_exact(const int8_t* x, int rows, int k, uint8_t* data, uint8_t* meta, uint32_t* counts, uint32_t* ovf);
+void orc_residual_24_i8(const int8_t* x, const uint8_t* meta, int rows, int k, uint8_t* data2, uint8_t* meta2);
 void orc_decompress_24(const uint8_t* data, const uint8_t* meta, int rows, int k, uint8_t* x);
 
 /* ---- GEMM references ------------------------------------------------------ */

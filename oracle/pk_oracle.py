@@ -67,6 +67,7 @@ def _declare(l):
         "orc_quantize_int4_rows": (None, [P, I, I, I, P, P]),
         "orc_layer_norm_quantize": (None, [P, P, P, I, I, I, F, I, P, P, P]),
         "orc_compress_24_i8_exact": (None, [P, I, I, P, P, P, P]),
+        "orc_residual_24_i8": (None, [P, P, I, I, P, P]),
         "orc_compress_24": (None, [P, I, I, P, P]),
         "orc_decompress_24": (None, [P, P, I, I, P]),
         "orc_gemm_i8_i32": (None, [P, P, I, I, I, P]),
@@ -343,6 +344,18 @@ def compress_24_i8_exact(x8: np.ndarray):
     ovf = np.zeros((m, k // 2), np.uint32)
     lib().orc_compress_24_i8_exact(_p(x8), m, k, _p(data), _p(meta), _p(counts), _p(ovf))
     return data, meta, counts, ovf
+
+
+def residual_24_i8(x8: np.ndarray, meta: np.ndarray):
+    """INT8 rows and their 2:4 metadata -> (residual data, residual metadata):
+    per quartet the two positions the metadata does not keep, ascending."""
+    x8 = np.ascontiguousarray(x8, dtype=np.int8)
+    meta = np.ascontiguousarray(meta, dtype=np.uint8)
+    m, k = x8.shape
+    data2 = np.empty((m, k // 2), np.uint8)
+    meta2 = np.empty((m, k // 8), np.uint8)
+    lib().orc_residual_24_i8(_p(x8), _p(meta), m, k, _p(data2), _p(meta2))
+    return data2, meta2
 
 
 def decompress_24(data: np.ndarray, meta: np.ndarray) -> np.ndarray:

@@ -184,17 +184,23 @@ def test_argument_checks_reject_before_any_launch(lib):
     assert qr(1, None, ok["o"], ok["s"], 4, 4, 1024, None) == E_ARG
     # exact 2:4 sparse FF2: producer and contract checks
     sq = lib.pk_quantize_rows_int8_sparse24
-    sq.argtypes = [vp, vp, vp, vp, vp, vp, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, vp]
+    sq.argtypes = [vp] * 8 + [ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, vp]
     sq.restype = ctypes.c_int32
-    assert sq(ok["i"], ok["o"], ok["b"], ok["s"], ok["w"], 0x60000, 4, 4, 1000, None) == E_SHAPE
-    assert sq(ok["i"], ok["o"], ok["b"], ok["s"], ok["w"], 0x60000, 4, 4, 8192, None) == E_SHAPE
-    assert sq(0x10008, ok["o"], ok["b"], ok["s"], ok["w"], 0x60000, 4, 4, 4096, None) == E_ALIGN
-    assert sq(ok["i"], ok["o"], ok["b"], ok["s"], None, 0x60000, 4, 4, 4096, None) == E_ARG
+    assert sq(ok["i"], ok["o"], ok["b"], ok["s"], ok["w"], 0x60000, None, None, 4, 4, 1000, None) == E_SHAPE
+    assert sq(ok["i"], ok["o"], ok["b"], ok["s"], ok["w"], 0x60000, None, None, 4, 4, 8192, None) == E_SHAPE
+    assert sq(0x10008, ok["o"], ok["b"], ok["s"], ok["w"], 0x60000, None, None, 4, 4, 4096, None) == E_ALIGN
+    assert sq(ok["i"], ok["o"], ok["b"], ok["s"], ok["w"], 0x60000, 0x70002, 0x80000, 4, 4, 4096, None) == E_ALIGN
+    assert sq(ok["i"], ok["o"], ok["b"], ok["s"], None, 0x60000, None, None, 4, 4, 4096, None) == E_ARG
+    assert sq(ok["i"], ok["o"], ok["b"], ok["s"], ok["w"], 0x60000, 0x70000, None, 4, 4, 4096, None) == E_ARG
+    assert b"residual" in err()
     sc = lib.pk_ffn_contract_int8_sparse24
-    sc.argtypes = [vp] * 9 + [ctypes.c_int32, vp]
+    sc.argtypes = [vp] * 11 + [ctypes.c_int32, vp]
     sc.restype = ctypes.c_int32
-    args = [0x10000, 0x20000, 0x30000, 0x40000, 0x50000, 0x60000, 0x70000, 0x80000, 0x90000]
+    args = [0x10000, 0x20000, 0x30000, 0x40000, 0x50000, None, None, 0x60000, 0x70000, 0x80000, 0x90000]
     assert sc(*args, -1, None) == E_SHAPE
-    assert sc(*args[:6], None, *args[7:], 8, None) == E_ARG
+    assert sc(*args[:8], None, *args[9:], 8, None) == E_ARG
     assert b"weight_t" in err()
+    assert sc(*args[:5], 0xa0000, None, *args[7:], 8, None) == E_ARG
+    assert b"residual" in err()
+    assert sc(*args[:5], 0xa0000, 0xb0008, *args[7:], 8, None) == E_ALIGN
     assert sc(0x10004, *args[1:], 8, None) == E_ALIGN

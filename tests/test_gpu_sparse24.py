@@ -56,20 +56,22 @@ def topk_silu(t, k, sparsity, gen):
     return torch.where(a.abs().float() >= thr, a, torch.zeros_like(a))
 
 
-def produce(pk, x, valid_rows=None):
+def produce(pk, x, valid_rows=None, residual=False):
     t, k = x.shape
     data = torch.empty((t, k // 2), dtype=torch.uint8, device="cuda")
     meta = torch.empty((t, k // 8), dtype=torch.uint8, device="cuda")
     scales = torch.empty(t, dtype=torch.float32, device="cuda")
     counts = torch.empty(t, dtype=torch.int32, device="cuda")
     ovf = torch.zeros((t, k // 2), dtype=torch.int32, device="cuda")
-    pk.call("pk_quantize_rows_int8_sparse24", x, data, meta, scales, counts, ovf, t,
+    data2 = torch.full((t, k // 2), 0x5A, dtype=torch.uint8, device="cuda") if residual else None
+    meta2 = torch.full((t, k // 8), 0x5A, dtype=torch.uint8, device="cuda") if residual else None
+    pk.call("pk_quantize_rows_int8_sparse24", x, data, meta, scales, counts, ovf, data2, meta2, t,
             t if valid_rows is None else valid_rows, k)
-    return data, meta, scales, counts, ovf
+    return data, meta, scales, counts, ovf, data2, meta2
 
 
-def check_producer(pk, orc, x, valid_rows=None, rows=None):
-    data, meta, scales, counts, ovf = produce(pk, x, valid_rows)
+def check_producer(pk, orc, x, valid_rows=None, rows=None, residual=False):
+    data, meta, scales, counts, ovf, data2, meta2 = produce(pk, x, valid_rows, residual)
     xh = host(x)
     q, s = orc.quantize_int8_rows(xh, valid_rows)
     rd, rm, rc, ro = orc.compress_24_i8_exact(q)
@@ -82,7 +84,11 @@ def check_producer(pk, orc, x, valid_rows=None, rows=None):
     o = host(ovf).view(np.uint32)
     for r in idx:
         assert np.array_equal(o[r, :c[r]], ro[r, :rc[r]]), f"overflow list of row {r}"
-    return q, s, (data, meta, scales, counts, ovf)
+    if residual:
+        r2d, r2m = orc.residual_24_i8(q, rm)
+        assert np.array_equal(host(data2)[idx], r2d[idx]), "residual data"
+        assert np.array_equal(host(meta2)[idx], r2m[idx]), "residual metadata"
+    return q, s
 
 
 @pytest.mark.parametrize("k", [1024, 1152, 4096])
@@ -101,6 +107,7 @@ def test_producer_exact_edge_rows(pk, orc, k):
     x[7, ::2] = -0.5
     x[7, 1::2] = 0.5
     x[8] = topk_silu(1, k, 0.9, gen)[0]
+    check_producer(pk, orc, x, valid_rows=36, residual=True)
     check_producer(pk, orc, x, valid_rows=36)
 
 
@@ -111,7 +118,7 @@ def test_producer_exact_T7500(pk, orc, sparsity):
     gen.manual_seed(int(sparsity * 1000))
     x = topk_silu(7500, 4096, sparsity, gen)
     rows = np.unique(np.concatenate([np.arange(0, 7500, 97), [7499]]))
-    check_producer(pk, orc, x, rows=rows)
+    check_producer(pk, orc, x, rows=rows, residual=True)
 
 
 def test_transpose_int8(pk):
@@ -134,12 +141,12 @@ def int8_weights(pk, gen, n=1024, k=4096):
     return wq, wt, ws
 
 
-def run_contract(pk, orc, x, gen, sample):
+def run_contract(pk, orc, x, gen, sample, residual):
     t, k = x.shape
     wq, wt, ws = int8_weights(pk, gen)
-    data, meta, scales, counts, ovf = produce(pk, x)
+    data, meta, scales, counts, ovf, data2, meta2 = produce(pk, x, residual=residual)
     out = torch.empty((t, 1024), dtype=torch.float32, device="cuda")
-    pk.call("pk_ffn_contract_int8_sparse24", data, meta, scales, counts, ovf, wq, wt, ws, out, t)
+    pk.call("pk_ffn_contract_int8_sparse24", data, meta, scales, counts, ovf, data2, meta2, wq, wt, ws, out, t)
     # dense INT8 rows of the same quantizer, through the dense row-skip contract
     xq = torch.empty((t, k), dtype=torch.int8, device="cuda")
     xs = torch.empty(t, dtype=torch.float32, device="cuda")
@@ -154,28 +161,33 @@ def run_contract(pk, orc, x, gen, sample):
     return int(host(counts).sum())
 
 
+@pytest.mark.parametrize("residual", [False, True])
 @pytest.mark.parametrize("sparsity", [0.5, 0.8, 0.9, 0.95])
-def test_contract_exact_T7500(pk, orc, sparsity):
-    note(f"sparse24 contract T=7500 sparsity={sparsity}")
+def test_contract_exact_T7500(pk, orc, sparsity, residual):
+    """With the residual form, the 50 % and 80 % tiles (385 / 30 overflow
+    entries per row) take the second sparse pass, the 90 % and 95 % tiles
+    (4 / 0.5) the lists."""
+    note(f"sparse24 contract T=7500 sparsity={sparsity} residual={residual}")
     gen = torch.Generator(device="cuda")
     gen.manual_seed(7 + int(sparsity * 100))
     x = topk_silu(7500, 4096, sparsity, gen)
     sample = np.unique(np.concatenate([np.arange(0, 7500, 128) + (np.arange(59) * 37) % 128, [7499]]))
     sample = sample[sample < 7500]
-    entries = run_contract(pk, orc, x, gen, sample)
+    entries = run_contract(pk, orc, x, gen, sample, residual)
     note(f"  overflow entries per row {entries / 7500:.2f}")
 
 
+@pytest.mark.parametrize("residual", [False, True])
 @pytest.mark.parametrize("t", [1, 5, 129, 300])
-def test_contract_exact_dense_and_ragged(pk, orc, t):
+def test_contract_exact_dense_and_ragged(pk, orc, t, residual):
     """Dense random rows (about two overflow entries per quartet: hundreds of
     thousands per 128-row tile, so many overflow chunks), zero rows, ragged
     row counts."""
-    note(f"sparse24 contract dense/ragged t={t}")
+    note(f"sparse24 contract dense/ragged t={t} residual={residual}")
     gen = torch.Generator(device="cuda")
     gen.manual_seed(100 + t)
     x = torch.randn((t, 4096), generator=gen, device="cuda").half()
     if t > 3:
         x[2] = 0
         x[3] = topk_silu(1, 4096, 0.95, gen)[0]
-    run_contract(pk, orc, x, gen, np.arange(t))
+    run_contract(pk, orc, x, gen, np.arange(t), residual)

@@ -275,6 +275,45 @@ def test_compress_24_i8_exact_rebuilds_rows(oracle):
     assert counts[3] == 256 and counts[2] == 0
 
 
+def test_residual_24_i8_complements_the_selection(oracle):
+    """Every quartet over the same alphabet: the residual metadata names the
+    two positions the 2:4 selection does not keep, ascending and distinct; its
+    bytes are the row's there; its nonzeros are exactly the overflow entries;
+    and (2:4 part) + (residual part) rebuild the row, disjointly."""
+    alphabet = [0, 1, -1, 2, -2, 127, -127, -128]
+    quartets = np.array(list(itertools.product(alphabet, repeat=4)), np.int8)
+    row = quartets.reshape(1, -1)
+    data, meta, counts, ovf = oracle.compress_24_i8_exact(row)
+    data2, meta2 = oracle.residual_24_i8(row, meta)
+    m1, m2, d2 = meta.reshape(-1), meta2.reshape(-1), data2.reshape(-1, 2).view(np.int8)
+    residual_entries = []
+    for p, quartet in enumerate(quartets):
+        kept = [int(m1[p // 2] >> (4 * (p % 2))) & 3, int(m1[p // 2] >> (4 * (p % 2) + 2)) & 3]
+        nib = (m2[p // 2] >> (4 * (p % 2))) & 15
+        rest = [int(nib & 3), int((nib >> 2) & 3)]
+        assert rest == sorted(set(range(4)) - set(kept)), (p, kept, rest)
+        assert d2[p].tolist() == [int(quartet[rest[0]]), int(quartet[rest[1]])]
+        residual_entries += [((4 * p + i) << 8) | (int(quartet[i]) & 255) for i in rest if quartet[i] != 0]
+    assert residual_entries == ovf[0, :counts[0]].tolist()
+    a = oracle.decompress_24(data, meta).view(np.int8)
+    b = oracle.decompress_24(data2, meta2).view(np.int8)
+    assert not np.any((a != 0) & (b != 0))
+    assert np.array_equal(a.astype(np.int16) + b.astype(np.int16), row.astype(np.int16))
+
+
+def test_residual_24_i8_rebuilds_rows(oracle):
+    rng = np.random.default_rng(12)
+    x = rng.integers(-128, 128, (5, 1024), dtype=np.int8)
+    x[1, rng.random(1024) < 0.8] = 0
+    x[2] = 0
+    data, meta, _, _ = oracle.compress_24_i8_exact(x)
+    data2, meta2 = oracle.residual_24_i8(x, meta)
+    a = oracle.decompress_24(data, meta).view(np.int8).astype(np.int16)
+    b = oracle.decompress_24(data2, meta2).view(np.int8).astype(np.int16)
+    assert np.array_equal(a + b, x.astype(np.int16))
+    assert not data2[2].any()
+
+
 # ---- GEMMs against numpy --------------------------------------------------------------
 
 def test_gemm_i8_exact(oracle):
