@@ -341,35 +341,35 @@ __global__ __launch_bounds__((Sp8<kAI, kWM>::kThreads), (Sp8<kAI, kWM>::kOcc)) v
         for (int jj = 0; jj < 4; ++jj) acc[i][jj] = v4i{0, 0, 0, 0};
 
     auto kloop = [&]() {
-    const int pre = min(kS - 1, steps);
-    for (int st = 0; st < pre; ++st) issue(st);
-    for (int step = 0; step < steps; ++step) {
-        // stage `step` has landed once only the younger stages' loads are pending
-        sp8_wait_stages<L::kOps>(min(step + kS - 2, steps - 1) - step);
-        __syncthreads();
-        if (step + kS - 1 < steps) issue(step + kS - 1);
-        const uint8_t* Ds = lds + (step % kS) * L::kStage;
-        const uint8_t* Ms = Ds + L::kData;
-        const uint8_t* Ws = Ms + L::kMeta;
-        v8i wf[4];
+        const int pre = min(kS - 1, steps);
+        for (int st = 0; st < pre; ++st) issue(st);
+        for (int step = 0; step < steps; ++step) {
+            // stage `step` has landed once only the younger stages' loads are pending
+            sp8_wait_stages<L::kOps>(min(step + kS - 2, steps - 1) - step);
+            __syncthreads();
+            if (step + kS - 1 < steps) issue(step + kS - 1);
+            const uint8_t* Ds = lds + (step % kS) * L::kStage;
+            const uint8_t* Ms = Ds + L::kData;
+            const uint8_t* Ws = Ms + L::kMeta;
+            v8i wf[4];
 #pragma unroll
-        for (int bj = 0; bj < 4; ++bj) {
-            const int row = wn * 64 + 4 * l16 + bj;
-            const uint4 w0 = *(const uint4*)(Ws + sp8w(row, g));
-            const uint4 w1 = *(const uint4*)(Ws + sp8w(row, 4 + g));
-            wf[bj] = v8i{(int)w0.x, (int)w0.y, (int)w0.z, (int)w0.w, (int)w1.x, (int)w1.y, (int)w1.z, (int)w1.w};
+            for (int bj = 0; bj < 4; ++bj) {
+                const int row = wn * 64 + 4 * l16 + bj;
+                const uint4 w0 = *(const uint4*)(Ws + sp8w(row, g));
+                const uint4 w1 = *(const uint4*)(Ws + sp8w(row, 4 + g));
+                wf[bj] = v8i{(int)w0.x, (int)w0.y, (int)w0.z, (int)w0.w, (int)w1.x, (int)w1.y, (int)w1.z, (int)w1.w};
+            }
+#pragma unroll
+            for (int ai = 0; ai < kAI; ++ai) {
+                const int row = wm * 16 * kAI + ai * 16 + l16;
+                const uint4 d = *(const uint4*)(Ds + row * 64 + ((g ^ sp_key(row)) << 4));
+                const int idx = *(const int*)(Ms + row * 16 + g * 4);
+                const v4i dv = {(int)d.x, (int)d.y, (int)d.z, (int)d.w};
+#pragma unroll
+                for (int bj = 0; bj < 4; ++bj) acc[ai][bj] = __builtin_amdgcn_smfmac_i32_16x16x128_i8(dv, wf[bj], acc[ai][bj], idx, 0, 0);
+            }
         }
-#pragma unroll
-        for (int ai = 0; ai < kAI; ++ai) {
-            const int row = wm * 16 * kAI + ai * 16 + l16;
-            const uint4 d = *(const uint4*)(Ds + row * 64 + ((g ^ sp_key(row)) << 4));
-            const int idx = *(const int*)(Ms + row * 16 + g * 4);
-            const v4i dv = {(int)d.x, (int)d.y, (int)d.z, (int)d.w};
-#pragma unroll
-            for (int bj = 0; bj < 4; ++bj) acc[ai][bj] = __builtin_amdgcn_smfmac_i32_16x16x128_i8(dv, wf[bj], acc[ai][bj], idx, 0, 0);
-        }
-    }
-    __syncthreads();  // every wave is done with the ring
+        __syncthreads();  // every wave is done with the ring
     };
     kloop();
 
