@@ -497,16 +497,6 @@ __global__ __launch_bounds__(256) void layer_norm_quantize_kernel(const uint16_t
     }
     gb_finite = __syncthreads_and(gb_finite);
     const size_t out_row = kInt4 ? 512 : 1024;
-    // The next row's input words are loaded while the current row runs its
-    // reductions, so every wave keeps one row of loads in flight.
-    uint2 raw[4] = {};
-    auto load_row = [&](int r) {
-        if (r < rows) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) raw[i] = *(const uint2*)(in + (size_t)r * 1024 + 256 * i + 4 * lane);
-        }
-    };
-    load_row(blockIdx.x * 4 + wave);
     for (int row = blockIdx.x * 4 + wave; row < padded_rows; row += nw) {
         uint8_t* o = out + (size_t)row * out_row;
         uint16_t* nrm = normalized ? normalized + (size_t)row * 1024 : nullptr;
@@ -523,11 +513,11 @@ __global__ __launch_bounds__(256) void layer_norm_quantize_kernel(const uint16_t
         float v[16];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const uint16_t* h = (const uint16_t*)&raw[i];
+            const uint2 w = *(const uint2*)(in + (size_t)row * 1024 + 256 * i + 4 * lane);
+            const uint16_t* h = (const uint16_t*)&w;
 #pragma unroll
             for (int u = 0; u < 4; ++u) v[4 * i + u] = h2f(h[u]);
         }
-        load_row(row + nw);
         float part[4];
 #pragma unroll
         for (int u = 0; u < 4; ++u) part[u] = ((v[u] + v[4 + u]) + v[8 + u]) + v[12 + u];
