@@ -426,7 +426,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm3_kernel(GemmArgs p) {
                 // block), its two MFMAs, then the eight conversions / FMAs of
                 // block b - 2, so the VALU work interleaves with the MFMAs
                 // (INT4-g128 x INT8 linears at T = 45000: 4-7 % faster; the
-                // residual variant, short of registers, ran 5 % slower with it).
+                // residual variant, short of registers, ran 5-7 % slower with it).
                 if constexpr (E != EPI_F16_RES)
 #pragma unroll
                 for (int b = 0; b < 4 * kAI + 2; ++b) {
