@@ -181,6 +181,17 @@ int32_t pk_layer_norm_quantize_int4_dynamic(const uint16_t* input, const uint16_
                                             uint8_t* output, float* scales, int32_t rows, int32_t padded_rows,
                                             float epsilon, void* stream);
 
+/* encoder.cu:128-209 pk_sm89_layer_norm_pair (launched at encoder.rs:1394-1433):
+ * output = fp16(LN(input; weight, bias)) [padded_rows x 1024], then
+ * LN(output; next_weight, next_bias) into next_output, as fp16 when
+ * inverse_scale == 0, else as e4m3(fp16 value * inverse_scale) bytes (the
+ * reference passes 56 = 448 / 8 for an FP8 next FF1).  Rows in [rows,
+ * padded_rows) are zero in both outputs.  fp16 pointers 8-byte aligned,
+ * next_output 4-byte (e4m3) / 8-byte (fp16) aligned (PK_E_ALIGN). */
+int32_t pk_layer_norm_pair(const uint16_t* input, const uint16_t* weight, const uint16_t* bias, uint16_t* output,
+                           const uint16_t* next_weight, const uint16_t* next_bias, void* next_output, int32_t rows,
+                           int32_t padded_rows, float epsilon, float inverse_scale, void* stream);
+
 /* ---- linears (linear.cu) ---------------------------------------------------- */
 
 /* linear.cu:83-171 pk_sm89_fp16_linear_epilogue (+ the _m64 variant and the

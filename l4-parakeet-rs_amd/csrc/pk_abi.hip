@@ -206,6 +206,23 @@ int32_t pk_layer_norm_quantize_int4_dynamic(const uint16_t* in, const uint16_t* 
     return ln_quantize(true, in, w, b, out, scales, rows, padded_rows, eps, stream);
 }
 
+int32_t pk_layer_norm_pair(const uint16_t* in, const uint16_t* w, const uint16_t* b, uint16_t* out, const uint16_t* next_w,
+                           const uint16_t* next_b, void* next_out, int32_t rows, int32_t padded_rows, float eps, float inverse_scale,
+                           void* stream) {
+    if (rows < 0 || padded_rows < rows) { set_error("need 0 <= rows <= padded_rows"); return PK_E_SHAPE; }
+    if (padded_rows && (!need(in, "input") || !need(w, "weight") || !need(b, "bias") || !need(out, "output") ||
+                        !need(next_w, "next_weight") || !need(next_b, "next_bias") || !need(next_out, "next_output")))
+        return PK_E_ARG;
+    const uintptr_t a8 = (uintptr_t)in | (uintptr_t)w | (uintptr_t)b | (uintptr_t)out | (uintptr_t)next_w | (uintptr_t)next_b;
+    if (a8 & 7 || (uintptr_t)next_out & (inverse_scale != 0.0f ? 3 : 7)) {
+        set_error("layer_norm_pair needs 8-byte aligned fp16 vectors and a %d-byte aligned next_output",
+                  inverse_scale != 0.0f ? 4 : 8);
+        return PK_E_ALIGN;
+    }
+    launch_layer_norm_pair(in, w, b, out, next_w, next_b, next_out, rows, padded_rows, eps, inverse_scale, STREAM);
+    return check_launch("layer_norm_pair");
+}
+
 // ---- linears ---------------------------------------------------------------------
 
 int32_t pk_gemm(int32_t format, int32_t epilogue, const void* a, const void* b, int32_t m, int32_t n, int32_t k,

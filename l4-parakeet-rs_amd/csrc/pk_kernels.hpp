@@ -27,6 +27,8 @@ int launch_q4k_dequant(const uint8_t* blocks, uint16_t* out, int n, int k, hipSt
 int launch_pack_g128(const void* w, uint32_t* q, uint16_t* scales, uint16_t* zeros, int n, int k, hipStream_t s);
 int launch_layer_norm_quantize(bool int4, const void* in, const void* gamma, const void* beta, void* out, float* scales,
                                void* normalized, int rows, int padded_rows, float epsilon, hipStream_t s);
+int launch_layer_norm_pair(const void* in, const void* g1, const void* b1, void* out, const void* g2, const void* b2, void* next_out,
+                           int rows, int padded_rows, float epsilon, float inverse_scale, hipStream_t s);
 int launch_joint(const void* w, int w_int8, const float* w_scales, const float* bias, const void* enc, const float* pred,
                  float* scores, int* decision, int outputs, int hidden, int token_outputs, int durations, int steps,
                  int enc_stride, hipStream_t s);

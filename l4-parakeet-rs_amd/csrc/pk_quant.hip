@@ -586,6 +586,101 @@ __global__ __launch_bounds__(256) void layer_norm_quantize_kernel(const uint16_t
     }
 }
 
+// LayerNorm pair (encoder.cu:128-209): layer i's norm_out and layer i+1's
+// norm_ff1 from one read of the row.  first = fp16(LN(x; weight, bias)) is
+// written to `out` (the next FF1 residual needs it); second =
+// fp16(LN(first; next_weight, next_bias)) goes to `next_out` as fp16, or, when
+// inverse_scale != 0, as e4m3(second * inverse_scale) bytes (the fixed-scale
+// FF1 FP8 input).  Both LayerNorms use the reduction shape of
+// layer_norm_quantize_kernel above (the reference's second one sums the four
+// rounded first values of a thread in the same order as the first sums x).
+// Rows in [rows, padded_rows) are written as zeros.  Same wave-per-row
+// layout; the four fp16 parameter vectors are staged as fp32 in LDS.
+template <bool kFp8>
+__global__ __launch_bounds__(256) void layer_norm_pair_kernel(const uint16_t* __restrict__ in, const uint16_t* __restrict__ g1,
+                                                              const uint16_t* __restrict__ b1, uint16_t* __restrict__ out,
+                                                              const uint16_t* __restrict__ g2, const uint16_t* __restrict__ b2,
+                                                              void* __restrict__ next_out, int rows, int padded_rows, float epsilon,
+                                                              float inverse_scale) {
+    __shared__ __attribute__((aligned(16))) float red[4][2][256];
+    // prm[p][i][lane]: parameter p (weight, bias, next weight, next bias) at
+    // features 256 i + 4 lane .. + 3
+    __shared__ __attribute__((aligned(16))) float4 prm[4][4][64];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int nw = gridDim.x * 4;
+    {
+        const uint16_t* src[4] = {g1, b1, g2, b2};
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const uint2 w = *(const uint2*)(src[p] + 256 * wave + 4 * lane);
+            const uint16_t* h = (const uint16_t*)&w;
+            prm[p][wave][lane] = float4{h2f(h[0]), h2f(h[1]), h2f(h[2]), h2f(h[3])};
+        }
+    }
+    __syncthreads();
+    for (int row = blockIdx.x * 4 + wave; row < padded_rows; row += nw) {
+        uint16_t* o1 = out + (size_t)row * 1024;
+        if (row >= rows) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                *(uint2*)(o1 + 256 * i + 4 * lane) = uint2{0, 0};
+                if (kFp8) *(uint32_t*)((uint8_t*)next_out + (size_t)row * 1024 + 256 * i + 4 * lane) = 0u;
+                else *(uint2*)((uint16_t*)next_out + (size_t)row * 1024 + 256 * i + 4 * lane) = uint2{0, 0};
+            }
+            continue;
+        }
+        float v[16];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint2 w = *(const uint2*)(in + (size_t)row * 1024 + 256 * i + 4 * lane);
+            const uint16_t* h = (const uint16_t*)&w;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) v[4 * i + u] = h2f(h[u]);
+        }
+#pragma unroll
+        for (int pass = 0; pass < 2; ++pass) {
+            float part[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) part[u] = ((v[u] + v[4 + u]) + v[8 + u]) + v[12 + u];
+            const float mean = ln_partials_sum(part, red[wave][0]) / 1024.0f;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                float sq = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float d = v[4 * i + u] - mean;
+                    sq += d * d;
+                }
+                part[u] = sq;
+            }
+            const float inverse_std = 1.0f / sqrtf(ln_partials_sum(part, red[wave][1]) / 1024.0f + epsilon);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float4 g4 = prm[2 * pass][i][lane], b4 = prm[2 * pass + 1][i][lane];
+                const float g[4] = {g4.x, g4.y, g4.z, g4.w}, b[4] = {b4.x, b4.y, b4.z, b4.w};
+                uint16_t h[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const int e = 4 * i + u;
+                    h[u] = f2h((v[e] - mean) * inverse_std * g[u] + b[u]);
+                    v[e] = h2f(h[u]);
+                }
+                const uint2 packed{h[0] | ((uint32_t)h[1] << 16), h[2] | ((uint32_t)h[3] << 16)};
+                if (pass == 0) {
+                    *(uint2*)(o1 + 256 * i + 4 * lane) = packed;
+                } else if (kFp8) {
+                    const uint32_t q = e4m3x2(v[4 * i] * inverse_scale, v[4 * i + 1] * inverse_scale) |
+                                       (e4m3x2(v[4 * i + 2] * inverse_scale, v[4 * i + 3] * inverse_scale) << 16);
+                    *(uint32_t*)((uint8_t*)next_out + (size_t)row * 1024 + 256 * i + 4 * lane) = q;
+                } else {
+                    *(uint2*)((uint16_t*)next_out + (size_t)row * 1024 + 256 * i + 4 * lane) = packed;
+                }
+            }
+        }
+    }
+}
+
 // ---- launchers -------------------------------------------------------------
 
 // Q4_K superblocks -> fp16 [n x k] (linear.cu:459-472): one thread per 8
@@ -675,6 +770,21 @@ int launch_layer_norm_quantize(bool int4, const void* in, const void* gamma, con
     else
         layer_norm_quantize_kernel<false><<<grid, 256, 0, s>>>((const uint16_t*)in, (const uint16_t*)gamma, (const uint16_t*)beta,
                                                                 (uint8_t*)out, scales, (uint16_t*)normalized, rows, padded_rows, epsilon);
+    return 0;
+}
+
+int launch_layer_norm_pair(const void* in, const void* g1, const void* b1, void* out, const void* g2, const void* b2, void* next_out,
+                           int rows, int padded_rows, float epsilon, float inverse_scale, hipStream_t s) {
+    if (padded_rows == 0) return 0;
+    const unsigned grid = row_grid(padded_rows);
+    const uint16_t *x = (const uint16_t*)in, *w1 = (const uint16_t*)g1, *c1 = (const uint16_t*)b1, *w2 = (const uint16_t*)g2,
+                   *c2 = (const uint16_t*)b2;
+    if (inverse_scale != 0.0f)
+        layer_norm_pair_kernel<true><<<grid, 256, 0, s>>>(x, w1, c1, (uint16_t*)out, w2, c2, next_out, rows, padded_rows, epsilon,
+                                                           inverse_scale);
+    else
+        layer_norm_pair_kernel<false><<<grid, 256, 0, s>>>(x, w1, c1, (uint16_t*)out, w2, c2, next_out, rows, padded_rows, epsilon,
+                                                            inverse_scale);
     return 0;
 }
 

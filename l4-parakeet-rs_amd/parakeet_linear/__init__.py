@@ -66,6 +66,7 @@ SIGNATURES = {
     "pk_quantize_rows": (I, [I, P, P, P, I, I, I, P]),
     "pk_layer_norm_quantize_fp8_dynamic": (I, [P, P, P, P, P, I, I, F, P]),
     "pk_layer_norm_quantize_int4_dynamic": (I, [P, P, P, P, P, I, I, F, P]),
+    "pk_layer_norm_pair": (I, [P, P, P, P, P, P, P, I, I, F, F, P]),
     "pk_linear_fp16_epilogue": (I, [P, P, P, P, P, I, I, I, F, F, I, P]),
     "pk_linear_fp16_qkv": (I, [P, P, P, P, P, I, I, I, P]),
     "pk_linear_fp8_epilogue": (I, [P, P, P, P, P, I, I, I, F, I, P]),

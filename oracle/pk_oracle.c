@@ -669,6 +669,60 @@ void orc_layer_norm_quantize(const uint16_t* x, const uint16_t* gamma, const uin
     }
 }
 
+/* LayerNorm pair (encoder.cu:128-209): first = f16(LN(x; w1, b1)) into out;
+ * second = f16(LN(first; w2, b2)) into next_out as fp16 (inverse_scale == 0)
+ * or as e4m3(second * inverse_scale) bytes.  Both statistics in the
+ * reduction shape of orc_layer_norm_quantize (the reference's second LN sums
+ * a thread's four rounded first values in feature order, :181-184).  Rows >=
+ * valid_rows are zeros in both outputs.  next_out holds rows x 1024 uint16
+ * (fp16) or uint8 (e4m3) codes. */
+static void ln_row(const float* x, const uint16_t* gamma, const uint16_t* beta, float epsilon, uint16_t* h) {
+    float partial[256];
+    for (int t = 0; t < 256; ++t) {
+        float s = 0.0f;
+        for (int item = 0; item < 4; ++item) s += x[t + item * 256];
+        partial[t] = s;
+    }
+    const float mean = tree_sum_256(partial) / 1024.0f;
+    for (int t = 0; t < 256; ++t) {
+        float s = 0.0f;
+        for (int item = 0; item < 4; ++item) {
+            const float d = x[t + item * 256] - mean;
+            s += d * d;
+        }
+        partial[t] = s;
+    }
+    const float inverse_std = 1.0f / sqrtf(tree_sum_256(partial) / 1024.0f + epsilon);
+    for (int i = 0; i < 1024; ++i)
+        h[i] = orc_f32_to_f16((x[i] - mean) * inverse_std * orc_f16_to_f32(gamma[i]) + orc_f16_to_f32(beta[i]));
+}
+
+void orc_layer_norm_pair(const uint16_t* x, const uint16_t* w1, const uint16_t* b1, const uint16_t* w2,
+                         const uint16_t* b2, int rows, int valid_rows, float epsilon, float inverse_scale,
+                         uint16_t* out, void* next_out) {
+    for (int r = 0; r < rows; ++r) {
+        uint16_t* first = out + (size_t)r * 1024;
+        if (r >= valid_rows) {
+            memset(first, 0, 2048);
+            memset((uint8_t*)next_out + (size_t)r * (inverse_scale != 0.0f ? 1024 : 2048), 0,
+                   inverse_scale != 0.0f ? 1024 : 2048);
+            continue;
+        }
+        float v[1024];
+        uint16_t second[1024];
+        for (int i = 0; i < 1024; ++i) v[i] = orc_f16_to_f32(x[(size_t)r * 1024 + i]);
+        ln_row(v, w1, b1, epsilon, first);
+        for (int i = 0; i < 1024; ++i) v[i] = orc_f16_to_f32(first[i]);
+        ln_row(v, w2, b2, epsilon, second);
+        if (inverse_scale != 0.0f) {
+            uint8_t* q = (uint8_t*)next_out + (size_t)r * 1024;
+            for (int i = 0; i < 1024; ++i) q[i] = orc_f32_to_e4m3(orc_f16_to_f32(second[i]) * inverse_scale);
+        } else {
+            memcpy((uint16_t*)next_out + (size_t)r * 1024, second, 2048);
+        }
+    }
+}
+
 /* 2:4 compression of FP8 activations (encoder.cu:685-704, epilogue 7 at
  * :1037-1053): in each quartet keep the two largest |e4m3| (bits & 127), ties
  * to the lower index, in index order.  data is [rows x k/2]; meta is

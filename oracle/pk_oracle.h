@@ -60,6 +60,9 @@ void orc_quantize_int4_rows(const uint16_t* x, int rows, int valid_rows, int k, 
 void orc_layer_norm_quantize(const uint16_t* x, const uint16_t* gamma, const uint16_t* beta,
                              int rows, int valid_rows, int k, float epsilon, int int4,
                              uint8_t* q, float* scales, uint16_t* normalized);
+void orc_layer_norm_pair(const uint16_t* x, const uint16_t* w1, const uint16_t* b1, const uint16_t* w2,
+                         const uint16_t* b2, int rows, int valid_rows, float epsilon, float inverse_scale,
+                         uint16_t* out, void* next_out);
 void orc_compress_24(const uint8_t* x, int rows, int k, uint8_t* data, uint8_t* meta);
 void orc_compress_24_i8_exact(const int8_t* x, int rows, int k, uint8_t* data, uint8_t* meta, uint32_t* counts, uint32_t* ovf);
 void orc_residual_24_i8(const int8_t* x, const uint8_t* meta, int rows, int k, uint8_t* data2, uint8_t* meta2);

@@ -66,6 +66,7 @@ def _declare(l):
         "orc_quantize_int8_rows": (None, [P, I, I, I, P, P]),
         "orc_quantize_int4_rows": (None, [P, I, I, I, P, P]),
         "orc_layer_norm_quantize": (None, [P, P, P, I, I, I, F, I, P, P, P]),
+        "orc_layer_norm_pair": (None, [P, P, P, P, P, I, I, F, F, P, P]),
         "orc_compress_24_i8_exact": (None, [P, I, I, P, P, P, P]),
         "orc_residual_24_i8": (None, [P, P, I, I, P, P]),
         "orc_compress_24": (None, [P, I, I, P, P]),
@@ -322,6 +323,20 @@ def layer_norm_quantize(x16, gamma16, beta16, epsilon=1e-5, int4=False, valid_ro
                                   m if valid_rows is None else valid_rows, k, epsilon,
                                   1 if int4 else 0, _p(q), _p(s), _p(normalized))
     return q, s, normalized
+
+
+def layer_norm_pair(x16, w1, b1, w2, b2, epsilon=1e-5, inverse_scale=0.0, valid_rows=None):
+    """LayerNorm pair (encoder.cu:128-209): returns (first fp16 [m x 1024],
+    second as fp16 [m x 1024] or e4m3 bytes when inverse_scale != 0)."""
+    x16 = _h(x16)
+    m, k = x16.shape
+    assert k == 1024
+    out = np.empty((m, k), np.float16)
+    nxt = np.empty((m, k), np.uint8 if inverse_scale != 0.0 else np.float16)
+    lib().orc_layer_norm_pair(_p(x16), _p(_h(w1)), _p(_h(b1)), _p(_h(w2)), _p(_h(b2)), m,
+                              m if valid_rows is None else valid_rows, epsilon, inverse_scale,
+                              _p(out), _p(nxt))
+    return out, nxt
 
 
 def compress_24(x8: np.ndarray):

@@ -499,3 +499,53 @@ def test_tdt_decode_composition(oracle):
     h1, _ = oracle.lstm_step(lstm[4], lstm[5], lstm[6], lstm[7], h0, z, z)
     ref = proj[0].astype(np.float64) @ h1.astype(np.float64) + proj[1]
     assert np.allclose(pred, ref, atol=1e-5)
+
+
+def _ln64(x, g, b, eps=1e-5):
+    x = np.asarray(x, np.float64)
+    mean = x.mean(axis=1, keepdims=True)
+    var = ((x - mean) ** 2).mean(axis=1, keepdims=True)
+    return (x - mean) / np.sqrt(var + eps) * np.asarray(g, np.float64) + np.asarray(b, np.float64)
+
+
+def _f16_ulp(v):
+    a = np.maximum(np.abs(np.asarray(v, np.float64)), 2.0 ** -14)
+    return 2.0 ** (np.floor(np.log2(a)) - 10)
+
+
+@pytest.mark.parametrize("inverse_scale", [0.0, 56.0])
+def test_layer_norm_pair_matches_float64(oracle, inverse_scale):
+    """encoder.cu:128-209: the first output is the float64 LayerNorm of x
+    rounded to fp16 (within one fp16 ulp; the fp32 statistics may move a
+    rounding boundary), the second the float64 LayerNorm of the *rounded*
+    first output with the next layer's parameters; the e4m3 form is
+    torch's e4m3 of fp16(second) * 56.  The first output also equals the
+    normalized output of the single LayerNorm producer bit for bit, and
+    padding rows are zero in both outputs."""
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(21)
+    x = (rng.standard_normal((9, 1024)) * 2.5 + 0.7).astype(np.float16)
+    g1 = rng.uniform(0.5, 1.5, 1024).astype(np.float16)
+    b1 = (rng.standard_normal(1024) * 0.1).astype(np.float16)
+    g2 = rng.uniform(0.2, 2.0, 1024).astype(np.float16)
+    b2 = (rng.standard_normal(1024) * 0.3).astype(np.float16)
+    first, second = oracle.layer_norm_pair(x, g1, b1, g2, b2, 1e-5, inverse_scale, valid_rows=7)
+    ref1 = _ln64(x[:7], g1, b1)
+    f1 = first[:7].astype(np.float64)
+    assert np.all(np.abs(f1 - ref1) <= _f16_ulp(ref1))
+    assert np.mean(f1 == ref1.astype(np.float16)) > 0.99
+    _, _, normalized = oracle.layer_norm_quantize(x, g1, b1, 1e-5, valid_rows=7)
+    assert np.array_equal(first.view(np.uint16), normalized.view(np.uint16))
+    ref2 = _ln64(f1, g2, b2)
+    sec16 = oracle.layer_norm_pair(x, g1, b1, g2, b2, 1e-5, 0.0, valid_rows=7)[1]
+    s2 = sec16[:7].astype(np.float64)
+    assert np.all(np.abs(s2 - ref2) <= _f16_ulp(ref2))
+    assert np.mean(s2 == ref2.astype(np.float16)) > 0.99
+    # the second LayerNorm must not run on x itself
+    assert np.max(np.abs(s2 - _ln64(x[:7], g2, b2))) > 1e-2
+    if inverse_scale:
+        want = torch.from_numpy(np.clip(sec16[:7].astype(np.float32) * np.float32(56.0), -448, 448))
+        assert np.array_equal(second[:7], want.to(torch.float8_e4m3fn).view(torch.uint8).numpy())
+    else:
+        assert np.array_equal(second.view(np.uint16), sec16.view(np.uint16))
+    assert not first[7:].view(np.uint16).any() and not np.asarray(second[7:]).view(np.uint8).any()
