@@ -120,6 +120,247 @@ class Stack:
                 self.linear(layer, idx, stream)
 
 
+class RefPlanStack:
+    """The reference's own precision plan for T >= 1040 (pipeline.rs:13-17,
+    the per-layer sequence of encoder.rs run_layer), 24 layers at T frames:
+
+    FF1   e4m3 x56 input from the previous layer's LayerNorm pair, FP8 expand
+          at the fixed scale 8/448 with the packed x16 e4m3 output
+          (pk_ffn_expand_fp8_packed), request-time FP8 packing of the contract
+          weight (pk_quantize_ffn_contract), FP8 contract at 1/16 with
+          out += 0.5 Y (pk_ffn_contract_fp8)                 encoder.rs:960-1008
+    QKV   LayerNorm -> dynamic per-row FP8, FP8 QKV 1024 -> 3072 to fp16 (the
+          reference's fp16 cuBLAS QKV, a fused FP8 GEMM here)
+    out   request-time FP8 o_proj (pk_quantize_rows1024), o_proj on the e4m3
+          x28 attention context, out += Y (pk_attention_output_fp8)
+    conv  LayerNorm -> dynamic FP8, request-time pw1 / pw2 packing, pointwise 1
+          + GLU (pk_conv_glu_fp8), per-row FP8 of the depthwise output
+          (pk_quantize_rows1024), pointwise 2 with out += Y
+          (pk_conv_residual_fp8)                             encoder.rs:1471-1560
+    FF2   LayerNorm -> dynamic INT4, s4 x s4 expand with SiLU x16 e4m3 and 2:4
+          compression (pk_ffn_expand_int4_sparse), request-time FP8 contract
+          weight, sparse FP8 contract on v_smfmac (pk_ffn_contract_fp8_sparse)
+                                                             encoder.rs:1015-1081
+    norm  LayerNorm pair: this layer's norm_out and the next layer's norm_ff1
+          with the e4m3 x56 output (pk_layer_norm_pair)      encoder.rs:1093-1115
+
+    The attention core and the depthwise convolution are outside the linear
+    path: their outputs are synthetic buffers of the right shape and format.
+    Weights are random-init fp16 ~N(0, 0.02) with the real shapes, packed by
+    the library's load-time packers (FF1 expand FP8, QKV FP8, FF2 expand
+    per-row INT4) or kept fp16 for the request-time packers, as the reference
+    keeps them.  `gemm_step` runs the eight linears of each layer only (the
+    same 1.1576 GFLOP per frame as the mixed stack, the sparse contract counted
+    dense-equivalent); `step` adds the activation producers and the
+    request-time weight packing."""
+
+    def __init__(self, pk, torch, t_frames):
+        self.pk, self.torch, self.t = pk, torch, t_frames
+        dev = "cuda"
+        g = torch.Generator(device=dev)
+        g.manual_seed(4321)
+        t = t_frames
+        w16 = lambda n, k: (torch.randn((n, k), generator=g, device=dev) * 0.02).half()
+        ln = lambda: ((torch.rand(D, generator=g, device=dev) + 0.5).half(), (torch.randn(D, generator=g, device=dev) * 0.1).half())
+        self.layers = []
+        for _ in range(LAYERS):
+            L = {}
+            L["ff1_e"] = torch.empty((FF, D), dtype=torch.uint8, device=dev)
+            L["ff1_es"] = torch.empty(FF, dtype=torch.float32, device=dev)
+            pk.call("pk_pack_fp8_rows", w16(FF, D), FF, D, L["ff1_e"], L["ff1_es"])
+            L["ff1_c16"] = w16(D, FF)
+            L["qkv"] = torch.empty((3 * D, D), dtype=torch.uint8, device=dev)
+            L["qkv_s"] = torch.empty(3 * D, dtype=torch.float32, device=dev)
+            pk.call("pk_pack_fp8_rows", w16(3 * D, D), 3 * D, D, L["qkv"], L["qkv_s"])
+            L["o16"] = w16(D, D)
+            L["pw1_16"] = w16(CONV, D)
+            L["pw2_16"] = w16(D, D)
+            L["ff2_e"] = torch.empty((FF, D // 2), dtype=torch.uint8, device=dev)
+            L["ff2_es"] = torch.empty(FF, dtype=torch.float32, device=dev)
+            pk.call("pk_pack_int4_rows", w16(FF, D), FF, D, L["ff2_e"], L["ff2_es"])
+            L["ff2_c16"] = w16(D, FF)
+            L["n_att"], L["n_conv"], L["n_ff2"], L["n_out"], L["n_ff1"] = (ln() for _ in range(5))
+            self.layers.append(L)
+        # request-time packed weights: one arena reused by every layer (the
+        # reference writes them into dead activation arenas, encoder.rs:1138-1157)
+        self.wc = torch.empty((D, FF), dtype=torch.uint8, device=dev)
+        self.wc_s = torch.empty(D, dtype=torch.float32, device=dev)
+        self.wo = torch.empty((CONV, D), dtype=torch.uint8, device=dev)
+        self.wo_s = torch.empty(CONV, dtype=torch.float32, device=dev)
+        # FF contract weights packed once, for gemm_step (the GEMMs without the
+        # request-time packers)
+        self.pre = []
+        for L in self.layers:
+            c1 = torch.empty((D, FF), dtype=torch.uint8, device=dev)
+            c1s = torch.empty(D, dtype=torch.float32, device=dev)
+            pk.call("pk_quantize_ffn_contract", L["ff1_c16"], c1, c1s)
+            c2 = torch.empty((D, FF), dtype=torch.uint8, device=dev)
+            c2s = torch.empty(D, dtype=torch.float32, device=dev)
+            pk.call("pk_quantize_ffn_contract", L["ff2_c16"], c2, c2s)
+            o = torch.empty((D, D), dtype=torch.uint8, device=dev)
+            os_ = torch.empty(D, dtype=torch.float32, device=dev)
+            pk.call("pk_quantize_rows1024", L["o16"], o, os_, D)
+            p1 = torch.empty((CONV, D), dtype=torch.uint8, device=dev)
+            p1s = torch.empty(CONV, dtype=torch.float32, device=dev)
+            pk.call("pk_quantize_rows1024", L["pw1_16"], p1, p1s, CONV)
+            p2 = torch.empty((D, D), dtype=torch.uint8, device=dev)
+            p2s = torch.empty(D, dtype=torch.float32, device=dev)
+            pk.call("pk_quantize_rows1024", L["pw2_16"], p2, p2s, D)
+            self.pre.append({"c1": (c1, c1s), "c2": (c2, c2s), "o": (o, os_), "p1": (p1, p1s), "p2": (p2, p2s)})
+        # activations
+        self.state = torch.randn((t, D), generator=g, device=dev).half()
+        self.normed = torch.empty((t, D), dtype=torch.float16, device=dev)
+        self.x8 = torch.empty((t, D), dtype=torch.uint8, device=dev)       # e4m3 FF1 input (x56) / dynamic FP8
+        self.xs = torch.empty(t, dtype=torch.float32, device=dev)
+        self.x4 = torch.empty((t, D // 2), dtype=torch.uint8, device=dev)  # INT4 FF2 input
+        self.h8 = torch.empty((t, FF), dtype=torch.uint8, device=dev)      # x16 e4m3 FF1 hidden
+        self.sp = torch.empty(t * (FF // 2 + FF // 8), dtype=torch.uint8, device=dev)  # 2:4 FF2 hidden
+        self.qkv = torch.empty((t, 3 * D), dtype=torch.float16, device=dev)
+        ctx = (torch.randn((t, D), generator=g, device=dev) * 0.5).half()
+        self.ctx8 = torch.empty((t, D), dtype=torch.uint8, device=dev)     # attention context e4m3 x28
+        pk.call("pk_quantize_fp8_fixed", ctx, self.ctx8, t * D, 28.0)
+        self.glu = torch.empty((t, D), dtype=torch.float16, device=dev)
+        self.dw = torch.randn((t, D), generator=g, device=dev).half()      # depthwise conv output stand-in
+        self.dw8 = torch.empty((t, D), dtype=torch.uint8, device=dev)
+        self.dws = torch.empty(t, dtype=torch.float32, device=dev)
+        # the first layer's FF1 input: the LayerNorm pair of layer "-1"
+        L0 = self.layers[0]
+        pk.call("pk_layer_norm_pair", self.state, *L0["n_out"], self.normed, *L0["n_ff1"], self.x8, t, t, 1e-5,
+                448.0 / 8.0)
+        torch.cuda.synchronize()
+
+    def gemms(self, i, stream=None, request_time=False):
+        """Layer i's eight linears; with request_time, also the producers and
+        the request-time weight packing, in the reference's order."""
+        pk, t, L, P = self.pk, self.t, self.layers[i], self.pre[i]
+        c = lambda *a: pk.call(*a, stream=stream)
+        inv56 = 448.0 / 8.0
+        # FF1 (its input x8 = e4m3 x56 from the previous LayerNorm pair)
+        c("pk_ffn_expand_fp8_packed", self.x8, L["ff1_e"], L["ff1_es"], None, self.h8, t, 8.0 / 448.0, 0)
+        if request_time:
+            c("pk_quantize_ffn_contract", L["ff1_c16"], self.wc, self.wc_s)
+            c("pk_ffn_contract_fp8", self.h8, self.wc, self.wc_s, self.state, t)
+        else:
+            c("pk_ffn_contract_fp8", self.h8, *P["c1"], self.state, t)
+        # attention: QKV on LN -> dynamic FP8, o_proj on the e4m3 x28 context
+        if request_time:
+            c("pk_layer_norm_quantize_fp8_dynamic", self.state, *L["n_att"], self.x8, self.xs, t, t, 1e-5)
+        pk.gemm(pk.FMT_FP8, pk.EPI_F16, self.x8, L["qkv"], t, 3 * D, D, self.qkv, w_scales=L["qkv_s"],
+                row_scales=self.xs, stream=stream)
+        if request_time:
+            c("pk_quantize_rows1024", L["o16"], self.wo, self.wo_s, D)
+            c("pk_attention_output_fp8", self.ctx8, self.wo, self.wo_s, self.state, t)
+        else:
+            c("pk_attention_output_fp8", self.ctx8, *P["o"], self.state, t)
+        # conv module
+        if request_time:
+            c("pk_layer_norm_quantize_fp8_dynamic", self.state, *L["n_conv"], self.x8, self.xs, t, t, 1e-5)
+            c("pk_quantize_rows1024", L["pw1_16"], self.wo, self.wo_s, CONV)
+            c("pk_conv_glu_fp8", self.x8, self.wo, self.wo_s, self.xs, self.glu, t, t)
+            c("pk_quantize_rows1024", self.dw, self.dw8, self.dws, t)
+            c("pk_quantize_rows1024", L["pw2_16"], self.wo, self.wo_s, D)
+            c("pk_conv_residual_fp8", self.dw8, self.wo, self.wo_s, self.dws, self.state, t)
+        else:
+            c("pk_conv_glu_fp8", self.x8, *P["p1"], self.xs, self.glu, t, t)
+            c("pk_conv_residual_fp8", self.dw8, *P["p2"], self.dws, self.state, t)
+        # FF2: LN -> INT4, s4 expand with 2:4, sparse FP8 contract
+        if request_time:
+            c("pk_layer_norm_quantize_int4_dynamic", self.state, *L["n_ff2"], self.x4, self.xs, t, t, 1e-5)
+        c("pk_ffn_expand_int4_sparse", self.x4, L["ff2_e"], L["ff2_es"], self.xs, self.sp, t, 1.0, 1)
+        if request_time:
+            c("pk_quantize_ffn_contract", L["ff2_c16"], self.wc, self.wc_s)
+            c("pk_ffn_contract_fp8_sparse", self.sp, self.wc, self.wc_s, self.state, t, FF)
+        else:
+            c("pk_ffn_contract_fp8_sparse", self.sp, *P["c2"], self.state, t, FF)
+        # LayerNorm pair: norm_out of this layer, norm_ff1 of the next -> e4m3 x56
+        if request_time:
+            nxt = self.layers[(i + 1) % LAYERS]
+            c("pk_layer_norm_pair", self.state, *L["n_out"], self.normed, *nxt["n_ff1"], self.x8, t, t, 1e-5, inv56)
+
+    def gemm_step(self, stream=None):
+        for i in range(LAYERS):
+            self.gemms(i, stream)
+
+    def step(self, stream=None):
+        for i in range(LAYERS):
+            self.gemms(i, stream, request_time=True)
+
+    def classes(self, stream, reps=3):
+        """Average launch time of each of a layer's eight linears over the 24
+        layers (each class's 24 launches back to back `reps` times)."""
+        pk, t = self.pk, self.t
+        torch = self.torch
+        spec = [
+            ("ff1_expand_fp8_packed", 2.0 * t * FF * D,
+             lambda i: pk.call("pk_ffn_expand_fp8_packed", self.x8, self.layers[i]["ff1_e"], self.layers[i]["ff1_es"],
+                               None, self.h8, t, 8.0 / 448.0, 0, stream=stream)),
+            ("ff1_contract_fp8", 2.0 * t * D * FF,
+             lambda i: pk.call("pk_ffn_contract_fp8", self.h8, *self.pre[i]["c1"], self.state, t, stream=stream)),
+            ("qkv_fp8_dyn", 2.0 * t * 3 * D * D,
+             lambda i: pk.gemm(pk.FMT_FP8, pk.EPI_F16, self.x8, self.layers[i]["qkv"], t, 3 * D, D, self.qkv,
+                               w_scales=self.layers[i]["qkv_s"], row_scales=self.xs, stream=stream)),
+            ("attention_output_fp8", 2.0 * t * D * D,
+             lambda i: pk.call("pk_attention_output_fp8", self.ctx8, *self.pre[i]["o"], self.state, t, stream=stream)),
+            ("conv_glu_fp8", 2.0 * t * CONV * D,
+             lambda i: pk.call("pk_conv_glu_fp8", self.x8, *self.pre[i]["p1"], self.xs, self.glu, t, t, stream=stream)),
+            ("conv_residual_fp8", 2.0 * t * D * D,
+             lambda i: pk.call("pk_conv_residual_fp8", self.dw8, *self.pre[i]["p2"], self.dws, self.state, t,
+                               stream=stream)),
+            ("ffn_expand_int4_sparse", 2.0 * t * FF * D,
+             lambda i: pk.call("pk_ffn_expand_int4_sparse", self.x4, self.layers[i]["ff2_e"], self.layers[i]["ff2_es"],
+                               self.xs, self.sp, t, 1.0, 1, stream=stream)),
+            ("ffn_contract_fp8_sparse", 2.0 * t * D * FF,
+             lambda i: pk.call("pk_ffn_contract_fp8_sparse", self.sp, *self.pre[i]["c2"], self.state, t, FF,
+                               stream=stream)),
+        ]
+        out = []
+        for name, flops, fn in spec:
+            run = lambda: [fn(i) for i in range(LAYERS)]
+            run()
+            ms = time_events(torch, run, reps, stream) / LAYERS
+            out.append({"linear": name, "avg_ms": round(ms, 4), "step_ms": round(ms * LAYERS, 3),
+                        "TOPS": round(flops / (ms * 1e-3) / 1e12, 1)})
+        out.sort(key=lambda e: -e["step_ms"])
+        return out
+
+
+def refplan_bench(pk, torch, t, stream, steps=5):
+    """The reference-plan stack: GEMM-only and full (producers + request-time
+    weight packing) step times, per-linear classes, a finite-output check."""
+    rp = RefPlanStack(pk, torch, t)
+    rp.step(stream)  # every activation buffer written once
+    rp.gemm_step(stream)
+    torch.cuda.synchronize()
+    gemm_ms = time_events(torch, lambda: rp.gemm_step(stream), steps, stream)
+    full_ms = time_events(torch, lambda: rp.step(stream), steps, stream)
+    finite = bool(torch.isfinite(rp.state.float()).all().item())
+    classes = rp.classes(stream)
+    flops = FLOP_PER_FRAME * t
+    top = classes[0]
+    dom_flops = {"ff1_expand_fp8_packed": FF * D, "ff1_contract_fp8": D * FF, "qkv_fp8_dyn": 3 * D * D,
+                 "attention_output_fp8": D * D, "conv_glu_fp8": CONV * D, "conv_residual_fp8": D * D,
+                 "ffn_expand_int4_sparse": FF * D, "ffn_contract_fp8_sparse": D * FF}[top["linear"]] * 2.0 * t
+    achieved = dom_flops / (top["avg_ms"] * 1e-3) / 1e12
+    del rp
+    torch.cuda.empty_cache()
+    return {"plan": "pipeline.rs:13-17: FF1 FP8 fixed scale (x56 in, x16 e4m3 hidden), FF2 INT4 x INT4 expand with "
+                    "2:4 e4m3 output and the v_smfmac FP8 sparse contract, FP8 QKV / attention-out / pointwise, "
+                    "request-time FP8 packing of contract / o_proj / pointwise weights",
+            "frames": t, "gemm_ms_per_step": round(gemm_ms, 3),
+            "gemm_TOPS_dense_equivalent": round(flops / (gemm_ms * 1e-3) / 1e12, 2),
+            "gemm_pct_peak": round(100.0 * flops / (gemm_ms * 1e-3) / 1e12 / PEAK["fp8"], 2),
+            "step_ms_with_producers": round(full_ms, 3),
+            "step_TOPS_with_producers": round(flops / (full_ms * 1e-3) / 1e12, 2),
+            "flop_per_step_dense_equivalent": flops,
+            "note": "the FF2 contract's work counted dense-equivalent (2:4 halves its MACs); attention core and "
+                    "depthwise conv are synthetic stand-ins outside the linear path",
+            "outputs_finite": finite, "classes": classes,
+            "roofline": {"kernel": top["linear"], "bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK["fp8"],
+                         "unit": "TFLOP/s", "frac": round(achieved / PEAK["fp8"], 4), "avg_ms": top["avg_ms"],
+                         "flop_per_launch": dom_flops,
+                         "note": "dense-equivalent (2:4 halves the MACs)" if top["linear"] == "ffn_contract_fp8_sparse" else ""}}
+
+
 FMT_ID = {"fp8": 0, "int8": 1, "int4g128": 3}  # pk_gemm formats
 EPI_NAME = {"f8": "EPI_F8 (e4m3 SiLU)", "f16": "EPI_F16", "res": "EPI_F16_RES (fp16 + residual)"}
 
@@ -232,11 +473,22 @@ def verify_stack(pk, torch, stack, rows=64):
                 got = stack.out16.view(-1)[:t * n].view(t, n)[idx].double()
             else:
                 half = LINEARS[li][3] == "res_half"
-                got = stack.state[idx].double() - before
+                after = stack.state[idx].double()
                 ref = ref * (0.5 if half else 1.0)
+                # the stated form: max|err| <= 1e-2 * RMS of the output (residual + update)
+                want = before + ref
+                err = (after - want).abs().max().item() / want.pow(2).mean().sqrt().item()
+                # and the update alone within 2e-2 of its own RMS
+                upd = (after - before - ref).abs().max().item() / ref.pow(2).mean().sqrt().item()
+                ok = err <= 1e-2 and upd <= 2e-2
+                report.append({"format": fmt, "epilogue": kind, "n": n, "k": k, "rows": int(idx.numel()),
+                               "err": round(err, 6), "err_update": round(upd, 6), "ok": bool(ok)})
+                if not ok:
+                    raise SystemExit(f"bench sample check failed: {report[-1]}")
+                continue
             rms = ref.pow(2).mean().sqrt().item()
             err = (got - ref).abs().max().item() / rms
-            ok = err <= (2e-2 if kind == "res" else 1e-2)
+            ok = err <= 1e-2
         report.append({"format": fmt, "epilogue": kind, "n": n, "k": k, "rows": int(idx.numel()),
                        "err": round(err, 6), "ok": bool(ok)})
         if not ok:
@@ -958,6 +1210,8 @@ def main():
     ap.add_argument("--hipblaslt", action="store_true",
                     help="yardstick: hipBLASLt (torch._scaled_mm) against this library's FP8 kernels on the stack's shapes")
     ap.add_argument("--only-configs", action="store_true", help="run only the BASELINE config 1-4 measurements")
+    ap.add_argument("--only-refplan", action="store_true",
+                    help="run only the reference-plan stack (pipeline.rs precision plan) measurements")
     ap.add_argument("--only-stack", action="store_true",
                     help="run only the 24-layer stack (warmup + steps, no other measurement), for rocprofv3 passes")
     args = ap.parse_args()
@@ -1011,6 +1265,9 @@ def main():
     if args.only_configs:
         print(json.dumps(config_results(pk, torch, stream)), flush=True)
         return
+    if args.only_refplan:
+        print(json.dumps(refplan_bench(pk, torch, args.frames, stream, steps=args.steps)), flush=True)
+        return
     plan = format_plan()
     print(f"[bench] building stack T={args.frames}", file=sys.stderr, flush=True)
     stack = Stack(pk, torch, args.frames, plan)
@@ -1058,6 +1315,7 @@ def main():
     decode = decode_bench(pk, torch, stream, args.frames)
     attention = attention_bench(pk, torch, stream, args.frames)
     configs = config_results(pk, torch, stream)
+    refplan = refplan_bench(pk, torch, args.frames, stream)
     cpu = None if args.no_cpu else cpu_baseline(plan)
 
     audio_min = args.frames * 0.08 / 60.0
@@ -1103,6 +1361,7 @@ def main():
                                         "achieved": round(f_tflops, 2), "frac": round(f_tflops / PEAK["fp8"], 4),
                                         "avg_ms": round(f_ms, 4), "algorithmic_bytes": f_bytes,
                                         "traffic": measured_traffic(("fp8", "f8", FF, D))}},
+        "reference_plan_stack": refplan,
         "stack_classes": classes,
         "sample_check": check,
         "producers": dict(producers, stack_with_producers_ms=round(ms_step + producers["ms_per_step"], 3),

@@ -397,9 +397,10 @@ def test_residual_linears(pk, orc, name):
         pk.call(name, dev(xq), dev(wq), dev(ws), out, rows)
         mode = 2 if name == "pk_ffn_contract_fp8" else 6
         ref = orc.epilogue(orc.gemm_e4m3(xq, wq), mode, ws, in_scale=in_scale, residual=residual)
+    assert_close(host(out).astype(np.float32), ref.astype(np.float32))  # 1e-2 * RMS(output)
     delta_ref = ref.astype(np.float32) - residual.astype(np.float32)
     delta_got = host(out).astype(np.float32) - residual.astype(np.float32)
-    assert_close(delta_got, delta_ref, tol=2e-2)
+    assert_close(delta_got, delta_ref, tol=2e-2)  # the update alone
 
 
 # ---- FP16 ------------------------------------------------------------------------------
@@ -654,9 +655,10 @@ def test_ffn_contract_fp8_sparse(pk, orc):
     pk.call("pk_ffn_contract_fp8_sparse", dev(buf), dev(wq), dev(ws), out, rows, 4096)
     ref = orc.epilogue(orc.gemm_e4m3(orc.decompress_24(data, meta), wq), 8, ws, in_scale=1.0 / 16.0,
                        residual=residual)
+    assert_close(host(out).astype(np.float32), ref.astype(np.float32))  # 1e-2 * RMS(output)
     delta_ref = ref.astype(np.float32) - residual.astype(np.float32)
     delta_got = host(out).astype(np.float32) - residual.astype(np.float32)
-    assert_close(delta_got, delta_ref, tol=2e-2)
+    assert_close(delta_got, delta_ref, tol=2e-2)  # the update alone
 
 
 @pytest.mark.parametrize("int8", [False, True])
