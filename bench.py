@@ -138,8 +138,12 @@ class RefPlanStack:
           (pk_quantize_rows1024), pointwise 2 with out += Y
           (pk_conv_residual_fp8)                             encoder.rs:1471-1560
     FF2   LayerNorm -> dynamic INT4, s4 x s4 expand with SiLU x16 e4m3 and 2:4
-          compression (pk_ffn_expand_int4_sparse), request-time FP8 contract
-          weight, sparse FP8 contract on v_smfmac (pk_ffn_contract_fp8_sparse)
+          compression, request-time FP8 contract weight, sparse FP8 contract
+          on v_smfmac (pk_ffn_contract_fp8_sparse); the INT4 codes of the
+          activations and of the weights are kept as int8 bytes, the operand
+          the INT8 MFMA reads (pk_layer_norm_quantize_int4_codes,
+          pk_unpack_int4 at load time, pk_ffn_expand_int4_sparse_codes: the
+          same accumulators and output bytes as the nibble-pair entry points)
                                                              encoder.rs:1015-1081
     norm  LayerNorm pair: this layer's norm_out and the next layer's norm_ff1
           with the e4m3 x56 output (pk_layer_norm_pair)      encoder.rs:1093-1115
@@ -178,6 +182,9 @@ class RefPlanStack:
             L["ff2_e"] = torch.empty((FF, D // 2), dtype=torch.uint8, device=dev)
             L["ff2_es"] = torch.empty(FF, dtype=torch.float32, device=dev)
             pk.call("pk_pack_int4_rows", w16(FF, D), FF, D, L["ff2_e"], L["ff2_es"])
+            # the operand form (int8 codes) derived at load time
+            L["ff2_ec"] = torch.empty((FF, D), dtype=torch.int8, device=dev)
+            pk.call("pk_unpack_int4", L["ff2_e"], L["ff2_ec"], FF * D)
             L["ff2_c16"] = w16(D, FF)
             L["n_att"], L["n_conv"], L["n_ff2"], L["n_out"], L["n_ff1"] = (ln() for _ in range(5))
             self.layers.append(L)
@@ -212,7 +219,8 @@ class RefPlanStack:
         self.normed = torch.empty((t, D), dtype=torch.float16, device=dev)
         self.x8 = torch.empty((t, D), dtype=torch.uint8, device=dev)       # e4m3 FF1 input (x56) / dynamic FP8
         self.xs = torch.empty(t, dtype=torch.float32, device=dev)
-        self.x4 = torch.empty((t, D // 2), dtype=torch.uint8, device=dev)  # INT4 FF2 input
+        self.x4 = torch.empty((t, D // 2), dtype=torch.uint8, device=dev)  # INT4 FF2 input (nibble pairs)
+        self.x4c = torch.empty((t, D), dtype=torch.int8, device=dev)      # the same codes as int8 bytes
         self.h8 = torch.empty((t, FF), dtype=torch.uint8, device=dev)      # x16 e4m3 FF1 hidden
         self.sp = torch.empty(t * (FF // 2 + FF // 8), dtype=torch.uint8, device=dev)  # 2:4 FF2 hidden
         self.qkv = torch.empty((t, 3 * D), dtype=torch.float16, device=dev)
@@ -265,8 +273,8 @@ class RefPlanStack:
             c("pk_conv_residual_fp8", self.dw8, *P["p2"], self.dws, self.state, t)
         # FF2: LN -> INT4, s4 expand with 2:4, sparse FP8 contract
         if request_time:
-            c("pk_layer_norm_quantize_int4_dynamic", self.state, *L["n_ff2"], self.x4, self.xs, t, t, 1e-5)
-        c("pk_ffn_expand_int4_sparse", self.x4, L["ff2_e"], L["ff2_es"], self.xs, self.sp, t, 1.0, 1)
+            c("pk_layer_norm_quantize_int4_codes", self.state, *L["n_ff2"], self.x4c, self.xs, t, t, 1e-5)
+        c("pk_ffn_expand_int4_sparse_codes", self.x4c, L["ff2_ec"], L["ff2_es"], self.xs, self.sp, t, 1.0, 1)
         if request_time:
             c("pk_quantize_ffn_contract", L["ff2_c16"], self.wc, self.wc_s)
             c("pk_ffn_contract_fp8_sparse", self.sp, self.wc, self.wc_s, self.state, t, FF)
@@ -306,9 +314,9 @@ class RefPlanStack:
             ("conv_residual_fp8", 2.0 * t * D * D,
              lambda i: pk.call("pk_conv_residual_fp8", self.dw8, *self.pre[i]["p2"], self.dws, self.state, t,
                                stream=stream)),
-            ("ffn_expand_int4_sparse", 2.0 * t * FF * D,
-             lambda i: pk.call("pk_ffn_expand_int4_sparse", self.x4, self.layers[i]["ff2_e"], self.layers[i]["ff2_es"],
-                               self.xs, self.sp, t, 1.0, 1, stream=stream)),
+            ("ffn_expand_int4_sparse_codes", 2.0 * t * FF * D,
+             lambda i: pk.call("pk_ffn_expand_int4_sparse_codes", self.x4c, self.layers[i]["ff2_ec"],
+                               self.layers[i]["ff2_es"], self.xs, self.sp, t, 1.0, 1, stream=stream)),
             ("ffn_contract_fp8_sparse", 2.0 * t * D * FF,
              lambda i: pk.call("pk_ffn_contract_fp8_sparse", self.sp, *self.pre[i]["c2"], self.state, t, FF,
                                stream=stream)),
@@ -321,6 +329,13 @@ class RefPlanStack:
             out.append({"linear": name, "avg_ms": round(ms, 4), "step_ms": round(ms * LAYERS, 3),
                         "TOPS": round(flops / (ms * 1e-3) / 1e12, 1)})
         out.sort(key=lambda e: -e["step_ms"])
+        # the drop-in form (nibble pairs decoded in the K-loop), not in the step
+        run = lambda: [pk.call("pk_ffn_expand_int4_sparse", self.x4, self.layers[i]["ff2_e"], self.layers[i]["ff2_es"],
+                               self.xs, self.sp, t, 1.0, 1, stream=stream) for i in range(LAYERS)]
+        run()
+        ms = time_events(torch, run, reps, stream) / LAYERS
+        out.append({"linear": "ffn_expand_int4_sparse (nibble-pair operands, not in the step)", "avg_ms": round(ms, 4),
+                    "TOPS": round(2.0 * t * FF * D / (ms * 1e-3) / 1e12, 1)})
         return out
 
 
@@ -339,7 +354,7 @@ def refplan_bench(pk, torch, t, stream, steps=5):
     top = classes[0]
     dom_flops = {"ff1_expand_fp8_packed": FF * D, "ff1_contract_fp8": D * FF, "qkv_fp8_dyn": 3 * D * D,
                  "attention_output_fp8": D * D, "conv_glu_fp8": CONV * D, "conv_residual_fp8": D * D,
-                 "ffn_expand_int4_sparse": FF * D, "ffn_contract_fp8_sparse": D * FF}[top["linear"]] * 2.0 * t
+                 "ffn_expand_int4_sparse_codes": FF * D, "ffn_contract_fp8_sparse": D * FF}[top["linear"]] * 2.0 * t
     achieved = dom_flops / (top["avg_ms"] * 1e-3) / 1e12
     del rp
     torch.cuda.empty_cache()

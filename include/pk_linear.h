@@ -192,6 +192,19 @@ int32_t pk_layer_norm_pair(const uint16_t* input, const uint16_t* weight, const 
                            const uint16_t* next_weight, const uint16_t* next_bias, void* next_output, int32_t rows,
                            int32_t padded_rows, float epsilon, float inverse_scale, void* stream);
 
+/* The LayerNorm + dynamic INT4 producer above (same scales, same codes) with
+ * the codes written as int8 bytes [padded_rows x 1024] instead of nibble
+ * pairs: the operand form the INT8 MFMA reads (CDNA4 has no 4-bit integer
+ * MFMA), consumed by pk_ffn_expand_int4_sparse_codes.  output 4-byte aligned. */
+int32_t pk_layer_norm_quantize_int4_codes(const uint16_t* input, const uint16_t* weight, const uint16_t* bias,
+                                          int8_t* output, float* scales, int32_t rows, int32_t padded_rows,
+                                          float epsilon, void* stream);
+/* Nibble pairs (byte j = q[2j] & 15 | q[2j+1] << 4, the encoder.rs:405 order of
+ * pk_pack_int4_rows and of the INT4 producer) -> sign-extended int8 codes,
+ * `elements` codes (a multiple of 32); both pointers 16-byte aligned.  The
+ * load-time derivation of the per-row INT4 FF2 weights' operand form. */
+int32_t pk_unpack_int4(const uint8_t* packed, int8_t* codes, int64_t elements, void* stream);
+
 /* ---- linears (linear.cu) ---------------------------------------------------- */
 
 /* linear.cu:83-171 pk_sm89_fp16_linear_epilogue (+ the _m64 variant and the
@@ -275,6 +288,14 @@ int32_t pk_ffn_expand_fp8_packed(const uint8_t* input, const uint8_t* weight, co
 int32_t pk_ffn_expand_int4_sparse(const uint8_t* input, const uint8_t* weight, const float* weight_scales,
                                   const float* input_scales, uint8_t* output, int32_t rows, float input_scale,
                                   int32_t dynamic_scale, void* stream);
+/* pk_ffn_expand_int4_sparse on the operand form of the same INT4 values: int8
+ * codes [rows x 1024] (pk_layer_norm_quantize_int4_codes) x int8 codes [4096 x
+ * 1024] (pk_unpack_int4 of the per-row INT4 weights), on the INT8 MFMA with no
+ * nibble decode in the K-loop.  Same exact int32 accumulators, so the output
+ * (data + metadata, same layout) is identical to pk_ffn_expand_int4_sparse's. */
+int32_t pk_ffn_expand_int4_sparse_codes(const int8_t* input, const int8_t* weight, const float* weight_scales,
+                                        const float* input_scales, uint8_t* output, int32_t rows, float input_scale,
+                                        int32_t dynamic, void* stream);
 /* encoder.cu:1095-1103 pk_sm89_ffn_contract_fp8: FF contract 4096 -> 1024 on
  * FP8 input at scale 1/16; output (fp16 [rows x 1024]) += 0.5 * Y in place. */
 int32_t pk_ffn_contract_fp8(const uint8_t* input, const uint8_t* weight, const float* weight_scales,

@@ -184,8 +184,9 @@ int32_t pk_quantize_ffn_contract(const uint16_t* in, uint8_t* out, float* scales
     return pk_quantize_rows(0, in, out, scales, 1024, 1024, 4096, stream);
 }
 
-static int32_t ln_quantize(bool int4, const uint16_t* in, const uint16_t* w, const uint16_t* b, uint8_t* out, float* scales,
+static int32_t ln_quantize(int mode, const uint16_t* in, const uint16_t* w, const uint16_t* b, uint8_t* out, float* scales,
                            int32_t rows, int32_t padded_rows, float eps, void* stream) {
+    const bool int4 = mode == 1;
     if (rows < 0 || padded_rows < rows) { set_error("need 0 <= rows <= padded_rows"); return PK_E_SHAPE; }
     if (padded_rows && (!need(in, "input") || !need(w, "weight") || !need(b, "bias") || !need(out, "output") || !need(scales, "scales")))
         return PK_E_ARG;
@@ -193,17 +194,30 @@ static int32_t ln_quantize(bool int4, const uint16_t* in, const uint16_t* w, con
         set_error("layer_norm_quantize needs 8-byte aligned input, weight and bias and a %d-byte aligned output", int4 ? 2 : 4);
         return PK_E_ALIGN;
     }
-    launch_layer_norm_quantize(int4, in, w, b, out, scales, nullptr, rows, padded_rows, eps, STREAM);
+    launch_layer_norm_quantize(mode, in, w, b, out, scales, nullptr, rows, padded_rows, eps, STREAM);
     return check_launch("layer_norm_quantize");
 }
 
 int32_t pk_layer_norm_quantize_fp8_dynamic(const uint16_t* in, const uint16_t* w, const uint16_t* b, uint8_t* out, float* scales,
                                            int32_t rows, int32_t padded_rows, float eps, void* stream) {
-    return ln_quantize(false, in, w, b, out, scales, rows, padded_rows, eps, stream);
+    return ln_quantize(0, in, w, b, out, scales, rows, padded_rows, eps, stream);
 }
 int32_t pk_layer_norm_quantize_int4_dynamic(const uint16_t* in, const uint16_t* w, const uint16_t* b, uint8_t* out, float* scales,
                                             int32_t rows, int32_t padded_rows, float eps, void* stream) {
-    return ln_quantize(true, in, w, b, out, scales, rows, padded_rows, eps, stream);
+    return ln_quantize(1, in, w, b, out, scales, rows, padded_rows, eps, stream);
+}
+int32_t pk_layer_norm_quantize_int4_codes(const uint16_t* in, const uint16_t* w, const uint16_t* b, int8_t* out, float* scales,
+                                          int32_t rows, int32_t padded_rows, float eps, void* stream) {
+    return ln_quantize(2, in, w, b, (uint8_t*)out, scales, rows, padded_rows, eps, stream);
+}
+
+int32_t pk_unpack_int4(const uint8_t* packed, int8_t* codes, int64_t elements, void* stream) {
+    if (elements < 0 || elements % 32) { set_error("unpack_int4 needs a multiple of 32 elements (got %lld)", (long long)elements); return PK_E_SHAPE; }
+    if (elements == 0) return 0;
+    if (!need(packed, "packed") || !need(codes, "codes")) return PK_E_ARG;
+    if (((uintptr_t)packed | (uintptr_t)codes) & 15) { set_error("packed and codes must be 16-byte aligned"); return PK_E_ALIGN; }
+    launch_unpack_s4(packed, codes, (size_t)elements / 2, STREAM);
+    return check_launch("unpack_int4");
 }
 
 int32_t pk_layer_norm_pair(const uint16_t* in, const uint16_t* w, const uint16_t* b, uint16_t* out, const uint16_t* next_w,
@@ -389,6 +403,20 @@ int32_t pk_ffn_expand_int4_sparse(const uint8_t* in, const uint8_t* w, const flo
     g.in_scale = in_scale;
     g.out_meta = out + (size_t)rows * 2048;
     return launch_gemm(FMT_S4, EPI_F8_24, g, STREAM);
+}
+
+int32_t pk_ffn_expand_int4_sparse_codes(const int8_t* in, const int8_t* w, const float* ws, const float* in_scales, uint8_t* out,
+                                        int32_t rows, float in_scale, int32_t dynamic, void* stream) {
+    if (!need(in, "input") || !need(w, "weight") || !need(out, "output") || !need(ws, "weight_scales") ||
+        (dynamic && !need(in_scales, "input_scales")))
+        return PK_E_ARG;
+    if (rows < 0) { set_error("negative rows"); return PK_E_SHAPE; }
+    GemmArgs g = base_args(in, w, rows, 4096, 1024, out, 4096);
+    g.w_scales = ws;
+    g.row_scales = dynamic ? in_scales : nullptr;
+    g.in_scale = in_scale;
+    g.out_meta = out + (size_t)rows * 2048;
+    return launch_gemm(FMT_I8, EPI_F8_24, g, STREAM);
 }
 
 int32_t pk_ffn_contract_fp8(const uint8_t* in, const uint8_t* w, const float* ws, uint16_t* out, int32_t rows, void* stream) {

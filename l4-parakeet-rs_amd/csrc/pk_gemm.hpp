@@ -239,25 +239,18 @@ __device__ __forceinline__ uint32_t silu_fp8x4(float a, float b, float c, float 
 // encoder.cu:685-704: of one quartet of e4m3 bytes keep the two largest
 // magnitudes (bits & 127, ties to the lower index) in index order.  Returns
 // the two kept bytes in bits 0-15 and idx0 | idx1 << 2 in bits 16-19.
+// Branch-free: key i = magnitude << 2 | (3 - i) orders the elements by
+// magnitude, then lower index, with distinct keys; the two largest keys of
+// the four come from one max / min exchange per pair and a merge.
 __device__ __forceinline__ uint32_t compress_quartet(uint32_t packed) {
-    uint32_t d = 0, md = 0;
-    int count = 0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint32_t mi = (packed >> (8 * i)) & 127;
-        int rank = 0;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint32_t mj = (packed >> (8 * j)) & 127;
-            rank += (mj > mi) || (mj == mi && j < i);
-        }
-        if (rank < 2) {
-            d |= ((packed >> (8 * i)) & 255u) << (8 * count);
-            md |= (uint32_t)i << (2 * count);
-            ++count;
-        }
-    }
-    return d | (md << 16);
+    const uint32_t k0 = ((packed << 2) & 0x1fcu) | 3u, k1 = ((packed >> 6) & 0x1fcu) | 2u;
+    const uint32_t k2 = ((packed >> 14) & 0x1fcu) | 1u, k3 = (packed >> 22) & 0x1fcu;
+    const uint32_t a = max(k0, k1), b = min(k0, k1), c = max(k2, k3), d = min(k2, k3);
+    const uint32_t i1 = 3u - (max(a, c) & 3u), i2 = 3u - (max(min(a, c), max(b, d)) & 3u);
+    const uint32_t lo = min(i1, i2), hi = max(i1, i2);
+    // v_perm selector: byte lo, byte hi, then two zero bytes (selector 0x0c)
+    const uint32_t data = __builtin_amdgcn_perm(0u, packed, lo | (hi << 8) | 0x0c0c0000u);
+    return data | ((lo | (hi << 2)) << 16);
 }
 
 // fp16 row-block stores that write whole cache lines.  A lane holds 16

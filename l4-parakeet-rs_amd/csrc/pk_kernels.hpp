@@ -24,8 +24,10 @@ int launch_quantize_rows_sp24(const void* in, uint8_t* data, uint8_t* meta, floa
                               uint8_t* data2, uint8_t* meta2, int rows, int valid_rows, int k, hipStream_t s);
 int launch_pack_rows(int kind, const void* w, void* out, float* scales, int n, int k, hipStream_t s);
 int launch_q4k_dequant(const uint8_t* blocks, uint16_t* out, int n, int k, hipStream_t s);
+int launch_unpack_s4(const uint8_t* in, int8_t* out, size_t bytes, hipStream_t s);
 int launch_pack_g128(const void* w, uint32_t* q, uint16_t* scales, uint16_t* zeros, int n, int k, hipStream_t s);
-int launch_layer_norm_quantize(bool int4, const void* in, const void* gamma, const void* beta, void* out, float* scales,
+// mode 0: FP8, 1: INT4 nibble pairs, 2: INT4 codes as int8 bytes
+int launch_layer_norm_quantize(int mode, const void* in, const void* gamma, const void* beta, void* out, float* scales,
                                void* normalized, int rows, int padded_rows, float epsilon, hipStream_t s);
 int launch_layer_norm_pair(const void* in, const void* g1, const void* b1, void* out, const void* g2, const void* b2, void* next_out,
                            int rows, int padded_rows, float epsilon, float inverse_scale, hipStream_t s);

@@ -470,7 +470,9 @@ __device__ __forceinline__ float ln_partials_sum(const float (&part)[4], float* 
 // divisions, the others the fast paths: the maximum comes from the row's
 // extremes (x / 7 rounded is monotone in x), the quotients from div_rn and
 // the INT4 codes need no clamp (|y / scale| <= 8 (1 + 2^-23)).
-template <bool kInt4>
+// kCodes (with kInt4): the INT4 codes as int8 bytes [rows x 1024] instead of
+// nibble pairs -- the operand the INT8 MFMA consumes, which has no 4-bit form.
+template <bool kInt4, bool kCodes = false>
 __global__ __launch_bounds__(256) void layer_norm_quantize_kernel(const uint16_t* __restrict__ in, const uint16_t* __restrict__ gamma,
                                                                   const uint16_t* __restrict__ beta, uint8_t* __restrict__ out,
                                                                   float* __restrict__ scales, uint16_t* __restrict__ normalized,
@@ -496,14 +498,15 @@ __global__ __launch_bounds__(256) void layer_norm_quantize_kernel(const uint16_t
         for (int u = 0; u < 4; ++u) gb_finite = gb_finite && __builtin_isfinite(h2f(gh[u])) && __builtin_isfinite(h2f(bh[u]));
     }
     gb_finite = __syncthreads_and(gb_finite);
-    const size_t out_row = kInt4 ? 512 : 1024;
+    static_assert(kInt4 || !kCodes, "codes are an INT4 output");
+    const size_t out_row = (kInt4 && !kCodes) ? 512 : 1024;
     for (int row = blockIdx.x * 4 + wave; row < padded_rows; row += nw) {
         uint8_t* o = out + (size_t)row * out_row;
         uint16_t* nrm = normalized ? normalized + (size_t)row * 1024 : nullptr;
         if (row >= rows) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                if (kInt4) *(uint16_t*)(o + 128 * i + 2 * lane) = 0;
+                if (kInt4 && !kCodes) *(uint16_t*)(o + 128 * i + 2 * lane) = 0;
                 else *(uint32_t*)(o + 256 * i + 4 * lane) = 0u;
                 if (nrm) *(uint2*)(nrm + 256 * i + 4 * lane) = uint2{0, 0};
             }
@@ -574,8 +577,11 @@ __global__ __launch_bounds__(256) void layer_norm_quantize_kernel(const uint16_t
                 uint32_t q[4];
 #pragma unroll
                 for (int u = 0; u < 4; ++u) q[u] = fast ? rne_bits(div_rn(y[u], scale, inv)) : (uint32_t)rne_clamp(y[u] / scale, -8, 7);
-                *(uint16_t*)(o + 128 * i + 2 * lane) =
-                    (uint16_t)((q[0] & 15u) | ((q[1] & 15u) << 4) | ((q[2] & 15u) << 8) | ((q[3] & 15u) << 12));
+                if constexpr (kCodes)
+                    *(uint32_t*)(o + 256 * i + 4 * lane) = low_bytes4(q[0], q[1], q[2], q[3]);
+                else
+                    *(uint16_t*)(o + 128 * i + 2 * lane) =
+                        (uint16_t)((q[0] & 15u) | ((q[1] & 15u) << 4) | ((q[2] & 15u) << 8) | ((q[3] & 15u) << 12));
             } else {
                 const uint32_t w = fast ? e4m3x4_sat(div_rn(y[0], scale, inv), div_rn(y[1], scale, inv), div_rn(y[2], scale, inv),
                                                      div_rn(y[3], scale, inv))
@@ -681,6 +687,31 @@ __global__ __launch_bounds__(256) void layer_norm_pair_kernel(const uint16_t* __
     }
 }
 
+// Nibble pairs (byte j = q[2j] & 15 | q[2j+1] << 4, encoder.rs:405) -> signed
+// int8 codes in k order, 16 bytes in and 32 out per thread: the operand form
+// of per-row INT4 weights / activations for the INT8 MFMA.  A nibble n becomes
+// n | 0xf0 when its bit 3 is set: t = nibbles & 0x08 per byte, t * 30 = 0xf0.
+__device__ __forceinline__ uint32_t s4x4_to_s8(uint32_t nib) {
+    const uint32_t t = nib & 0x08080808u;
+    return nib | ((t << 5) - (t << 1));
+}
+__global__ __launch_bounds__(256) void unpack_s4_kernel(const uint4* __restrict__ in, uint4* __restrict__ out, size_t chunks) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= chunks) return;
+    const uint4 w = in[i];
+    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+    uint32_t o[8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        // bytes b0..b3 of word j hold k = 8j' + 2b (low) and 2b + 1 (high)
+        const uint32_t lo = s4x4_to_s8(ws[j] & 0x0f0f0f0fu), hi = s4x4_to_s8((ws[j] >> 4) & 0x0f0f0f0fu);
+        o[2 * j] = __builtin_amdgcn_perm(hi, lo, 0x05010400u);      // lo0 hi0 lo1 hi1
+        o[2 * j + 1] = __builtin_amdgcn_perm(hi, lo, 0x07030602u);  // lo2 hi2 lo3 hi3
+    }
+    out[2 * i] = uint4{o[0], o[1], o[2], o[3]};
+    out[2 * i + 1] = uint4{o[4], o[5], o[6], o[7]};
+}
+
 // ---- launchers -------------------------------------------------------------
 
 // Q4_K superblocks -> fp16 [n x k] (linear.cu:459-472): one thread per 8
@@ -760,11 +791,14 @@ int launch_pack_g128(const void* w, uint32_t* q, uint16_t* scales, uint16_t* zer
     return 0;
 }
 
-int launch_layer_norm_quantize(bool int4, const void* in, const void* gamma, const void* beta, void* out, float* scales,
+int launch_layer_norm_quantize(int mode, const void* in, const void* gamma, const void* beta, void* out, float* scales,
                                void* normalized, int rows, int padded_rows, float epsilon, hipStream_t s) {
     if (padded_rows == 0) return 0;
     const unsigned grid = row_grid(padded_rows);
-    if (int4)
+    if (mode == 2)
+        layer_norm_quantize_kernel<true, true><<<grid, 256, 0, s>>>((const uint16_t*)in, (const uint16_t*)gamma, (const uint16_t*)beta,
+                                                                    (uint8_t*)out, scales, (uint16_t*)normalized, rows, padded_rows, epsilon);
+    else if (mode == 1)
         layer_norm_quantize_kernel<true><<<grid, 256, 0, s>>>((const uint16_t*)in, (const uint16_t*)gamma, (const uint16_t*)beta,
                                                                (uint8_t*)out, scales, (uint16_t*)normalized, rows, padded_rows, epsilon);
     else
@@ -785,6 +819,13 @@ int launch_layer_norm_pair(const void* in, const void* g1, const void* b1, void*
     else
         layer_norm_pair_kernel<false><<<grid, 256, 0, s>>>(x, w1, c1, (uint16_t*)out, w2, c2, next_out, rows, padded_rows, epsilon,
                                                             inverse_scale);
+    return 0;
+}
+
+int launch_unpack_s4(const uint8_t* in, int8_t* out, size_t bytes, hipStream_t s) {
+    const size_t chunks = bytes / 16;
+    if (chunks == 0) return 0;
+    unpack_s4_kernel<<<(unsigned)((chunks + 255) / 256), 256, 0, s>>>((const uint4*)in, (uint4*)out, chunks);
     return 0;
 }
 

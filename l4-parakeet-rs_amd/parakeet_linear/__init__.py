@@ -67,6 +67,8 @@ SIGNATURES = {
     "pk_layer_norm_quantize_fp8_dynamic": (I, [P, P, P, P, P, I, I, F, P]),
     "pk_layer_norm_quantize_int4_dynamic": (I, [P, P, P, P, P, I, I, F, P]),
     "pk_layer_norm_pair": (I, [P, P, P, P, P, P, P, I, I, F, F, P]),
+    "pk_layer_norm_quantize_int4_codes": (I, [P, P, P, P, P, I, I, F, P]),
+    "pk_unpack_int4": (I, [P, P, ctypes.c_int64, P]),
     "pk_linear_fp16_epilogue": (I, [P, P, P, P, P, I, I, I, F, F, I, P]),
     "pk_linear_fp16_qkv": (I, [P, P, P, P, P, I, I, I, P]),
     "pk_linear_fp8_epilogue": (I, [P, P, P, P, P, I, I, I, F, I, P]),
@@ -81,6 +83,7 @@ SIGNATURES = {
     "pk_ffn_expand_fp8": (I, [P, P, P, P, P, I, F, I, P]),
     "pk_ffn_expand_fp8_packed": (I, [P, P, P, P, P, I, F, I, P]),
     "pk_ffn_expand_int4_sparse": (I, [P, P, P, P, P, I, F, I, P]),
+    "pk_ffn_expand_int4_sparse_codes": (I, [P, P, P, P, P, I, F, I, P]),
     "pk_ffn_contract_fp8": (I, [P, P, P, P, I, P]),
     "pk_ffn_contract_fp8_sparse": (I, [P, P, P, P, I, I, P]),
     "pk_conv_residual_fp8": (I, [P, P, P, P, P, I, P]),

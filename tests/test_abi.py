@@ -204,3 +204,12 @@ def test_argument_checks_reject_before_any_launch(lib):
     assert b"residual" in err()
     assert sc(*args[:5], 0xa0000, 0xb0008, *args[7:], 8, None) == E_ALIGN
     assert sc(0x10004, *args[1:], 8, None) == E_ALIGN
+
+
+def test_unpack_int4_rejects_bad_shapes(lib):
+    fn = lib.pk_unpack_int4
+    fn.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p]
+    fn.restype = ctypes.c_int32
+    assert fn(None, None, 0, None) == 0          # nothing to do, no GPU work
+    assert fn(None, None, 33, None) < 0          # not a multiple of 32
+    assert fn(None, None, 64, None) < 0          # missing pointers

@@ -259,3 +259,53 @@ def test_attention_output(pk, orc, t):
     pk.call("pk_attention_output_fp8", cq, w, s, state, pad)
     ref = orc.epilogue(orc.gemm_e4m3(rows_of(cq, idx), host(w)), 6, host(s), in_scale=1.0 / 28.0, residual=before)
     check_residual(rows_of(state, idx), ref, before, f"attention_output T={t}")
+
+
+# ---- FF2 on the operand form of the INT4 codes ---------------------------------------
+
+def nibbles_to_codes(packed):
+    """byte j = q[2j] & 15 | q[2j+1] << 4 -> signed codes in k order (closed form)."""
+    p = packed.astype(np.int16)
+    lo, hi = p & 15, p >> 4
+    codes = np.stack([lo, hi], axis=-1).reshape(packed.shape[0], -1)
+    return np.where(codes >= 8, codes - 16, codes).astype(np.int8)
+
+
+@pytest.mark.parametrize("t", [7500, 45000])
+def test_ff2_int4_codes_equal_packed(pk, orc, t):
+    """pk_layer_norm_quantize_int4_codes writes the codes of the packed
+    producer (same scales), pk_unpack_int4 is the closed-form sign extension,
+    and pk_ffn_expand_int4_sparse_codes on the codes writes exactly the bytes
+    pk_ffn_expand_int4_sparse writes on the nibble pairs (same int32
+    accumulators, same epilogue)."""
+    pad = padded(t) + 16
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(1700 + t)
+    x = (torch.randn((pad, D), generator=gen, device="cuda") * 2).half()
+    g, b = ln_params(gen)
+    xq = torch.empty((pad, D // 2), dtype=torch.uint8, device="cuda")
+    xs = torch.empty(pad, dtype=torch.float32, device="cuda")
+    xc = torch.full((pad, D), 5, dtype=torch.int8, device="cuda")
+    xcs = torch.empty(pad, dtype=torch.float32, device="cuda")
+    note(f"int4 codes producer T={t} padded={pad}")
+    pk.call("pk_layer_norm_quantize_int4_dynamic", x, g, b, xq, xs, t, pad, 1e-5)
+    pk.call("pk_layer_norm_quantize_int4_codes", x, g, b, xc, xcs, t, pad, 1e-5)
+    assert torch.equal(xs, xcs)
+    idx = np.union1d(sample_rows(pad, t + 5, per_strip=2), np.arange(t - 2, pad))
+    assert np.array_equal(rows_of(xc, idx), nibbles_to_codes(rows_of(xq, idx)))
+    xu = torch.empty((pad, D), dtype=torch.int8, device="cuda")
+    pk.call("pk_unpack_int4", xq, xu, pad * D)
+    assert torch.equal(xu, xc)
+    w16 = fp16_weight(FF, D, gen)
+    wq = torch.empty((FF, D // 2), dtype=torch.uint8, device="cuda")
+    ws = torch.empty(FF, dtype=torch.float32, device="cuda")
+    pk.call("pk_pack_int4_rows", w16, FF, D, wq, ws)
+    wc = torch.empty((FF, D), dtype=torch.int8, device="cuda")
+    pk.call("pk_unpack_int4", wq, wc, FF * D)
+    assert np.array_equal(host(wc), nibbles_to_codes(host(wq)))
+    a = torch.empty(pad * (FF // 2 + FF // 8), dtype=torch.uint8, device="cuda")
+    c = torch.full_like(a, 0x33)
+    note(f"ffn_expand_int4_sparse_codes T={t} tile={pk.gemm_tile(pk.FMT_I8, pk.EPI_F8_24, pad, FF)}")
+    pk.call("pk_ffn_expand_int4_sparse", xq, wq, ws, xs, a, pad, 1.0, 1)
+    pk.call("pk_ffn_expand_int4_sparse_codes", xc, wc, ws, xs, c, pad, 1.0, 1)
+    assert torch.equal(a, c)
