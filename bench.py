@@ -62,7 +62,10 @@ class Stack:
         self.x8d = self.x8[:, :D].contiguous()
         self.xid = self.xi[:, :D].contiguous()
         del src
-        self.out8 = torch.empty((t_frames, FF), dtype=torch.uint8, device=dev)
+        self.out8 = torch.empty((t_frames, FF), dtype=torch.uint8, device=dev)  # FF hidden: e4m3 x16 or INT8 x16
+        # INT4-g128 contracts read the e4m3 hidden with their weights expanded
+        # per call to e4m3 (q - z) into this buffer (pk_expand_int4_g128_e4m3)
+        self.wexp = torch.empty((D, FF), dtype=torch.uint8, device=dev)
         self.out16 = torch.empty((t_frames, 3 * D), dtype=torch.float16, device=dev)
         self.state = torch.randn((t_frames, D), generator=g, device=dev, dtype=torch.float16)
         self.weights = []
@@ -90,10 +93,32 @@ class Stack:
             self.weights.append(lw)
         torch.cuda.synchronize()
 
+    def hidden_int8(self, layer, idx):
+        """True when FF `idx`'s hidden is the static INT8 form (its contract
+        has INT8 weights), else e4m3 x16."""
+        name = LINEARS[idx][0]
+        contract = idx + 1 if name.endswith("expand") else idx
+        return self.weights[layer][contract][0] == "int8"
+
     def linear(self, layer, idx, stream=None):
         pk = self.pk
         name, n, k, epi = LINEARS[idx]
         fmt, q, s, z = self.weights[layer][idx]
+        t = self.t
+        if name.endswith("contract"):
+            # the FF contract reads the hidden its expand wrote, at scale 1/16:
+            # e4m3 for FP8 and INT4-g128 weights, static INT8 for INT8 weights
+            if fmt == "fp8":
+                pk.gemm(pk.FMT_FP8, pk.EPI_F16, self.out8, q, t, n, k, self.state, w_scales=s, in_scale=1.0 / 16,
+                        residual=self.state, out_scale=0.5, res_scale=1.0, stream=stream)
+            elif fmt == "int8":
+                pk.gemm(pk.FMT_I8, pk.EPI_F16, self.out8, q, t, n, k, self.state, w_scales=s, in_scale=1.0 / 16,
+                        residual=self.state, out_scale=0.5, res_scale=1.0, stream=stream)
+            else:
+                pk.call("pk_expand_int4_g128_e4m3", q, z, n, k, self.wexp, stream=stream)
+                pk.gemm(pk.FMT_G128F8, pk.EPI_F16, self.out8, self.wexp, t, n, k, self.state, in_scale=1.0 / 16,
+                        residual=self.state, out_scale=0.5, res_scale=1.0, g_scales=s, stream=stream)
+            return
         if fmt == "fp8":
             a, rows, f = (self.x8 if k == FF else self.x8d), self.xs8, pk.FMT_FP8
         elif fmt == "int8":
@@ -102,9 +127,9 @@ class Stack:
             a, rows, f = (self.xi if k == FF else self.xid), self.xsi, pk.FMT_G128A8
         ws = s if fmt != "int4g128" else None
         gs, gz = (s, z) if fmt == "int4g128" else (None, None)
-        t = self.t
         if epi == "f8":
-            pk.gemm(f, pk.EPI_F8, a, q, t, n, k, self.out8, w_scales=ws, row_scales=rows,
+            e = EPI_I8S if self.hidden_int8(layer, idx) else pk.EPI_F8
+            pk.gemm(f, e, a, q, t, n, k, self.out8, w_scales=ws, row_scales=rows,
                     g_scales=gs, g_zeros=gz, stream=stream)
         elif epi == "f16":
             pk.gemm(f, pk.EPI_F16, a, q, t, n, k, self.out16, w_scales=ws, row_scales=rows,
@@ -377,7 +402,10 @@ def refplan_bench(pk, torch, t, stream, steps=5):
 
 
 FMT_ID = {"fp8": 0, "int8": 1, "int4g128": 3}  # pk_gemm formats
-EPI_NAME = {"f8": "EPI_F8 (e4m3 SiLU)", "f16": "EPI_F16", "res": "EPI_F16_RES (fp16 + residual)"}
+FMT_G128F8 = 8  # e4m3 activations x INT4-g128 weights (expanded per call)
+EPI_I8S = 7     # static INT8 FF hidden (rne(clamp(fp16(SiLU) * 16, +-127)))
+EPI_NAME = {"f8": "EPI_F8 (e4m3 SiLU)", "i8s": "EPI_I8S (static INT8 SiLU x16)", "f16": "EPI_F16",
+            "res": "EPI_F16_RES (fp16 + residual)"}
 
 
 def stack_classes(stack):
@@ -387,8 +415,20 @@ def stack_classes(stack):
     for layer in range(LAYERS):
         for idx, (_, n, k, epi) in enumerate(LINEARS):
             kind = "res" if epi.startswith("res") else epi
+            if kind == "f8" and stack.hidden_int8(layer, idx):
+                kind = "i8s"
             classes.setdefault((stack.weights[layer][idx][0], kind, n, k), []).append((layer, idx))
     return classes
+
+
+def class_kernel(fmt, kind, n, k, rows):
+    """The kernel a stack class launches (FF contracts, k = 4096 with the
+    residual epilogue, read the FF hidden; INT4-g128 ones as format 8)."""
+    contract = kind == "res" and k == FF
+    f = {"fp8": "FP8", "int8": "I8", "int4g128": "G128F8" if contract else "G128A8"}[fmt]
+    e = EPI_NAME[kind] + (" on the x16 hidden" if contract else "")
+    pre = "pk_expand_int4_g128_e4m3 + " if fmt == "int4g128" and contract else ""
+    return f"{pre}g3::gemm3_kernel<{f}, {e}, {rows}-row tiles>"
 
 
 def class_times(pk, torch, stack, stream, reps=3):
@@ -403,13 +443,12 @@ def class_times(pk, torch, stack, stream, reps=3):
                 stack.linear(layer, idx, stream)
         run()
         ms = time_events(torch, run, reps, stream) / len(members)
-        epi = {"f8": pk.EPI_F8, "f16": pk.EPI_F16, "res": pk.EPI_F16}[kind]
-        rows, cols = pk.gemm_tile(FMT_ID[fmt], epi, stack.t, n)
+        epi = {"f8": pk.EPI_F8, "i8s": EPI_I8S, "f16": pk.EPI_F16, "res": pk.EPI_F16}[kind]
+        f = FMT_G128F8 if (fmt == "int4g128" and kind == "res" and k == FF) else FMT_ID[fmt]
+        rows, cols = pk.gemm_tile(f, epi, stack.t, n)
         out.append({"format": fmt, "epilogue": kind, "n": n, "k": k, "launches": len(members),
                     "avg_ms": ms, "step_ms": ms * len(members), "flop_per_launch": 2.0 * stack.t * n * k,
-                    "tile": [rows, cols],
-                    "kernel": f"g3::gemm3_kernel<{ {'fp8': 'FP8', 'int8': 'I8', 'int4g128': 'G128A8'}[fmt]}, "
-                              f"{EPI_NAME[kind]}, {rows}-row tiles>"})
+                    "tile": [rows, cols], "kernel": class_kernel(fmt, kind, n, k, rows)})
     out.sort(key=lambda e: -e["step_ms"])
     for e in out:
         e["TOPS"] = round(e["flop_per_launch"] / (e["avg_ms"] * 1e-3) / 1e12, 1)
@@ -423,7 +462,7 @@ def class_bytes(t, fmt, kind, n, k):
     weights (+ scales / group tables), output (+ residual read)."""
     a = t * k + 4 * t
     w = n * k + 4 * n if fmt != "int4g128" else n * k // 2 + 4 * n * (k // 128)
-    o = {"f8": t * n, "f16": 2 * t * n, "res": 4 * t * n}[kind]
+    o = {"f8": t * n, "i8s": t * n, "f16": 2 * t * n, "res": 4 * t * n}[kind]
     return a + w + o
 
 
@@ -446,19 +485,32 @@ def verify_stack(pk, torch, stack, rows=64):
     `rows` output rows spread over all row strips (first and last included)
     against a float64 torch matmul of the same dequantized operands (the
     quant_benchmark.rs:832-909 sample check).  fp16 outputs within 1e-2 x
-    RMS, e4m3 outputs within one e4m3 step on >= 99 % of codes equal.
-    Raises on a mismatch; returns the checked cases."""
+    RMS (residual outputs: of the output, and the update within 2e-2 of its
+    own RMS), e4m3 outputs within one e4m3 step and static INT8 hidden codes
+    within one code, each on >= 99 % of codes equal.  FF contracts are checked
+    on the hidden their expand writes.  Raises on a mismatch; returns the
+    checked cases."""
     t = stack.t
     stack.state.normal_()  # a fresh O(1) residual, so its fp16 rounding stays small against the products
     idx = torch.unique(torch.cat([torch.linspace(0, t - 1, rows).long(), torch.tensor([0, t - 1])])).cuda()
-    done, report = set(), []
+    report = []
     for (fmt, kind, n, k), members in stack_classes(stack).items():
-        if (fmt, kind) in done:
-            continue
-        done.add((fmt, kind))
         layer, li = members[0]
         _, q, s, z = stack.weights[layer][li]
-        if fmt == "fp8":
+        contract = kind == "res" and k == FF
+        if contract:
+            # the hidden this contract reads, as its expand writes it
+            stack.linear(layer, li - 1)
+            torch.cuda.synchronize()
+            h = stack.out8[idx]
+            x = (h.view(torch.int8).double() if fmt == "int8" else e4m3_to_float(torch, h).double()) / 16.0
+            if fmt == "fp8":
+                w = e4m3_to_float(torch, q).double() * s.double()[:, None]
+            elif fmt == "int8":
+                w = q.double() * s.double()[:, None]
+            else:
+                w = g128_dequant(torch, q, s, z)
+        elif fmt == "fp8":
             a = (stack.x8 if k == FF else stack.x8d)[idx]
             x = e4m3_to_float(torch, a).double() * stack.xs8[idx].double()[:, None]
             w = e4m3_to_float(torch, q).double() * s.double()[:, None]
@@ -471,7 +523,14 @@ def verify_stack(pk, torch, stack, rows=64):
             x = a.double() * stack.xsi[idx].double()[:, None]
             w = g128_dequant(torch, q, s, z)
         ref = x @ w.t()
-        if kind == "f8":
+        if kind == "i8s":
+            stack.linear(layer, li)
+            got = stack.out8.view(-1)[:t * n].view(t, n)[idx].view(torch.int8).double()
+            want = (torch.nn.functional.silu(ref).half().double() * 16.0).clamp(-127, 127).round()
+            same = (got == want).double().mean().item()
+            ok = same >= 0.99 and bool(((got - want).abs() <= 1).all().item())
+            err = 1.0 - same
+        elif kind == "f8":
             stack.linear(layer, li)
             got = e4m3_to_float(torch, stack.out8.view(-1)[:t * n].view(t, n)[idx]).double()
             want = e4m3_to_float(torch, (torch.nn.functional.silu(ref).half().float() * 16.0).clamp(-448, 448)
@@ -550,10 +609,18 @@ def kernel_run(pk, torch, t, fmt, kind, n, k, stream, seed=99):
     g = torch.Generator(device=dev)
     g.manual_seed(seed)
     f = FMT_ID[fmt]
+    contract = kind == "res" and k == FF
     src = torch.randn((t, k), generator=g, device=dev, dtype=torch.float16)
     xs = torch.empty(t, dtype=torch.float32, device=dev)
-    x = torch.empty((t, k), dtype=torch.uint8 if fmt == "fp8" else torch.int8, device=dev)
-    pk.call("pk_quantize_rows", 0 if fmt == "fp8" else 1, src, x, xs, t, t, k)
+    x = torch.empty((t, k), dtype=torch.int8 if fmt == "int8" else torch.uint8, device=dev)
+    if contract:
+        # the x16 FF hidden of SiLU outputs: e4m3, or static INT8 for INT8 weights
+        src = torch.nn.functional.silu(src.float()).half()
+        pk.call("pk_quantize_int8" if fmt == "int8" else "pk_quantize_fp8", src, x, 16.0, t * k)
+        xs = None
+    else:
+        x = x.view(torch.uint8 if fmt == "fp8" else torch.int8)
+        pk.call("pk_quantize_rows", 0 if fmt == "fp8" else 1, src, x, xs, t, t, k)
     del src
     w16 = (torch.randn((n, k), generator=g, device=dev, dtype=torch.float32) * 0.02).half()
     ws = gs = gz = None
@@ -567,9 +634,16 @@ def kernel_run(pk, torch, t, fmt, kind, n, k, stream, seed=99):
         ws = torch.empty(n, dtype=torch.float32, device=dev)
         pk.call("pk_pack_fp8_rows" if fmt == "fp8" else "pk_pack_int8_rows", w16, n, k, w, ws)
     del w16
-    if kind == "f8":
+    ins = 1.0 / 16 if contract else 1.0
+    if contract and fmt == "int4g128":
+        # the contract's GEMM on the per-call expanded e4m3 weights
+        we = torch.empty((n, k), dtype=torch.uint8, device=dev)
+        pk.call("pk_expand_int4_g128_e4m3", w, gz, n, k, we)
+        f, w, gz = FMT_G128F8, we, None
+    if kind in ("f8", "i8s"):
         out = torch.empty((t, n), dtype=torch.uint8, device=dev)
-        run = lambda: pk.gemm(f, pk.EPI_F8, x, w, t, n, k, out, w_scales=ws, row_scales=xs, g_scales=gs, g_zeros=gz,
+        e = pk.EPI_F8 if kind == "f8" else EPI_I8S
+        run = lambda: pk.gemm(f, e, x, w, t, n, k, out, w_scales=ws, row_scales=xs, g_scales=gs, g_zeros=gz,
                               stream=stream)
     elif kind == "f16":
         out = torch.empty((t, n), dtype=torch.float16, device=dev)
@@ -577,7 +651,7 @@ def kernel_run(pk, torch, t, fmt, kind, n, k, stream, seed=99):
                               stream=stream)
     else:
         out = (torch.randn((t, n), generator=g, device=dev) * 0.01).half()
-        run = lambda: pk.gemm(f, pk.EPI_F16, x, w, t, n, k, out, w_scales=ws, row_scales=xs, residual=out,
+        run = lambda: pk.gemm(f, pk.EPI_F16, x, w, t, n, k, out, w_scales=ws, row_scales=xs, in_scale=ins, residual=out,
                               out_scale=0.5, res_scale=1.0, g_scales=gs, g_zeros=gz, stream=stream)
     return run, 2.0 * t * n * k, class_bytes(t, fmt, kind, n, k)
 
@@ -641,31 +715,28 @@ def producers_bench(pk, torch, stack, stream, reps=3):
     (encoder.rs:1020-1080 runs them between the GEMMs), timed on their own at
     T frames: per layer the LayerNorm + dynamic per-row quantization of the
     four LayerNorm-fed linears (FF1 / FF2 expand, QKV, pointwise 1;
-    pk_layer_norm_quantize_fp8_dynamic, [T x 1024] fp16 in), the per-row
-    quantization of pointwise 2's input ([T x 1024]), and, for every FF
-    contract whose format reads INT8 activations, the per-row INT8
-    quantization of its [T x 4096] fp16 input (FP8 contracts read the expand
-    epilogue's e4m3 output directly).  Returns ms per stack step."""
+    pk_layer_norm_quantize_fp8_dynamic, [T x 1024] fp16 in) and the per-row
+    quantization of pointwise 2's input ([T x 1024]).  The FF contracts need
+    no producer: they read the x16 hidden (e4m3, or static INT8 for INT8
+    weights) that their expand's epilogue writes, as the reference's FF
+    contract reads the expand's x16 e4m3 (encoder.cu:1010-1025).  Returns ms
+    per stack step."""
     t = stack.t
     g = torch.Generator(device="cuda")
     g.manual_seed(31)
     x = torch.randn((t, D), generator=g, device="cuda").half()
     gamma = (torch.rand(D, generator=g, device="cuda") + 0.5).half()
     beta = (torch.randn(D, generator=g, device="cuda") * 0.1).half()
-    q = torch.empty((t, FF), dtype=torch.uint8, device="cuda")
+    q = torch.empty((t, D), dtype=torch.uint8, device="cuda")
     sc = torch.empty(t, dtype=torch.float32, device="cuda")
-    h = torch.randn((t, FF), generator=g, device="cuda").half()
-    int8_contracts = sum(1 for layer in range(LAYERS) for idx, (name, _, _, _) in enumerate(LINEARS)
-                         if name.endswith("contract") and stack.plan[layer][idx] != "fp8")
     ln = lambda: pk.call("pk_layer_norm_quantize_fp8_dynamic", x, gamma, beta, q, sc, t, t, 1e-5, stream=stream)
     rq = lambda: pk.call("pk_quantize_rows", 0, x, q, sc, t, t, D, stream=stream)
-    cq = lambda: pk.call("pk_quantize_rows", 1, h, q, sc, t, t, FF, stream=stream)
-    for f in (ln, rq, cq):
+    for f in (ln, rq):
         f()
-    ln_ms, rq_ms, cq_ms = (time_events(torch, f, reps, stream) for f in (ln, rq, cq))
-    total = LAYERS * (4 * ln_ms + rq_ms) + int8_contracts * cq_ms
+    ln_ms, rq_ms = (time_events(torch, f, reps, stream) for f in (ln, rq))
+    total = LAYERS * (4 * ln_ms + rq_ms)
     return {"layer_norm_quantize_ms": round(ln_ms, 4), "quantize_rows_1024_ms": round(rq_ms, 4),
-            "quantize_rows_int8_4096_ms": round(cq_ms, 4), "int8_contract_inputs": int8_contracts,
+            "ff_contract_inputs": "written by the expand epilogue (no re-quantization pass)",
             "ms_per_step": round(total, 3)}
 
 

@@ -120,7 +120,8 @@ static int launch_splitk(const GemmArgs& a, hipStream_t s) {
 // output: the smallest tile (32, 64 or 128 rows) whose tile count fits one
 // workgroup per CU, or 0 when even 128-row tiles outnumber the CUs.
 static bool has_ring(int fmt, int epi) {
-    return (fmt == FMT_FP8 || fmt == FMT_I8 || fmt == FMT_G128A8 || fmt == FMT_G128A16) && epi != EPI_GLU && epi != EPI_F8_24;
+    return (fmt == FMT_FP8 || fmt == FMT_I8 || fmt == FMT_G128A8 || fmt == FMT_G128A16) && epi != EPI_GLU && epi != EPI_F8_24 &&
+           epi != EPI_I8S;
 }
 template <int F> static int ring_stages_of(int kAI) {
     return kAI == 1 ? g3::LS<F, 1>::kS : (kAI == 2 ? g3::LS<F, 2>::kS : g3::LS<F, 4>::kS);
@@ -239,12 +240,12 @@ static int launch_fmt(const GemmArgs& a, hipStream_t s) {
     int cols = 0, stages = 0;
     const int rows = tile_plan(F, E == EPI_F16_RES ? EPI_F16 : E, a.m, a.n, &cols, &stages);
     if constexpr (F == FMT_G128A8 || F == FMT_G128A16) {
-        if constexpr (E != EPI_GLU && E != EPI_F8_24) {
+        if constexpr (E != EPI_GLU && E != EPI_F8_24 && E != EPI_I8S) {
             if (k_split(F, E == EPI_F16_RES ? EPI_F16 : E, a.m, a.n, a.k) == 4) return launch_splitk<F, E>(a, s);
         }
     }
     if constexpr (F == FMT_FP8 || F == FMT_I8 || F == FMT_G128A8 || F == FMT_G128A16) {
-        if constexpr (E != EPI_GLU && E != EPI_F8_24) {
+        if constexpr (E != EPI_GLU && E != EPI_F8_24 && E != EPI_I8S) {
             if (stages > 2) {
                 if constexpr (F == FMT_G128A8) {
                     if (ring_occ2(F, a.m, a.n)) return launch_ring<F, E, 2, 2>(a, s);
@@ -280,7 +281,11 @@ static int by_epi(int epi, const GemmArgs& a, hipStream_t s) {
         if constexpr (F != FMT_Q4K) return launch_fmt<F, EPI_F8>(a, s);
         break;
     case EPI_F8_24:
-        if constexpr (F != FMT_Q4K) return launch_fmt<F, EPI_F8_24>(a, s);
+        if constexpr (F != FMT_Q4K && F != FMT_G128F8) return launch_fmt<F, EPI_F8_24>(a, s);
+        break;
+    case EPI_I8S:
+        // the byte-activation formats on the occupancy-2 engine
+        if constexpr (F == FMT_FP8 || F == FMT_I8 || F == FMT_G128A8 || F == FMT_G128F8) return launch_fmt<F, EPI_I8S>(a, s);
         break;
     case EPI_I32:
         if constexpr (F == FMT_I8 || F == FMT_S4 || F == FMT_I8_SKIP) return launch_fmt<F, EPI_I32>(a, s);
@@ -303,7 +308,7 @@ static int by_epi(int epi, const GemmArgs& a, hipStream_t s) {
 
 static int k_step(int fmt) {
     switch (fmt) {
-    case FMT_FP8: case FMT_I8: case FMT_G128A8: case FMT_I8_SKIP: return 128;
+    case FMT_FP8: case FMT_I8: case FMT_G128A8: case FMT_I8_SKIP: case FMT_G128F8: return 128;
     case FMT_S4: case FMT_Q4K: return 256;
     default: return 64;
     }
@@ -314,11 +319,11 @@ int launch_gemm(int fmt, int epi, const GemmArgs& a, hipStream_t s) {
         set_error("invalid GEMM shape m=%d n=%d k=%d", a.m, a.n, a.k);
         return -1;
     }
-    if ((fmt == FMT_G128A8 || fmt == FMT_G128A16) && a.k > 128 * kMaxG128Groups) {
+    if ((fmt == FMT_G128A8 || fmt == FMT_G128A16 || fmt == FMT_G128F8) && a.k > 128 * kMaxG128Groups) {
         set_error("k=%d exceeds the %d groups of 128 the g128 kernels stage in LDS", a.k, kMaxG128Groups);
         return -1;
     }
-    if (a.k % k_step(fmt) != 0 || ((fmt == FMT_G128A8 || fmt == FMT_G128A16) && a.k % 128 != 0)) {
+    if (a.k % k_step(fmt) != 0 || ((fmt == FMT_G128A8 || fmt == FMT_G128A16 || fmt == FMT_G128F8) && a.k % 128 != 0)) {
         set_error("k=%d must be a multiple of %d for format %d", a.k, k_step(fmt), fmt);
         return -1;
     }
@@ -354,6 +359,7 @@ int launch_gemm(int fmt, int epi, const GemmArgs& a, hipStream_t s) {
     case FMT_G128A16: return by_epi<FMT_G128A16>(epi, a, s);
     case FMT_I8_SKIP: return by_epi<FMT_I8_SKIP>(epi, a, s);
     case FMT_Q4K: return by_epi<FMT_Q4K>(epi, a, s);
+    case FMT_G128F8: return by_epi<FMT_G128F8>(epi, a, s);
     default: break;
     }
     set_error("unknown format %d", fmt);
@@ -361,13 +367,13 @@ int launch_gemm(int fmt, int epi, const GemmArgs& a, hipStream_t s) {
 }
 
 int gemm_k_split(int fmt, int epi, int m, int n, int k) {
-    if (fmt < FMT_FP8 || fmt > FMT_Q4K) return -4;
+    if (fmt < FMT_FP8 || fmt > FMT_G128F8) return -4;
     if (forced_tile_rows() < 0) return -1;
     return k_split(fmt, epi == EPI_F16_RES ? EPI_F16 : epi, m, n, k);
 }
 
 int gemm_tile_plan(int fmt, int epi, int m, int n, int* cols, int* stages) {
-    if (fmt < FMT_FP8 || fmt > FMT_Q4K) return -4;
+    if (fmt < FMT_FP8 || fmt > FMT_G128F8) return -4;
     if (forced_tile_rows() < 0) return -1;
     return tile_plan(fmt, epi == EPI_F16_RES ? EPI_F16 : epi, m, n, cols, stages);
 }

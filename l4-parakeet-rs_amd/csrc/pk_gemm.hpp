@@ -29,13 +29,16 @@
 //   G128A16 f16((q-z)*s) x f16, INT4 weights dequantized in registers
 //   Q4K     f16(d*sc*q - dmin*mn) x f16, GGUF Q4_K superblocks (144 bytes
 //           per 256 K) dequantized in registers, K/step 64 = one group pair
+//   G128F8  e4m3 activations x group-wise INT4 weights given as e4m3 (q - z)
+//           bytes (exact: |q - z| <= 15), one f8f6f4 MFMA per 128-K group
+//           (fp32 group sum), fp32 fma of each group sum with its fp16 scale
 #pragma once
 
 #include "pk_common.hpp"
 
 namespace pk {
 
-enum Fmt { FMT_FP8 = 0, FMT_I8 = 1, FMT_S4 = 2, FMT_G128A8 = 3, FMT_F16 = 4, FMT_G128A16 = 5, FMT_I8_SKIP = 6, FMT_Q4K = 7 };
+enum Fmt { FMT_FP8 = 0, FMT_I8 = 1, FMT_S4 = 2, FMT_G128A8 = 3, FMT_F16 = 4, FMT_G128A16 = 5, FMT_I8_SKIP = 6, FMT_Q4K = 7, FMT_G128F8 = 8 };
 
 enum Epi {
     EPI_F16 = 0,     // fp16 out: act(scale(acc) [+bias]) * out_scale [+ res_scale * residual]
@@ -45,6 +48,7 @@ enum Epi {
     EPI_I32 = 4,     // raw int32 accumulators (integer formats only)
     EPI_F16_RES = 5, // EPI_F16 with a residual (chosen by the launcher when one is given)
     EPI_GLU = 6,     // fp16 out [M x N/2]: fp16(v) / (1 + exp(-fp16(g))), v = column c, g = column c + N/2
+    EPI_I8S = 7,     // int8 out: rne(clamp(fp16(silu(scale(acc))) * 16, +-127)) (static INT8 at the x16 hidden scale)
 };
 
 struct GemmArgs {
@@ -87,6 +91,7 @@ template <> struct FmtTraits<FMT_F16> { static constexpr int kStep = 64, bRow = 
 template <> struct FmtTraits<FMT_G128A16> { static constexpr int kStep = 64, bRow = 32, aElemNum = 2, aElemDen = 1, bNum = 1, bDen = 2; static constexpr bool kInt = false; };
 // Q4_K: per column and 64-K step the superblock's 16-byte header (d, dmin,
 // 12 bytes of 6-bit scales/mins) and the step's 32 quant bytes.
+template <> struct FmtTraits<FMT_G128F8> { static constexpr int kStep = 128, bRow = 128, aElemNum = 1, aElemDen = 1, bNum = 1, bDen = 1; static constexpr bool kInt = false; };
 template <> struct FmtTraits<FMT_Q4K> { static constexpr int kStep = 64, bRow = 48, aElemNum = 2, aElemDen = 1, bNum = 9, bDen = 16; static constexpr bool kInt = false; };
 
 // LDS of one workgroup.  A stage holds one K-step of the activation and
@@ -184,6 +189,14 @@ __device__ __forceinline__ void mfma_step(v4f& accf, v4i& acci, const uint4& w0,
         accf[1] = __builtin_fmaf((float)g[1], gscale[1], accf[1]);
         accf[2] = __builtin_fmaf((float)g[2], gscale[2], accf[2]);
         accf[3] = __builtin_fmaf((float)g[3], gscale[3], accf[3]);
+    } else if constexpr (F == FMT_G128F8) {
+        const v8i W = {(int)w0.x, (int)w0.y, (int)w0.z, (int)w0.w, (int)w1.x, (int)w1.y, (int)w1.z, (int)w1.w};
+        const v8i X = {(int)x0.x, (int)x0.y, (int)x0.z, (int)x0.w, (int)x1.x, (int)x1.y, (int)x1.z, (int)x1.w};
+        const v4f g = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(W, X, v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0, 0, 0, 0);
+        accf[0] = __builtin_fmaf(g[0], gscale[0], accf[0]);
+        accf[1] = __builtin_fmaf(g[1], gscale[1], accf[1]);
+        accf[2] = __builtin_fmaf(g[2], gscale[2], accf[2]);
+        accf[3] = __builtin_fmaf(g[3], gscale[3], accf[3]);
     } else {  // F16, G128A16 and Q4K (weights already dequantized to halves)
         accf = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, w0), __builtin_bit_cast(v8h, x0), accf, 0, 0, 0);
         accf = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, w1), __builtin_bit_cast(v8h, x1), accf, 0, 0, 0);
@@ -234,6 +247,24 @@ __device__ __forceinline__ uint32_t silu_fp8x4(float a, float b, float c, float 
     v2s o = __builtin_amdgcn_cvt_scalef32_pk_fp8_f16(v2s{0, 0}, h01, 0.0625f, false);
     o = __builtin_amdgcn_cvt_scalef32_pk_fp8_f16(o, h23, 0.0625f, true);
     return __builtin_bit_cast(uint32_t, o);
+}
+
+// int8 of 16 * fp16(SiLU(v)) for four values packed in a dword: the
+// reference's static INT8 quantizer (linear.cu:549-560, rne(clamp(x * s,
+// +-127))) at the FF hidden scale 16 of the e4m3 epilogue above.  The fp16
+// value times 16 is exact in fp32; adding 1.5 * 2^23 leaves rne(q) in the low
+// mantissa bits (|q| <= 127).
+__device__ __forceinline__ uint32_t silu_i8x4(float a, float b, float c, float d) {
+    const float x[4] = {a, b, c, d};
+    uint32_t q[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float h = round_f16(silu(x[i])) * 16.0f;
+        q[i] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_fmed3f(h, -127.0f, 127.0f) + 12582912.0f);
+    }
+    const uint32_t ab = __builtin_amdgcn_perm(q[1], q[0], 0x0c0c0400u);
+    const uint32_t cd = __builtin_amdgcn_perm(q[3], q[2], 0x0c0c0400u);
+    return __builtin_amdgcn_perm(cd, ab, 0x05040100u);
 }
 
 // encoder.cu:685-704: of one quartet of e4m3 bytes keep the two largest
@@ -375,6 +406,11 @@ __device__ __forceinline__ void epilogue(const GemmArgs& p, v4f (&accf)[kAI][4],
                 o[0] = uint4{h[0], h[1], h[2], h[3]};
                 o[1] = uint4{h[4], h[5], h[6], h[7]};
             }
+        } else if constexpr (E == EPI_I8S) {
+            uint32_t w[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) w[j] = silu_i8x4(v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]);
+            if (live) *(uint4*)((uint8_t*)p.out + (size_t)grow * p.ldo + gcol) = uint4{w[0], w[1], w[2], w[3]};
         } else {  // EPI_F8, EPI_F8_24
             uint32_t w[4];
 #pragma unroll
@@ -446,7 +482,7 @@ __device__ __forceinline__ void weight_frag(const uint8_t* Bs, int row, int g, i
 }
 
 // Output bytes per element of an epilogue.
-template <int E> struct EpiBytes { static constexpr int v = (E == EPI_F8 || E == EPI_F8_24) ? 1 : (E == EPI_F16 ? 2 : 4); };
+template <int E> struct EpiBytes { static constexpr int v = (E == EPI_F8 || E == EPI_F8_24 || E == EPI_I8S) ? 1 : (E == EPI_F16 ? 2 : 4); };
 
 // Epilogue through LDS for outputs without a residual: the waves convert
 // their accumulators to output bytes and place them in the stage buffer the

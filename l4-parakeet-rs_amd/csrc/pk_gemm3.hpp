@@ -301,10 +301,22 @@ __global__ __launch_bounds__(kThreads, 2) void gemm3_kernel(GemmArgs p) {
         }
     };
 
+    // G128F8 keeps no LDS table (its 80 KiB of tiles leave no room at two
+    // workgroups per CU): lane l of a wave holds the current step's group
+    // scale of column n0 + 64 wn + l (sc_cur) and loads the next step's
+    // (sc_nxt) a step ahead; a lane's 16 accumulator columns 16 g + 4 bj + r
+    // are lanes of its own 16-lane row, read with ds_bpermute.
+    float sc_cur = 0.0f, sc_nxt = 0.0f;
+    auto load_sc = [&](int cn0, int st) -> float {
+        const int col = min(cn0 + wn * 64 + lane, p.n - 1);
+        return h2f(p.g_scales[(size_t)col * groups + ((st * T::kStep) >> 7)]);
+    };
+
     int t = tile_slot(G);
     if (t >= ntiles) return;
     int m0, n0;
     set_tile(t, m0, n0);
+    if constexpr (F == FMT_G128F8) sc_nxt = load_sc(n0, 0);
     issue_a(0, 0);
     issue_b(0);
     if constexpr (L::kG128) {
@@ -360,6 +372,10 @@ __global__ __launch_bounds__(kThreads, 2) void gemm3_kernel(GemmArgs p) {
                 set_tile(t_next, m0, n0);
                 nstep = 0;
             }
+            if constexpr (F == FMT_G128F8) {
+                sc_cur = sc_nxt;
+                if (nstep >= 0) sc_nxt = load_sc(n0, nstep);
+            }
             if (nstep >= 0) issue_a(nstep, buf ^ 1);
             const uint8_t* As = lds + buf * kATile;
             const uint8_t* Bs = lds + kB;
@@ -369,6 +385,13 @@ __global__ __launch_bounds__(kThreads, 2) void gemm3_kernel(GemmArgs p) {
             for (int bj = 0; bj < 4; ++bj)
                 weight_frag<F>(Bs, wn * 64 + wrow(l16, bj), g, bj, wn, step, tab_s + (step & 1) * kBN, tab_z + (step & 1) * kBN,
                                w0[bj], w1[bj], gs[bj]);
+            if constexpr (F == FMT_G128F8) {
+#pragma unroll
+                for (int bj = 0; bj < 4; ++bj)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        gs[bj][r] = __int_as_float(__builtin_amdgcn_ds_bpermute((g * 16 + bj * 4 + r) << 2, __float_as_int(sc_cur)));
+            }
             uint4 x0, x1, y0, y1;
             uint4 xr0[3], xr1[3];  // kAhead2: row blocks ai, ai + 1, ai + 2 in slots ai % 3 ...
             if constexpr (kAhead2) {
@@ -435,6 +458,43 @@ __global__ __launch_bounds__(kThreads, 2) void gemm3_kernel(GemmArgs p) {
                         __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
                     }
                     if (b >= 2) __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
+                }
+            } else if constexpr (F == FMT_G128F8) {
+                // One MFMA per block and 128-K group: its fp32 group sum goes
+                // to one of three rotating registers while block b - 2's is
+                // scaled into the accumulators (one fma per value).
+                v4f gf[3];
+#pragma unroll
+                for (int b = 0; b < 4 * kAI + 2; ++b) {
+                    const int ai = b >> 2, bj = b & 3;
+                    if (b < 4 * kAI) {
+                        if (bj == 0 && ai + 1 < kAI) {
+                            const int row = wm * 16 * kAI + (ai + 1) * 16 + l16;
+                            y0 = *(const uint4*)(As + swz(row, g));
+                            y1 = *(const uint4*)(As + swz(row, 4 + g));
+                        }
+                        const v8i W = {(int)w0[bj].x, (int)w0[bj].y, (int)w0[bj].z, (int)w0[bj].w,
+                                       (int)w1[bj].x, (int)w1[bj].y, (int)w1[bj].z, (int)w1[bj].w};
+                        const v8i X = {(int)x0.x, (int)x0.y, (int)x0.z, (int)x0.w, (int)x1.x, (int)x1.y, (int)x1.z, (int)x1.w};
+                        gf[b % 3] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(W, X, v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0, 0, 0, 0);
+                        if (bj == 3) {
+                            x0 = y0;
+                            x1 = y1;
+                        }
+                    }
+                    if (b >= 2) {
+                        const int pa = (b - 2) >> 2, pj = (b - 2) & 3;
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) accf[pa][pj][r] = __builtin_fmaf(gf[(b - 2) % 3][r], gs[pj][r], accf[pa][pj][r]);
+                    }
+                }
+#pragma unroll
+                for (int b = 0; b < 4 * kAI + 2; ++b) {
+                    if (b < 4 * kAI) {
+                        if ((b & 3) == 0 && (b >> 2) + 1 < kAI) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    }
+                    if (b >= 2) __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
                 }
             } else if constexpr (kAhead2) {
 #pragma unroll

@@ -712,6 +712,37 @@ __global__ __launch_bounds__(256) void unpack_s4_kernel(const uint4* __restrict_
     out[2 * i + 1] = uint4{o[4], o[5], o[6], o[7]};
 }
 
+// INT4-g128 weights (pk_pack_int4_g128 layout) -> e4m3 (q - z) bytes [n x k]
+// in k order (|q - z| <= 15 is exact in e4m3), the weight operand of the
+// G128F8 GEMM: one thread per 4 words (32 K values of one group).
+// HBM-bound: reads k/2 + 2 k/128 bytes and writes k bytes per row.
+__global__ __launch_bounds__(256) void expand_g128_e4m3_kernel(const uint4* __restrict__ q, const uint16_t* __restrict__ zeros,
+                                                               uint4* __restrict__ out, int k, size_t quads) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= quads) return;
+    const size_t per_row = (size_t)k / 32;  // quads per row
+    const size_t row = i / per_row;
+    const int group = (int)(i - row * per_row) >> 2;
+    const float z = h2f(zeros[row * (size_t)(k >> 7) + group]);
+    const uint4 w = q[i];
+    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+    uint32_t o[8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        // word j: byte b holds k 8j + b (low nibble) and 8j + 4 + b (high)
+        float v[8];
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            v[b] = (float)((ws[j] >> (8 * b)) & 15u) - z;
+            v[4 + b] = (float)((ws[j] >> (8 * b + 4)) & 15u) - z;
+        }
+        o[2 * j] = e4m3x2(v[0], v[1]) | (e4m3x2(v[2], v[3]) << 16);
+        o[2 * j + 1] = e4m3x2(v[4], v[5]) | (e4m3x2(v[6], v[7]) << 16);
+    }
+    out[2 * i] = uint4{o[0], o[1], o[2], o[3]};
+    out[2 * i + 1] = uint4{o[4], o[5], o[6], o[7]};
+}
+
 // ---- launchers -------------------------------------------------------------
 
 // Q4_K superblocks -> fp16 [n x k] (linear.cu:459-472): one thread per 8
@@ -826,6 +857,13 @@ int launch_unpack_s4(const uint8_t* in, int8_t* out, size_t bytes, hipStream_t s
     const size_t chunks = bytes / 16;
     if (chunks == 0) return 0;
     unpack_s4_kernel<<<(unsigned)((chunks + 255) / 256), 256, 0, s>>>((const uint4*)in, (uint4*)out, chunks);
+    return 0;
+}
+
+int launch_expand_g128_e4m3(const uint32_t* q, const uint16_t* zeros, uint8_t* out, int n, int k, hipStream_t s) {
+    const size_t quads = (size_t)n * (k / 32);
+    if (quads == 0) return 0;
+    expand_g128_e4m3_kernel<<<(unsigned)((quads + 255) / 256), 256, 0, s>>>((const uint4*)q, zeros, (uint4*)out, k, quads);
     return 0;
 }
 

@@ -56,6 +56,7 @@ SIGNATURES = {
     "pk_pack_int8_rows": (I, [P, I, I, P, P, P]),
     "pk_pack_int4_rows": (I, [P, I, I, P, P, P]),
     "pk_pack_int4_g128": (I, [P, I, I, P, P, P, P]),
+    "pk_expand_int4_g128_e4m3": (I, [P, P, I, I, P, P]),
     "pk_q4_k_dequantize": (I, [P, P, I, I, P]),
     "pk_quantize_fp8": (I, [P, P, F, I, P]),
     "pk_quantize_int8": (I, [P, P, F, I, P]),
@@ -227,7 +228,7 @@ def gemm_k_split(fmt, epi, m, n, k):
     return r
 
 
-FMT_FP8, FMT_I8, FMT_S4, FMT_G128A8, FMT_F16, FMT_G128A16, FMT_I8_SKIP, FMT_Q4K = range(8)
+FMT_FP8, FMT_I8, FMT_S4, FMT_G128A8, FMT_F16, FMT_G128A16, FMT_I8_SKIP, FMT_Q4K, FMT_G128F8 = range(9)
 EPI_F16, EPI_F8, EPI_F8_24, EPI_F32, EPI_I32 = range(5)
 
 

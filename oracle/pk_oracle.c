@@ -967,6 +967,34 @@ void orc_gemm_g128_a8(const int8_t* x, const float* x_scales, const uint32_t* q,
     }
 }
 
+/* e4m3 activations x INT4-g128 weights (no reference counterpart; the
+ * weights' dequant is (q - z) * s, pk_pack_int4_g128 layout): per output, each
+ * 128-K group's sum of e4m3(x) * (q - z) -- every product exact in fp32 --
+ * accumulated in double and rounded once to fp32 (the device's MFMA sums a
+ * group in fp32 in its own order, so device results agree within a
+ * tolerance, not bit for bit), then folded in K order as fmaf(sum, s, acc).
+ * out is the accumulator before the epilogue's activation scale. */
+void orc_gemm_g128_f8(const uint8_t* x, const uint32_t* q, const uint16_t* scales, const uint16_t* zeros, int m,
+                      int n, int k, float* out) {
+    const int groups = k / 128;
+    float table[256];
+    for (int c = 0; c < 256; ++c) table[c] = orc_e4m3_to_f32((uint8_t)c);
+#pragma omp parallel for schedule(static) num_threads(g_threads)
+    for (int i = 0; i < m; ++i) {
+        for (int j = 0; j < n; ++j) {
+            float acc = 0.0f;
+            for (int g = 0; g < groups; ++g) {
+                const int z = (int)orc_f16_to_f32(zeros[(size_t)j * groups + g]);
+                double sum = 0.0;
+                for (int t = g * 128; t < g * 128 + 128; ++t)
+                    sum += (double)table[x[(size_t)i * k + t]] * (double)(g128_level(q, k, j, t) - z);
+                acc = fmaf((float)sum, orc_f16_to_f32(scales[(size_t)j * groups + g]), acc);
+            }
+            out[(size_t)i * n + j] = acc;
+        }
+    }
+}
+
 /* q4k_benchmark.rs:910-945: fp16 activations times f16(dequant(Q4_K)). */
 void orc_gemm_q4k_f32(const uint16_t* x, const uint8_t* blocks, int m, int n, int k, float* acc) {
     int per_row = k / 256;
@@ -1004,7 +1032,10 @@ static float round_f16(float v) { return orc_f16_to_f32(orc_f32_to_f16(v)); }
  *      (out16 is [m x width])
  *   6: out16 = fp16(value + out16)      (residual, scale 1)
  *   7: as 1 (the 2:4 compression is orc_compress_24 on its output)
- *   8: as 2 (sparse-input contract) */
+ *   8: as 2 (sparse-input contract)
+ *   9: SiLU -> fp16 -> x16 -> static INT8 (out8 as int8 bytes): the FF
+ *      hidden at the scale of mode 1 through the static INT8 quantizer of
+ *      linear.cu:549-560, rne(clamp(v, -127, 127)) */
 void orc_epilogue(const float* acc, const float* row_scales, float in_scale,
                   const float* w_scales, const float* bias, int m, int n, int mode,
                   int valid_rows, uint16_t* out16, uint8_t* out8) {
@@ -1037,6 +1068,12 @@ void orc_epilogue(const float* acc, const float* row_scales, float in_scale,
             case 8:
                 out16[idx] = orc_f32_to_f16(fmaf(0.5f, value, orc_f16_to_f32(out16[idx])));
                 break;
+            case 9: {
+                float h = round_f16(silu(value)) * 16.0f;
+                h = fminf(fmaxf(h, -127.0f), 127.0f);
+                out8[idx] = (uint8_t)(int8_t)rintf(h);
+                break;
+            }
             case 3:
                 out16[idx] = orc_f32_to_f16(value + bias[c]);
                 break;

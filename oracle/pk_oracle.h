@@ -63,6 +63,8 @@ void orc_layer_norm_quantize(const uint16_t* x, const uint16_t* gamma, const uin
 void orc_layer_norm_pair(const uint16_t* x, const uint16_t* w1, const uint16_t* b1, const uint16_t* w2,
                          const uint16_t* b2, int rows, int valid_rows, float epsilon, float inverse_scale,
                          uint16_t* out, void* next_out);
+void orc_gemm_g128_f8(const uint8_t* x, const uint32_t* q, const uint16_t* scales, const uint16_t* zeros, int m,
+                      int n, int k, float* out);
 void orc_compress_24(const uint8_t* x, int rows, int k, uint8_t* data, uint8_t* meta);
 void orc_compress_24_i8_exact(const int8_t* x, int rows, int k, uint8_t* data, uint8_t* meta, uint32_t* counts, uint32_t* ovf);
 void orc_residual_24_i8(const int8_t* x, const uint8_t* meta, int rows, int k, uint8_t* data2, uint8_t* meta2);

@@ -78,6 +78,7 @@ def _declare(l):
         "orc_gemm_g128_a16": (None, [P, P, P, P, I, I, I, P]),
         "orc_gemm_g128_a8": (None, [P, P, P, P, P, I, I, I, I, P, P]),
         "orc_gemm_q4k_f32": (None, [P, P, I, I, I, P]),
+        "orc_gemm_g128_f8": (None, [P, P, P, P, I, I, I, P]),
         "orc_epilogue": (None, [P, P, F, P, P, I, I, I, I, P, P]),
         "orc_epilogue_linear": (None, [P, P, P, I, I, F, F, I, P]),
         "orc_epilogue_quantized": (None, [P, F, P, P, I, I, I, P]),
@@ -446,6 +447,17 @@ def gemm_g128_a8(x8, x_scales, q, s, z, want_group_acc=False, parts=1):
     return (out, gacc) if want_group_acc else out
 
 
+def gemm_g128_f8(x8, q, s, z) -> np.ndarray:
+    """e4m3 activations [m x k] x INT4-g128 weights: the fp32 accumulator
+    before the epilogue (group sums rounded once, folded with one fma each)."""
+    x8 = np.ascontiguousarray(x8, np.uint8)
+    m, k = x8.shape
+    n = q.shape[0]
+    out = np.empty((m, n), np.float32)
+    lib().orc_gemm_g128_f8(_p(x8), _p(np.ascontiguousarray(q, np.uint32)), _p(_h(s)), _p(_h(z)), m, n, k, _p(out))
+    return out
+
+
 def gemm_q4k(x16, blocks) -> np.ndarray:
     x16 = _h(x16)
     m, k = x16.shape
@@ -473,11 +485,11 @@ def epilogue(acc, mode, w_scales, row_scales=None, in_scale=1.0, bias=None, resi
         out16 = np.array(residual, dtype=np.float16, copy=True, order="C")
     else:
         out16 = np.zeros((m, n), np.float16)
-    if mode in (1, 7):
+    if mode in (1, 7, 9):
         out8 = np.zeros((m, n), np.uint8)
     lib().orc_epilogue(_p(acc), _p(rs), in_scale, _p(ws), _p(b), m, n, mode,
                        m if valid_rows is None else valid_rows, _p(out16), _p(out8))
-    return out8 if mode in (1, 7) else out16
+    return out8 if mode in (1, 7, 9) else out16
 
 
 def epilogue_linear(acc, bias=None, residual=None, out_scale=1.0, res_scale=0.0,

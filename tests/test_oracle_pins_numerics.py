@@ -294,3 +294,40 @@ def test_joint_scores_i8_matches_float64(oracle):
     # the relu is on (enc + pred), not on each term
     bad = ws.astype(np.float64) * (w.astype(np.float64) @ (np.maximum(enc.astype(np.float64), 0) + pred)) + bias
     assert not np.allclose(got, bad, rtol=1e-3)
+
+
+def test_ffn_epilogue_static_int8(oracle):
+    """Mode 9: rint(clip(fp16(silu(v)) * 16, +-127)) -- the static INT8
+    quantizer of linear.cu:549-560 on the x16 FF hidden."""
+    m, n = 128, 512
+    acc = _acc(m, n, 24, integer=True)
+    rng = np.random.default_rng(25)
+    rs = rng.uniform(1e-3, 1e-2, m).astype(F32)
+    ws = rng.uniform(1e-3, 3e-2, n).astype(F32)
+    v = (acc * rs[:, None]).astype(F32) * ws[None, :]
+    silu = torch.nn.functional.silu(torch.from_numpy(v).double()).numpy()
+    ref = np.rint(np.clip(silu.astype(np.float16).astype(F32) * F32(16.0), -127, 127)).astype(np.int8)
+    got = oracle.epilogue(acc, 9, ws, row_scales=rs).view(np.int8)
+    assert np.mean(got == ref) > 0.995
+    assert np.all(np.abs(got.astype(np.int32) - ref) <= 1)
+    assert (np.abs(ref) == 127).any() and (ref < 0).any()  # both clamps and SiLU's negative lobe reached
+
+
+def test_gemm_g128_f8_matches_float64(oracle):
+    """e4m3 x INT4-g128: the float64 matmul of the decoded e4m3 activations and
+    the dequantized weights (q - z) * s agrees to fp32 rounding of the group
+    sums and the folds; a dropped zero point or a wrong group's scale does not."""
+    rng = np.random.default_rng(26)
+    w = (rng.standard_normal((24, 512)) * 0.02).astype(np.float16)
+    q, s, z = oracle.pack_int4_g128(w)
+    x8 = e4m3(rng.standard_normal((9, 512)) * 2)
+    xf = oracle.e4m3_table()[x8].astype(np.float64)
+    b = q.view(np.uint8).reshape(24, -1, 4).astype(np.int64)
+    lv = np.concatenate([b & 15, b >> 4], axis=2).reshape(24, -1)
+    g = np.arange(512) // 128
+    wd = (lv - z.astype(np.float64)[:, g]) * s.astype(np.float64)[:, g]
+    ref = xf @ wd.T
+    got = oracle.gemm_g128_f8(x8, q, s, z).astype(np.float64)
+    assert np.max(np.abs(got - ref)) <= 1e-5 * np.sqrt(np.mean(ref ** 2))
+    wrong = xf @ (lv * s.astype(np.float64)[:, g]).T
+    assert np.max(np.abs(got - wrong)) > 1e-2 * np.sqrt(np.mean(ref ** 2))
