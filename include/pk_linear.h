@@ -449,8 +449,9 @@ int32_t pk_joint_gemv(const void* weight, int32_t weight_int8, const float* w_sc
  * steps run}; state[2] = -2 if the workgroups failed to meet at a barrier
  * (not co-resident).  The weights stay in registers for the whole scan:
  * hidden % 128 == 0, hidden <= 1024, durations <= 8, token_outputs +
- * durations <= 2048.  workspace is a device uint32[512] the call overwrites
- * (the per-step decision words the workgroups exchange). */
+ * durations <= 2048.  workspace is a device uint32[2304] the call overwrites
+ * (the decision words the workgroups exchange: per round of 8 frames one
+ * word per workgroup and frame, two rounds' worth). */
 int32_t pk_joint_scan(const void* weight, int32_t weight_int8, const float* w_scales, const float* bias,
                       const uint16_t* enc, const float* pred, int32_t outputs, int32_t hidden,
                       int32_t token_outputs, int32_t durations, int32_t frames, int32_t enc_stride,
@@ -459,7 +460,7 @@ int32_t pk_joint_scan(const void* weight, int32_t weight_int8, const float* w_sc
 /* pk_joint_scan without the workspace argument, for callers that cannot
  * allocate device memory (code under HIP graph capture, serving loops,
  * harnesses that forbid hipMalloc).  No counterpart in the reference.  The
- * 512 words of scratch are a static device array of the library (one copy
+ * 2304 words (9 KiB) of scratch are a static device array of the library (one copy
  * per GPU, held until the process ends; its address is looked up once per
  * device), cleared by a fill kernel at the start of every call.  Same
  * arguments, limits and results as pk_joint_scan; token_outputs + durations

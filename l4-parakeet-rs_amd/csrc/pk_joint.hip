@@ -167,19 +167,23 @@ __global__ __launch_bounds__(256) void joint_decide_kernel(const float* __restri
 // ---- persistent blank scan (decoder.cu:690-783) ---------------------------------
 //
 // Between two emitted tokens the prediction vector is fixed, so the greedy TDT
-// loop is a sequence of joint steps that only move the frame index.  One
-// persistent launch runs those steps.  Every active workgroup keeps its slice
-// of W in registers for the whole scan (8 rows per wave; lane l holds
-// k = 2l + 128j, j < hidden/128).  Per step it scores its rows for the current
-// frame and publishes ONE 64-bit word: its best token as an order-preserving
-// key (score bits, then 0xffff - id), the duration decision when it owns the
-// duration rows, and the step's tag.  The words double as the grid barrier:
-// each workgroup polls all of them in parallel (one lane per workgroup) until
-// every tag is the current one, then takes the maximum.  So a step costs about
-// one memory round trip; the encoder rows of every frame the decision can move
-// to are loaded while the poll waits.  The scan stops after the first
-// non-blank token (the prediction network must run before the next step) or
-// when the frames run out.
+// loop is a sequence of joint steps that only move the frame index, and the
+// decision at a frame does not depend on how the scan got there.  One
+// persistent launch runs those steps in rounds: every active workgroup keeps
+// its slice of W in registers for the whole scan (8 rows per wave; lane l
+// holds k = 2l + 128j, j < hidden/128) and, per round, scores its rows for the
+// kScanRound frames frame, frame + 1, ... and publishes one 64-bit word per
+// frame: its best token as an order-preserving key (score bits, then 0xffff -
+// id), the duration decision when it owns the duration rows, and the round's
+// tag.  The words are the grid barrier: each workgroup polls all of them
+// (lane b reads workgroup b's words) until every tag is the current one, then
+// takes the maximum per frame, and every thread applies the greedy rules over
+// the round's decisions, identically, until a non-blank token (the prediction
+// network must run before the next step), the frames run out, or the frame
+// leaves the round.  A barrier costs a memory round trip through the device-
+// coherent level; a round amortises it over the steps its frames cover.  The
+// encoder rows come from a window of kScanWin frames each workgroup keeps in
+// LDS, refilled when the round would leave it.
 //
 // Logical row i of the scan is joint row T + i for i < D (the durations, all
 // in workgroup 0's wave 0) and row i - D for the tokens.  Workgroups are
@@ -187,9 +191,11 @@ __global__ __launch_bounds__(256) void joint_decide_kernel(const float* __restri
 // work, so the active ones share one XCD's L2.
 
 constexpr int kScanRows = 8;      // joint rows per wave
-constexpr int kScanCand = 8;      // frames the decision can move to: +0 .. +7
+constexpr int kScanRound = 8;     // frames scored per round
+constexpr int kScanWin = 32;      // encoder frames in the LDS window (32 x hidden x 2 bytes <= 64 KiB)
 constexpr int kScanMaxBlocks = 64;
 constexpr uint32_t kScanSpinLimit = 1u << 22;
+static_assert(8 + 2 * 2 * kScanRound * kScanMaxBlocks <= kJointScanWorkspaceWords, "scan words fit the workspace");
 
 struct ScanArgs {
     const void* w;
@@ -198,7 +204,7 @@ struct ScanArgs {
     const uint16_t* enc;
     const float* pred;
     int* state;
-    uint32_t* ws;  // [0] abort flag; words 8.. : 2 x kScanMaxBlocks published u64 (by step parity)
+    uint32_t* ws;  // [0] abort flag; words 8.. : u64 [2 parities][kScanRound frames][kScanMaxBlocks]
     int outputs, hidden, token_outputs, durations, frames, enc_stride, max_symbols;
 };
 
@@ -208,19 +214,20 @@ __device__ __forceinline__ uint32_t ordered_bits(float score) {
     return (bits & 0x80000000u) ? ~bits : (bits ^ 0x80000000u);
 }
 
-// KP = hidden / 128 pairs of k per lane.
+// KP = hidden / 128 pairs of k per lane.  At most 256 VGPRs (two workgroups
+// per CU): the up to 64 active workgroups must all be resident on the 32 CUs
+// of one XCD, or the first round's barrier never completes.
 template <bool kInt8, int KP>
-__global__ __launch_bounds__(256) void joint_scan_kernel(ScanArgs p) {
+__global__ __launch_bounds__(256, 2) void joint_scan_kernel(ScanArgs p) {
     if (blockIdx.x & 7) return;
-    __shared__ float best_s[4];
-    __shared__ int best_i[4];
-    __shared__ int dur_s;
+    __shared__ unsigned long long wave_key[4][kScanRound];
+    __shared__ int dur_s[kScanRound];
+    __shared__ int dec_tok[kScanRound], dec_dur[kScanRound];
     const int blk = blockIdx.x >> 3;
     const int nblocks = gridDim.x >> 3;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int T = p.token_outputs, D = p.durations;
-    unsigned long long* const pub = (unsigned long long*)(p.ws + 8) + blk;
-    const unsigned long long* const watch = (const unsigned long long*)(p.ws + 8) + (lane < nblocks ? lane : 0);
+    unsigned long long* const words = (unsigned long long*)(p.ws + 8);
     const bool watcher = lane < nblocks;
 
     uint32_t w[kScanRows][KP];
@@ -246,29 +253,43 @@ __global__ __launch_bounds__(256) void joint_scan_kernel(ScanArgs p) {
         pv[2 * j] = p.pred[2 * lane + 128 * j];
         pv[2 * j + 1] = p.pred[2 * lane + 128 * j + 1];
     }
-    auto enc_pairs = [&](int f, uint32_t (&e)[KP]) {
-        const uint16_t* row = p.enc + (size_t)min(f, p.frames - 1) * p.enc_stride + 2 * lane;
-#pragma unroll
-        for (int j = 0; j < KP; ++j) e[j] = *(const uint32_t*)(row + 128 * j);
+    // encoder window: frames [win_base, win_base + kScanWin) as fp16 pairs
+    extern __shared__ uint32_t enc_win[];
+    constexpr int kPairs = 64 * KP;  // hidden / 2
+    int win_base = 0;
+    auto load_win = [&](int base) {
+        for (int i = threadIdx.x; i < kScanWin * kPairs; i += 256) {
+            const int f = base + i / kPairs;
+            enc_win[i] = f < p.frames ? *(const uint32_t*)(p.enc + (size_t)f * p.enc_stride + 2 * (i % kPairs)) : 0u;
+        }
+        win_base = base;
+        __syncthreads();
     };
 
     int frame = p.state[0], symbols = p.state[1];
-    int token = -1, steps = 0;
-    bool failed = false;
+    int token = -1, steps = 0, rounds = 0;
+    bool failed = false, done = false;
     const int blank = T - 1;
-    uint32_t ev[KP];  // the current frame's encoder pairs
-    enc_pairs(frame, ev);
+    if (frame < p.frames) load_win(frame);
 
-    while (frame < p.frames) {
-        float bs = -__builtin_huge_valf(), dbest = 0.0f;
-        int bi = 0x7fffffff, dur = 0;
-        {
+    while (frame < p.frames && !done) {
+        // every workgroup takes the same decisions, so the refill is uniform
+        if (frame + kScanRound > win_base + kScanWin) load_win(frame);
+        const int f0 = frame;
+        // per round frame: this wave's 8 row scores, reduced over the lanes,
+        // then the wave's best token (and, in workgroup 0's wave 0, the
+        // duration) into LDS
+#pragma unroll 1
+        for (int c = 0; c < kScanRound; ++c) {
+            const int f = min(f0 + c, p.frames - 1) - win_base;
             float x[2 * KP];
 #pragma unroll
             for (int j = 0; j < KP; ++j) {
-                x[2 * j] = __builtin_fmaxf(h2f((uint16_t)(ev[j] & 0xffffu)) + pv[2 * j], 0.0f);
-                x[2 * j + 1] = __builtin_fmaxf(h2f((uint16_t)(ev[j] >> 16)) + pv[2 * j + 1], 0.0f);
+                const uint32_t ev = enc_win[f * kPairs + lane + 64 * j];
+                x[2 * j] = __builtin_fmaxf(h2f((uint16_t)(ev & 0xffffu)) + pv[2 * j], 0.0f);
+                x[2 * j + 1] = __builtin_fmaxf(h2f((uint16_t)(ev >> 16)) + pv[2 * j + 1], 0.0f);
             }
+            float acc[kScanRows];
 #pragma unroll
             for (int r = 0; r < kScanRows; ++r) {
                 float sum = 0.0f;
@@ -285,9 +306,17 @@ __global__ __launch_bounds__(256) void joint_scan_kernel(ScanArgs p) {
                     sum = __builtin_fmaf(w0, x[2 * j], sum);
                     sum = __builtin_fmaf(w1, x[2 * j + 1], sum);
                 }
+                acc[r] = sum;
+            }
 #pragma unroll
-                for (int off = 1; off < 64; off <<= 1) sum = add_level(sum, off);
-                const float score = __builtin_fmaf(wsc[r], sum, wb[r]);
+            for (int off = 1; off < 64; off <<= 1)
+#pragma unroll
+                for (int r = 0; r < kScanRows; ++r) acc[r] = add_level(acc[r], off);
+            float bs = -__builtin_huge_valf(), dbest = 0.0f;
+            int bi = 0x7fffffff, dur = 0;
+#pragma unroll
+            for (int r = 0; r < kScanRows; ++r) {
+                const float score = __builtin_fmaf(wsc[r], acc[r], wb[r]);
                 const int id = rid[r];
                 if (id >= T) {  // duration id - T, first maximum wins
                     if (id == T || score > dbest) { dbest = score; dur = id - T; }
@@ -295,33 +324,38 @@ __global__ __launch_bounds__(256) void joint_scan_kernel(ScanArgs p) {
                     if (score > bs || (score == bs && id < bi)) { bs = score; bi = id; }
                 }
             }
-        }
-        if (lane == 0) {
-            best_s[wave] = bs;
-            best_i[wave] = bi;
-            if (blk == 0 && wave == 0) dur_s = dur;
+            if (lane == 0) {
+                wave_key[wave][c] = bi == 0x7fffffff ? 0ull
+                                                     : (((unsigned long long)ordered_bits(bs) << 32) |
+                                                        ((unsigned long long)(0xffffu - (uint32_t)bi) << 16));
+                if (blk == 0 && wave == 0) dur_s[c] = dur;
+            }
         }
         __syncthreads();
-        const int par = (steps & 1) * kScanMaxBlocks;
-        const uint32_t tag = (uint32_t)(steps + 1) & 0x1fffu;
-        if (threadIdx.x == 0) {
-            for (int i = 1; i < 4; ++i)
-                if (best_s[i] > bs || (best_s[i] == bs && best_i[i] < bi)) { bs = best_s[i]; bi = best_i[i]; }
-            const bool any = bi != 0x7fffffff;
-            const uint32_t lo = ((any ? 0xffffu - (uint32_t)bi : 0u) << 16) | ((uint32_t)(blk == 0 ? dur_s : 0) << 13) | tag;
-            const unsigned long long word = any ? ((unsigned long long)ordered_bits(bs) << 32) | lo : (unsigned long long)lo;
-            __hip_atomic_store(pub + par, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int par = (rounds & 1) * kScanRound * kScanMaxBlocks;
+        const uint32_t tag = (uint32_t)(rounds + 1) & 0x1fffu;
+        // thread c publishes this workgroup's word for round frame c
+        if (threadIdx.x < kScanRound) {
+            const int c = threadIdx.x;
+            unsigned long long key = wave_key[0][c];
+            for (int i = 1; i < 4; ++i) key = wave_key[i][c] > key ? wave_key[i][c] : key;
+            key |= (unsigned long long)((uint32_t)(blk == 0 ? dur_s[c] : 0) << 13) | tag;
+            __hip_atomic_store(words + par + c * kScanMaxBlocks + blk, key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
-        // Encoder rows of every frame the decision can move to, while polling.
-        uint32_t cand[kScanCand][KP];
-#pragma unroll
-        for (int c = 0; c < kScanCand; ++c) enc_pairs(frame + c, cand[c]);
-        // Poll: lane b watches workgroup b's word for this step's tag.
-        unsigned long long mine = 0;
+        // poll: lane b of every wave reads workgroup b's words; wave w reduces
+        // frames w and w + 4
+        unsigned long long got[2] = {0ull, 0ull};
         uint32_t spins = 0;
         while (true) {
-            mine = __hip_atomic_load(watch + par, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            const bool ready = !watcher || ((uint32_t)mine & 0x1fffu) == tag;
+            bool ready = true;
+            if (watcher) {
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    got[h] = __hip_atomic_load(words + par + (wave + 4 * h) * kScanMaxBlocks + lane, __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT);
+                    ready = ready && ((uint32_t)got[h] & 0x1fffu) == tag;
+                }
+            }
             if (__builtin_amdgcn_ballot_w64(!ready) == 0) break;
             if ((++spins & 63) == 0 &&
                 (spins > kScanSpinLimit || __hip_atomic_load(&p.ws[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u)) {
@@ -331,32 +365,48 @@ __global__ __launch_bounds__(256) void joint_scan_kernel(ScanArgs p) {
             }
             __builtin_amdgcn_s_sleep(1);
         }
-        if (failed) break;
-        // Workgroup 0's word carries the duration; the maximum word the token.
-        dur = (int)(((uint32_t)__shfl(mine, 0, 64) >> 13) & 7u);
-        unsigned long long best = watcher ? mine : 0ull;
-#pragma unroll
-        for (int off = 1; off < 64; off <<= 1) best = max_level(best, off);
-        token = (int)(0xffffu - (((uint32_t)best) >> 16));
-        // the LDS reduction slots are reused next step
-        __syncthreads();
-        ++steps;
-        ++symbols;
-        const int prev = frame;
-        frame += dur;
-        if (dur != 0 || symbols == p.max_symbols) {
-            if (dur == 0) ++frame;
-            symbols = 0;
+        // a wave that gave up stops the workgroup (the flag makes every other
+        // workgroup's poll give up too)
+        if (__syncthreads_or(failed)) {
+            failed = true;
+            break;
         }
-        if (token != blank) break;
-        token = -1;
-        const int c = frame - prev;
 #pragma unroll
-        for (int cc = 0; cc < kScanCand; ++cc)
-            if (cc == c) {
+        for (int h = 0; h < 2; ++h) {
+            // workgroup 0's word carries the duration; the maximum word the token
+            const int dur = (int)(((uint32_t)__shfl(got[h], 0, 64) >> 13) & 7u);
+            unsigned long long best = watcher ? got[h] : 0ull;
 #pragma unroll
-                for (int j = 0; j < KP; ++j) ev[j] = cand[cc][j];
+            for (int off = 1; off < 64; off <<= 1) best = max_level(best, off);
+            if (lane == 0) {
+                dec_tok[wave + 4 * h] = (int)(0xffffu - (((uint32_t)best) >> 16));
+                dec_dur[wave + 4 * h] = dur;
             }
+        }
+        __syncthreads();
+        ++rounds;
+        // the greedy rules (decoder.cu:773-783) over the round's decisions, in
+        // every thread alike
+        while (true) {
+            const int c = frame - f0;
+            token = dec_tok[c];
+            const int dur = dec_dur[c];
+            ++steps;
+            ++symbols;
+            frame += dur;
+            if (dur != 0 || symbols == p.max_symbols) {
+                if (dur == 0) ++frame;
+                symbols = 0;
+            }
+            if (token != blank) {
+                done = true;
+                break;
+            }
+            token = -1;
+            if (frame >= p.frames || frame - f0 >= kScanRound) break;
+        }
+        // the LDS decision and key slots are rewritten next round
+        __syncthreads();
     }
     if (blk == 0 && threadIdx.x == 0) {
         p.state[0] = frame;
@@ -366,20 +416,23 @@ __global__ __launch_bounds__(256) void joint_scan_kernel(ScanArgs p) {
     }
 }
 
-__global__ void scan_clear_kernel(uint32_t* ws) { ws[threadIdx.x] = 0u; }
+__global__ void scan_clear_kernel(uint32_t* ws) {
+    for (int i = threadIdx.x; i < kJointScanWorkspaceWords; i += blockDim.x) ws[i] = 0u;
+}
 
 int launch_joint_scan(const void* w, int w_int8, const float* w_scales, const float* bias, const uint16_t* enc, const float* pred,
                       int outputs, int hidden, int token_outputs, int durations, int frames, int enc_stride, int max_symbols,
                       int* state, uint32_t* workspace, hipStream_t s) {
     const int active = (token_outputs + durations + 4 * kScanRows - 1) / (4 * kScanRows);
     ScanArgs a{w, w_scales, bias, enc, pred, state, workspace, outputs, hidden, token_outputs, durations, frames, enc_stride, max_symbols};
-    scan_clear_kernel<<<1, kJointScanWorkspaceWords, 0, s>>>(workspace);
+    scan_clear_kernel<<<1, 256, 0, s>>>(workspace);
     const dim3 grid(8 * active);
+    const size_t win = (size_t)kScanWin * (hidden / 2) * sizeof(uint32_t);
     switch (hidden >> 7) {
 #define PK_SCAN_CASE(KP)                                                              \
     case KP:                                                                          \
-        if (w_int8) joint_scan_kernel<true, KP><<<grid, 256, 0, s>>>(a);             \
-        else joint_scan_kernel<false, KP><<<grid, 256, 0, s>>>(a);                   \
+        if (w_int8) joint_scan_kernel<true, KP><<<grid, 256, win, s>>>(a);           \
+        else joint_scan_kernel<false, KP><<<grid, 256, win, s>>>(a);                 \
         break;
         PK_SCAN_CASE(1) PK_SCAN_CASE(2) PK_SCAN_CASE(3) PK_SCAN_CASE(4)
         PK_SCAN_CASE(5) PK_SCAN_CASE(6) PK_SCAN_CASE(7) PK_SCAN_CASE(8)

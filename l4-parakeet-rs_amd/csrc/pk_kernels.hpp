@@ -36,7 +36,8 @@ int launch_joint(const void* w, int w_int8, const float* w_scales, const float* 
                  float* scores, int* decision, int outputs, int hidden, int token_outputs, int durations, int steps,
                  int enc_stride, hipStream_t s);
 
-constexpr int kJointScanWorkspaceWords = 512;
+// abort flag + 2 parities x 8 round frames x 64 workgroups of published u64 words
+constexpr int kJointScanWorkspaceWords = 2304;
 int launch_joint_scan(const void* w, int w_int8, const float* w_scales, const float* bias, const uint16_t* enc, const float* pred,
                       int outputs, int hidden, int token_outputs, int durations, int frames, int enc_stride, int max_symbols,
                       int* state, uint32_t* workspace, hipStream_t s);

@@ -683,7 +683,7 @@ def test_joint_scan(pk, orc, int8):
         score = lambda t, pred: orc.joint_scores_f16(w, bias, enc[t], pred)
     d_bias, d_enc = dev(bias), dev(enc)
     state = torch.zeros(4, dtype=torch.int32, device="cuda")
-    work = torch.zeros(512, dtype=torch.int32, device="cuda")
+    work = torch.zeros(2304, dtype=torch.int32, device="cuda")
     frame = symbols = 0
     tokens, scans = [], 0
     while True:

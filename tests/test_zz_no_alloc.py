@@ -51,7 +51,7 @@ def scan(pk, c, start, noalloc):
     if noalloc:
         pk.call("pk_joint_scan_noalloc", *args)
     else:
-        work = torch.full((512,), -1, dtype=torch.int32, device="cuda")  # garbage the call must clear
+        work = torch.full((2304,), -1, dtype=torch.int32, device="cuda")  # garbage the call must clear
         pk.call("pk_joint_scan", *args, work)
     torch.cuda.synchronize()
     return tuple(int(v) for v in state.cpu())
