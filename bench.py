@@ -812,7 +812,7 @@ def joint_bench(pk, torch, stream, reps=2000):
 
     # Effective GB/s = the step's weight bytes / its time. Only single_launch
     # reads W from memory each step; batched and scan keep W on chip (L2 /
-    # registers), so their figure is not HBM traffic and gets no HBM fraction
+    # registers), so their figure is not HBM traffic (pct_hbm is only that ratio to 8 TB/s)
     # (kernel_bandwidth_yardstick_stacked is the HBM-bound measurement of the same kernel).
     # batch-1 per-step latency first (the workload: one joint per greedy step)
     out = {"per_step_batch1": {}, "bytes_per_step": nbytes}

@@ -22,6 +22,15 @@
  *     256 for packed INT4, 64 for FP16) and N a multiple of 16; M is free
  *     (the reference pads M to 16, N to 128 and K to 128, which satisfies
  *     this).  Operand base pointers must be 16-byte aligned.
+ *   - Every GEMM entry point (pk_gemm, the pk_linear_* linears and the encoder
+ *     wrappers) also needs 16-byte aligned bias, weight-scale and residual
+ *     pointers: the epilogue reads them as 16-byte vectors, so a slice at a
+ *     4-byte offset returns PK_E_ALIGN (copy it to an aligned buffer first).
+ *   - Results do not depend on M or on the GPU's CU count, with one stated
+ *     exception: INT4-g128 launches on small grids that split K over the
+ *     waves of a workgroup (pk_gemm_k_split reports 4) fold the group sums
+ *     by parts, so their fp32 results are associated differently from the
+ *     same rows' on a large grid (each part is exact; see pk_gemm_k_split).
  */
 #ifndef PK_LINEAR_H
 #define PK_LINEAR_H
@@ -370,7 +379,8 @@ int32_t pk_ffn_contract_int8_rowskip(const int8_t* input, const float* input_sca
  * two positions the selection did not keep, ascending, with their bytes, in
  * the layout of data / meta.  k % 128 == 0, k <= 4096; input 16-byte
  * aligned, data / residual_data / overflow / overflow_counts 4-byte aligned.
- * Rows >= valid_rows are zero, scale 1. */
+ * Rows >= valid_rows are zero, scale 1.  Other k are for other consumers:
+ * pk_ffn_contract_int8_sparse24 reads only k = 4096 buffers. */
 int32_t pk_quantize_rows_int8_sparse24(const uint16_t* input, uint8_t* data, uint8_t* meta, float* scales,
                                        uint32_t* overflow_counts, uint32_t* overflow, uint8_t* residual_data,
                                        uint8_t* residual_meta, int32_t rows, int32_t valid_rows, int32_t k, void* stream);
@@ -384,7 +394,9 @@ int32_t pk_transpose_int8(const int8_t* weight, int8_t* weight_t, int32_t n, int
  * whose rows hold more than 8 overflow entries each on average add the
  * residual 2:4 form in a second sparse pass instead of walking the lists.
  * data, meta, residual data / meta, weight, weight_t, weight_scales and
- * output 16-byte aligned. */
+ * output 16-byte aligned.  The contract is the FF2 shape only (n = 1024,
+ * k = 4096): data / metadata / overflow / residual buffers must come from
+ * pk_quantize_rows_int8_sparse24 with k = 4096. */
 int32_t pk_ffn_contract_int8_sparse24(const uint8_t* data, const uint8_t* meta, const float* input_scales,
                                       const uint32_t* overflow_counts, const uint32_t* overflow, const uint8_t* residual_data,
                                       const uint8_t* residual_meta, const int8_t* weight, const int8_t* weight_t,

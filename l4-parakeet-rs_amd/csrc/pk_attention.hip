@@ -395,7 +395,7 @@ __device__ void attention_query(float* scores, const uint16_t* __restrict__ quer
     float mx = -FLT_MAX;
     for (int slot = lane; slot < count; slot += 64) mx = __builtin_fmaxf(mx, scores[slot]);
     mx = wave_max(mx);
-    for (int slot = lane; slot < count; slot += 64) scores[slot] = expf(scores[slot] - mx);
+    for (int slot = lane; slot < count; slot += 64) scores[slot] = softmax_exp(scores[slot] - mx);
     wave_sync();
     float den = 0.0f;
     if (lane < 32)

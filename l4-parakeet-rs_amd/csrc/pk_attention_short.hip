@@ -154,7 +154,7 @@ __global__ __launch_bounds__(256) void attention_short_kernel(ShortArgs a) {
     mx = wave_max(mx);
     float den = 0.0f;
     for (int slot = lane; slot < count; slot += 64) {
-        const float e = expf(sc[slot] - mx);
+        const float e = __expf(sc[slot] - mx);  // the reference's fast-math exponential (build.rs:68-73)
         sc[slot] = e;
         den += e;
     }

@@ -40,6 +40,14 @@ __device__ __forceinline__ uint32_t asm_load1(const void* ptr) {
     asm volatile("global_load_dword %0, %1, off" : "=v"(r) : "v"(ptr) : "memory");
     return r;
 }
+// A 16-byte global store issued from inline asm: the deferred epilogue below
+// waits for the next tile's loads with vmcnt(its store count), which is exact
+// only if every store it makes is one instruction the compiler cannot split,
+// merge, predicate away or move past that wait.
+__device__ __forceinline__ void asm_store4(void* ptr, uint4 v) {
+    const v4i x = __builtin_bit_cast(v4i, v);
+    asm volatile("global_store_dwordx4 %0, %1, off" ::"v"(ptr), "v"(x) : "memory");
+}
 __device__ __forceinline__ uint32_t launder(uint32_t x) {
     asm volatile("" : "+v"(x));
     return x;
@@ -120,9 +128,10 @@ __device__ __forceinline__ void epilogue_defer(const GemmArgs& p, v4f (&accf)[kA
         }
         if constexpr (E == EPI_F32) {
             if (live) {
-                float4* o = (float4*)((float*)p.out + (size_t)grow * p.ldo + gcol);
+                float* o = (float*)p.out + (size_t)grow * p.ldo + gcol;
 #pragma unroll
-                for (int j = 0; j < 4; ++j) o[j] = float4{v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]};
+                for (int j = 0; j < 4; ++j)
+                    asm_store4(o + 4 * j, __builtin_bit_cast(uint4, float4{v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]}));
             }
         } else if constexpr (E == EPI_F16) {
             uint32_t h[8];
@@ -134,9 +143,9 @@ __device__ __forceinline__ void epilogue_defer(const GemmArgs& p, v4f (&accf)[kA
                 h[j] = (uint32_t)f2h(x0) | ((uint32_t)f2h(x1) << 16);
             }
             if (live) {
-                uint4* o = (uint4*)((uint16_t*)p.out + (size_t)grow * p.ldo + gcol);
-                o[0] = uint4{h[0], h[1], h[2], h[3]};
-                o[1] = uint4{h[4], h[5], h[6], h[7]};
+                uint16_t* o = (uint16_t*)p.out + (size_t)grow * p.ldo + gcol;
+                asm_store4(o, uint4{h[0], h[1], h[2], h[3]});
+                asm_store4(o + 8, uint4{h[4], h[5], h[6], h[7]});
             }
         } else {
             uint32_t w[4];
@@ -334,6 +343,8 @@ __global__ __launch_bounds__(kThreads, 2) void gemm3_kernel(GemmArgs p) {
     // step of the next tile then waits for them with vmcnt(stores issued
     // since), not for the epilogue's stores (QKV at T = 45000: 174 -> 162 us).
     constexpr bool kDefer = kAhead2 && (E == EPI_F16 || E == EPI_F32);
+    // stores of one deferred epilogue: asm_store4 instructions, 2 (fp16) or 4
+    // (fp32) per row block of a wave, every one issued when the tile is full
     constexpr int kStores = kAI * (E == EPI_F16 ? 2 : 4);
     bool prev_full = false;  // the last epilogue issued all kStores stores
 
