@@ -472,11 +472,15 @@ __global__ __launch_bounds__(kThreads, 2) void gemm3_kernel(GemmArgs p) {
                 }
             } else if constexpr (F == FMT_G128F8) {
                 // One MFMA per block and 128-K group: its fp32 group sum goes
-                // to one of three rotating registers while block b - 2's is
-                // scaled into the accumulators (one fma per value).
-                v4f gf[3];
+                // to one of two rotating registers while block b - 1's is
+                // scaled into the accumulators (one fma per value).  Issue
+                // order left to the compiler: at a distance of one block and
+                // without sched_group_barrier pinning the contract runs
+                // 255.6 us against 279.5 us at a distance of two with the
+                // MFMA / VALU interleave pinned (T = 45000, N = 1024, K = 4096).
+                v4f gf[2];
 #pragma unroll
-                for (int b = 0; b < 4 * kAI + 2; ++b) {
+                for (int b = 0; b < 4 * kAI + 1; ++b) {
                     const int ai = b >> 2, bj = b & 3;
                     if (b < 4 * kAI) {
                         if (bj == 0 && ai + 1 < kAI) {
@@ -487,25 +491,17 @@ __global__ __launch_bounds__(kThreads, 2) void gemm3_kernel(GemmArgs p) {
                         const v8i W = {(int)w0[bj].x, (int)w0[bj].y, (int)w0[bj].z, (int)w0[bj].w,
                                        (int)w1[bj].x, (int)w1[bj].y, (int)w1[bj].z, (int)w1[bj].w};
                         const v8i X = {(int)x0.x, (int)x0.y, (int)x0.z, (int)x0.w, (int)x1.x, (int)x1.y, (int)x1.z, (int)x1.w};
-                        gf[b % 3] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(W, X, v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0, 0, 0, 0);
+                        gf[b & 1] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(W, X, v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0, 0, 0, 0);
                         if (bj == 3) {
                             x0 = y0;
                             x1 = y1;
                         }
                     }
-                    if (b >= 2) {
-                        const int pa = (b - 2) >> 2, pj = (b - 2) & 3;
+                    if (b >= 1) {
+                        const int pa = (b - 1) >> 2, pj = (b - 1) & 3;
 #pragma unroll
-                        for (int r = 0; r < 4; ++r) accf[pa][pj][r] = __builtin_fmaf(gf[(b - 2) % 3][r], gs[pj][r], accf[pa][pj][r]);
+                        for (int r = 0; r < 4; ++r) accf[pa][pj][r] = __builtin_fmaf(gf[(b - 1) & 1][r], gs[pj][r], accf[pa][pj][r]);
                     }
-                }
-#pragma unroll
-                for (int b = 0; b < 4 * kAI + 2; ++b) {
-                    if (b < 4 * kAI) {
-                        if ((b & 3) == 0 && (b >> 2) + 1 < kAI) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                    }
-                    if (b >= 2) __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
                 }
             } else if constexpr (kAhead2) {
 #pragma unroll
