@@ -1448,8 +1448,11 @@ def main():
         "local_attention": attention,
         "roofline": {"kernel": top["kernel"] + f" ({dom[0]} {dom[1]} {dom[3]}->{dom[2]}, T={args.frames})",
                      "bound": "mfma", "achieved": round(k_tflops, 2), "peak": PEAK["fp8"],
-                     "unit": "TFLOP/s" if dom[0] == "fp8" else "TOP/s", "frac": round(k_tflops / PEAK["fp8"], 4),
-                     "traffic": measured_traffic(dom), "avg_ms": round(k_ms, 4), "flop_per_launch": k_flops,
+                     "unit": "TFLOP/s" if (dom[0] == "fp8" or (dom[0] == "int4g128" and dom[1] == "res" and dom[3] == FF)) else "TOP/s", "frac": round(k_tflops / PEAK["fp8"], 4),
+                     "traffic": measured_traffic(dom),
+                     "traffic_source": os.path.relpath(traffic_file(dom), ROOT) + " (committed rocprofv3 FETCH_SIZE / "
+                                       "WRITE_SIZE passes over bench.py --only-dominant, copy-calibrated; not this run)",
+                     "avg_ms": round(k_ms, 4), "flop_per_launch": k_flops,
                      "algorithmic_bytes": k_bytes, "stack_share": round(top["step_ms"] / ms_step, 4),
                      "dominant_as_committed": dom == DOMINANT,
                      "ff1_expand_fp8": {"kernel": "g3::gemm3_kernel<FP8, EPI_F8 (e4m3 SiLU), 256-row tiles>",
