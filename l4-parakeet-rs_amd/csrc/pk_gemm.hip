@@ -92,22 +92,25 @@ static int launch_ring(const GemmArgs& a, hipStream_t s) {
     return 0;
 }
 
-// One 32-row tile per workgroup with K split over its 4 waves (INT4-g128
-// formats, grids that take 32-row ring tiles, K >= 1024).
-template <int F, int E>
+// One 32-row tile per workgroup with K split in four parts, each part's
+// ring shared by kCH waves that take 128 / kCH columns each (INT4-g128
+// formats, grids that take 32-row ring tiles, K >= 1024).  kCH = 4 (16 waves)
+// by measurement: C3 FF2 at T = 750 x INT8 / x fp16 14.8 / 23.4 us with 8
+// waves, 13.5 / 22.8 with 16 (4 waves, one per SIMD: 17.0 / 24.9).
+template <int F, int E, int kCH>
 static int launch_splitk(const GemmArgs& a, hipStream_t s) {
-    using L = g3::LK<F>;
+    using L = g3::LK<F, kCH>;
     static std::once_flag once;
     static hipError_t attr = hipSuccess;
     std::call_once(once, [] {
-        attr = hipFuncSetAttribute((const void*)g3::gemm3_splitk_kernel<F, E>, hipFuncAttributeMaxDynamicSharedMemorySize, L::kBytes);
+        attr = hipFuncSetAttribute((const void*)g3::gemm3_splitk_kernel<F, E, kCH>, hipFuncAttributeMaxDynamicSharedMemorySize, L::kBytes);
     });
     if (attr != hipSuccess) {
         set_error("hipFuncSetAttribute(LDS %d bytes) failed: %s", L::kBytes, hipGetErrorString(attr));
         return -3;
     }
     const int tiles = ((a.m + L::kBM - 1) / L::kBM) * ((a.n + g3::kBN - 1) / g3::kBN);
-    hipLaunchKernelGGL((g3::gemm3_splitk_kernel<F, E>), dim3(tiles), dim3(g3::kThreads), L::kBytes, s, a);
+    hipLaunchKernelGGL((g3::gemm3_splitk_kernel<F, E, kCH>), dim3(tiles), dim3(L::kThreads), L::kBytes, s, a);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
         set_error("gemm launch (fmt %d, epi %d) failed: %s", F, E, hipGetErrorString(e));
@@ -117,14 +120,15 @@ static int launch_splitk(const GemmArgs& a, hipStream_t s) {
 }
 
 // Formats with a ring variant and the tile rows it takes for an m x n
-// output: the smallest tile (32, 64 or 128 rows) whose tile count fits one
-// workgroup per CU, or 0 when even 128-row tiles outnumber the CUs.
+// output: the smallest tile (32, 64, 96 (INT4-g128 x fp16 only) or 128 rows)
+// whose tile count fits one workgroup per CU, or 0 when even 128-row tiles
+// outnumber the CUs.
 static bool has_ring(int fmt, int epi) {
     return (fmt == FMT_FP8 || fmt == FMT_I8 || fmt == FMT_G128A8 || fmt == FMT_G128A16) && epi != EPI_GLU && epi != EPI_F8_24 &&
            epi != EPI_I8S;
 }
 template <int F> static int ring_stages_of(int kAI) {
-    return kAI == 1 ? g3::LS<F, 1>::kS : (kAI == 2 ? g3::LS<F, 2>::kS : g3::LS<F, 4>::kS);
+    return kAI == 1 ? g3::LS<F, 1>::kS : (kAI == 2 ? g3::LS<F, 2>::kS : (kAI == 3 ? g3::LS<F, 3>::kS : g3::LS<F, 4>::kS));
 }
 static int ring_stages(int fmt, int kAI) {
     switch (fmt) {
@@ -139,24 +143,30 @@ static int ring_stages(int fmt, int kAI) {
 // rings of 16 KiB stages, 68 KiB each): twice the workgroups for the chain of
 // K-steps (C3 FF1 at T = 750, 384 tiles: 16.6 -> 14.2 us).  Measured and not
 // taken for INT8 (C1: 13.4 vs 13.5 us) and INT4-g128 x fp16 (23.2 -> 24.9 us).
-static int ring_rows(int m, int n);
+static int ring_rows(int fmt, int m, int n);
 static bool ring_occ2(int fmt, int m, int n) {
-    if (fmt != FMT_G128A8 || ring_rows(m, n) != 128) return false;
+    if (fmt != FMT_G128A8 || ring_rows(fmt, m, n) != 128) return false;
     return ((m + 63) / 64) * ((n + g3::kBN - 1) / g3::kBN) <= 2 * cu_count();
 }
 
 // The K split of a launch: 4 (gemm3_splitk_kernel) for the INT4-g128 formats
 // when the ring takes 32-row tiles and K >= 1024 (C3 FF2 at T = 750: the ring
-// kernel's 64 / 32 K-steps per tile become 16 / 8 per wave), else 1.
+// kernel's 64 / 32 K-steps per tile become 16 / 8 per part), else 1.
 static int k_split(int fmt, int epi, int m, int n, int k) {
     if ((fmt != FMT_G128A8 && fmt != FMT_G128A16) || !has_ring(fmt, epi) || k < 1024) return 1;
-    return ring_rows(m, n) == 32 ? 4 : 1;
+    return ring_rows(fmt, m, n) == 32 ? 4 : 1;
 }
-static int ring_rows(int m, int n) {
+static int ring_rows(int fmt, int m, int n) {
     if (forced_tile_rows() != 0) return 0;
     const int cols = (n + g3::kBN - 1) / g3::kBN;
-    for (int rows = 32; rows <= 128; rows *= 2)
+    for (int rows = 32; rows <= 128; rows += 32) {
+        // 96-row tiles (every CU busy where 128-row tiles leave a quarter
+        // idle, e.g. 750 x 4096: 256 vs 192 tiles) pay for INT4-g128 x fp16
+        // only (C3 FF1 at T = 750: 22.7 -> 19.2 us); measured slower for INT8
+        // (12.8 -> 14.3 us) and INT4-g128 x INT8, equal for FP8
+        if (rows == 96 && fmt != FMT_G128A16) continue;
         if (((m + rows - 1) / rows) * cols <= cu_count()) return rows;
+    }
     return 0;
 }
 
@@ -214,7 +224,7 @@ static int tile_plan(int fmt, int epi, int m, int n, int* cols, int* stages) {
             *stages = g3::LS<FMT_G128A8, 2, 2>::kS;
             return 64;
         }
-        const int r = ring_rows(m, n);
+        const int r = ring_rows(fmt, m, n);
         if (r) {
             *stages = ring_stages(fmt, r / 32);
             return r;
@@ -241,7 +251,7 @@ static int launch_fmt(const GemmArgs& a, hipStream_t s) {
     const int rows = tile_plan(F, E == EPI_F16_RES ? EPI_F16 : E, a.m, a.n, &cols, &stages);
     if constexpr (F == FMT_G128A8 || F == FMT_G128A16) {
         if constexpr (E != EPI_GLU && E != EPI_F8_24 && E != EPI_I8S) {
-            if (k_split(F, E == EPI_F16_RES ? EPI_F16 : E, a.m, a.n, a.k) == 4) return launch_splitk<F, E>(a, s);
+            if (k_split(F, E == EPI_F16_RES ? EPI_F16 : E, a.m, a.n, a.k) == 4) return launch_splitk<F, E, 4>(a, s);
         }
     }
     if constexpr (F == FMT_FP8 || F == FMT_I8 || F == FMT_G128A8 || F == FMT_G128A16) {
@@ -249,6 +259,9 @@ static int launch_fmt(const GemmArgs& a, hipStream_t s) {
             if (stages > 2) {
                 if constexpr (F == FMT_G128A8) {
                     if (ring_occ2(F, a.m, a.n)) return launch_ring<F, E, 2, 2>(a, s);
+                }
+                if constexpr (F == FMT_G128A16) {
+                    if (rows == 96) return launch_ring<F, E, 3>(a, s);
                 }
                 return rows == 32 ? launch_ring<F, E, 1>(a, s) : (rows == 64 ? launch_ring<F, E, 2>(a, s) : launch_ring<F, E, 4>(a, s));
             }

@@ -26,6 +26,55 @@ namespace g3 {
 
 constexpr int kBN = 128, kThreads = 256;
 
+// Group tables of one 128-column tile for all K groups, laid out
+// [group][column] in LDS: scales (fp32, or the fp16 bits when S is
+// uint16_t) and u8 zero points.  The tile's rows of the [N x groups] fp16
+// tables are one contiguous run of 128 * groups halves; when groups % 8 == 0
+// (<= 32), every column is in range and the tables are 16-byte aligned, it is
+// read with 16-byte loads, all issued before the first LDS write (one load
+// latency instead of one per element the threads loop over).
+template <typename S, int kT = kThreads>
+__device__ __forceinline__ void load_group_tables(const GemmArgs& p, int n0, int groups, S* tab_s, uint8_t* tab_z, int tid) {
+    const bool vec = (groups & 7) == 0 && n0 + kBN <= p.n &&
+                     ((((uintptr_t)p.g_scales) | ((uintptr_t)p.g_zeros)) & 15) == 0;
+    if (vec) {
+        const int chunks = kBN * groups / 8;  // <= 512 for groups <= 32
+        const uint4* gs = (const uint4*)(p.g_scales + (size_t)n0 * groups);
+        const uint4* gz = (const uint4*)(p.g_zeros + (size_t)n0 * groups);
+        uint4 vs[2], vz[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int c = tid + i * kT;
+            vs[i] = c < chunks ? gs[c] : uint4{0, 0, 0, 0};
+            vz[i] = c < chunks ? gz[c] : uint4{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int c = tid + i * kT;
+            if (c >= chunks) continue;
+            const int e = c * 8, col = e / groups, grp = e % groups;
+            const uint32_t sw[4] = {vs[i].x, vs[i].y, vs[i].z, vs[i].w};
+            const uint32_t zw[4] = {vz[i].x, vz[i].y, vz[i].z, vz[i].w};
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const uint16_t sh = (uint16_t)(sw[j >> 1] >> ((j & 1) * 16));
+                const uint16_t zh = (uint16_t)(zw[j >> 1] >> ((j & 1) * 16));
+                if constexpr (sizeof(S) == 4) tab_s[(grp + j) * kBN + col] = h2f(sh);
+                else tab_s[(grp + j) * kBN + col] = sh;
+                tab_z[(grp + j) * kBN + col] = (uint8_t)(int)h2f(zh);
+            }
+        }
+        return;
+    }
+    for (int e = tid; e < kBN * groups; e += kT) {
+        const int col = e % kBN, grp = e / kBN;
+        const size_t gi = (size_t)min(n0 + col, p.n - 1) * groups + grp;
+        if constexpr (sizeof(S) == 4) tab_s[grp * kBN + col] = h2f(p.g_scales[gi]);
+        else tab_s[grp * kBN + col] = p.g_scales[gi];
+        tab_z[grp * kBN + col] = (uint8_t)(int)h2f(p.g_zeros[gi]);
+    }
+}
+
 // Loads issued from inline asm are invisible to the compiler's wait
 // insertion: the code waits for them with an explicit s_waitcnt and then
 // passes the destinations through an empty asm (launder), so that no use is
@@ -689,14 +738,7 @@ __global__ __launch_bounds__(kThreads, kOcc) void gemm3_ring_kernel(GemmArgs p) 
     // Group tables of the tile's columns, all K groups, loaded after the
     // first stages (whose latency they share): [group][column] fp32 scales
     // and u8 zero points.
-    if constexpr (L::kG128) {
-        for (int e = tid; e < kBN * groups; e += kThreads) {
-            const int col = e % kBN, grp = e / kBN;
-            const size_t gi = (size_t)min(n0 + col, p.n - 1) * groups + grp;
-            tab_s[grp * kBN + col] = h2f(p.g_scales[gi]);
-            tab_z[grp * kBN + col] = (uint8_t)(int)h2f(p.g_zeros[gi]);
-        }
-    }
+    if constexpr (L::kG128) load_group_tables(p, n0, groups, tab_s, tab_z, tid);
 
     v4f accf[kAI][4];
     v4i acci[kAI][4];
@@ -745,21 +787,25 @@ __global__ __launch_bounds__(kThreads, kOcc) void gemm3_ring_kernel(GemmArgs p) 
 
 // ---- small grids, long K: one 32 x 128 tile per workgroup, K split over its 4 waves ----
 //
-// For the group-wise INT4 formats at small T (BASELINE config 3 at T = 750:
-// 192 tiles of 32 rows for FF2, K = 4096) the ring kernel above is a chain of
-// K-steps whose every link is an LDS read, the INT4 decode and the MFMAs; the
-// tile count cannot grow.  Here each wave takes a quarter of the K-steps and
-// computes the whole 32 x 128 tile (2 x 8 blocks of 16 x 16) over it, with a
-// private LDS ring (its own direct-to-LDS loads, waited for by vmcnt; no
-// barrier inside the K-loop), so the chain is a quarter as long.  The group
-// tables of the tile's columns (fp16 scales, u8 zero points, all groups) are
-// loaded once.  Then the four partial tiles meet in LDS and wave q adds the
-// partials of quarter q in K order, ((p0 + p1) + p2) + p3, and runs the
-// epilogue of the ring kernel's wave q on them.  Within a part the arithmetic
-// is the ring kernel's (INT4-g128 x INT8: exact int32 group sums, each scaled
-// and added in group order), so the result is the ring kernel's with the fp32
-// sum over groups associated by parts.
-template <int F> struct LK {
+// For the group-wise INT4 formats at small T (FF2 at T = 750: 192 tiles of
+// 32 rows, K = 4096) the ring kernel above is a chain of K-steps whose every
+// link is an LDS read, the INT4 decode and the MFMAs; the tile count cannot
+// grow.  Here the workgroup has 4 kCH waves: K-part kp = wave % 4 takes a
+// quarter of the K-steps through a private LDS ring, and the part's kCH
+// waves (column slice ch = wave / 4) share that ring, each computing 32 rows
+// x 128 / kCH columns (2 x 4 / (kCH / 2) blocks of 16 x 16) over it: kCH
+// waves per SIMD hide each other's LDS and decode latency, and the chain is a
+// quarter as long.  Each wave of a part issues its share of the stage's
+// direct-to-LDS loads and waits for its own (vmcnt); one barrier per K-step
+// makes the whole stage visible and frees the slot refilled after it.  The group tables of the tile's columns
+// (fp16 scales, u8 zero points, all groups) are loaded once.  Then the four
+// parts meet in LDS and wave q < 4 adds the partials of quarter q (rows
+// 16 (q / 2), columns 64 (q % 2)) in K order, ((p0 + p1) + p2) + p3, and runs
+// the ring kernel's epilogue of its wave q on them.  Within a part the
+// arithmetic is the ring kernel's (INT4-g128 x INT8: exact int32 group sums,
+// each scaled and added in group order), so the result is the ring kernel's
+// with the fp32 sum over groups associated by parts.
+template <int F, int kCH> struct LK {
     static constexpr int kBM = 32;
     static constexpr int kATile = kBM * kRowBytes;
     static constexpr int kBTile = kBN * FmtTraits<F>::bRow;
@@ -767,23 +813,27 @@ template <int F> struct LK {
     static constexpr int kTabBytes = kMaxG128Groups * kBN * 3;  // fp16 scales + u8 zero points [group][column]
     static constexpr int kFit = (160 * 1024 - kTabBytes) / (4 * kStage);
     static constexpr int kS = kFit > 4 ? 4 : kFit;
-    static constexpr int kWave = kS * kStage;  // one wave's ring
-    static constexpr int kTab = 4 * kWave;
+    static constexpr int kPart = kS * kStage;  // one K-part's ring
+    static constexpr int kTab = 4 * kPart;
     static constexpr int kBytes = kTab + kTabBytes;
     static constexpr int kBLoads = kBTile / 1024;
-    static constexpr int kOps = 4 + kBLoads;  // direct-to-LDS loads per wave and stage
-    static constexpr int kRed = 16 * 64 * 64;  // partials [quarter][wave][block][lane] x 4 floats
-    static_assert(kS >= 2 && kS <= 4 && kBytes <= 160 * 1024 && kRed <= kTab, "split-K layout");
+    static constexpr int kThreads = 256 * kCH;
+    static constexpr int kAW = 4 / kCH, kBW = kBLoads / kCH;  // a wave's share of a stage's loads
+    static constexpr int kOps = kAW + kBW;                    // direct-to-LDS loads per wave and stage
+    static constexpr int kRed = 16 * 64 * 64;     // partials [quarter][part][block][lane] x 4 floats
+    static_assert(kS >= 2 && kS <= 4 && kBytes <= 160 * 1024 && kRed <= kTab && kBLoads % kCH == 0, "split-K layout");
 };
 
-template <int F, int E>
-__global__ __launch_bounds__(kThreads, 1) void gemm3_splitk_kernel(GemmArgs p) {
+template <int F, int E, int kCH>
+__global__ __launch_bounds__(256 * kCH, 1) void gemm3_splitk_kernel(GemmArgs p) {
     static_assert(F == FMT_G128A8 || F == FMT_G128A16, "group-wise INT4 formats");
     using T = FmtTraits<F>;
-    using L = LK<F>;
+    using L = LK<F, kCH>;
+    constexpr int kNB = 4 / (kCH / 2);  // 16-column blocks per wave (64 or 32 columns)
     constexpr int kS = L::kS;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int kp = wave & 3, ch = wave >> 2;
     const int g = lane >> 4, l16 = lane & 15;
     const int tiles_n = (p.n + kBN - 1) / kBN;
     const int tiles_m = (p.m + L::kBM - 1) / L::kBM;
@@ -794,25 +844,31 @@ __global__ __launch_bounds__(kThreads, 1) void gemm3_splitk_kernel(GemmArgs p) {
     const size_t ldb = (size_t)p.k * T::bNum / T::bDen;
     const int steps = p.k / T::kStep;
     const int groups = p.k >> 7;
-    // this wave's K-steps (wave-uniform: the loads' global base is a scalar operand)
-    const int s0 = __builtin_amdgcn_readfirstlane(steps * wave / 4);
-    const int ns = __builtin_amdgcn_readfirstlane(steps * (wave + 1) / 4) - s0;
+    // this part's K-steps (wave-uniform: the loads' global base is a scalar
+    // operand); part sizes differ by at most one, and every wave runs the
+    // longest part's iteration count so that all 8 meet at every barrier
+    const int s0 = __builtin_amdgcn_readfirstlane(steps * kp / 4);
+    const int ns = __builtin_amdgcn_readfirstlane(steps * (kp + 1) / 4) - s0;
+    const int nmax = (steps + 3) / 4;
     const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)lds;
-    const uint32_t ring = lds_base + (uint32_t)(wave * L::kWave);
+    const uint32_t ring = lds_base + (uint32_t)(kp * L::kPart);
     uint16_t* tab_s = (uint16_t*)(lds + L::kTab);
     uint8_t* tab_z = lds + L::kTab + kMaxG128Groups * kBN * 2;
 
-    // activation load i: tile rows 8i + lane / 8, 16-byte chunk position lane % 8
-    // (holding source chunk position ^ swz_key(row)); weight loads as the ring kernel's
-    uint32_t a_off[4], b_off[L::kBLoads];
+    // this wave's half of a stage: activation loads 2 half + i (tile rows
+    // 8 (2 half + i) + lane / 8, 16-byte chunk position lane % 8 holding source
+    // chunk position ^ swz_key(row)); weight loads kBLoads / 2 * half + i as
+    // the ring kernel's
+    constexpr int kAW = L::kAW, kHB = L::kBW;
+    uint32_t a_off[kAW], b_off[kHB];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int r = 8 * i + (lane >> 3);
+    for (int i = 0; i < kAW; ++i) {
+        const int r = 8 * (kAW * ch + i) + (lane >> 3);
         a_off[i] = (uint32_t)min(m0 + r, p.m - 1) * (uint32_t)lda + (uint32_t)((((lane & 7) ^ swz_key(r))) << 4);
     }
 #pragma unroll
-    for (int i = 0; i < L::kBLoads; ++i) {
-        const int o = i * 1024 + lane * 16;
+    for (int i = 0; i < kHB; ++i) {
+        const int o = (kHB * ch + i) * 1024 + lane * 16;
         int row, c;
         if constexpr (F == FMT_G128A8) {
             row = o >> 6;
@@ -827,37 +883,38 @@ __global__ __launch_bounds__(kThreads, 1) void gemm3_splitk_kernel(GemmArgs p) {
         const int step = s0 + j;
         const uint32_t base = ring + (uint32_t)((j % kS) * L::kStage);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) dma16(p.a + (size_t)step * kRowBytes, a_off[i], base + i * 1024);
+        for (int i = 0; i < kAW; ++i) dma16(p.a + (size_t)step * kRowBytes, a_off[i], base + (kAW * ch + i) * 1024);
 #pragma unroll
-        for (int i = 0; i < L::kBLoads; ++i) dma16(p.b + (size_t)step * T::bRow, b_off[i], base + L::kATile + i * 1024);
+        for (int i = 0; i < kHB; ++i)
+            dma16(p.b + (size_t)step * T::bRow, b_off[i], base + L::kATile + (kHB * ch + i) * 1024);
     };
     const int pre = min(kS - 1, ns);
     for (int j = 0; j < pre; ++j) issue(j);
-    for (int e = tid; e < kBN * groups; e += kThreads) {
-        const int col = e % kBN, grp = e / kBN;
-        const size_t gi = (size_t)min(n0 + col, p.n - 1) * groups + grp;
-        tab_s[grp * kBN + col] = p.g_scales[gi];
-        tab_z[grp * kBN + col] = (uint8_t)(int)h2f(p.g_zeros[gi]);
-    }
-    __syncthreads();
+    load_group_tables<uint16_t, L::kThreads>(p, n0, groups, tab_s, tab_z, tid);
 
-    v4f accf[2][8];
-    v4i acci[2][8];
+    // this wave's columns: 64-column half cw, blocks bj0 .. bj0 + kNB - 1 of it
+    const int cw = kCH == 2 ? ch : ch >> 1, bj0 = kCH == 2 ? 0 : (ch & 1) * 2;
+    v4f accf[2][kNB];
+    v4i acci[2][kNB];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int c = 0; c < 8; ++c) {
+        for (int c = 0; c < kNB; ++c) {
             accf[i][c] = v4f{0.f, 0.f, 0.f, 0.f};
             acci[i][c] = v4i{0, 0, 0, 0};
         }
-    for (int j = 0; j < ns; ++j) {
-        switch (min(j + kS - 2, ns - 1) - j) {  // younger stages still loading: 0 .. kS - 2 <= 2
-        case 0: wait_vm<0>(); break;
-        case 1: wait_vm<L::kOps>(); break;
-        default: wait_vm<2 * L::kOps>(); break;
+    for (int j = 0; j < nmax; ++j) {
+        if (j < ns) {
+            switch (min(j + kS - 2, ns - 1) - j) {  // younger stages still loading: 0 .. kS - 2 <= 2
+            case 0: wait_vm<0>(); break;
+            case 1: wait_vm<L::kOps>(); break;
+            default: wait_vm<2 * L::kOps>(); break;
+            }
         }
+        __syncthreads();  // the partner's half of stage j has landed; slot j - 1 is free (and, at j = 0, the tables)
+        if (j >= ns) continue;
         if (j + kS - 1 < ns) issue(j + kS - 1);
-        const uint8_t* As = lds + wave * L::kWave + (j % kS) * L::kStage;
+        const uint8_t* As = lds + kp * L::kPart + (j % kS) * L::kStage;
         const uint8_t* Bs = As + L::kATile;
         const int grp = ((s0 + j) * T::kStep) >> 7;
         const uint16_t* ts = tab_s + grp * kBN;
@@ -869,8 +926,8 @@ __global__ __launch_bounds__(kThreads, 1) void gemm3_splitk_kernel(GemmArgs p) {
             x1[rw] = *(const uint4*)(As + swz(rw * 16 + l16, 4 + g));
         }
 #pragma unroll
-        for (int cb = 0; cb < 8; ++cb) {
-            const int cw = cb >> 2, bj = cb & 3;
+        for (int b = 0; b < kNB; ++b) {
+            const int bj = bj0 + b;
             const int row = cw * 64 + wrow(l16, bj);
             const uint32_t z = tz[row];
             uint4 w0, w1;
@@ -880,9 +937,9 @@ __global__ __launch_bounds__(kThreads, 1) void gemm3_splitk_kernel(GemmArgs p) {
                 gs = v4f{h2f((uint16_t)(sc.x & 0xffffu)), h2f((uint16_t)(sc.x >> 16)), h2f((uint16_t)(sc.y & 0xffffu)),
                          h2f((uint16_t)(sc.y >> 16))};
                 const uint32_t zz = z * 0x01010101u;
-                const int key = g128a8_key(row), half = (g & 1) << 3;
-                const uint2 q0 = *(const uint2*)(Bs + row * 64 + ((((g >> 1)) ^ key) << 4) + half);
-                const uint2 q1 = *(const uint2*)(Bs + row * 64 + (((2 + (g >> 1)) ^ key) << 4) + half);
+                const int key = g128a8_key(row), hb = (g & 1) << 3;
+                const uint2 q0 = *(const uint2*)(Bs + row * 64 + ((((g >> 1)) ^ key) << 4) + hb);
+                const uint2 q1 = *(const uint2*)(Bs + row * 64 + (((2 + (g >> 1)) ^ key) << 4) + hb);
                 u4x8_minus_z(q0.x, zz, w0.x, w0.y);
                 u4x8_minus_z(q0.y, zz, w0.z, w0.w);
                 u4x8_minus_z(q1.x, zz, w1.x, w1.y);
@@ -897,22 +954,22 @@ __global__ __launch_bounds__(kThreads, 1) void gemm3_splitk_kernel(GemmArgs p) {
                 w1 = __builtin_bit_cast(uint4, u4x8_to_h(q1, zzh, ss));
             }
 #pragma unroll
-            for (int rw = 0; rw < 2; ++rw) mfma_step<F>(accf[rw][cb], acci[rw][cb], w0, w1, x0[rw], x1[rw], gs);
+            for (int rw = 0; rw < 2; ++rw) mfma_step<F>(accf[rw][b], acci[rw][b], w0, w1, x0[rw], x1[rw], gs);
         }
     }
 
-    // partials of quarter q = (rows 16 (q / 2), columns 64 (q % 2)) to LDS
     __syncthreads();  // every wave is done with its ring
-    // [quarter][wave][block][lane] float4: consecutive lanes write consecutive 16 bytes
+    // [quarter][part][block][lane] float4: consecutive lanes write consecutive 16 bytes
     float4* red = (float4*)lds;
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
+    for (int rw = 0; rw < 2; ++rw)
 #pragma unroll
-        for (int bj = 0; bj < 4; ++bj) {
-            const v4f v = accf[q >> 1][(q & 1) * 4 + bj];
-            red[((q * 4 + wave) * 4 + bj) * 64 + lane] = float4{v[0], v[1], v[2], v[3]};
+        for (int b = 0; b < kNB; ++b) {
+            const v4f v = accf[rw][b];
+            red[(((rw * 2 + cw) * 4 + kp) * 4 + bj0 + b) * 64 + lane] = float4{v[0], v[1], v[2], v[3]};
         }
     __syncthreads();
+    if (wave >= 4) return;
     v4f sum[1][4];
     v4i isum[1][4];
 #pragma unroll

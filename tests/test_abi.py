@@ -106,7 +106,7 @@ def test_gemm_tile_plan(lib):
     when no GPU is visible, and MI355X's count): the BASELINE sizes the
     full-size parity tests use reach the 256-row kernels; grids of at most
     one tile per CU take the one-tile-per-workgroup ring (more stages)."""
-    FP8, I8, G128A8, F16, I8SKIP, Q4K = 0, 1, 3, 4, 6, 7
+    FP8, I8, G128A8, F16, G128A16, I8SKIP, Q4K = 0, 1, 3, 4, 5, 6, 7
     EPI_F16, EPI_F8, EPI_F32 = 0, 1, 3
     assert _tile(lib, FP8, EPI_F8, 7500, 4096) == (256, 128, 2)
     # 720 tiles of 256 rows would leave the second round of 512 slots 40 % full
@@ -131,6 +131,9 @@ def test_gemm_tile_plan(lib):
     assert _tile(lib, G128A8, EPI_F16, 750, 4096) == (64, 128, 3)
     rows, cols, stages = _tile(lib, I8, EPI_F32, 750, 4096)
     assert (rows, cols) == (128, 128) and stages > 3
+    # INT4-g128 x fp16 at 750 x 4096: 96-row ring tiles, 8 x 32 = one per CU
+    rows, cols, stages = _tile(lib, G128A16, EPI_F16, 750, 4096)
+    assert (rows, cols) == (96, 128) and stages > 3
     assert _tile(lib, 99, EPI_F16, 16, 256)[0] == -4
 
 
