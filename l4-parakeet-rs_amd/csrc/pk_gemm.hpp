@@ -133,6 +133,20 @@ __device__ __forceinline__ int wrow(int i, int bj) { return ((i >> 2) << 4) + (b
 // 8-byte reads fall on distinct banks (64 banks; at most 2 lanes a bank with 32).
 __device__ __forceinline__ int g128a8_key(int row) { return (row >> 4) & 3; }
 
+// G128A16 weight tile: per column and 64-K step 32 bytes (two 16-byte
+// chunks).  A fragment read covers rows wrow(0..15, bj) = {0-3, 16-19, 32-35,
+// 48-51} + 4 bj at one chunk position; stored at row * 32 + 16 c, rows 16
+// apart fall on the same banks (four LDS cycles a read).  Row pairs share a
+// 64-byte unit whose four chunk slots are XOR-keyed by (row >> 4) & 3, which
+// spreads a read's sixteen chunks over every 16-byte bank group twice.
+__device__ __forceinline__ int a16_slot(int row, int c) { return (row >> 1) * 4 + ((((row & 1) << 1) | c) ^ ((row >> 4) & 3)); }
+// the (row, chunk) that 16-byte slot s of the tile holds (inverse of a16_slot)
+__device__ __forceinline__ void a16_chunk_of_slot(int s, int& row, int& c) {
+    const int u = s >> 2, y = (s & 3) ^ ((u >> 3) & 3);
+    row = 2 * u + (y >> 1);
+    c = y & 1;
+}
+
 // Four unsigned nibbles (byte j of `w`, low nibble = k j, high = k 4+j) ->
 // eight int8 (q - z), natural k order, as two dwords.
 __device__ __forceinline__ void u4x8_minus_z(uint32_t w, uint32_t zz, uint32_t& first, uint32_t& second) {
@@ -473,8 +487,8 @@ __device__ __forceinline__ void weight_frag(const uint8_t* Bs, int row, int g, i
             const _Float16 s = (_Float16)sc[row];
             const _Float16 zh = (_Float16)(1024 + z);
             const v2h ss = {s, s}, zz = {zh, zh};
-            const uint32_t q0 = *(const uint32_t*)(Bs + row * 32 + 4 * g);
-            const uint32_t q1 = *(const uint32_t*)(Bs + row * 32 + 16 + 4 * g);
+            const uint32_t q0 = *(const uint32_t*)(Bs + a16_slot(row, 0) * 16 + 4 * g);
+            const uint32_t q1 = *(const uint32_t*)(Bs + a16_slot(row, 1) * 16 + 4 * g);
             w0 = __builtin_bit_cast(uint4, u4x8_to_h(q0, zz, ss));
             w1 = __builtin_bit_cast(uint4, u4x8_to_h(q1, zz, ss));
         }
@@ -732,6 +746,8 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs p) {
             if constexpr (T::bRow == 128) {
                 row = o >> 7;
                 c = ((o >> 4) & 7) ^ swz_key(row);
+            } else if constexpr (F == FMT_G128A16) {
+                a16_chunk_of_slot(o >> 4, row, c);
             } else {
                 row = o / T::bRow;
                 c = (o % T::bRow) / 16;

@@ -291,6 +291,8 @@ __global__ __launch_bounds__(kThreads, 2) void gemm3_kernel(GemmArgs p) {
             } else if constexpr (F == FMT_G128A8) {
                 row = o >> 6;
                 c = ((o >> 4) & 3) ^ g128a8_key(row);
+            } else if constexpr (F == FMT_G128A16) {
+                a16_chunk_of_slot(o >> 4, row, c);
             } else {
                 row = o / T::bRow;
                 c = (o % T::bRow) / 16;
@@ -718,6 +720,8 @@ __global__ __launch_bounds__(kThreads, kOcc) void gemm3_ring_kernel(GemmArgs p) 
         } else if constexpr (F == FMT_G128A8) {
             row = o >> 6;
             c = ((o >> 4) & 3) ^ g128a8_key(row);
+        } else if constexpr (F == FMT_G128A16) {
+            a16_chunk_of_slot(o >> 4, row, c);
         } else {
             row = o / T::bRow;
             c = (o % T::bRow) / 16;
@@ -873,6 +877,8 @@ __global__ __launch_bounds__(256 * kCH, 1) void gemm3_splitk_kernel(GemmArgs p) 
         if constexpr (F == FMT_G128A8) {
             row = o >> 6;
             c = ((o >> 4) & 3) ^ g128a8_key(row);
+        } else if constexpr (F == FMT_G128A16) {
+            a16_chunk_of_slot(o >> 4, row, c);
         } else {
             row = o / T::bRow;
             c = (o % T::bRow) / 16;
@@ -948,8 +954,8 @@ __global__ __launch_bounds__(256 * kCH, 1) void gemm3_splitk_kernel(GemmArgs p) 
                 const _Float16 sh = __builtin_bit_cast(_Float16, ts[row]);
                 const _Float16 zh = (_Float16)(1024 + (int)z);
                 const v2h ss = {sh, sh}, zzh = {zh, zh};
-                const uint32_t q0 = *(const uint32_t*)(Bs + row * 32 + 4 * g);
-                const uint32_t q1 = *(const uint32_t*)(Bs + row * 32 + 16 + 4 * g);
+                const uint32_t q0 = *(const uint32_t*)(Bs + a16_slot(row, 0) * 16 + 4 * g);
+                const uint32_t q1 = *(const uint32_t*)(Bs + a16_slot(row, 1) * 16 + 4 * g);
                 w0 = __builtin_bit_cast(uint4, u4x8_to_h(q0, zzh, ss));
                 w1 = __builtin_bit_cast(uint4, u4x8_to_h(q1, zzh, ss));
             }
