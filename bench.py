@@ -66,6 +66,7 @@ class Stack:
         # INT4-g128 contracts read the e4m3 hidden with their weights expanded
         # per call to e4m3 (q - z) into this buffer (pk_expand_int4_g128_e4m3)
         self.wexp = torch.empty((D, FF), dtype=torch.uint8, device=dev)
+        self.sexp = torch.empty((FF // 128, D), dtype=torch.float16, device=dev)  # their group-major scales
         self.out16 = torch.empty((t_frames, 3 * D), dtype=torch.float16, device=dev)
         self.state = torch.randn((t_frames, D), generator=g, device=dev, dtype=torch.float16)
         self.weights = []
@@ -115,9 +116,9 @@ class Stack:
                 pk.gemm(pk.FMT_I8, pk.EPI_F16, self.out8, q, t, n, k, self.state, w_scales=s, in_scale=1.0 / 16,
                         residual=self.state, out_scale=0.5, res_scale=1.0, stream=stream)
             else:
-                pk.call("pk_expand_int4_g128_e4m3", q, z, n, k, self.wexp, stream=stream)
+                pk.call("pk_expand_int4_g128_e4m3", q, z, s, n, k, self.wexp, self.sexp, stream=stream)
                 pk.gemm(pk.FMT_G128F8, pk.EPI_F16, self.out8, self.wexp, t, n, k, self.state, in_scale=1.0 / 16,
-                        residual=self.state, out_scale=0.5, res_scale=1.0, g_scales=s, stream=stream)
+                        residual=self.state, out_scale=0.5, res_scale=1.0, g_scales=self.sexp, stream=stream)
             return
         if fmt == "fp8":
             a, rows, f = (self.x8 if k == FF else self.x8d), self.xs8, pk.FMT_FP8
@@ -638,8 +639,9 @@ def kernel_run(pk, torch, t, fmt, kind, n, k, stream, seed=99):
     if contract and fmt == "int4g128":
         # the contract's GEMM on the per-call expanded e4m3 weights
         we = torch.empty((n, k), dtype=torch.uint8, device=dev)
-        pk.call("pk_expand_int4_g128_e4m3", w, gz, n, k, we)
-        f, w, gz = FMT_G128F8, we, None
+        gst = torch.empty((k // 128, n), dtype=torch.float16, device=dev)
+        pk.call("pk_expand_int4_g128_e4m3", w, gz, gs, n, k, we, gst)
+        f, w, gz, gs = FMT_G128F8, we, None, gst
     if kind in ("f8", "i8s"):
         out = torch.empty((t, n), dtype=torch.uint8, device=dev)
         e = pk.EPI_F8 if kind == "f8" else EPI_I8S

@@ -153,11 +153,12 @@ int32_t pk_pack_int4_g128(const uint16_t* weight, int32_t n, int32_t k, uint32_t
                           uint16_t* scales, uint16_t* zeros, void* stream);
 /* No reference counterpart: INT4-g128 weights (pk_pack_int4_g128 layout,
  * zeros [n x k/128]) as e4m3 (q - z) bytes [n x k] in k order, exact since
- * |q - z| <= 15; the weight operand of pk_gemm format 8 (e4m3 activations x
- * INT4-g128 weights), expanded per call into a caller buffer.  packed and
- * expanded 16-byte aligned. */
-int32_t pk_expand_int4_g128_e4m3(const uint32_t* packed, const uint16_t* zeros, int32_t n, int32_t k,
-                                 uint8_t* expanded, void* stream);
+ * |q - z| <= 15, and their fp16 scales moved to group-major order
+ * (scales_t [k/128 x n]); the weight and g_scales operands of pk_gemm format 8
+ * (e4m3 activations x INT4-g128 weights), expanded per call into caller
+ * buffers.  packed and expanded 16-byte aligned. */
+int32_t pk_expand_int4_g128_e4m3(const uint32_t* packed, const uint16_t* zeros, const uint16_t* scales, int32_t n,
+                                 int32_t k, uint8_t* expanded, uint16_t* scales_t, void* stream);
 /* linear.cu:459-472 pk_sm89_q4_k_dequantize: GGUF Q4_K superblocks (144 bytes
  * per 256 values: fp16 d, fp16 dmin, 12 bytes of 6-bit scales/mins, 128 quant
  * bytes) [n x k/256] -> fp16 [n x k], value = f16(d*sc*q - dmin*mn). */
@@ -406,7 +407,8 @@ int32_t pk_ffn_contract_int8_sparse24(const uint8_t* data, const uint8_t* meta, 
  * format: 0 FP8, 1 INT8, 2 INT4 (s4 x s4), 3 INT4-g128 x INT8, 4 FP16,
  * 5 INT4-g128 x FP16, 6 INT8 with zero-block skip, 7 Q4_K x FP16 (epilogues
  * 0 and 3 only), 8 e4m3 activations x INT4-g128 weights given as e4m3 (q - z)
- * bytes (b from pk_expand_int4_g128_e4m3, g_scales required, g_zeros unused;
+ * bytes (b from pk_expand_int4_g128_e4m3; g_scales required, group-major
+ * [k/128 x n] as that call writes them, 16-byte aligned; g_zeros unused;
  * each 128-K group summed in fp32 by one MFMA, then folded in K order with
  * one fma by its fp16 scale; epilogues 0, 1 and 3).  epilogue: 0 fp16 (act(v [+bias]) * out_scale
  * [+ res_scale * residual]), 1 e4m3(fp16(SiLU(v)) * 16), 2 as 1 + 2:4

@@ -136,12 +136,15 @@ int32_t pk_pack_int4_g128(const uint16_t* w, int32_t n, int32_t k, uint32_t* q, 
     return check_launch("pack_int4_g128");
 }
 
-int32_t pk_expand_int4_g128_e4m3(const uint32_t* q, const uint16_t* z, int32_t n, int32_t k, uint8_t* out, void* stream) {
+int32_t pk_expand_int4_g128_e4m3(const uint32_t* q, const uint16_t* z, const uint16_t* scales, int32_t n, int32_t k,
+                                 uint8_t* out, uint16_t* scales_t, void* stream) {
     if (n < 0 || k <= 0 || k % 128) { set_error("g128 expansion needs k %% 128 == 0 (k=%d)", k); return PK_E_SHAPE; }
     if (n == 0) return 0;
-    if (!need(q, "packed") || !need(z, "zeros") || !need(out, "expanded")) return PK_E_ARG;
+    if (!need(q, "packed") || !need(z, "zeros") || !need(scales, "scales") || !need(out, "expanded") ||
+        !need(scales_t, "scales_t"))
+        return PK_E_ARG;
     if (((uintptr_t)q | (uintptr_t)out) & 15) { set_error("packed and expanded must be 16-byte aligned"); return PK_E_ALIGN; }
-    launch_expand_g128_e4m3(q, z, out, n, k, STREAM);
+    launch_expand_g128_e4m3(q, z, scales, scales_t, out, n, k, STREAM);
     return check_launch("expand_int4_g128_e4m3");
 }
 
@@ -255,6 +258,10 @@ int32_t pk_gemm(int32_t format, int32_t epilogue, const void* a, const void* b, 
     if (!need(a, "a") || !need(b, "b") || !need(out, "out")) return PK_E_ARG;
     if ((format == FMT_G128A8 || format == FMT_G128A16) && (!need(g_scales, "g_scales") || !need(g_zeros, "g_zeros"))) return PK_E_ARG;
     if (format == FMT_G128F8 && !need(g_scales, "g_scales")) return PK_E_ARG;
+    if (format == FMT_G128F8 && ((uintptr_t)g_scales & 15)) {
+        set_error("format 8 reads its group-major scales as 16-byte vectors: g_scales must be 16-byte aligned");
+        return PK_E_ALIGN;
+    }
     if (epilogue == EPI_F8_24 && !need(out_meta, "out_meta")) return PK_E_ARG;
     if (activation < 0 || activation > 2) { set_error("activation must be 0, 1 or 2"); return PK_E_ARG; }
     GemmArgs g = base_args(a, b, m, n, k, out, ldo);

@@ -362,21 +362,24 @@ __global__ __launch_bounds__(kThreads, 2) void gemm3_kernel(GemmArgs p) {
     };
 
     // G128F8 keeps no LDS table (its 80 KiB of tiles leave no room at two
-    // workgroups per CU): lane l of a wave holds the current step's group
-    // scale of column n0 + 64 wn + l (sc_cur) and loads the next step's
-    // (sc_nxt) a step ahead; a lane's 16 accumulator columns 16 g + 4 bj + r
-    // are lanes of its own 16-lane row, read with ds_bpermute.
-    float sc_cur = 0.0f, sc_nxt = 0.0f;
-    auto load_sc = [&](int cn0, int st) -> float {
-        const int col = min(cn0 + wn * 64 + lane, p.n - 1);
-        return h2f(p.g_scales[(size_t)col * groups + ((st * T::kStep) >> 7)]);
+    // workgroups per CU): its scales are group-major ([K/128][N] fp16), so a
+    // lane's 16 accumulator columns n0 + 64 wn + 16 g .. + 15 of a step's
+    // group are 32 contiguous bytes, loaded a step ahead (sc_nxt) with two
+    // 16-byte loads.  N % 16 == 0 (checked by the host): a 16-column run is in
+    // range or wholly past N, then read from the last run and unused.
+    uint4 sc_cur[2] = {}, sc_nxt[2] = {};
+    auto load_sc = [&](int cn0, int st) {
+        const int col = min(cn0 + wn * 64 + g * 16, p.n - 16);
+        const uint4* src = (const uint4*)(p.g_scales + (size_t)st * p.n + col);
+        sc_nxt[0] = src[0];
+        sc_nxt[1] = src[1];
     };
 
     int t = tile_slot(G);
     if (t >= ntiles) return;
     int m0, n0;
     set_tile(t, m0, n0);
-    if constexpr (F == FMT_G128F8) sc_nxt = load_sc(n0, 0);
+    if constexpr (F == FMT_G128F8) load_sc(n0, 0);
     issue_a(0, 0);
     issue_b(0);
     if constexpr (L::kG128) {
@@ -435,8 +438,9 @@ __global__ __launch_bounds__(kThreads, 2) void gemm3_kernel(GemmArgs p) {
                 nstep = 0;
             }
             if constexpr (F == FMT_G128F8) {
-                sc_cur = sc_nxt;
-                if (nstep >= 0) sc_nxt = load_sc(n0, nstep);
+                sc_cur[0] = sc_nxt[0];
+                sc_cur[1] = sc_nxt[1];
+                if (nstep >= 0) load_sc(n0, nstep);
             }
             if (nstep >= 0) issue_a(nstep, buf ^ 1);
             const uint8_t* As = lds + buf * kATile;
@@ -448,11 +452,13 @@ __global__ __launch_bounds__(kThreads, 2) void gemm3_kernel(GemmArgs p) {
                 weight_frag<F>(Bs, wn * 64 + wrow(l16, bj), g, bj, wn, step, tab_s + (step & 1) * kBN, tab_z + (step & 1) * kBN,
                                w0[bj], w1[bj], gs[bj]);
             if constexpr (F == FMT_G128F8) {
+                const uint32_t sw[8] = {sc_cur[0].x, sc_cur[0].y, sc_cur[0].z, sc_cur[0].w,
+                                        sc_cur[1].x, sc_cur[1].y, sc_cur[1].z, sc_cur[1].w};
 #pragma unroll
                 for (int bj = 0; bj < 4; ++bj)
 #pragma unroll
                     for (int r = 0; r < 4; ++r)
-                        gs[bj][r] = __int_as_float(__builtin_amdgcn_ds_bpermute((g * 16 + bj * 4 + r) << 2, __float_as_int(sc_cur)));
+                        gs[bj][r] = h2f((uint16_t)(sw[(4 * bj + r) >> 1] >> (((4 * bj + r) & 1) * 16)));
             }
             uint4 x0, x1, y0, y1;
             uint4 xr0[3], xr1[3];  // kAhead2: row blocks ai, ai + 1, ai + 2 in slots ai % 3 ...

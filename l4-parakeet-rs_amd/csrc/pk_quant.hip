@@ -717,13 +717,16 @@ __global__ __launch_bounds__(256) void unpack_s4_kernel(const uint4* __restrict_
 // G128F8 GEMM: one thread per 4 words (32 K values of one group).
 // HBM-bound: reads k/2 + 2 k/128 bytes and writes k bytes per row.
 __global__ __launch_bounds__(256) void expand_g128_e4m3_kernel(const uint4* __restrict__ q, const uint16_t* __restrict__ zeros,
-                                                               uint4* __restrict__ out, int k, size_t quads) {
+                                                               const uint16_t* __restrict__ scales, uint16_t* __restrict__ scales_t,
+                                                               uint4* __restrict__ out, int n, int k, size_t quads) {
     const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= quads) return;
     const size_t per_row = (size_t)k / 32;  // quads per row
     const size_t row = i / per_row;
-    const int group = (int)(i - row * per_row) >> 2;
+    const int quad = (int)(i - row * per_row), group = quad >> 2;
     const float z = h2f(zeros[row * (size_t)(k >> 7) + group]);
+    // the group's first quad also moves its scale to the group-major table
+    if ((quad & 3) == 0) scales_t[(size_t)group * n + row] = scales[row * (size_t)(k >> 7) + group];
     const uint4 w = q[i];
     const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
     uint32_t o[8];
@@ -860,10 +863,12 @@ int launch_unpack_s4(const uint8_t* in, int8_t* out, size_t bytes, hipStream_t s
     return 0;
 }
 
-int launch_expand_g128_e4m3(const uint32_t* q, const uint16_t* zeros, uint8_t* out, int n, int k, hipStream_t s) {
+int launch_expand_g128_e4m3(const uint32_t* q, const uint16_t* zeros, const uint16_t* scales, uint16_t* scales_t, uint8_t* out,
+                            int n, int k, hipStream_t s) {
     const size_t quads = (size_t)n * (k / 32);
     if (quads == 0) return 0;
-    expand_g128_e4m3_kernel<<<(unsigned)((quads + 255) / 256), 256, 0, s>>>((const uint4*)q, zeros, (uint4*)out, k, quads);
+    expand_g128_e4m3_kernel<<<(unsigned)((quads + 255) / 256), 256, 0, s>>>((const uint4*)q, zeros, scales, scales_t, (uint4*)out, n,
+                                                                              k, quads);
     return 0;
 }
 

@@ -56,7 +56,7 @@ SIGNATURES = {
     "pk_pack_int8_rows": (I, [P, I, I, P, P, P]),
     "pk_pack_int4_rows": (I, [P, I, I, P, P, P]),
     "pk_pack_int4_g128": (I, [P, I, I, P, P, P, P]),
-    "pk_expand_int4_g128_e4m3": (I, [P, P, I, I, P, P]),
+    "pk_expand_int4_g128_e4m3": (I, [P, P, P, I, I, P, P, P]),
     "pk_q4_k_dequantize": (I, [P, P, I, I, P]),
     "pk_quantize_fp8": (I, [P, P, F, I, P]),
     "pk_quantize_int8": (I, [P, P, F, I, P]),

@@ -58,8 +58,10 @@ def test_expand_int4_g128_e4m3(pk, orc, n, k):
     gen.manual_seed(n * 3 + k)
     q, s, z = g128(pk, n, k, gen)
     out = torch.empty((n, k), dtype=torch.uint8, device="cuda")
+    st = torch.empty((k // 128, n), dtype=torch.float16, device="cuda")
     note(f"expand_int4_g128_e4m3 n={n} k={k}")
-    pk.call("pk_expand_int4_g128_e4m3", q, z, n, k, out)
+    pk.call("pk_expand_int4_g128_e4m3", q, z, s, n, k, out, st)
+    assert np.array_equal(host(st).view(np.uint16), host(s).view(np.uint16).T)
     b = host(q).view(np.uint8).reshape(n, -1, 4).astype(np.int64)
     lv = np.concatenate([b & 15, b >> 4], axis=2).reshape(n, -1)
     want = lv - np.repeat(host(z).astype(np.int64), 128, axis=1)
@@ -141,10 +143,11 @@ def test_g128_f8_contract(pk, orc):
         h = (torch.randn((T, k), generator=gen, device="cuda") * 2).to(torch.float8_e4m3fn).view(torch.uint8)
         q, s, z = g128(pk, n, k, gen)
         we = torch.empty((n, k), dtype=torch.uint8, device="cuda")
-        pk.call("pk_expand_int4_g128_e4m3", q, z, n, k, we)
+        st = torch.empty((k // 128, n), dtype=torch.float16, device="cuda")
+        pk.call("pk_expand_int4_g128_e4m3", q, z, s, n, k, we, st)
         note(f"g128 f8 n={n} k={k} T={T} tile={pk.gemm_tile(pk.FMT_G128F8, pk.EPI_F32, T, n)}")
         out = torch.empty((T, n), dtype=torch.float32, device="cuda")
-        pk.gemm(pk.FMT_G128F8, pk.EPI_F32, h, we, T, n, k, out, in_scale=1.0 / 16, g_scales=s)
+        pk.gemm(pk.FMT_G128F8, pk.EPI_F32, h, we, T, n, k, out, in_scale=1.0 / 16, g_scales=st)
         ref = orc.gemm_g128_f8(rows_of(h, idx), host(q).view(np.uint32), host(s), host(z)) * np.float32(1.0 / 16)
         got = rows_of(out, idx)
         assert_close(got, ref, what=f"g128 f8 fp32 n={n}")
@@ -153,7 +156,7 @@ def test_g128_f8_contract(pk, orc):
             state = torch.randn((T, D), generator=gen, device="cuda").half()
             before = rows_of(state, idx)
             pk.gemm(pk.FMT_G128F8, pk.EPI_F16, h, we, T, n, k, state, in_scale=1.0 / 16, residual=state,
-                    out_scale=0.5, res_scale=1.0, g_scales=s)
+                    out_scale=0.5, res_scale=1.0, g_scales=st)
             ref16 = orc.epilogue(ref * np.float32(16.0), 2, np.ones(n, np.float32), in_scale=1.0 / 16,
                                  residual=before)
             after = rows_of(state, idx)
@@ -163,7 +166,7 @@ def test_g128_f8_contract(pk, orc):
                          what="g128 f8 + residual (update)")
         else:
             o16 = torch.empty((T, n), dtype=torch.float16, device="cuda")
-            pk.gemm(pk.FMT_G128F8, pk.EPI_F16, h, we, T, n, k, o16, in_scale=1.0 / 16, g_scales=s)
+            pk.gemm(pk.FMT_G128F8, pk.EPI_F16, h, we, T, n, k, o16, in_scale=1.0 / 16, g_scales=st)
             assert_close(rows_of(o16, idx), ref, what="g128 f8 fp16")
         del h, we, out
     torch.cuda.empty_cache()
