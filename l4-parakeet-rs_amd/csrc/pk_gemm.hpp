@@ -323,9 +323,15 @@ __device__ __forceinline__ void store_f16_rowpair(uint16_t* out, size_t ldo, int
 // lane finishes columns [gcol, gcol + 16) of one row (16 contiguous outputs,
 // one to four 16-byte stores).  Column scales / bias and the 8 row scales are
 // loaded once per tile; a residual row (kRes) is loaded one block ahead.
+// With `stage` (4 KiB of LDS private to the wave, free), fp32 outputs of a
+// row block pass through it so that every store instruction writes 8 rows x
+// 128 contiguous bytes (whole cache lines): the direct stores put a row's
+// 16-byte pieces 64 bytes apart per instruction, and a burst of such stores
+// drains at about 60 % of the whole-line rate (C1, 192 tiles of 128 x 128
+// fp32: 12.8 -> 11.1 us).  Measured no faster for fp16 outputs.
 template <int F, int E, bool kRes = true, int kAI = 8>
 __device__ __forceinline__ void epilogue(const GemmArgs& p, v4f (&accf)[kAI][4], v4i (&acci)[kAI][4], int m0, int n0, int wm,
-                                         int wn, int lane) {
+                                         int wn, int lane, uint8_t* stage = nullptr) {
     using T = FmtTraits<F>;
     const int g = lane >> 4, l16 = lane & 15;
     const int gcol = n0 + wn * 64 + g * 16;
@@ -387,7 +393,20 @@ __device__ __forceinline__ void epilogue(const GemmArgs& p, v4f (&accf)[kAI][4],
             for (int j = 0; j < 16; ++j) v[j] = __builtin_fmaf(v[j] * rs, wsv[j], bsv[j]);
         }
         if constexpr (E == EPI_F32) {
-            if (live) {
+            if (stage != nullptr) {
+                // row l16 of the block, 16-byte chunk q = 4 g + j of its 256-byte
+                // slab at slot q ^ l16 (8 consecutive lanes: distinct banks)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    *(float4*)(stage + l16 * 256 + (((4 * g + j) ^ l16) << 4)) = float4{v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int r = (j & 1) * 8 + (lane >> 3), q = (j >> 1) * 8 + (lane & 7);
+                    const float4 x = *(const float4*)(stage + r * 256 + ((q ^ r) << 4));
+                    const int orow = m0 + wm * 16 * kAI + ai * 16 + r, ocol = n0 + wn * 64 + 4 * q;
+                    if (orow < p.m && ocol < p.n) *(float4*)((float*)p.out + (size_t)orow * p.ldo + ocol) = x;
+                }
+            } else if (live) {
                 float4* o = (float4*)((float*)p.out + (size_t)grow * p.ldo + gcol);
 #pragma unroll
                 for (int j = 0; j < 4; ++j) o[j] = float4{v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]};

@@ -790,8 +790,14 @@ __global__ __launch_bounds__(kThreads, kOcc) void gemm3_ring_kernel(GemmArgs p) 
             for (int bj = 0; bj < 4; ++bj) mfma_step<F>(accf[ai][bj], acci[ai][bj], w0[bj], w1[bj], xr0[ai % 3], xr1[ai % 3], gs[bj]);
         }
     }
-    if constexpr (E == EPI_F16_RES) epilogue<F, EPI_F16, true, kAI>(p, accf, acci, m0, n0, wm, wn, lane);
-    else epilogue<F, E, false, kAI>(p, accf, acci, m0, n0, wm, wn, lane);
+    if constexpr (E == EPI_F16_RES) {
+        epilogue<F, EPI_F16, true, kAI>(p, accf, acci, m0, n0, wm, wn, lane);
+    } else if constexpr (E == EPI_F32) {
+        __syncthreads();  // every wave is done with the ring: 4 KiB of it per wave stage the output rows
+        epilogue<F, E, false, kAI>(p, accf, acci, m0, n0, wm, wn, lane, lds + wave * 4096);
+    } else {
+        epilogue<F, E, false, kAI>(p, accf, acci, m0, n0, wm, wn, lane);
+    }
 }
 
 
