@@ -27,8 +27,8 @@
  *     pointers: the epilogue reads them as 16-byte vectors, so a slice at a
  *     4-byte offset returns PK_E_ALIGN (copy it to an aligned buffer first).
  *   - Results do not depend on M or on the GPU's CU count, with one stated
- *     exception: INT4-g128 launches on small grids that split K over the
- *     waves of a workgroup (pk_gemm_k_split reports 4) fold the group sums
+ *     exception: INT4-g128 launches on small grids that split K in four
+ *     parts within a workgroup (pk_gemm_k_split reports 4) fold the group sums
  *     by parts, so their fp32 results are associated differently from the
  *     same rows' on a large grid (each part is exact; see pk_gemm_k_split).
  */
@@ -430,10 +430,11 @@ int32_t pk_gemm(int32_t format, int32_t epilogue, const void* a, const void* b, 
  * which kernel variant a shape runs. */
 int32_t pk_gemm_tile(int32_t format, int32_t epilogue, int32_t m, int32_t n, int32_t* tile_cols, int32_t* stages);
 /* K split of pk_gemm's launch for an m x n x k output (host only): 4 when each
- * 32-row tile's K-steps are divided over the four waves of its workgroup and
- * the partial tiles summed in K order (INT4-g128 formats on grids that take
- * 32-row tiles, k >= 1024; each wave then has its own LDS ring, and *stages
- * of pk_gemm_tile is the plain ring's), else 1; or a negative PK_E_* status.
+ * 32-row tile's K-steps are divided in four K-ordered parts within its
+ * workgroup (16 waves, each part's LDS ring shared by four of them) and the
+ * partial tiles summed in K order (INT4-g128 formats on grids that take
+ * 32-row tiles, k >= 1024; *stages of pk_gemm_tile is the plain ring's), else
+ * 1; or a negative PK_E_* status.
  * No counterpart in the reference. */
 int32_t pk_gemm_k_split(int32_t format, int32_t epilogue, int32_t m, int32_t n, int32_t k);
 

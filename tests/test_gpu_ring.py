@@ -120,7 +120,7 @@ def test_ring_fp8_epilogues(pk, orc, m, n, k):
                  tol=2e-2)
 
 
-# shapes whose 32-row ring tiles split K over the workgroup's four waves
+# shapes whose 32-row ring tiles split K in four parts within the workgroup
 SPLIT_SHAPES = {(750, 1024, 4096), (97, 1024, 4096), (45, 1024, 1280), (33, 256, 1024)}
 
 
@@ -129,7 +129,7 @@ SPLIT_SHAPES = {(750, 1024, 4096), (97, 1024, 4096), (45, 1024, 1280), (33, 256,
 def test_ring_int4g128_a8_exact(pk, orc, m, n, k):
     """INT4-g128 x INT8: fp32 (and fp16 + residual) outputs bit for bit; the
     ring loads each tile's group tables once and indexes them by K-step.  The
-    split-K shapes (10 groups over 4 waves: runs of 2, 3, 2, 3; 8 over 4)
+    split-K shapes (10 groups in 4 parts: runs of 2, 3, 2, 3; 8 in 4)
     compare with the oracle's matching association of the group sum."""
     rows = ring(pk, pk.FMT_G128A8, pk.EPI_F32, m, n)
     note(f"g128 a8 m={m} n={n} k={k} ring rows={rows}")
