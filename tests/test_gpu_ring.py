@@ -91,6 +91,26 @@ def test_ring_int8_dyn_config1(pk, orc):
     assert np.array_equal(host(out), ref.astype(np.float32))
 
 
+@pytest.mark.parametrize("m,n,k,ldo", [(97, 1040, 512, 1040), (750, 4096, 128, 4112), (5, 272, 1024, 304)])
+def test_ring_fp32_staged_ragged(pk, orc, m, n, k, ldo):
+    """fp32 ring outputs go through per-wave LDS and whole-line stores: ragged
+    M, N not a multiple of the 128-column tile, a row stride beyond N (the
+    columns past N stay untouched), one K-step; INT8 bit for bit."""
+    rows = ring(pk, pk.FMT_I8, pk.EPI_F32, m, n)
+    note(f"int8 fp32 staged m={m} n={n} k={k} ldo={ldo} ring rows={rows}")
+    rng = np.random.default_rng(m * 3 + n + k)
+    x = rng.standard_normal((m, k)).astype(np.float16)
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float16)
+    xq, xs = orc.quantize_int8_rows(x)
+    wq, ws = orc.pack_int8_rows(w)
+    out = torch.full((m, ldo), -7.0, dtype=torch.float32, device="cuda")
+    pk.gemm(pk.FMT_I8, pk.EPI_F32, dev(xq), dev(wq), m, n, k, out, w_scales=dev(ws), row_scales=dev(xs), ldo=ldo)
+    got = host(out)
+    ref = (orc.gemm_i8(xq, wq).astype(np.float32) * xs[:, None]).astype(np.float32) * ws[None, :]
+    assert np.array_equal(got[:, :n], ref.astype(np.float32))
+    assert np.all(got[:, n:] == -7.0)
+
+
 @pytest.mark.parametrize("m,n,k", [(750, 4096, 1024), (300, 1024, 4096), (45, 3072, 1024)])
 def test_ring_fp8_epilogues(pk, orc, m, n, k):
     rows = ring(pk, pk.FMT_FP8, pk.EPI_F16, m, n)
