@@ -803,6 +803,108 @@ __global__ __launch_bounds__(kThreads, kOcc) void gemm3_ring_kernel(GemmArgs p) 
 
 // ---- small grids, long K: one 32 x 128 tile per workgroup, K split over its 4 waves ----
 //
+// The ring kernel with two waves per SIMD (FP8 / INT8, 64- or 128-row
+// tiles): waves w and w + 4 share quadrant w % 4 of the tile (the same 64
+// columns and 16 kAI rows) and take its upper / lower kAI / 2 row blocks, so
+// each SIMD runs two independent MFMA / fragment-read chains of a K-step.
+// Stages, swizzles and epilogue as gemm3_ring_kernel; a wave issues kAI / 2
+// activation and two weight loads of a stage.
+template <int F, int E, int kAI>
+__global__ __launch_bounds__(2 * kThreads, 1) void gemm3_ring8_kernel(GemmArgs p) {
+    static_assert((F == FMT_FP8 || F == FMT_I8) && (kAI == 2 || kAI == 4), "byte formats, 64- or 128-row tiles");
+    using T = FmtTraits<F>;
+    using L = LS<F, kAI, 1>;
+    constexpr int kS = L::kS, kBM = L::kBM, kH = kAI / 2;
+    constexpr int kOps = kH + L::kBLoads / 8;  // direct-to-LDS loads per wave and stage
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int qd = wave & 3, half = wave >> 2;
+    const int wm = qd >> 1, wn = qd & 1;
+    const int g = lane >> 4, l16 = lane & 15;
+    const int tiles_n = (p.n + kBN - 1) / kBN;
+    const int tiles_m = (p.m + kBM - 1) / kBM;
+    const int tile = blockIdx.x;
+    if (tile >= tiles_m * tiles_n) return;
+    const int m0 = (tile % tiles_m) * kBM, n0 = (tile / tiles_m) * kBN;
+    const size_t lda = (size_t)p.k * T::aElemNum / T::aElemDen;
+    const size_t ldb = (size_t)p.k * T::bNum / T::bDen;
+    const int steps = p.k / T::kStep;
+    const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)lds;
+
+    // activation load i of this wave: 8-row group x = wave * kH + i (rows 8 x + q)
+    const int q = lane >> 3;
+    const uint32_t a_cq = (uint32_t)((lane & 7) ^ ((q >> 1) & 1) ^ (((q >> 2) & 1) << 1) ^ ((q & 1) << 2));
+    uint32_t a_off[kH], b_off[2];
+#pragma unroll
+    for (int i = 0; i < kH; ++i) {
+        const int x = wave * kH + i;
+        const int xs = x & 7;
+        const uint32_t ki = (uint32_t)((((xs >> 1) & 1) << 1) | (((xs ^ (xs >> 2)) & 1) << 2));
+        a_off[i] = (uint32_t)min(m0 + 8 * x + q, p.m - 1) * (uint32_t)lda + ((a_cq ^ ki) << 4);
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int o = (i * 8 + wave) * 1024 + lane * 16;
+        const int row = o >> 7;
+        const int c = ((o >> 4) & 7) ^ swz_key(row);
+        b_off[i] = (uint32_t)min(n0 + row, p.n - 1) * (uint32_t)ldb + (uint32_t)(c * 16);
+    }
+    auto issue = [&](int step) {
+        const uint32_t sbase = lds_base + (uint32_t)((step % kS) * L::kStageBytes);
+#pragma unroll
+        for (int i = 0; i < kH; ++i) dma16(p.a + (size_t)step * kRowBytes, a_off[i], sbase + (wave * kH + i) * 1024);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) dma16(p.b + (size_t)step * T::bRow, b_off[i], sbase + L::kATile + (i * 8 + wave) * 1024);
+    };
+
+    const int pre = min(kS - 1, steps);
+    for (int s = 0; s < pre; ++s) issue(s);
+
+    v4f accf[kH][4];
+    v4i acci[kH][4];
+#pragma unroll
+    for (int i = 0; i < kH; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            accf[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+            acci[i][j] = v4i{0, 0, 0, 0};
+        }
+    const int rb0 = wm * kAI + half * kH;  // this wave's first 16-row block of the tile
+    for (int step = 0; step < steps; ++step) {
+        wait_stages<kOps>(min(step + kS - 2, steps - 1) - step);
+        __syncthreads();
+        if (step + kS - 1 < steps) issue(step + kS - 1);
+        const uint8_t* As = lds + (step % kS) * L::kStageBytes;
+        const uint8_t* Bs = As + L::kATile;
+        uint4 w0[4], w1[4];
+        v4f gs[4];
+#pragma unroll
+        for (int bj = 0; bj < 4; ++bj)
+            weight_frag<F>(Bs, wn * 64 + wrow(l16, bj), g, bj, wn, step, nullptr, nullptr, w0[bj], w1[bj], gs[bj]);
+        uint4 xr0[kH], xr1[kH];
+#pragma unroll
+        for (int i = 0; i < kH; ++i) {
+            const int row = (rb0 + i) * 16 + l16;
+            xr0[i] = *(const uint4*)(As + swz(row, g));
+            xr1[i] = *(const uint4*)(As + swz(row, 4 + g));
+        }
+#pragma unroll
+        for (int i = 0; i < kH; ++i)
+#pragma unroll
+            for (int bj = 0; bj < 4; ++bj) mfma_step<F>(accf[i][bj], acci[i][bj], w0[bj], w1[bj], xr0[i], xr1[i], gs[bj]);
+    }
+    // rows of this wave: m0 + 16 rb0 + 16 a + l16 (a < kH), as the register
+    // epilogue's wave 0 of a kH-block tile at m0 + 16 rb0
+    if constexpr (E == EPI_F16_RES) {
+        epilogue<F, EPI_F16, true, kH>(p, accf, acci, m0 + 16 * rb0, n0, 0, wn, lane);
+    } else if constexpr (E == EPI_F32) {
+        __syncthreads();  // every wave is done with the ring: 4 KiB of it per wave stage the output rows
+        epilogue<F, E, false, kH>(p, accf, acci, m0 + 16 * rb0, n0, 0, wn, lane, lds + wave * 4096);
+    } else {
+        epilogue<F, E, false, kH>(p, accf, acci, m0 + 16 * rb0, n0, 0, wn, lane);
+    }
+}
+
 // For the group-wise INT4 formats at small T (FF2 at T = 750: 192 tiles of
 // 32 rows, K = 4096) the ring kernel above is a chain of K-steps whose every
 // link is an LDS read, the INT4 decode and the MFMAs; the tile count cannot
