@@ -64,7 +64,8 @@ def ring(pk, fmt, epi, m, n):
     return rows
 
 
-@pytest.mark.parametrize("m,n,k", [(750, 4096, 1024), (97, 1024, 4096), (1, 640, 1024), (33, 256, 128), (200, 1024, 512)])
+@pytest.mark.parametrize("m,n,k", [(750, 4096, 1024), (97, 1024, 4096), (1, 640, 1024), (33, 256, 128), (200, 1024, 512),
+                                   (750, 1536, 1024), (700, 1536, 384)])
 def test_ring_int8_accumulators_exact(pk, orc, m, n, k):
     rows = ring(pk, pk.FMT_I8, pk.EPI_I32, m, n)
     note(f"int8 m={m} n={n} k={k} ring rows={rows}")
@@ -111,7 +112,7 @@ def test_ring_fp32_staged_ragged(pk, orc, m, n, k, ldo):
     assert np.all(got[:, n:] == -7.0)
 
 
-@pytest.mark.parametrize("m,n,k", [(750, 4096, 1024), (300, 1024, 4096), (45, 3072, 1024)])
+@pytest.mark.parametrize("m,n,k", [(750, 4096, 1024), (300, 1024, 4096), (45, 3072, 1024), (750, 1536, 1024)])
 def test_ring_fp8_epilogues(pk, orc, m, n, k):
     rows = ring(pk, pk.FMT_FP8, pk.EPI_F16, m, n)
     note(f"fp8 m={m} n={n} k={k} ring rows={rows}")
