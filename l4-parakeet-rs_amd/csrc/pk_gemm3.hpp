@@ -803,19 +803,22 @@ __global__ __launch_bounds__(kThreads, kOcc) void gemm3_ring_kernel(GemmArgs p) 
 
 // ---- small grids, long K: one 32 x 128 tile per workgroup, K split over its 4 waves ----
 //
-// The ring kernel with two waves per SIMD (FP8 / INT8, 64- or 128-row
-// tiles): waves w and w + 4 share quadrant w % 4 of the tile (the same 64
-// columns and 16 kAI rows) and take its upper / lower kAI / 2 row blocks, so
-// each SIMD runs two independent MFMA / fragment-read chains of a K-step.
-// Stages, swizzles and epilogue as gemm3_ring_kernel; a wave issues kAI / 2
-// activation and two weight loads of a stage.
+// The ring kernel with two waves per SIMD: waves w and w + 4 share quadrant
+// w % 4 of the tile (its 64 columns and 16 kAI rows) and take its first
+// ceil(kAI / 2) / remaining row blocks, so each SIMD runs two independent
+// fragment-read / decode / MFMA chains of a K-step.  A stage's direct-to-LDS
+// loads (4 kAI activation row groups, then the weight chunks, L in all, a
+// multiple of 8) are dealt out as load j to wave j % 8.  Stages, swizzles,
+// group tables and epilogue as gemm3_ring_kernel.
+template <int F> constexpr int ring8_loads(int kAI) { return 4 * kAI + LS<F, 1, 1>::kBLoads; }
 template <int F, int E, int kAI>
 __global__ __launch_bounds__(2 * kThreads, 1) void gemm3_ring8_kernel(GemmArgs p) {
-    static_assert((F == FMT_FP8 || F == FMT_I8) && (kAI == 2 || kAI == 4), "byte formats, 64- or 128-row tiles");
     using T = FmtTraits<F>;
     using L = LS<F, kAI, 1>;
-    constexpr int kS = L::kS, kBM = L::kBM, kH = kAI / 2;
-    constexpr int kOps = kH + L::kBLoads / 8;  // direct-to-LDS loads per wave and stage
+    constexpr int kS = L::kS, kBM = L::kBM;
+    constexpr int kH0 = (kAI + 1) / 2, kH1 = kAI - kH0;  // row blocks of the first / second wave of a quadrant
+    constexpr int kL = ring8_loads<F>(kAI), kOps = kL / 8;
+    static_assert(kH1 >= 1 && kL % 8 == 0 && kOps <= 4, "8-wave ring layout");
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int qd = wave & 3, half = wave >> 2;
@@ -829,79 +832,100 @@ __global__ __launch_bounds__(2 * kThreads, 1) void gemm3_ring8_kernel(GemmArgs p
     const size_t lda = (size_t)p.k * T::aElemNum / T::aElemDen;
     const size_t ldb = (size_t)p.k * T::bNum / T::bDen;
     const int steps = p.k / T::kStep;
+    const int groups = p.k >> 7;
     const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)lds;
+    float* tab_s = (float*)(lds + L::kTab);
+    uint8_t* tab_z = lds + L::kTab + kMaxG128Groups * kBN * 4;
 
-    // activation load i of this wave: 8-row group x = wave * kH + i (rows 8 x + q)
+    // load slot i of this wave: j = wave + 8 i; activation row group j (rows
+    // 8 j + q) for j < 4 kAI, else weight chunk j - 4 kAI
     const int q = lane >> 3;
     const uint32_t a_cq = (uint32_t)((lane & 7) ^ ((q >> 1) & 1) ^ (((q >> 2) & 1) << 1) ^ ((q & 1) << 2));
-    uint32_t a_off[kH], b_off[2];
+    uint32_t off[kOps], dst[kOps];
 #pragma unroll
-    for (int i = 0; i < kH; ++i) {
-        const int x = wave * kH + i;
-        const int xs = x & 7;
-        const uint32_t ki = (uint32_t)((((xs >> 1) & 1) << 1) | (((xs ^ (xs >> 2)) & 1) << 2));
-        a_off[i] = (uint32_t)min(m0 + 8 * x + q, p.m - 1) * (uint32_t)lda + ((a_cq ^ ki) << 4);
-    }
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int o = (i * 8 + wave) * 1024 + lane * 16;
-        const int row = o >> 7;
-        const int c = ((o >> 4) & 7) ^ swz_key(row);
-        b_off[i] = (uint32_t)min(n0 + row, p.n - 1) * (uint32_t)ldb + (uint32_t)(c * 16);
+    for (int i = 0; i < kOps; ++i) {
+        const int j = wave + 8 * i;
+        if (j < 4 * kAI) {
+            const int xs = j & 7;
+            const uint32_t ki = (uint32_t)((((xs >> 1) & 1) << 1) | (((xs ^ (xs >> 2)) & 1) << 2));
+            off[i] = (uint32_t)min(m0 + 8 * j + q, p.m - 1) * (uint32_t)lda + ((a_cq ^ ki) << 4);
+            dst[i] = (uint32_t)(j * 1024);
+        } else {
+            const int c = j - 4 * kAI;
+            const int o = c * 1024 + lane * 16;
+            int row, ch;
+            if constexpr (T::bRow == 128) {
+                row = o >> 7;
+                ch = ((o >> 4) & 7) ^ swz_key(row);
+            } else if constexpr (F == FMT_G128A8) {
+                row = o >> 6;
+                ch = ((o >> 4) & 3) ^ g128a8_key(row);
+            } else {
+                a16_chunk_of_slot(o >> 4, row, ch);
+            }
+            off[i] = (uint32_t)min(n0 + row, p.n - 1) * (uint32_t)ldb + (uint32_t)(ch * 16);
+            dst[i] = (uint32_t)(L::kATile + c * 1024);
+        }
     }
     auto issue = [&](int step) {
         const uint32_t sbase = lds_base + (uint32_t)((step % kS) * L::kStageBytes);
 #pragma unroll
-        for (int i = 0; i < kH; ++i) dma16(p.a + (size_t)step * kRowBytes, a_off[i], sbase + (wave * kH + i) * 1024);
-#pragma unroll
-        for (int i = 0; i < 2; ++i) dma16(p.b + (size_t)step * T::bRow, b_off[i], sbase + L::kATile + (i * 8 + wave) * 1024);
+        for (int i = 0; i < kOps; ++i) {
+            if (wave + 8 * i < 4 * kAI) dma16(p.a + (size_t)step * kRowBytes, off[i], sbase + dst[i]);
+            else dma16(p.b + (size_t)step * T::bRow, off[i], sbase + dst[i]);
+        }
     };
 
     const int pre = min(kS - 1, steps);
     for (int s = 0; s < pre; ++s) issue(s);
+    if constexpr (L::kG128) load_group_tables<float, 2 * kThreads>(p, n0, groups, tab_s, tab_z, tid);
 
-    v4f accf[kH][4];
-    v4i acci[kH][4];
+    v4f accf[kH0][4];
+    v4i acci[kH0][4];
 #pragma unroll
-    for (int i = 0; i < kH; ++i)
+    for (int i = 0; i < kH0; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             accf[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
             acci[i][j] = v4i{0, 0, 0, 0};
         }
-    const int rb0 = wm * kAI + half * kH;  // this wave's first 16-row block of the tile
+    const int nb = half ? kH1 : kH0;            // this wave's row blocks (wave-uniform)
+    const int rb0 = wm * kAI + half * kH0;      // its first 16-row block of the tile
     for (int step = 0; step < steps; ++step) {
         wait_stages<kOps>(min(step + kS - 2, steps - 1) - step);
         __syncthreads();
         if (step + kS - 1 < steps) issue(step + kS - 1);
         const uint8_t* As = lds + (step % kS) * L::kStageBytes;
         const uint8_t* Bs = As + L::kATile;
+        const int grp = (step * T::kStep) >> 7;
         uint4 w0[4], w1[4];
         v4f gs[4];
 #pragma unroll
         for (int bj = 0; bj < 4; ++bj)
-            weight_frag<F>(Bs, wn * 64 + wrow(l16, bj), g, bj, wn, step, nullptr, nullptr, w0[bj], w1[bj], gs[bj]);
-        uint4 xr0[kH], xr1[kH];
+            weight_frag<F>(Bs, wn * 64 + wrow(l16, bj), g, bj, wn, step, tab_s + grp * kBN, tab_z + grp * kBN, w0[bj], w1[bj], gs[bj]);
 #pragma unroll
-        for (int i = 0; i < kH; ++i) {
-            const int row = (rb0 + i) * 16 + l16;
-            xr0[i] = *(const uint4*)(As + swz(row, g));
-            xr1[i] = *(const uint4*)(As + swz(row, 4 + g));
+        for (int i = 0; i < kH0; ++i) {
+            if (i < nb) {
+                const int row = (rb0 + i) * 16 + l16;
+                const uint4 x0 = *(const uint4*)(As + swz(row, g));
+                const uint4 x1 = *(const uint4*)(As + swz(row, 4 + g));
+#pragma unroll
+                for (int bj = 0; bj < 4; ++bj) mfma_step<F>(accf[i][bj], acci[i][bj], w0[bj], w1[bj], x0, x1, gs[bj]);
+            }
         }
-#pragma unroll
-        for (int i = 0; i < kH; ++i)
-#pragma unroll
-            for (int bj = 0; bj < 4; ++bj) mfma_step<F>(accf[i][bj], acci[i][bj], w0[bj], w1[bj], xr0[i], xr1[i], gs[bj]);
     }
-    // rows of this wave: m0 + 16 rb0 + 16 a + l16 (a < kH), as the register
-    // epilogue's wave 0 of a kH-block tile at m0 + 16 rb0
+    // rows of this wave: m0 + 16 rb0 + 16 a + l16 (a < nb), as the register
+    // epilogue's wave 0 of a kH0-block tile at m0 + 16 rb0 whose rows end
+    // after nb blocks (the accumulators past them hold zeros and are not stored)
+    GemmArgs pe = p;
+    pe.m = min(p.m, m0 + 16 * (rb0 + nb));
     if constexpr (E == EPI_F16_RES) {
-        epilogue<F, EPI_F16, true, kH>(p, accf, acci, m0 + 16 * rb0, n0, 0, wn, lane);
+        epilogue<F, EPI_F16, true, kH0>(pe, accf, acci, m0 + 16 * rb0, n0, 0, wn, lane);
     } else if constexpr (E == EPI_F32) {
         __syncthreads();  // every wave is done with the ring: 4 KiB of it per wave stage the output rows
-        epilogue<F, E, false, kH>(p, accf, acci, m0 + 16 * rb0, n0, 0, wn, lane, lds + wave * 4096);
+        epilogue<F, E, false, kH0>(pe, accf, acci, m0 + 16 * rb0, n0, 0, wn, lane, lds + wave * 4096);
     } else {
-        epilogue<F, E, false, kH>(p, accf, acci, m0 + 16 * rb0, n0, 0, wn, lane);
+        epilogue<F, E, false, kH0>(pe, accf, acci, m0 + 16 * rb0, n0, 0, wn, lane);
     }
 }
 
