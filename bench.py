@@ -33,7 +33,7 @@ LINEARS = [
 ]
 FORMATS = ("fp8", "int8", "int4g128")
 FLOP_PER_FRAME = sum(2 * n * k for _, n, k, _ in LINEARS) * LAYERS  # 1.1576e9
-PEAK = {"fp8": 5000.0, "int8": 5000.0}  # dense TFLOP/s (TOP/s) MI355X
+PEAK = {"fp8": 5000.0, "int8": 5000.0, "fp16": 2500.0}  # dense TFLOP/s (TOP/s) MI355X
 
 
 def format_plan(seed=0x5EED0005):
@@ -1009,7 +1009,9 @@ def roof(flops, nbytes, peak_tops):
 
 def config_results(pk, torch, stream, reps=10):
     """BASELINE configs 1-4 on the GPU: per GEMM TOPS, GB/s (algorithmic bytes)
-    and the fraction of its roofline min(5.0 PF, AI x 8 TB/s), from the average
+    and the fraction of its roofline min(MFMA peak, AI x 8 TB/s) (5.0 PF for
+    FP8 / INT8 MFMAs, 2.5 PF for the fp16 MFMAs of the INT4-g128 x fp16
+    kernels, which also report the 5.0 PF fraction), from the average
     of `reps` back-to-back launches; beside it, the quant_benchmark.rs:600-641
     timing method: the median of 7 single warm launches and the median of 7
     single cold launches, each after a 512 MiB scrub (twice the MALL) evicts
@@ -1036,13 +1038,17 @@ def config_results(pk, torch, stream, reps=10):
         cold = sorted(single(fn, True) for _ in range(7))[3]
         return avg, warm, cold
 
-    def entry(ms, flops, nbytes, useful=None):
+    def entry(ms, flops, nbytes, useful=None, mfma="fp8"):
+        # the roofline's MFMA peak is the kernel's own MFMA type: FP8 / INT8
+        # 5.0 PF, fp16 (the INT4-g128 x fp16 kernels dequantize to fp16) 2.5 PF
         ms, warm, cold = ms
         tops = flops / (ms * 1e-3) / 1e12
-        r = roof(flops, nbytes, PEAK["fp8"])
+        r = roof(flops, nbytes, PEAK[mfma])
         e = {"us": round(ms * 1e3, 1), "TOPS": round(tops, 1), "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1),
-             "roofline_TOPS": round(r, 1), "frac": round(tops / r, 3), "warm_median_us": round(warm * 1e3, 1),
-             "cold_median_us": round(cold * 1e3, 1)}
+             "mfma_peak_TOPS": PEAK[mfma], "roofline_TOPS": round(r, 1), "frac": round(tops / r, 3),
+             "warm_median_us": round(warm * 1e3, 1), "cold_median_us": round(cold * 1e3, 1)}
+        if mfma != "fp8":
+            e["frac_of_fp8_peak_roofline"] = round(tops / roof(flops, nbytes, PEAK["fp8"]), 3)
         if useful is not None:
             e["useful_TOPS"] = round(useful / (ms * 1e-3) / 1e12, 1)
         return e
@@ -1126,7 +1132,7 @@ def config_results(pk, torch, stream, reps=10):
             wb = n * k // 2 + 4 * n * (k // 128)
             ms = timed(lambda: pk.gemm(pk.FMT_G128A16, pk.EPI_F16, x, q, t, n, k, o, g_scales=s, g_zeros=z,
                                        stream=stream))
-            c3[f"{name}_a16_T{t}"] = entry(ms, 2 * t * n * k, 2 * t * k + wb + 2 * t * n)
+            c3[f"{name}_a16_T{t}"] = entry(ms, 2 * t * n * k, 2 * t * k + wb + 2 * t * n, mfma="fp16")
             xq, xs = rows_q(1, t, k, x)
             ms = timed(lambda: pk.gemm(pk.FMT_G128A8, pk.EPI_F16, xq, q, t, n, k, o, row_scales=xs, g_scales=s,
                                        g_zeros=z, stream=stream))
