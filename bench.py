@@ -687,6 +687,69 @@ def measured_traffic(spec):
         return None
 
 
+def clock_probe(pk, torch, stream, t=T, reps=20, samples=3):
+    """The shader clock the FP8 / INT8 GEMMs run at: the FF1 expand (FP8,
+    e4m3 SiLU epilogue, T frames) timed over `reps` launches with random
+    e4m3 operands and with all-zero operands, and `rocm-smi --showclocks`
+    sampled while the same launches run back to back on a second thread.
+    MFMA power depends on the operand bits: where the random operands hold
+    the clock below its maximum, the 5.0 PF dense peak (quoted at 2.4 GHz)
+    is not reachable at the running clock."""
+    import re
+    import subprocess
+    import threading
+
+    out = {"kernel": "FF1 expand FP8 45000 x 1024 -> 4096, e4m3 SiLU out", "clock_source": "rocm-smi --showclocks"}
+    n, k = FF, D
+    for name in ("random", "zero"):
+        g = torch.Generator(device="cuda")
+        g.manual_seed(5)
+        a = torch.randint(0, 256, (t, k), generator=g, device="cuda", dtype=torch.uint8)
+        w = torch.randint(0, 256, (n, k), generator=g, device="cuda", dtype=torch.uint8)
+        a = (a & 0x80) | (a & 0x3F)  # finite e4m3 codes of magnitude < 2
+        w = (w & 0x80) | (w & 0x3F)
+        if name == "zero":
+            a.zero_()
+            w.zero_()
+        ws = torch.full((n,), 0.01, device="cuda")
+        xs = torch.full((t,), 0.01, device="cuda")
+        o = torch.empty((t, n), dtype=torch.uint8, device="cuda")
+        fn = lambda: pk.gemm(pk.FMT_FP8, pk.EPI_F8, a, w, t, n, k, o, w_scales=ws, row_scales=xs, stream=stream)
+        fn()
+        warm_up(torch, fn, 0.3)
+        us = time_events(torch, fn, reps, stream) * 1e3
+        stop = [False]
+
+        def spin():
+            while not stop[0]:
+                for _ in range(40):
+                    fn()
+                torch.cuda.synchronize()
+
+        th = threading.Thread(target=spin)
+        th.start()
+        mhz = []
+        try:
+            time.sleep(0.5)
+            for _ in range(samples):
+                r = subprocess.run(["rocm-smi", "--showclocks"], capture_output=True, text=True, timeout=30)
+                m = re.search(r"sclk clock level: \d+: \((\d+)Mhz\)", r.stdout)
+                if m:
+                    mhz.append(int(m.group(1)))
+                time.sleep(0.3)
+        except (OSError, subprocess.SubprocessError):
+            pass
+        finally:
+            stop[0] = True
+            th.join()
+        out[name] = {"us": round(us, 1), "TOPS": round(2.0 * t * n * k / (us * 1e-6) / 1e12, 1), "sclk_MHz": mhz or None}
+        del a, w, o
+    if out["random"]["sclk_MHz"]:
+        f = sum(out["random"]["sclk_MHz"]) / len(out["random"]["sclk_MHz"]) / 2400.0
+        out["fp8_peak_at_running_clock_TOPS"] = round(PEAK["fp8"] * f, 1)
+    return out
+
+
 def hipblaslt_yardstick(pk, torch, stream, t=T, reps=20):
     """A yardstick, not part of this library's path: torch._scaled_mm (hipBLASLt)
     on the stack's three FP8 GEMM shapes (per-tensor scales, bf16 output, no
@@ -1313,6 +1376,8 @@ def main():
     ap.add_argument("--hipblaslt", action="store_true",
                     help="yardstick: hipBLASLt (torch._scaled_mm) against this library's FP8 kernels on the stack's shapes")
     ap.add_argument("--only-configs", action="store_true", help="run only the BASELINE config 1-4 measurements")
+    ap.add_argument("--only-clock", action="store_true",
+                    help="run only the shader-clock probe (FF1 expand FP8 with random vs all-zero operands)")
     ap.add_argument("--only-refplan", action="store_true",
                     help="run only the reference-plan stack (pipeline.rs precision plan) measurements")
     ap.add_argument("--only-stack", action="store_true",
@@ -1332,6 +1397,9 @@ def main():
     stream = torch.cuda.current_stream()
     if args.hipblaslt:
         print(json.dumps(hipblaslt_yardstick(pk, torch, stream, args.frames)), flush=True)
+        return
+    if args.only_clock:
+        print(json.dumps(clock_probe(pk, torch, stream, args.frames)), flush=True)
         return
     if args.only_joint:
         res = joint_streaming(pk, torch, stream, reps=20)
@@ -1419,6 +1487,7 @@ def main():
     attention = attention_bench(pk, torch, stream, args.frames)
     configs = config_results(pk, torch, stream)
     refplan = refplan_bench(pk, torch, args.frames, stream)
+    clock = clock_probe(pk, torch, stream, args.frames)
     cpu = None if args.no_cpu else cpu_baseline(plan)
 
     audio_min = args.frames * 0.08 / 60.0
@@ -1475,6 +1544,7 @@ def main():
                                                           / 1e12, 2)),
         "cold_step_ms": round(cold_ms, 3),
         "cold_step_TOPS": round(total_flops / (cold_ms * 1e-3) / 1e12, 2),
+        "shader_clock": clock,
         "cpu_baseline": cpu,
         "configs": configs,
         "wall_s_timed": round(wall, 3),
