@@ -755,7 +755,9 @@ def hipblaslt_yardstick(pk, torch, stream, t=T, reps=20):
     on the stack's three FP8 GEMM shapes (per-tensor scales, bf16 output, no
     epilogue) beside this library's FP8 kernels on the same shapes with their
     stack epilogues (FF1 expand: SiLU e4m3; FF contract: fp16 + residual; QKV:
-    fp16), each warmed up for a quarter second and averaged over `reps`."""
+    fp16), each warmed up for a quarter second and averaged over `reps`; and
+    this library's FP8 kernel with a plain fp16 epilogue on hipBLASLt's own
+    operands (randn cast to e4m3), since the clock depends on the operand bits."""
     out = {}
     sa = torch.tensor(1.0, device="cuda")
     sb = torch.tensor(1.0, device="cuda")
@@ -765,10 +767,19 @@ def hipblaslt_yardstick(pk, torch, stream, t=T, reps=20):
         f = lambda: torch._scaled_mm(a, b.t(), scale_a=sa, scale_b=sb, out_dtype=torch.bfloat16)
         warm_up(torch, f, 0.25)
         lib_ms = time_events(torch, f, reps, stream)
-        del a, b
+        # the same operand bits through this library's FP8 kernel with a plain
+        # fp16 epilogue (MFMA power, hence the clock, depends on the operands)
+        ws = torch.ones(n, device="cuda")
+        o16 = torch.empty((t, n), dtype=torch.float16, device="cuda")
+        g = lambda: pk.gemm(pk.FMT_FP8, pk.EPI_F16, a.view(torch.uint8), b.view(torch.uint8), t, n, k, o16,
+                            w_scales=ws, in_scale=1.0, stream=stream)
+        warm_up(torch, g, 0.25)
+        same_ms = time_events(torch, g, reps, stream)
+        del a, b, o16
         ours_ms, flops, _ = kernel_time(pk, torch, t, ("fp8", kind, n, k), stream, reps)
         out[name] = {"m": t, "n": n, "k": k, "hipblaslt_us": round(lib_ms * 1e3, 1),
                      "hipblaslt_TFLOPs": round(flops / (lib_ms * 1e-3) / 1e12, 1),
+                     "ours_same_operands_fp16_out_us": round(same_ms * 1e3, 1),
                      "ours_us": round(ours_ms * 1e3, 1), "ours_TFLOPs": round(flops / (ours_ms * 1e-3) / 1e12, 1),
                      "ours_epilogue": EPI_NAME[kind]}
         torch.cuda.empty_cache()
