@@ -92,10 +92,15 @@ __device__ __forceinline__ uint32_t asm_load1(const void* ptr) {
 // A 16-byte global store issued from inline asm: the deferred epilogue below
 // waits for the next tile's loads with vmcnt(its store count), which is exact
 // only if every store it makes is one instruction the compiler cannot split,
-// merge, predicate away or move past that wait.
+// merge, predicate away or move past that wait.  A store of more than 8 bytes
+// reads its data registers after issue: on this GPU a VALU write to them
+// needs two wait states after the store (one was measured not to suffice:
+// the compiler reused a store's data registers for the next address).  The
+// compiler inserts them for the stores it can see, not for inline asm, hence
+// the s_nop 1.
 __device__ __forceinline__ void asm_store4(void* ptr, uint4 v) {
     const v4i x = __builtin_bit_cast(v4i, v);
-    asm volatile("global_store_dwordx4 %0, %1, off" ::"v"(ptr), "v"(x) : "memory");
+    asm volatile("global_store_dwordx4 %0, %1, off\n\ts_nop 1" ::"v"(ptr), "v"(x) : "memory");
 }
 __device__ __forceinline__ uint32_t launder(uint32_t x) {
     asm volatile("" : "+v"(x));

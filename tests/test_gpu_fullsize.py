@@ -357,3 +357,31 @@ def test_quantize_rows_T45000(pk, orc, kind, k):
         rows_of(x, idx), int((idx < valid).sum()))
     assert np.array_equal(host(scales)[idx], ref[1])
     assert np.array_equal(rows_of(out, idx).view(np.uint8), ref[0].view(np.uint8))
+
+
+@pytest.mark.parametrize("m,n,k", [(7500, 1024, 4096), (45000, 4096, 1024), (2000, 3072, 1024)])
+def test_fp32_outputs_large_grid(pk, orc, m, n, k):
+    """fp32 outputs of the occupancy-2 engine (FP8 / INT8 formats store them
+    from the deferred epilogue, 16 bytes per instruction): INT8 at unit scales
+    equals its int32 accumulators exactly, FP8 matches the oracle on sampled
+    rows within 1e-2 * RMS.  Regression test for a store whose data registers
+    were rewritten before the store had read them (rows 12-15 of 16-row
+    blocks came out wrong)."""
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(m + n + k)
+    a = torch.randint(-127, 128, (m, k), generator=gen, device="cuda", dtype=torch.int8)
+    b = torch.randint(-127, 128, (n, k), generator=gen, device="cuda", dtype=torch.int8)
+    acc = torch.empty((m, n), dtype=torch.int32, device="cuda")
+    out = torch.full((m, n), float("nan"), dtype=torch.float32, device="cuda")
+    note(f"fp32 outputs INT8 m={m} n={n} k={k} tile={pk.gemm_tile(pk.FMT_I8, pk.EPI_F32, m, n)}")
+    pk.gemm(pk.FMT_I8, pk.EPI_I32, a, b, m, n, k, acc)
+    pk.gemm(pk.FMT_I8, pk.EPI_F32, a, b, m, n, k, out, in_scale=1.0)
+    assert torch.equal(out, acc.to(torch.float32))
+    x8 = (torch.randn((m, k), generator=gen, device="cuda") * 2).to(torch.float8_e4m3fn).view(torch.uint8)
+    w8 = (torch.randn((n, k), generator=gen, device="cuda") * 2).to(torch.float8_e4m3fn).view(torch.uint8)
+    out.fill_(float("nan"))
+    note(f"fp32 outputs FP8 m={m} n={n} k={k} tile={pk.gemm_tile(pk.FMT_FP8, pk.EPI_F32, m, n)}")
+    pk.gemm(pk.FMT_FP8, pk.EPI_F32, x8, w8, m, n, k, out, in_scale=1.0)
+    idx = sample_rows(m, m + 7)
+    assert_close(rows_of(out, idx), orc.gemm_e4m3(rows_of(x8, idx), host(w8)), what=f"fp8 fp32 out m={m}")
+    assert not torch.isnan(out).any()
