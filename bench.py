@@ -166,10 +166,12 @@ class RefPlanStack:
     FF2   LayerNorm -> dynamic INT4, s4 x s4 expand with SiLU x16 e4m3 and 2:4
           compression, request-time FP8 contract weight, sparse FP8 contract
           on v_smfmac (pk_ffn_contract_fp8_sparse); the INT4 codes of the
-          activations and of the weights are kept as int8 bytes, the operand
-          the INT8 MFMA reads (pk_layer_norm_quantize_int4_codes,
-          pk_unpack_int4 at load time, pk_ffn_expand_int4_sparse_codes: the
-          same accumulators and output bytes as the nibble-pair entry points)
+          activations and of the weights are kept as FP6 e3m2 (exact for
+          -8..7), the operand the f8f6f4 MFMA reads at the FP6 rate
+          (pk_layer_norm_quantize_int4_fp6, pk_unpack_int4_fp6 at load time,
+          pk_ffn_expand_int4_sparse_fp6: the same exact sums and output bytes
+          as the nibble-pair and int8-code entry points, which the classes
+          time beside it)
                                                              encoder.rs:1015-1081
     norm  LayerNorm pair: this layer's norm_out and the next layer's norm_ff1
           with the e4m3 x56 output (pk_layer_norm_pair)      encoder.rs:1093-1115
@@ -208,7 +210,10 @@ class RefPlanStack:
             L["ff2_e"] = torch.empty((FF, D // 2), dtype=torch.uint8, device=dev)
             L["ff2_es"] = torch.empty(FF, dtype=torch.float32, device=dev)
             pk.call("pk_pack_int4_rows", w16(FF, D), FF, D, L["ff2_e"], L["ff2_es"])
-            # the operand form (int8 codes) derived at load time
+            # the operand forms derived at load time: FP6 e3m2 codes (the step's)
+            # and int8 codes (timed beside it)
+            L["ff2_ef"] = torch.empty((FF, D), dtype=torch.uint8, device=dev)
+            pk.call("pk_unpack_int4_fp6", L["ff2_e"], L["ff2_ef"], FF * D)
             L["ff2_ec"] = torch.empty((FF, D), dtype=torch.int8, device=dev)
             pk.call("pk_unpack_int4", L["ff2_e"], L["ff2_ec"], FF * D)
             L["ff2_c16"] = w16(D, FF)
@@ -247,6 +252,7 @@ class RefPlanStack:
         self.xs = torch.empty(t, dtype=torch.float32, device=dev)
         self.x4 = torch.empty((t, D // 2), dtype=torch.uint8, device=dev)  # INT4 FF2 input (nibble pairs)
         self.x4c = torch.empty((t, D), dtype=torch.int8, device=dev)      # the same codes as int8 bytes
+        self.x4f = torch.empty((t, D), dtype=torch.uint8, device=dev)     # and as FP6 e3m2 chunks
         self.h8 = torch.empty((t, FF), dtype=torch.uint8, device=dev)      # x16 e4m3 FF1 hidden
         self.sp = torch.empty(t * (FF // 2 + FF // 8), dtype=torch.uint8, device=dev)  # 2:4 FF2 hidden
         self.qkv = torch.empty((t, 3 * D), dtype=torch.float16, device=dev)
@@ -299,8 +305,8 @@ class RefPlanStack:
             c("pk_conv_residual_fp8", self.dw8, *P["p2"], self.dws, self.state, t)
         # FF2: LN -> INT4, s4 expand with 2:4, sparse FP8 contract
         if request_time:
-            c("pk_layer_norm_quantize_int4_codes", self.state, *L["n_ff2"], self.x4c, self.xs, t, t, 1e-5)
-        c("pk_ffn_expand_int4_sparse_codes", self.x4c, L["ff2_ec"], L["ff2_es"], self.xs, self.sp, t, 1.0, 1)
+            c("pk_layer_norm_quantize_int4_fp6", self.state, *L["n_ff2"], self.x4f, self.xs, t, t, 1e-5)
+        c("pk_ffn_expand_int4_sparse_fp6", self.x4f, L["ff2_ef"], L["ff2_es"], self.xs, self.sp, t, 1.0, 1)
         if request_time:
             c("pk_quantize_ffn_contract", L["ff2_c16"], self.wc, self.wc_s)
             c("pk_ffn_contract_fp8_sparse", self.sp, self.wc, self.wc_s, self.state, t, FF)
@@ -340,8 +346,8 @@ class RefPlanStack:
             ("conv_residual_fp8", 2.0 * t * D * D,
              lambda i: pk.call("pk_conv_residual_fp8", self.dw8, *self.pre[i]["p2"], self.dws, self.state, t,
                                stream=stream)),
-            ("ffn_expand_int4_sparse_codes", 2.0 * t * FF * D,
-             lambda i: pk.call("pk_ffn_expand_int4_sparse_codes", self.x4c, self.layers[i]["ff2_ec"],
+            ("ffn_expand_int4_sparse_fp6", 2.0 * t * FF * D,
+             lambda i: pk.call("pk_ffn_expand_int4_sparse_fp6", self.x4f, self.layers[i]["ff2_ef"],
                                self.layers[i]["ff2_es"], self.xs, self.sp, t, 1.0, 1, stream=stream)),
             ("ffn_contract_fp8_sparse", 2.0 * t * D * FF,
              lambda i: pk.call("pk_ffn_contract_fp8_sparse", self.sp, *self.pre[i]["c2"], self.state, t, FF,
@@ -355,13 +361,22 @@ class RefPlanStack:
             out.append({"linear": name, "avg_ms": round(ms, 4), "step_ms": round(ms * LAYERS, 3),
                         "TOPS": round(flops / (ms * 1e-3) / 1e12, 1)})
         out.sort(key=lambda e: -e["step_ms"])
-        # the drop-in form (nibble pairs decoded in the K-loop), not in the step
-        run = lambda: [pk.call("pk_ffn_expand_int4_sparse", self.x4, self.layers[i]["ff2_e"], self.layers[i]["ff2_es"],
-                               self.xs, self.sp, t, 1.0, 1, stream=stream) for i in range(LAYERS)]
-        run()
-        ms = time_events(torch, run, reps, stream) / LAYERS
-        out.append({"linear": "ffn_expand_int4_sparse (nibble-pair operands, not in the step)", "avg_ms": round(ms, 4),
-                    "TOPS": round(2.0 * t * FF * D / (ms * 1e-3) / 1e12, 1)})
+        # the same expand on the other operand forms, not in the step: the drop-in
+        # nibble pairs (decoded in the K-loop) and int8 codes on the INT8 MFMA,
+        # their inputs written by the matching producers from the current state
+        n_ff2 = self.layers[0]["n_ff2"]
+        pk.call("pk_layer_norm_quantize_int4_dynamic", self.state, *n_ff2, self.x4, self.xs, t, t, 1e-5, stream=stream)
+        pk.call("pk_layer_norm_quantize_int4_codes", self.state, *n_ff2, self.x4c, self.xs, t, t, 1e-5, stream=stream)
+        for name, fn in (("ffn_expand_int4_sparse (nibble-pair operands, not in the step)",
+                          lambda i: pk.call("pk_ffn_expand_int4_sparse", self.x4, self.layers[i]["ff2_e"],
+                                            self.layers[i]["ff2_es"], self.xs, self.sp, t, 1.0, 1, stream=stream)),
+                         ("ffn_expand_int4_sparse_codes (int8 code operands, INT8 MFMA, not in the step)",
+                          lambda i: pk.call("pk_ffn_expand_int4_sparse_codes", self.x4c, self.layers[i]["ff2_ec"],
+                                            self.layers[i]["ff2_es"], self.xs, self.sp, t, 1.0, 1, stream=stream))):
+            run = lambda: [fn(i) for i in range(LAYERS)]
+            run()
+            ms = time_events(torch, run, reps, stream) / LAYERS
+            out.append({"linear": name, "avg_ms": round(ms, 4), "TOPS": round(2.0 * t * FF * D / (ms * 1e-3) / 1e12, 1)})
         return out
 
 
@@ -380,7 +395,7 @@ def refplan_bench(pk, torch, t, stream, steps=5):
     top = classes[0]
     dom_flops = {"ff1_expand_fp8_packed": FF * D, "ff1_contract_fp8": D * FF, "qkv_fp8_dyn": 3 * D * D,
                  "attention_output_fp8": D * D, "conv_glu_fp8": CONV * D, "conv_residual_fp8": D * D,
-                 "ffn_expand_int4_sparse_codes": FF * D, "ffn_contract_fp8_sparse": D * FF}[top["linear"]] * 2.0 * t
+                 "ffn_expand_int4_sparse_fp6": FF * D, "ffn_contract_fp8_sparse": D * FF}[top["linear"]] * 2.0 * t
     achieved = dom_flops / (top["avg_ms"] * 1e-3) / 1e12
     del rp
     torch.cuda.empty_cache()

@@ -216,6 +216,20 @@ int32_t pk_layer_norm_pair(const uint16_t* input, const uint16_t* weight, const 
 int32_t pk_layer_norm_quantize_int4_codes(const uint16_t* input, const uint16_t* weight, const uint16_t* bias,
                                           int8_t* output, float* scales, int32_t rows, int32_t padded_rows,
                                           float epsilon, void* stream);
+/* No reference counterpart: the same producer (same scales, same codes) with
+ * the codes written in the FP6 e3m2 chunk form: 16 codes a 16-byte chunk, code
+ * j of the chunk in bits 6j..6j+5 of its first 12 bytes (little-endian), then
+ * 4 zero bytes; e3m2 holds every code in -8..7 exactly.  [padded_rows x 1024]
+ * bytes, the operand pk_ffn_expand_int4_sparse_fp6 reads on the f8f6f4 MFMA,
+ * which multiplies FP6 at twice the FP8 / INT8 rate.  output 4-byte aligned. */
+int32_t pk_layer_norm_quantize_int4_fp6(const uint16_t* input, const uint16_t* weight, const uint16_t* bias,
+                                        uint8_t* output, float* scales, int32_t rows, int32_t padded_rows,
+                                        float epsilon, void* stream);
+/* No reference counterpart: nibble pairs (as pk_unpack_int4 reads them) -> the
+ * FP6 e3m2 chunk form above, `elements` codes (a multiple of 32) into as many
+ * bytes; both pointers 16-byte aligned.  The load-time derivation of the
+ * per-row INT4 FF2 weights' FP6 operand form. */
+int32_t pk_unpack_int4_fp6(const uint8_t* packed, uint8_t* codes, int64_t elements, void* stream);
 /* Nibble pairs (byte j = q[2j] & 15 | q[2j+1] << 4, the encoder.rs:405 order of
  * pk_pack_int4_rows and of the INT4 producer) -> sign-extended int8 codes,
  * `elements` codes (a multiple of 32); both pointers 16-byte aligned.  The
@@ -313,6 +327,15 @@ int32_t pk_ffn_expand_int4_sparse(const uint8_t* input, const uint8_t* weight, c
 int32_t pk_ffn_expand_int4_sparse_codes(const int8_t* input, const int8_t* weight, const float* weight_scales,
                                         const float* input_scales, uint8_t* output, int32_t rows, float input_scale,
                                         int32_t dynamic, void* stream);
+/* pk_ffn_expand_int4_sparse on the FP6 form of the same INT4 values: FP6 chunk
+ * codes [rows x 1024] (pk_layer_norm_quantize_int4_fp6) x FP6 chunk codes
+ * [4096 x 1024] (pk_unpack_int4_fp6 of the per-row INT4 weights), on the
+ * f8f6f4 MFMA at the FP6 rate.  Products of codes are exact in FP6 x FP6 and
+ * the fp32 sums of K = 1024 of them (|sum| <= 2^16) are exact, so the output
+ * (data + metadata, same layout) is identical to pk_ffn_expand_int4_sparse's. */
+int32_t pk_ffn_expand_int4_sparse_fp6(const uint8_t* input, const uint8_t* weight, const float* weight_scales,
+                                      const float* input_scales, uint8_t* output, int32_t rows, float input_scale,
+                                      int32_t dynamic, void* stream);
 /* encoder.cu:1095-1103 pk_sm89_ffn_contract_fp8: FF contract 4096 -> 1024 on
  * FP8 input at scale 1/16; output (fp16 [rows x 1024]) += 0.5 * Y in place. */
 int32_t pk_ffn_contract_fp8(const uint8_t* input, const uint8_t* weight, const float* weight_scales,
@@ -410,7 +433,10 @@ int32_t pk_ffn_contract_int8_sparse24(const uint8_t* data, const uint8_t* meta, 
  * bytes (b from pk_expand_int4_g128_e4m3; g_scales required, group-major
  * [k/128 x n] as that call writes them, 16-byte aligned; g_zeros unused;
  * each 128-K group summed in fp32 by one MFMA, then folded in K order with
- * one fma by its fp16 scale; epilogues 0, 1 and 3).  epilogue: 0 fp16 (act(v [+bias]) * out_scale
+ * one fma by its fp16 scale; epilogues 0, 1 and 3), 9 INT4 codes as FP6 e3m2
+ * chunks on both operands (pk_layer_norm_quantize_int4_fp6 /
+ * pk_unpack_int4_fp6; k a multiple of 128; f8f6f4 MFMA, exact integer sums in
+ * fp32; epilogues 2 and 3).  epilogue: 0 fp16 (act(v [+bias]) * out_scale
  * [+ res_scale * residual]), 1 e4m3(fp16(SiLU(v)) * 16), 2 as 1 + 2:4
  * compression (metadata to out_meta), 3 fp32 v [+bias], 4 raw int32.
  * v = acc * row_scale * w_scale with row_scale = row_scales[r] or in_scale. */

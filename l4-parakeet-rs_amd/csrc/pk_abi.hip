@@ -223,6 +223,20 @@ int32_t pk_layer_norm_quantize_int4_codes(const uint16_t* in, const uint16_t* w,
     return ln_quantize(2, in, w, b, (uint8_t*)out, scales, rows, padded_rows, eps, stream);
 }
 
+int32_t pk_layer_norm_quantize_int4_fp6(const uint16_t* in, const uint16_t* w, const uint16_t* b, uint8_t* out, float* scales,
+                                        int32_t rows, int32_t padded_rows, float eps, void* stream) {
+    return ln_quantize(3, in, w, b, out, scales, rows, padded_rows, eps, stream);
+}
+
+int32_t pk_unpack_int4_fp6(const uint8_t* packed, uint8_t* codes, int64_t elements, void* stream) {
+    if (elements < 0 || elements % 32) { set_error("unpack_int4_fp6 needs a multiple of 32 elements (got %lld)", (long long)elements); return PK_E_SHAPE; }
+    if (elements == 0) return 0;
+    if (!need(packed, "packed") || !need(codes, "codes")) return PK_E_ARG;
+    if (((uintptr_t)packed | (uintptr_t)codes) & 15) { set_error("packed and codes must be 16-byte aligned"); return PK_E_ALIGN; }
+    launch_unpack_s4_fp6(packed, codes, (size_t)elements / 2, STREAM);
+    return check_launch("unpack_int4_fp6");
+}
+
 int32_t pk_unpack_int4(const uint8_t* packed, int8_t* codes, int64_t elements, void* stream) {
     if (elements < 0 || elements % 32) { set_error("unpack_int4 needs a multiple of 32 elements (got %lld)", (long long)elements); return PK_E_SHAPE; }
     if (elements == 0) return 0;
@@ -434,6 +448,20 @@ int32_t pk_ffn_expand_int4_sparse_codes(const int8_t* in, const int8_t* w, const
     g.in_scale = in_scale;
     g.out_meta = out + (size_t)rows * 2048;
     return launch_gemm(FMT_I8, EPI_F8_24, g, STREAM);
+}
+
+int32_t pk_ffn_expand_int4_sparse_fp6(const uint8_t* in, const uint8_t* w, const float* ws, const float* in_scales, uint8_t* out,
+                                      int32_t rows, float in_scale, int32_t dynamic, void* stream) {
+    if (!need(in, "input") || !need(w, "weight") || !need(out, "output") || !need(ws, "weight_scales") ||
+        (dynamic && !need(in_scales, "input_scales")))
+        return PK_E_ARG;
+    if (rows < 0) { set_error("negative rows"); return PK_E_SHAPE; }
+    GemmArgs g = base_args(in, w, rows, 4096, 1024, out, 4096);
+    g.w_scales = ws;
+    g.row_scales = dynamic ? in_scales : nullptr;
+    g.in_scale = in_scale;
+    g.out_meta = out + (size_t)rows * 2048;
+    return launch_gemm(FMT_S4F6, EPI_F8_24, g, STREAM);
 }
 
 int32_t pk_ffn_contract_fp8(const uint8_t* in, const uint8_t* w, const float* ws, uint16_t* out, int32_t rows, void* stream) {

@@ -318,6 +318,13 @@ static int by_epi(int epi, const GemmArgs& a, hipStream_t s) {
             return -4;
         }
     }
+    if constexpr (F == FMT_S4F6) {
+        // the INT4 x INT4 FF2 expand (2:4 e4m3 out) and fp32 outputs (its exact sums)
+        if (epi == EPI_F8_24) return launch_fmt<F, EPI_F8_24>(a, s);
+        if (epi == EPI_F32) return launch_fmt<F, EPI_F32>(a, s);
+        set_error("unsupported epilogue %d for format %d", epi, F);
+        return -4;
+    }
     switch (epi) {
     case EPI_F16: return a.residual ? launch_fmt<F, EPI_F16_RES>(a, s) : launch_fmt<F, EPI_F16>(a, s);
     case EPI_F32: return launch_fmt<F, EPI_F32>(a, s);
@@ -352,7 +359,7 @@ static int by_epi(int epi, const GemmArgs& a, hipStream_t s) {
 
 static int k_step(int fmt) {
     switch (fmt) {
-    case FMT_FP8: case FMT_I8: case FMT_G128A8: case FMT_I8_SKIP: case FMT_G128F8: return 128;
+    case FMT_FP8: case FMT_I8: case FMT_G128A8: case FMT_I8_SKIP: case FMT_G128F8: case FMT_S4F6: return 128;
     case FMT_S4: case FMT_Q4K: return 256;
     default: return 64;
     }
@@ -404,6 +411,7 @@ int launch_gemm(int fmt, int epi, const GemmArgs& a, hipStream_t s) {
     case FMT_I8_SKIP: return by_epi<FMT_I8_SKIP>(epi, a, s);
     case FMT_Q4K: return by_epi<FMT_Q4K>(epi, a, s);
     case FMT_G128F8: return by_epi<FMT_G128F8>(epi, a, s);
+    case FMT_S4F6: return by_epi<FMT_S4F6>(epi, a, s);
     default: break;
     }
     set_error("unknown format %d", fmt);
@@ -411,13 +419,13 @@ int launch_gemm(int fmt, int epi, const GemmArgs& a, hipStream_t s) {
 }
 
 int gemm_k_split(int fmt, int epi, int m, int n, int k) {
-    if (fmt < FMT_FP8 || fmt > FMT_G128F8) return -4;
+    if (fmt < FMT_FP8 || fmt > FMT_S4F6) return -4;
     if (forced_tile_rows() < 0) return -1;
     return k_split(fmt, epi == EPI_F16_RES ? EPI_F16 : epi, m, n, k);
 }
 
 int gemm_tile_plan(int fmt, int epi, int m, int n, int* cols, int* stages) {
-    if (fmt < FMT_FP8 || fmt > FMT_G128F8) return -4;
+    if (fmt < FMT_FP8 || fmt > FMT_S4F6) return -4;
     if (forced_tile_rows() < 0) return -1;
     return tile_plan(fmt, epi == EPI_F16_RES ? EPI_F16 : epi, m, n, cols, stages);
 }

@@ -38,7 +38,13 @@
 
 namespace pk {
 
-enum Fmt { FMT_FP8 = 0, FMT_I8 = 1, FMT_S4 = 2, FMT_G128A8 = 3, FMT_F16 = 4, FMT_G128A16 = 5, FMT_I8_SKIP = 6, FMT_Q4K = 7, FMT_G128F8 = 8 };
+// FMT_S4F6: INT4 codes as FP6 e3m2 (exact for -8..8), 16 codes a 16-byte
+// chunk (12 bytes of 6-bit fields, code j at bits 6j.., then 4 zero bytes):
+// rows have the int8 codes' size and layout of 16-byte chunks, so the engine
+// moves them as FP8 bytes; the f8f6f4 MFMA multiplies them at the FP6 rate
+// and its fp32 sums of at most 2^24 are the exact int32 accumulators.
+enum Fmt { FMT_FP8 = 0, FMT_I8 = 1, FMT_S4 = 2, FMT_G128A8 = 3, FMT_F16 = 4, FMT_G128A16 = 5, FMT_I8_SKIP = 6, FMT_Q4K = 7, FMT_G128F8 = 8,
+           FMT_S4F6 = 9 };
 
 enum Epi {
     EPI_F16 = 0,     // fp16 out: act(scale(acc) [+bias]) * out_scale [+ res_scale * residual]
@@ -91,6 +97,7 @@ template <> struct FmtTraits<FMT_F16> { static constexpr int kStep = 64, bRow = 
 template <> struct FmtTraits<FMT_G128A16> { static constexpr int kStep = 64, bRow = 32, aElemNum = 2, aElemDen = 1, bNum = 1, bDen = 2; static constexpr bool kInt = false; };
 // Q4_K: per column and 64-K step the superblock's 16-byte header (d, dmin,
 // 12 bytes of 6-bit scales/mins) and the step's 32 quant bytes.
+template <> struct FmtTraits<FMT_S4F6> { static constexpr int kStep = 128, bRow = 128, aElemNum = 1, aElemDen = 1, bNum = 1, bDen = 1; static constexpr bool kInt = false; };
 template <> struct FmtTraits<FMT_G128F8> { static constexpr int kStep = 128, bRow = 128, aElemNum = 1, aElemDen = 1, bNum = 1, bDen = 1; static constexpr bool kInt = false; };
 template <> struct FmtTraits<FMT_Q4K> { static constexpr int kStep = 64, bRow = 48, aElemNum = 2, aElemDen = 1, bNum = 9, bDen = 16; static constexpr bool kInt = false; };
 
@@ -181,6 +188,12 @@ __device__ __forceinline__ void mfma_step(v4f& accf, v4i& acci, const uint4& w0,
         const v8i W = {(int)w0.x, (int)w0.y, (int)w0.z, (int)w0.w, (int)w1.x, (int)w1.y, (int)w1.z, (int)w1.w};
         const v8i X = {(int)x0.x, (int)x0.y, (int)x0.z, (int)x0.w, (int)x1.x, (int)x1.y, (int)x1.z, (int)x1.w};
         accf = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(W, X, accf, 0, 0, 0, 0, 0, 0);
+    } else if constexpr (F == FMT_S4F6) {
+        // 32 FP6 codes a lane: the 12 data bytes of chunk g, then of chunk 4 + g
+        const v8i W = {(int)w0.x, (int)w0.y, (int)w0.z, (int)w1.x, (int)w1.y, (int)w1.z, 0, 0};
+        const v8i X = {(int)x0.x, (int)x0.y, (int)x0.z, (int)x1.x, (int)x1.y, (int)x1.z, 0, 0};
+        // both operands e3m2; block scales 127 (E8M0 2^0) select the scaled encoding
+        accf = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(W, X, accf, 3, 3, 0, 127, 0, 127);
     } else if constexpr (F == FMT_I8 || F == FMT_I8_SKIP) {
         acci = __builtin_amdgcn_mfma_i32_16x16x64_i8(as_v4i(w0), as_v4i(x0), acci, 0, 0, 0);
         acci = __builtin_amdgcn_mfma_i32_16x16x64_i8(as_v4i(w1), as_v4i(x1), acci, 0, 0, 0);

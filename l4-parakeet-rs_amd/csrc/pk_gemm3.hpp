@@ -263,7 +263,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm3_kernel(GemmArgs p) {
     // FP8 / INT8 read activation fragments two row blocks ahead (three in
     // registers), the others one ahead; the formats with registers to spare
     // keep the 8 load offsets instead of deriving them at issue time.
-    constexpr bool kAhead2 = F == FMT_FP8 || F == FMT_I8;
+    constexpr bool kAhead2 = F == FMT_FP8 || F == FMT_I8 || F == FMT_S4F6;
     constexpr bool kPreOff = F == FMT_I8_SKIP || F == FMT_F16;
     uint32_t a_off[kPreOff ? kAI : 1];
     uint32_t b_off[L::kBPerWave];
@@ -576,7 +576,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm3_kernel(GemmArgs p) {
 #pragma unroll
                     for (int bj = 0; bj < 4; ++bj) mfma_step<F>(accf[ai][bj], acci[ai][bj], w0[bj], w1[bj], xr0[ai % 3], xr1[ai % 3], gs[bj]);
                 }
-                constexpr int kMfma = F == FMT_FP8 ? 4 : 8;
+                constexpr int kMfma = F == FMT_I8 ? 8 : 4;
 #pragma unroll
                 for (int ai = 0; ai < kAI; ++ai) {
                     if (ai + 2 < kAI) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);

@@ -25,6 +25,7 @@ int launch_quantize_rows_sp24(const void* in, uint8_t* data, uint8_t* meta, floa
 int launch_pack_rows(int kind, const void* w, void* out, float* scales, int n, int k, hipStream_t s);
 int launch_q4k_dequant(const uint8_t* blocks, uint16_t* out, int n, int k, hipStream_t s);
 int launch_unpack_s4(const uint8_t* in, int8_t* out, size_t bytes, hipStream_t s);
+int launch_unpack_s4_fp6(const uint8_t* in, uint8_t* out, size_t bytes, hipStream_t s);
 int launch_expand_g128_e4m3(const uint32_t* q, const uint16_t* zeros, const uint16_t* scales, uint16_t* scales_t, uint8_t* out,
                             int n, int k, hipStream_t s);
 int launch_pack_g128(const void* w, uint32_t* q, uint16_t* scales, uint16_t* zeros, int n, int k, hipStream_t s);

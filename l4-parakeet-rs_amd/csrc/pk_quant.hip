@@ -56,6 +56,41 @@ __device__ __forceinline__ uint32_t low_bytes4(uint32_t a, uint32_t b, uint32_t 
     const uint32_t cd = __builtin_amdgcn_perm(d, c, 0x0c0c0400u);
     return __builtin_amdgcn_perm(cd, ab, 0x05040100u);
 }
+
+// FP6 e3m2 (sign, 3 exponent bits of bias 3, 2 mantissa bits) of an INT4 code
+// in -8..7 (the low byte of q as int8), exact: 1..8 are 2^e (1 + m / 4).
+__device__ __forceinline__ uint32_t e3m2_of_code(uint32_t q) {
+    const int v = (int)(int8_t)(q & 0xffu);
+    const uint32_t a = (uint32_t)(v < 0 ? -v : v);
+    // magnitudes 0..8 as 6-bit fields of one 64-bit constant
+    constexpr uint64_t kMag = 0x00ull | 0x0cull << 6 | 0x10ull << 12 | 0x12ull << 18 | 0x14ull << 24 | 0x15ull << 30 |
+                              0x16ull << 36 | 0x17ull << 42 | 0x18ull << 48;
+    return (uint32_t)(kMag >> (6 * a)) & 0x1fu | (v < 0 ? 0x20u : 0u);
+}
+
+// e3m2 bytes of four int8 codes in -8..7 (one per byte of c): per-byte
+// magnitude, the e3m2 magnitudes of 0..7 from one byte permute of an 8-byte
+// table, 8 (only -8 has it) patched in, then the sign bit.
+__device__ __forceinline__ uint32_t e3m2_bytes4(uint32_t c) {
+    const uint32_t neg = (c >> 7) & 0x01010101u;                                      // 1 in each negative byte
+    const uint32_t a = (c ^ (neg * 0xffu)) + neg;                                     // |code| per byte, 0..8
+    const uint32_t big = (a >> 3) & 0x01010101u;                                      // |code| == 8
+    const uint32_t lut = __builtin_amdgcn_perm(0x17161514u, 0x12100c00u, a & 0x07070707u);  // 0..3 | 4..7
+    return lut | big * 0x18u | neg * 0x20u;
+}
+
+// FP6 chunk layout of 16 codes (one 16-byte chunk: code j at bits 6j.. of its
+// first 12 bytes, then 4 zero bytes).  Lane t = lane % 4 of a quad holds
+// codes 4t..4t+3 of the chunk (the int8 bytes of c) and writes its dword t:
+// the 24 bits of its own codes shifted into place and the first bits of lane
+// t + 1's.
+__device__ __forceinline__ uint32_t e3m2_chunk_dword(uint32_t c, int lane) {
+    const uint32_t e = e3m2_bytes4(c);
+    const uint32_t piece = (e & 0x3fu) | ((e >> 2) & 0xfc0u) | ((e >> 4) & 0x3f000u) | ((e >> 6) & 0xfc0000u);
+    const uint32_t next = (uint32_t)dpp_mov<0xF9>((int)piece);  // quad_perm [1, 2, 3, 3]: lane t + 1's piece
+    const int t = lane & 3;
+    return t == 3 ? 0u : (piece >> (8 * t)) | (next << (24 - 8 * t));
+}
 __device__ __forceinline__ uint32_t e4m3x4_sat(float a, float b, float c, float d) {
     const float lo = -448.0f, hi = 448.0f;
     uint32_t w = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(__builtin_amdgcn_fmed3f(a, lo, hi), __builtin_amdgcn_fmed3f(b, lo, hi), 0, false);
@@ -472,7 +507,9 @@ __device__ __forceinline__ float ln_partials_sum(const float (&part)[4], float* 
 // the INT4 codes need no clamp (|y / scale| <= 8 (1 + 2^-23)).
 // kCodes (with kInt4): the INT4 codes as int8 bytes [rows x 1024] instead of
 // nibble pairs -- the operand the INT8 MFMA consumes, which has no 4-bit form.
-template <bool kInt4, bool kCodes = false>
+// kFp6 (with kCodes): the same codes as FP6 e3m2 chunks (e3m2_chunk_dword),
+// the operand of the f8f6f4 MFMA at the FP6 rate; same row size and stores.
+template <bool kInt4, bool kCodes = false, bool kFp6 = false>
 __global__ __launch_bounds__(256) void layer_norm_quantize_kernel(const uint16_t* __restrict__ in, const uint16_t* __restrict__ gamma,
                                                                   const uint16_t* __restrict__ beta, uint8_t* __restrict__ out,
                                                                   float* __restrict__ scales, uint16_t* __restrict__ normalized,
@@ -577,7 +614,9 @@ __global__ __launch_bounds__(256) void layer_norm_quantize_kernel(const uint16_t
                 uint32_t q[4];
 #pragma unroll
                 for (int u = 0; u < 4; ++u) q[u] = fast ? rne_bits(div_rn(y[u], scale, inv)) : (uint32_t)rne_clamp(y[u] / scale, -8, 7);
-                if constexpr (kCodes)
+                if constexpr (kFp6)
+                    *(uint32_t*)(o + 256 * i + 4 * lane) = e3m2_chunk_dword(low_bytes4(q[0], q[1], q[2], q[3]), lane);
+                else if constexpr (kCodes)
                     *(uint32_t*)(o + 256 * i + 4 * lane) = low_bytes4(q[0], q[1], q[2], q[3]);
                 else
                     *(uint16_t*)(o + 128 * i + 2 * lane) =
@@ -712,6 +751,35 @@ __global__ __launch_bounds__(256) void unpack_s4_kernel(const uint4* __restrict_
     out[2 * i + 1] = uint4{o[4], o[5], o[6], o[7]};
 }
 
+// Nibble pairs -> the FP6 e3m2 chunk layout of the same codes (16 codes a
+// 16-byte chunk: code j at bits 6j.. of the first 12 bytes, 4 zero bytes), 16
+// bytes in and 32 out per thread: the operand form for the f8f6f4 MFMA.
+__global__ __launch_bounds__(256) void unpack_s4_fp6_kernel(const uint4* __restrict__ in, uint4* __restrict__ out, size_t chunks) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= chunks) return;
+    const uint4 w = in[i];
+    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+        uint64_t bits[2] = {0, 0};  // 96 bits of 16 codes
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const uint32_t byte = (ws[2 * c + (j >> 3)] >> (8 * ((j >> 1) & 3))) & 0xffu;
+            const uint32_t nib = (j & 1) ? byte >> 4 : byte & 15u;
+            const uint32_t code = nib >= 8 ? nib - 16u : nib;  // low byte: the int8 code
+            const uint64_t f = e3m2_of_code(code);
+            const int b = 6 * j;
+            if (b < 64) {
+                bits[0] |= f << b;
+                if (b > 58) bits[1] |= f >> (64 - b);  // a field across the 64-bit boundary
+            } else {
+                bits[1] |= f << (b - 64);
+            }
+        }
+        out[2 * i + c] = uint4{(uint32_t)bits[0], (uint32_t)(bits[0] >> 32), (uint32_t)bits[1], 0u};
+    }
+}
+
 // INT4-g128 weights (pk_pack_int4_g128 layout) -> e4m3 (q - z) bytes [n x k]
 // in k order (|q - z| <= 15 is exact in e4m3), the weight operand of the
 // G128F8 GEMM: one thread per 4 words (32 K values of one group).
@@ -829,7 +897,10 @@ int launch_layer_norm_quantize(int mode, const void* in, const void* gamma, cons
                                void* normalized, int rows, int padded_rows, float epsilon, hipStream_t s) {
     if (padded_rows == 0) return 0;
     const unsigned grid = row_grid(padded_rows);
-    if (mode == 2)
+    if (mode == 3)
+        layer_norm_quantize_kernel<true, true, true><<<grid, 256, 0, s>>>((const uint16_t*)in, (const uint16_t*)gamma, (const uint16_t*)beta,
+                                                                          (uint8_t*)out, scales, (uint16_t*)normalized, rows, padded_rows, epsilon);
+    else if (mode == 2)
         layer_norm_quantize_kernel<true, true><<<grid, 256, 0, s>>>((const uint16_t*)in, (const uint16_t*)gamma, (const uint16_t*)beta,
                                                                     (uint8_t*)out, scales, (uint16_t*)normalized, rows, padded_rows, epsilon);
     else if (mode == 1)
@@ -860,6 +931,13 @@ int launch_unpack_s4(const uint8_t* in, int8_t* out, size_t bytes, hipStream_t s
     const size_t chunks = bytes / 16;
     if (chunks == 0) return 0;
     unpack_s4_kernel<<<(unsigned)((chunks + 255) / 256), 256, 0, s>>>((const uint4*)in, (uint4*)out, chunks);
+    return 0;
+}
+
+int launch_unpack_s4_fp6(const uint8_t* in, uint8_t* out, size_t bytes, hipStream_t s) {
+    const size_t chunks = bytes / 16;
+    if (chunks == 0) return 0;
+    unpack_s4_fp6_kernel<<<(unsigned)((chunks + 255) / 256), 256, 0, s>>>((const uint4*)in, (uint4*)out, chunks);
     return 0;
 }
 

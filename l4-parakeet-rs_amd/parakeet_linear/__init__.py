@@ -70,6 +70,8 @@ SIGNATURES = {
     "pk_layer_norm_pair": (I, [P, P, P, P, P, P, P, I, I, F, F, P]),
     "pk_layer_norm_quantize_int4_codes": (I, [P, P, P, P, P, I, I, F, P]),
     "pk_unpack_int4": (I, [P, P, ctypes.c_int64, P]),
+    "pk_layer_norm_quantize_int4_fp6": (I, [P, P, P, P, P, I, I, F, P]),
+    "pk_unpack_int4_fp6": (I, [P, P, ctypes.c_int64, P]),
     "pk_linear_fp16_epilogue": (I, [P, P, P, P, P, I, I, I, F, F, I, P]),
     "pk_linear_fp16_qkv": (I, [P, P, P, P, P, I, I, I, P]),
     "pk_linear_fp8_epilogue": (I, [P, P, P, P, P, I, I, I, F, I, P]),
@@ -85,6 +87,7 @@ SIGNATURES = {
     "pk_ffn_expand_fp8_packed": (I, [P, P, P, P, P, I, F, I, P]),
     "pk_ffn_expand_int4_sparse": (I, [P, P, P, P, P, I, F, I, P]),
     "pk_ffn_expand_int4_sparse_codes": (I, [P, P, P, P, P, I, F, I, P]),
+    "pk_ffn_expand_int4_sparse_fp6": (I, [P, P, P, P, P, I, F, I, P]),
     "pk_ffn_contract_fp8": (I, [P, P, P, P, I, P]),
     "pk_ffn_contract_fp8_sparse": (I, [P, P, P, P, I, I, P]),
     "pk_conv_residual_fp8": (I, [P, P, P, P, P, I, P]),
@@ -228,7 +231,7 @@ def gemm_k_split(fmt, epi, m, n, k):
     return r
 
 
-FMT_FP8, FMT_I8, FMT_S4, FMT_G128A8, FMT_F16, FMT_G128A16, FMT_I8_SKIP, FMT_Q4K, FMT_G128F8 = range(9)
+FMT_FP8, FMT_I8, FMT_S4, FMT_G128A8, FMT_F16, FMT_G128A16, FMT_I8_SKIP, FMT_Q4K, FMT_G128F8, FMT_S4F6 = range(10)
 EPI_F16, EPI_F8, EPI_F8_24, EPI_F32, EPI_I32 = range(5)
 
 

@@ -128,6 +128,39 @@ float orc_e4m3_to_f32(uint8_t bits) {
     return sign ? -magnitude : magnitude;
 }
 
+/* FP6 e3m2 (OCP MX formats: sign bit 5, exponent bits 4..2 with bias 3,
+ * mantissa bits 1..0, subnormals at exponent 0, no infinity or NaN).  No
+ * reference counterpart: the operand form of INT4 codes for the f8f6f4 MFMA. */
+float orc_e3m2_to_f32(uint8_t bits) {
+    const int exponent = (bits >> 2) & 7, mantissa = bits & 3;
+    const float magnitude = exponent == 0 ? ldexpf((float)mantissa / 4.0f, -2) : ldexpf(1.0f + (float)mantissa / 4.0f, exponent - 3);
+    return (bits & 0x20) ? -magnitude : magnitude;
+}
+
+/* The e3m2 bits of an integer in -8..8, found by searching the 32 positive
+ * encodings for the exact value (255 when none holds it). */
+uint8_t orc_e3m2_of_int(int v) {
+    const int a = v < 0 ? -v : v;
+    for (int bits = 0; bits < 32; ++bits)
+        if (orc_e3m2_to_f32((uint8_t)bits) == (float)a) return (uint8_t)(bits | (v < 0 ? 0x20 : 0));
+    return 255;
+}
+
+/* int8 codes [count] (count a multiple of 16) -> the FP6 chunk form: each 16
+ * codes one 16-byte chunk, code j's e3m2 bits at bits 6j..6j+5 of the chunk's
+ * first 12 bytes read as a little-endian 96-bit number, then 4 zero bytes. */
+void orc_fp6_chunks(const int8_t* codes, size_t count, uint8_t* out) {
+    for (size_t c = 0; c < count / 16; ++c) {
+        uint8_t* o = out + 16 * c;
+        memset(o, 0, 16);
+        for (int j = 0; j < 16; ++j) {
+            const unsigned f = orc_e3m2_of_int(codes[16 * c + j]);
+            for (int b = 0; b < 6; ++b)
+                if ((f >> b) & 1u) o[(6 * j + b) >> 3] |= (uint8_t)(1u << ((6 * j + b) & 7));
+        }
+    }
+}
+
 /* quant_benchmark.rs:827-829: round half to even, then clamp to +-127. */
 int8_t orc_quantize_i8(float value) {
     float r = nearbyintf(value);

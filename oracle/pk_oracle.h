@@ -24,6 +24,9 @@ uint16_t orc_f32_to_f16(float value);
 float orc_f16_to_f32(uint16_t bits);
 uint8_t orc_f32_to_e4m3(float value);
 float orc_e4m3_to_f32(uint8_t bits);
+float orc_e3m2_to_f32(uint8_t bits);
+uint8_t orc_e3m2_of_int(int v);
+void orc_fp6_chunks(const int8_t* codes, size_t count, uint8_t* out);
 int8_t orc_quantize_i8(float value);
 float orc_pattern(uint64_t index, uint64_t salt, float amplitude);
 void orc_pattern_fill(float* out, size_t count, uint64_t first_index, uint64_t salt,

@@ -47,6 +47,9 @@ def _declare(l):
         "orc_f16_to_f32": (F, [ctypes.c_uint16]),
         "orc_f32_to_e4m3": (ctypes.c_uint8, [F]),
         "orc_e4m3_to_f32": (F, [ctypes.c_uint8]),
+        "orc_e3m2_to_f32": (F, [ctypes.c_uint8]),
+        "orc_e3m2_of_int": (ctypes.c_uint8, [I]),
+        "orc_fp6_chunks": (None, [P, S, P]),
         "orc_quantize_i8": (ctypes.c_int8, [F]),
         "orc_pattern": (F, [ctypes.c_uint64, ctypes.c_uint64, F]),
         "orc_pattern_fill": (None, [P, S, ctypes.c_uint64, ctypes.c_uint64, F]),
@@ -139,6 +142,23 @@ def e4m3_table() -> np.ndarray:
 
 def e4m3_to_f32(codes) -> np.ndarray:
     return e4m3_table()[np.asarray(codes, dtype=np.uint8)]
+
+
+def e3m2_to_f32(bits: int) -> float:
+    return lib().orc_e3m2_to_f32(int(bits))
+
+
+def e3m2_of_int(v: int) -> int:
+    return lib().orc_e3m2_of_int(int(v))
+
+
+def fp6_chunks(codes: np.ndarray) -> np.ndarray:
+    """int8 codes (any shape, size a multiple of 16) -> the FP6 e3m2 chunk form
+    as uint8 of the same shape (orc_fp6_chunks)."""
+    c = np.ascontiguousarray(codes, dtype=np.int8)
+    out = np.empty(c.shape, dtype=np.uint8)
+    lib().orc_fp6_chunks(_p(c), c.size, _p(out))
+    return out
 
 
 def f32_to_f16_bits(values) -> np.ndarray:
