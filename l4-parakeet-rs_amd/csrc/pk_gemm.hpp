@@ -234,14 +234,18 @@ __device__ __forceinline__ void mfma_step(v4f& accf, v4i& acci, const uint4& w0,
 // LDS bytes [lds_addr + 16 l, + 16).  lds_addr must be wave-uniform.  Issued
 // from inline asm so that the compiler does not order every later LDS read
 // behind the load (it cannot tell the DMA target from the buffer being read);
-// the step loop waits for these loads explicitly.
+// the step loop waits for these loads explicitly.  An LDS DMA reading M0
+// needs one wait state after the SALU write of M0 (the compiler inserts it
+// for the builtin, not inside inline asm), hence the s_nop.
 __device__ __forceinline__ void dma16(const void* src, uint32_t lds_addr) {
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(__builtin_amdgcn_readfirstlane(lds_addr))
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src),
+                 "s"(__builtin_amdgcn_readfirstlane(lds_addr))
                  : "memory", "m0");
 }
 // Same with a wave-uniform 64-bit base (SGPR pair) and a 32-bit lane offset.
 __device__ __forceinline__ void dma16(const uint8_t* base, uint32_t off, uint32_t lds_addr) {
-    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(__builtin_amdgcn_readfirstlane(lds_addr))
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base),
+                 "s"(__builtin_amdgcn_readfirstlane(lds_addr))
                  : "memory", "m0");
 }
 
