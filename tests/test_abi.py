@@ -216,3 +216,40 @@ def test_unpack_int4_rejects_bad_shapes(lib):
     assert fn(None, None, 0, None) == 0          # nothing to do, no GPU work
     assert fn(None, None, 33, None) < 0          # not a multiple of 32
     assert fn(None, None, 64, None) < 0          # missing pointers
+
+
+def test_fp6_entry_points_reject_before_any_launch(lib):
+    """The FP6 form of INT4 codes: pk_gemm format 9 takes only the 2:4 and fp32
+    epilogues and k a multiple of 128; the producer, unpack and expand entry
+    points check counts, nulls and alignment before touching a device."""
+    E_SHAPE, E_ALIGN, E_ARG = -1, -2, -4
+    vp, i32, f32 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_float
+    err = lib.pk_last_error
+    err.restype = ctypes.c_char_p
+    g = lib.pk_gemm
+    g.argtypes = [i32, i32, vp, vp, i32, i32, i32, vp, vp, f32, vp, vp, f32, f32, i32, vp, vp, vp, vp, i32, vp]
+    g.restype = i32
+    args = lambda epi, k: (9, epi, 0x10000, 0x20000, 16, 16, k, None, None, 1.0, None, None, 1.0, 0.0, 0, None, None,
+                           0x30000, 0x40000, 16, None)
+    assert g(*args(0, 128)) == E_ARG  # fp16 outputs are not a format 9 epilogue
+    assert b"unsupported epilogue" in err()
+    assert g(*args(3, 64)) == E_SHAPE  # k must be a multiple of 128
+    assert b"multiple of 128" in err()
+    u = lib.pk_unpack_int4_fp6
+    u.argtypes = [vp, vp, ctypes.c_int64, vp]
+    u.restype = i32
+    assert u(None, None, 0, None) == 0
+    assert u(None, None, 33, None) == E_SHAPE
+    assert u(None, None, 64, None) == E_ARG
+    assert u(0x10008, 0x20000, 64, None) == E_ALIGN
+    ln = lib.pk_layer_norm_quantize_int4_fp6
+    ln.argtypes = [vp, vp, vp, vp, vp, i32, i32, f32, vp]
+    ln.restype = i32
+    assert ln(0x10000, 0x20000, 0x30000, 0x40002, 0x50000, 4, 4, 1e-5, None) == E_ALIGN
+    assert ln(0x10000, 0x20000, 0x30000, 0x40000, 0x50000, 5, 4, 1e-5, None) == E_SHAPE
+    ex = lib.pk_ffn_expand_int4_sparse_fp6
+    ex.argtypes = [vp, vp, vp, vp, vp, i32, f32, i32, vp]
+    ex.restype = i32
+    assert ex(None, 0x20000, 0x30000, 0x40000, 0x50000, 16, 1.0, 1, None) == E_ARG
+    assert ex(0x10000, 0x20000, 0x30000, None, 0x50000, 16, 1.0, 1, None) == E_ARG  # dynamic needs input scales
+    assert ex(0x10000, 0x20000, 0x30000, 0x40000, 0x50000, -1, 1.0, 1, None) == E_SHAPE
