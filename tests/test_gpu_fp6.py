@@ -123,3 +123,28 @@ def test_fp6_expand_equals_codes(pk, t):
     pk.call("pk_ffn_expand_int4_sparse_codes", xc, wc, ws, xcs, c, pad, 1.0, 1)
     pk.call("pk_ffn_expand_int4_sparse_fp6", xf, wf, ws, xfs, f, pad, 1.0, 1)
     assert torch.equal(c, f)
+
+
+def test_fp6_producer_nonfinite_rows(pk, orc):
+    """Rows holding inf / NaN / huge values take the producer's exact
+    (slow) path; their FP6 codes still equal the FP6 form of the int8 codes."""
+    t, pad = 96, 112
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(2801)
+    x = (torch.randn((pad, D), generator=gen, device="cuda") * 2).half()
+    x[3, 17] = float("inf")
+    x[5, 900] = float("-inf")
+    x[8, 5] = float("nan")
+    x[11, :] = 65504.0
+    x[12, ::2] = -65504.0
+    g, b = ln_params(gen)
+    xc = torch.full((pad, D), 5, dtype=torch.int8, device="cuda")
+    xf = torch.full((pad, D), 0x5A, dtype=torch.uint8, device="cuda")
+    s1 = torch.empty(pad, dtype=torch.float32, device="cuda")
+    s2 = torch.empty(pad, dtype=torch.float32, device="cuda")
+    pk.call("pk_layer_norm_quantize_int4_codes", x, g, b, xc, s1, t, pad, 1e-5)
+    pk.call("pk_layer_norm_quantize_int4_fp6", x, g, b, xf, s2, t, pad, 1e-5)
+    assert np.array_equal(host(s1).view(np.uint32), host(s2).view(np.uint32))  # NaN scales compare by bits
+    codes = host(xc)
+    assert codes.min() >= -8 and codes.max() <= 7
+    assert np.array_equal(host(xf), orc.fp6_chunks(codes))
